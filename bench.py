@@ -1,0 +1,191 @@
+"""Prefill throughput of the 105M-scale PSSA model on one MI355X.
+
+Workload: d_latent=768, d_state=256, 12 layers,
+vocab 16384, d_mem_key=32, 512-slot banks (populated), bf16 weights with fp32
+accumulation and fp32 scan state; 32 lanes x 1024 uniform random token ids.
+One step = one prefill pass over the batch from zero carries, ending with the
+last-token head of every lane (src/pssa.rs:2399-2442).  Inputs (weights, banks,
+ids) are resident in HBM before the timed region.
+
+Prints one JSON line (driver contract).  `cpu_baseline` times the oracle's
+restatement of the reference's scalar prefill on the host cores over a bounded
+sample of the same workload (port).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+# MI355X published peaks.
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_TFLOPS = 2500.0
+FP32_TFLOPS = 157.3
+
+
+def model_config(args):
+    from pssa_amd import PSSAConfig
+
+    return PSSAConfig(depth=args.layers, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32,
+                      mem_capacity=512, tau_mem=0.1)
+
+
+def stage_work(cfg, lanes, T):
+    """Algorithmic flops / bytes per stage for one prefill pass."""
+    d, s, k, C, r, V, L = cfg.d_latent, cfg.d_state, cfg.d_mem_key, cfg.mem_capacity, cfg.adapter_rank, \
+        cfg.d_vocab, cfg.depth
+    N = lanes * T
+    n_in = 2 * d + 2 * s + k + r
+    gemm_mac_tok = d * n_in + d * k + C * d + d * d + d * r + 2 * d * d + 2 * d * d
+    return {
+        "gemm_flops": 2.0 * gemm_mac_tok * N * L + 2.0 * lanes * V * d,
+        "ssm_elems": float(N) * d * s * L,
+        # per element: v_mul (exponent), v_exp, v_mul (B x), fma (h), fma (y)
+        "ssm_flops": 7.0 * N * d * s * L,
+        # HBM bytes the scan must move once: delta, x, y (fp32 [N,d]) and B, C ([N,s]) per layer
+        "ssm_bytes": (3.0 * N * d + 2.0 * N * s) * 4 * L,
+        "dist_pairs": float(N) * C * L,
+    }
+
+
+def cpu_baseline(weights, ids, budget_s: float):
+    """Times the oracle's scalar prefill (one thread per lane) on a bounded
+    prefix sample of the benchmark workload."""
+    from oracle import oracle as O
+
+    threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1, 64))
+    lanes = min(threads, ids.shape[0])
+    om = O.OracleModel(weights)
+    # Probe the per-token cost, then size the sample to the budget.
+    probe = 4
+    st = om.zero_state(1)
+    t0 = time.perf_counter()
+    om.prefill_lanes(st, ids[:1, :probe], threads=1, logits=False)
+    per_tok = (time.perf_counter() - t0) / probe
+    T = int(max(8, min(ids.shape[1], budget_s / per_tok)))
+    states = om.zero_state(lanes)
+    t0 = time.perf_counter()
+    om.prefill_lanes(states, ids[:lanes, :T], threads=lanes, logits=True)
+    wall = time.perf_counter() - t0
+    return {
+        "value": lanes * T / wall,
+        "unit": "tokens/s",
+        "cores": lanes,
+        "kind": "port",
+        "sample": f"{lanes} lanes x first {T} tokens of the benchmark ids, one thread per lane, "
+                  f"oracle prefill_inference restatement (AVX2 dot tree), {wall:.1f} s wall",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--dtype", choices=["bf16", "f32"], default="bf16")
+    ap.add_argument("--lanes", type=int, default=32)
+    ap.add_argument("--seq", type=int, default=1024)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (sharding is described in "
+              "DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from pssa_amd import HipDevice, ModelWeights, PSSALayer
+
+    cfg = model_config(args)
+    log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
+    log("building weights", cfg)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    ids = np.random.default_rng(0).integers(0, cfg.d_vocab, (args.lanes, args.seq), dtype=np.uint32)
+
+    dev = HipDevice(0)
+    layer = PSSALayer(dev, w, lanes=args.lanes, max_tokens=args.lanes * args.seq, weight_dtype=args.dtype)
+    layer.stage_ids(ids)
+    log("device", dev.backend_label())
+
+    def step():
+        layer.reset_recurrent_state()
+        layer.prefill_staged()
+
+    for _ in range(args.warmup):
+        step()
+    dev.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    dev.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    tokens = args.lanes * args.seq
+    logits = layer.read_logits()
+    assert np.all(np.isfinite(logits))
+
+    # Per-kernel durations from HIP events on the library's stream (one extra pass).
+    layer.set_stage_timing(True)
+    step()
+    dev.synchronize()
+    stages = layer.stage_times()
+    layer.set_stage_timing(False)
+    log("stage ms", json.dumps({k: round(v, 3) for k, v in stages.items()}))
+
+    work = stage_work(cfg, args.lanes, args.seq)
+    ssm_ms = stages.get("ssm_scan", 0.0)
+    ssm_launch_ms = ssm_ms / cfg.depth
+    ssm_tflops = work["ssm_flops"] / (ssm_ms * 1e-3) / 1e12 if ssm_ms else 0.0
+    gemm_ms = sum(v for k_, v in stages.items() if k_.startswith("gemm") or k_ == "head")
+    roofline = {
+        "kernel": "ssm_scan",
+        "bound": "valu",
+        "achieved": round(ssm_tflops, 3),
+        "peak": FP32_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(ssm_tflops / FP32_TFLOPS, 4),
+        "traffic": None,
+        "launch_ms": round(ssm_launch_ms, 4),
+        "flops_per_launch": work["ssm_flops"] / cfg.depth,
+        "gemm_tflops": round(work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None,
+        "gemm_frac_bf16": round(work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12 / BF16_MFMA_TFLOPS, 4) if gemm_ms else None,
+    }
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(w, ids, args.cpu_budget)
+    line = {
+        "metric": "prefill tokens/sec + % roofline (MFMA util / HBM GB/s), 105M PSSA, 1xMI355X",
+        "value": tokens / (elapsed / args.steps),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (uniform random ids, seeded N(0,0.02) weights, banks filled with 512 slots)",
+        "config": {"workload": f"105M PSSA prefill: d768 s256 k32 L{cfg.depth} V16384 C512, "
+                               f"{args.lanes} lanes x {args.seq} tokens, {args.dtype} weights",
+                   "lanes": args.lanes, "seq_len": args.seq, "params": cfg.parameter_count()},
+        "stage_ms": {k_: round(v, 4) for k_, v in stages.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    layer.close()
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

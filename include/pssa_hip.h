@@ -1,0 +1,266 @@
+/*
+ * pssa_hip.h -- C ABI of the MI355X (gfx950) PSSA inference forward path.
+ *
+ * This is the drop-in boundary a Rust FFI crate binds to add a `Hip` variant
+ * next to the reference's CPU / WebGPU / CUDA backends.  It mirrors the
+ * reference's backend surface (Sparticle62ops/pssa):
+ *
+ *   enum Device / enum GpuDispatch ........ src/backend.rs:1013-1446
+ *   CudaContext::init / fatal policy ...... src/cuda.rs:169-192, 592-602
+ *   PSSALayerV2::{forward_inference,
+ *                 prefill_inference} ...... src/pssa.rs:2387-2442
+ *
+ * Conventions (same as the reference's contract, src/backend.rs:11-48,
+ * src/cuda.rs:520-589):
+ *   - All matrices are row-major.  Y = X * W^T with X [batch*M, K], W [N, K].
+ *   - Every pointer comes with its element count; counts and shapes are
+ *     validated before any allocation or launch.  On a validation error the
+ *     return is PSSA_HIP_EINVAL, `err` holds the reason, outputs are untouched.
+ *   - Calls taking host buffers are synchronous: they return after the results
+ *     are copied back and the stream is synchronised.
+ *   - Errors raised by the device after a launch are fatal
+ *     (pssa_hip_is_fatal() != 0): the caller must not fall back silently,
+ *     matching panic_if_fatal_cuda_error (src/cuda.rs:592-602).
+ *   - A context may be used from one thread at a time (the reference
+ *     serialises its CUDA context behind a Mutex, src/cuda.rs:155-166); this
+ *     library locks internally.
+ *   - `err`/`err_len` may be NULL/0.
+ */
+#ifndef PSSA_HIP_H
+#define PSSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PSSA_HIP_ABI_VERSION 1
+
+/* Status codes. */
+#define PSSA_HIP_OK 0
+#define PSSA_HIP_EINVAL (-1)      /* argument/shape validation failed, nothing ran */
+#define PSSA_HIP_ENODEV (-2)      /* no usable gfx950 device */
+#define PSSA_HIP_ENOMEM (-3)      /* device allocation failed, nothing ran */
+#define PSSA_HIP_EDEVICE (-4)     /* HIP runtime or kernel failure: fatal */
+#define PSSA_HIP_EUNSUPPORTED (-5)
+
+/* Weight storage types. */
+#define PSSA_HIP_F32 0
+#define PSSA_HIP_BF16 1
+
+/* Weight initialisation modes (pssa_hip_weights_init). */
+#define PSSA_HIP_INIT_REFERENCE 0 /* PSSALayerV2::new draw order, src/pssa.rs:2019-2072 */
+#define PSSA_HIP_INIT_BASELINE 1  /* seeded N(0, 0.02) for every matrix, HiPPO rates */
+
+typedef struct pssa_hip_ctx pssa_hip_ctx;       /* device context (CudaContext peer) */
+typedef struct pssa_hip_model pssa_hip_model;   /* device-resident weights + banks   */
+typedef struct pssa_hip_lanes pssa_hip_lanes;   /* per-lane carries + workspaces     */
+
+/* Model dimensions: PSSAConfigV2 (src/pssa.rs:254-331) fields used by the
+ * forward path.  adapter_rank is the adapter's fixed rank (16 in the
+ * reference, src/pssa.rs:644). */
+typedef struct {
+  uint64_t depth;
+  uint64_t d_vocab;
+  uint64_t d_latent;
+  uint64_t d_state;
+  uint64_t d_mem_key;
+  uint64_t mem_capacity;
+  uint64_t adapter_rank;
+  float tau_mem;
+  uint32_t _pad;
+} pssa_hip_config;
+
+/* Host view of one PSSAContinuousBlockV2 (src/pssa.rs:506-620).  d=d_latent,
+ * s=d_state, k=d_mem_key, C=mem_capacity, r=adapter_rank. */
+typedef struct {
+  float* norm_gamma;       /* [d]            norm_gamma.data                 */
+  float* norm_beta;        /* [d]            norm_beta.data                  */
+  float* a_raw;            /* [d*s]          a_mat.data (A = -softplus(raw)) */
+  float* w_delta;          /* [d,d]                                          */
+  float* w_b;              /* [s,d]                                          */
+  float* w_c;              /* [s,d]                                          */
+  float* w_qx;             /* [k,d]                                          */
+  float* w_qh;             /* [k,d]                                          */
+  float* w_gate;           /* [d,d]                                          */
+  float* w_proj;           /* [d,d]                                          */
+  float* adapter_down;     /* [r,d]          adapters[0].down_proj           */
+  float* adapter_up;       /* [d,r]          adapters[0].up_proj (fast)      */
+  float* adapter_slow;     /* [d,r]          adapters[0].consolidated_up     */
+  float* mlp_w1;           /* [2d,d]                                         */
+  float* mlp_w2;           /* [d,2d]                                         */
+  float* mem_keys;         /* [C,k]          memory.keys                     */
+  float* mem_values;       /* [C,d]          memory.values                   */
+  float* mem_norm_sq;      /* [C]            memory.norm_sq                  */
+  float* mem_confidence;   /* [C]            memory.confidence               */
+  uint64_t* mem_last_seen; /* [C]            memory.last_seen_step           */
+  uint64_t mem_count;      /*                memory.count                    */
+  uint64_t mem_write_head; /*                memory.write_head               */
+} pssa_hip_block;
+
+/* Host view of PSSALayerV2's inference parameters (src/pssa.rs:1920-1960). */
+typedef struct {
+  pssa_hip_config cfg;
+  float* embed;            /* [V,d] embed_w.data   */
+  float* unembed;          /* [V,d] unembed_w.data */
+  pssa_hip_block* blocks;  /* [depth]: block, extra_blocks... */
+} pssa_hip_weights;
+
+/* ---------------------------------------------------------------- context */
+
+int pssa_hip_abi_version(void);
+
+/* Device::try_gpu / CudaContext::init (src/backend.rs:1467-1482,
+ * src/cuda.rs:169-192).  Fails with PSSA_HIP_ENODEV unless `device` is a
+ * gfx950 agent. */
+int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len);
+void pssa_hip_destroy(pssa_hip_ctx* ctx);
+/* GpuDispatch::backend_label (src/backend.rs:1439). */
+int pssa_hip_device_name(const pssa_hip_ctx* ctx, char* out, size_t out_len);
+/* panic_if_fatal_cuda_error classification (src/cuda.rs:592-602). */
+int pssa_hip_is_fatal(int code);
+int pssa_hip_synchronize(pssa_hip_ctx* ctx, char* err, size_t err_len);
+
+/* ------------------------------------------------- host-side weight set-up
+ * These run on the host only (no device needed). */
+
+/* PSSALayerV2::new (src/pssa.rs:2019-2072) when mode == PSSA_HIP_INIT_REFERENCE:
+ * SimpleRng xorshift64* (src/linalg.rs:1-28), Xavier-uniform matrices
+ * (src/pssa.rs:86-101) in the reference draw order, HiPPO log-spaced rates
+ * (src/pssa.rs:649-665), zero mlp_w2 / adapter up (src/pssa.rs:683,
+ * src/adapter.rs:19), empty banks.  Returns the final RNG state in *rng_state. */
+int pssa_hip_weights_init(const pssa_hip_weights* w, uint64_t seed, int mode,
+                          uint64_t* rng_state, char* err, size_t err_len);
+/* Inserts `count` slots into every block's bank through insert()
+ * (src/memory.rs:264-303): keys and values uniform in direction with radius
+ * U[0, max_radius). */
+int pssa_hip_weights_populate_banks(const pssa_hip_weights* w, uint64_t seed, uint64_t count,
+                                    float max_radius, char* err, size_t err_len);
+
+/* ---------------------------------------------- stage dispatch (GpuDispatch)
+ * Host buffers in, host buffers out, synchronous. */
+
+/* GpuDispatch::try_dispatch_gemm_into (src/backend.rs:1049-1085):
+ * y[batch*m, n] = x[batch*m, k] * w[n, k]^T.  w_dtype selects the storage of
+ * `w` (F32, or BF16 as uint16 bit patterns); accumulation is fp32. */
+int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const void* w,
+                      size_t w_len, int w_dtype, size_t m, size_t n, size_t k, size_t batch,
+                      float* y, size_t y_len, char* err, size_t err_len);
+
+/* GpuDispatch::softplus_in_place (src/backend.rs:1419-1428). */
+int pssa_hip_softplus_in_place(pssa_hip_ctx* ctx, float* values, size_t len, char* err,
+                               size_t err_len);
+
+/* GpuDispatch::ssm_forward (src/backend.rs:1213-1244):
+ *   bar_a = exp(delta_i * rate_ij), bar_b = delta_i * b_j,
+ *   h_t = bar_a * h_{t-1} + bar_b * x_i,  y_ti = sum_j h_tij * c_tj.
+ * delta/x_norm [L,d], b_proj/c_proj [L,s], rates [d*s] (already -softplus),
+ * initial [d*s].  bar_a/bar_b [L*d*s], states [(L+1)*d*s] and final_state
+ * [d*s] are optional (NULL = not materialised); y_ssm [L,d] is required.
+ * delta_raw / rate_deriv are the reference's backward inputs; they are
+ * accepted for signature parity and may be NULL. */
+int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len,
+                         const float* delta_raw, const float* b_proj, size_t b_len,
+                         const float* x_norm, size_t x_len, const float* rates, size_t rates_len,
+                         const float* rate_deriv, const float* c_proj, size_t c_len,
+                         const float* initial, size_t initial_len, size_t seq_len, size_t d_m,
+                         size_t d_s, float* bar_a, float* bar_b, float* states, float* y_ssm,
+                         size_t y_len, float* final_state, char* err, size_t err_len);
+
+/* GpuDispatch::memory_forward (src/backend.rs:1345-1385) for seq_len rows:
+ *   q_euc = x_norm W_qx^T + y_ssm W_qh^T; q_pnc = project(q_euc);
+ *   soft read over `count` slots (retrieve_soft_into, src/memory.rs:344-426)
+ *   or exact top_k (top_k = 0: full soft read);
+ *   g_mem = sigmoid(x_norm W_gate^T); m_proj = m_val W_proj^T; m_inj = g_mem*m_proj.
+ * Outputs: q_euc/q_pnc [L,k], q_norm [L], weights [L,capacity], m_val/g_mem/
+ * m_proj/m_inj [L,d_val].  Any output except m_inj may be NULL. */
+int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float* y_ssm,
+                            const float* w_qx, const float* w_qh, const float* w_gate,
+                            const float* w_proj, const float* keys, const float* norm_sq,
+                            const float* values, size_t seq_len, size_t d_m, size_t d_k,
+                            size_t d_val, size_t capacity, size_t count, float tau, size_t top_k,
+                            float* q_euc, float* q_pnc, float* q_norm, float* weights,
+                            float* m_val, float* g_mem, float* m_proj, float* m_inj, char* err,
+                            size_t err_len);
+
+/* Batched retrieve_soft_into (src/memory.rs:344-426; the reference's parallel
+ * per-query read, src/gpu_batch.rs:700-740) for n_q projected queries
+ * q_pnc [n_q, d_key] over `count` occupied slots.  top_k = 0: full soft
+ * read; otherwise exact top-k by (distance bits, slot).  out_val
+ * [n_q, d_val] required; out_min [n_q], out_idx [n_q, top_k] (ascending slot
+ * order) and out_weights [n_q, capacity] optional. */
+int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                      const float* norm_sq, const float* values, size_t capacity, size_t count,
+                      size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
+                      float* out_min, uint32_t* out_idx, float* out_weights, char* err,
+                      size_t err_len);
+
+/* Dense-transition scan h_t = A_t h_{t-1} + b_t (no reference counterpart:
+ * the reference's SSM is diagonal; this is the standalone dense kernel).
+ * a [batch, L, s, s] row-major (h_t[r] = sum_c A_t[r][c] h_{t-1}[c] + b_t[r]),
+ * b [batch, L, s], h0 [batch, s] (NULL = zeros), h [batch, L, s]. */
+int pssa_hip_dense_scan(pssa_hip_ctx* ctx, const float* a, const float* b, const float* h0,
+                        size_t batch, size_t seq_len, size_t d_state, float* h, char* err,
+                        size_t err_len);
+
+/* Same recurrence on device-resident buffers (plain device pointers from any
+ * allocator); asynchronous on the context stream. */
+int pssa_hip_dense_scan_resident(pssa_hip_ctx* ctx, const float* d_a, const float* d_b,
+                                 const float* d_h0, size_t batch, size_t seq_len, size_t d_state,
+                                 float* d_h, char* err, size_t err_len);
+
+/* ------------------------------------------------------------ model paths */
+
+/* Upload the weights (converted to `weight_dtype`), banks and the cached
+ * rates -softplus(a_raw) (refresh_ssm_rates, src/pssa.rs:787-796). */
+int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight_dtype,
+                        pssa_hip_model** out, char* err, size_t err_len);
+void pssa_hip_model_free(pssa_hip_model* model);
+
+/* Independent lanes (SequenceBatch, src/sequence_batch.rs:21-78) sharing one
+ * model: each lane owns a carry [depth, d*s] (h_persistent per block).
+ * max_tokens bounds lanes*seq_len of a prefill call.  Carries start at zero. */
+int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t lanes,
+                          size_t max_tokens, pssa_hip_lanes** out, char* err, size_t err_len);
+void pssa_hip_lanes_free(pssa_hip_lanes* lanes);
+/* reset_recurrent_state (src/pssa.rs:2245-2250) for every lane. */
+int pssa_hip_lanes_reset(pssa_hip_lanes* lanes, char* err, size_t err_len);
+/* carry layout [lanes, depth, d*s]. */
+int pssa_hip_lanes_get_carry(pssa_hip_lanes* lanes, float* out, size_t len, char* err,
+                             size_t err_len);
+int pssa_hip_lanes_set_carry(pssa_hip_lanes* lanes, const float* in, size_t len, char* err,
+                             size_t err_len);
+
+/* prefill_inference (src/pssa.rs:2399-2442) on every lane: ids [lanes, seq_len]
+ * continue each lane's carry; logits_last [lanes, V] receives the last
+ * token's logits (may be NULL for a zero generation budget).  An id >= V
+ * fails with PSSA_HIP_EINVAL before anything runs. */
+int pssa_hip_prefill(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes, size_t seq_len,
+                     float* logits_last, size_t logits_len, char* err, size_t err_len);
+
+/* forward_inference (src/pssa.rs:2387-2391): one token per lane. */
+int pssa_hip_forward_inference(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
+                               float* logits, size_t logits_len, char* err, size_t err_len);
+
+/* Device-resident prefill for measurement: stage ids on the device once,
+ * then run prefill with no host traffic (asynchronous on the context stream;
+ * pssa_hip_synchronize or a read completes it). */
+int pssa_hip_lanes_stage_ids(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
+                             size_t seq_len, char* err, size_t err_len);
+int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* lanes, char* err, size_t err_len);
+int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, char* err,
+                               size_t err_len);
+
+/* Per-stage kernel time (ms, summed over layers) of the most recent prefill,
+ * recorded with HIP events on the stream the kernels run on.  enable = 1 turns
+ * recording on for later calls, 0 off, -1 leaves it unchanged.  names/ms
+ * arrays of `cap` entries (either may be NULL); returns the number of stages. */
+int pssa_hip_lanes_stage_times(pssa_hip_lanes* lanes, int enable, const char** names, float* ms,
+                               size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PSSA_HIP_H */

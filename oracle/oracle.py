@@ -1,0 +1,251 @@
+"""ctypes wrapper of oracle/liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+The CPU restatement of the reference's scalar path (oracle/pssa_oracle.cpp).
+Used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as the
+checker; never by the product path.  Model views are the product's own
+`pssa_hip_weights` structs (identical layout to `oracle_model`).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+fp = C.POINTER(C.c_float)
+u32p = C.POINTER(C.c_uint32)
+vp = C.c_void_p
+
+_lib = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-f", os.path.join("oracle", "Makefile"), "-B"], cwd=ROOT, check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    L = C.CDLL(LIB_PATH)
+    sig = {
+        "oracle_set_dot_avx2": ([C.c_int], None),
+        "oracle_get_dot_avx2": ([], C.c_int),
+        "oracle_rng_new": ([C.c_uint64], C.c_uint64),
+        "oracle_rng_next_u32": ([C.POINTER(C.c_uint64)], C.c_uint32),
+        "oracle_dot": ([fp, fp, C.c_size_t], C.c_float),
+        "oracle_softplus": ([C.c_float], C.c_float),
+        "oracle_sigmoid": ([C.c_float], C.c_float),
+        "oracle_init_reference": ([vp, C.c_uint64], C.c_uint64),
+        "oracle_init_baseline": ([vp, C.c_uint64], C.c_uint64),
+        "oracle_populate_banks": ([vp, C.c_uint64, C.c_uint64, C.c_float], None),
+        "oracle_squared_norm": ([fp, C.c_size_t], C.c_float),
+        "oracle_project": ([fp, fp, C.c_size_t], C.c_float),
+        "oracle_poincare_distance": ([fp, C.c_float, fp, C.c_float, C.c_size_t], C.c_float),
+        "oracle_rust_asinh": ([C.c_double], C.c_double),
+        "oracle_retrieve": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_float,
+                             C.c_size_t, fp, fp], C.c_float),
+        "oracle_retrieve_batch": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_size_t,
+                                   C.c_float, C.c_size_t, fp, fp, u32p, C.c_int], None),
+        "oracle_bank_insert": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp], C.c_int64),
+        "oracle_bank_insert_protected": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float,
+                                          C.c_uint64], C.c_int64),
+        "oracle_refractory_gain": ([C.c_uint64, C.c_float], C.c_float),
+        "oracle_gemm_xwt": ([fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp], None),
+        "oracle_ssm_forward": ([fp, fp, fp, fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, fp, fp], None),
+        "oracle_forward_inference": ([vp, fp, C.c_uint32, fp], None),
+        "oracle_prefill": ([vp, fp, u32p, C.c_size_t, fp], C.c_int),
+        "oracle_prefill_lanes": ([vp, fp, u32p, C.c_size_t, C.c_size_t, fp, C.c_int], C.c_int),
+        "oracle_train_chunk_forward": ([vp, fp, u32p, u32p, C.c_size_t, fp], C.c_float),
+        "oracle_forward_features": ([vp, fp, C.c_uint32, fp], None),
+        "oracle_greedy": ([fp, C.c_size_t], C.c_uint32),
+        "oracle_dense_scan": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_int], None),
+        "oracle_hebbian_update": ([fp, fp, fp, fp, C.c_size_t, C.c_size_t], None),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def ptr(a, ctype=C.c_float):
+    if a is None:
+        return None
+    return a.ctypes.data_as(C.POINTER(ctype))
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Dot:
+    """Context manager selecting the reference's dot reduction tree."""
+
+    def __init__(self, avx2: bool):
+        self.avx2 = avx2
+
+    def __enter__(self):
+        self.prev = lib().oracle_get_dot_avx2()
+        lib().oracle_set_dot_avx2(1 if self.avx2 else 0)
+
+    def __exit__(self, *exc):
+        lib().oracle_set_dot_avx2(self.prev)
+
+
+class OracleModel:
+    """Runs the oracle on a product ModelWeights (aliasing its numpy arrays)."""
+
+    def __init__(self, weights):
+        self.w = weights
+        self.cfg = weights.cfg
+        self.view, self.keep = weights.c_view()
+        self.ref = C.cast(C.pointer(self.view), vp)
+
+    def sync(self):
+        self.w.sync_from_c(self.keep)
+
+    def zero_state(self, lanes: int | None = None) -> np.ndarray:
+        shape = (self.cfg.depth, self.cfg.d_latent * self.cfg.d_state)
+        return np.zeros(shape if lanes is None else (lanes,) + shape, np.float32)
+
+    def init_reference(self, seed: int) -> int:
+        s = lib().oracle_init_reference(self.ref, seed)
+        self.sync()
+        return s
+
+    def init_baseline(self, seed: int) -> int:
+        s = lib().oracle_init_baseline(self.ref, seed)
+        self.sync()
+        return s
+
+    def populate_banks(self, seed: int, count: int, max_radius: float = 0.9) -> None:
+        lib().oracle_populate_banks(self.ref, seed, count, max_radius)
+        self.sync()
+
+    def forward_inference(self, state: np.ndarray, token: int, logits: bool = True):
+        out = np.empty(self.cfg.d_vocab, np.float32) if logits else None
+        lib().oracle_forward_inference(self.ref, ptr(state), token, ptr(out))
+        return out
+
+    def prefill(self, state: np.ndarray, ids, logits: bool = True):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.cfg.d_vocab, np.float32) if logits else None
+        rc = lib().oracle_prefill(self.ref, ptr(state), ptr(ids, C.c_uint32), ids.size, ptr(out))
+        if rc:
+            raise ValueError(f"oracle prefill rejected the ids ({rc})")
+        return out
+
+    def prefill_lanes(self, states: np.ndarray, ids: np.ndarray, threads: int = 1, logits: bool = True):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        lanes, n = ids.shape
+        out = np.empty((lanes, self.cfg.d_vocab), np.float32) if logits else None
+        rc = lib().oracle_prefill_lanes(self.ref, ptr(states), ptr(ids, C.c_uint32), lanes, n, ptr(out), threads)
+        if rc:
+            raise ValueError(f"oracle prefill rejected the ids ({rc})")
+        return out
+
+    def train_chunk_forward(self, state: np.ndarray, ids, targets):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        tg = np.ascontiguousarray(targets, dtype=np.uint32)
+        logits = np.empty((ids.size, self.cfg.d_vocab), np.float32)
+        loss = lib().oracle_train_chunk_forward(self.ref, ptr(state), ptr(ids, C.c_uint32),
+                                                ptr(tg, C.c_uint32), ids.size, ptr(logits))
+        return np.float32(loss), logits
+
+    def features(self, state: np.ndarray, token: int) -> np.ndarray:
+        out = np.empty(self.cfg.d_latent, np.float32)
+        lib().oracle_forward_features(self.ref, ptr(state), token, ptr(out))
+        return out
+
+
+# ---- stage twins -------------------------------------------------------------
+
+def gemm_xwt(x, w):
+    x, w = f32(x), f32(w)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().oracle_gemm_xwt(ptr(x), ptr(w), m, n, k, ptr(y))
+    return y
+
+
+def ssm_forward(delta, b_proj, x_norm, rates, c_proj, initial, L, dm, ds):
+    args = [f32(a).ravel() for a in (delta, b_proj, x_norm, rates, c_proj, initial)]
+    w = dm * ds
+    bar_a = np.empty(L * w, np.float32)
+    bar_b = np.empty(L * w, np.float32)
+    states = np.empty((L + 1) * w, np.float32)
+    y = np.empty(L * dm, np.float32)
+    lib().oracle_ssm_forward(*[ptr(a) for a in args], L, dm, ds, ptr(bar_a), ptr(bar_b), ptr(states), ptr(y))
+    return bar_a, bar_b, states, y
+
+
+def retrieve(keys, norm_sq, values, count, q_pnc, tau, top_k=0):
+    keys, norm_sq, values, q_pnc = (f32(a) for a in (keys, norm_sq, values, q_pnc))
+    capacity, dk = keys.shape
+    dv = values.shape[1]
+    out = np.empty(dv, np.float32)
+    # The full read writes weights[..count] only (src/memory.rs:409-425).
+    w = np.zeros(capacity, np.float32)
+    mn = lib().oracle_retrieve(ptr(keys), ptr(norm_sq), ptr(values), count, capacity, dk, dv, ptr(q_pnc),
+                               tau, top_k, ptr(out), ptr(w))
+    return out, w, np.float32(mn)
+
+
+def retrieve_batch(keys, norm_sq, values, count, q_pnc, tau, top_k=0, threads=1):
+    keys, norm_sq, values, q_pnc = (f32(a) for a in (keys, norm_sq, values, q_pnc))
+    capacity, dk = keys.shape
+    dv = values.shape[1]
+    n = q_pnc.shape[0]
+    out = np.empty((n, dv), np.float32)
+    mn = np.empty(n, np.float32)
+    idx = np.empty((n, top_k), np.uint32) if top_k else None
+    lib().oracle_retrieve_batch(ptr(keys), ptr(norm_sq), ptr(values), count, capacity, dk, dv, ptr(q_pnc), n,
+                                tau, top_k, ptr(out), ptr(mn), ptr(idx, C.c_uint32), threads)
+    return out, mn, idx
+
+
+def project(q):
+    q = f32(q)
+    out = np.empty_like(q)
+    r = lib().oracle_project(ptr(q), ptr(out), q.size)
+    return out, np.float32(r)
+
+
+def squared_norm(p):
+    p = f32(p)
+    return np.float32(lib().oracle_squared_norm(ptr(p), p.size))
+
+
+def poincare_distance(u, v):
+    u, v = f32(u), f32(v)
+    return np.float32(lib().oracle_poincare_distance(ptr(u), squared_norm(u), ptr(v), squared_norm(v), u.size))
+
+
+def dense_scan(a, b, h0=None, threads=1):
+    a, b = f32(a), f32(b)
+    batch, L, s = b.shape
+    h0 = np.zeros((batch, s), np.float32) if h0 is None else f32(h0)
+    h = np.empty((batch, L, s), np.float32)
+    lib().oracle_dense_scan(ptr(a), ptr(b), ptr(h0), batch, L, s, ptr(h), threads)
+    return h
+
+
+def greedy(logits) -> int:
+    logits = f32(logits)
+    return int(lib().oracle_greedy(ptr(logits), logits.size))
+
+
+def dot(a, b) -> np.float32:
+    a, b = f32(a), f32(b)
+    return np.float32(lib().oracle_dot(ptr(a), ptr(b), a.size))

@@ -1,0 +1,176 @@
+"""Reader of the reference's `.pssa` checkpoints (V6, V7 and V8).
+
+Container (src/checkpoint.rs:3-27, 1116-1126, 1288-1307):
+  b"PSSA" | version:u16 | payload_len:u64 | fnv1a64(payload):u64 | payload
+V6/V7 payload order: src/checkpoint.rs:912-956 (V7 appends the tokenizer /
+schedule tail, src/checkpoint.rs:1309-1342); V8: src/checkpoint.rs:961-1048.
+Only what the inference path needs is kept: parameters, banks and the
+per-block recurrent carry (h_persistent).  Gradients and Adam moments are
+read and dropped.
+"""
+from __future__ import annotations
+
+import dataclasses
+import struct
+
+import numpy as np
+
+from .weights import ADAPTER_RANK, ModelWeights, PSSAConfig
+
+HEADER_LEN = 22
+
+
+def fnv1a64(data: bytes) -> int:
+    h = 0xCBF29CE484222325
+    for b in data:
+        h ^= b
+        h = (h * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+class CheckpointError(ValueError):
+    pass
+
+
+class _Reader:
+    def __init__(self, b: bytes):
+        self.b = b
+        self.o = 0
+
+    def take(self, n: int, what: str) -> bytes:
+        if self.o + n > len(self.b):
+            raise CheckpointError(f"truncated while reading {what}")
+        out = self.b[self.o:self.o + n]
+        self.o += n
+        return out
+
+    def u64(self, what: str) -> int:
+        return struct.unpack("<Q", self.take(8, what))[0]
+
+    def f32(self, what: str) -> float:
+        x = struct.unpack("<f", self.take(4, what))[0]
+        if not np.isfinite(x):
+            raise CheckpointError(f"non-finite {what}")
+        return x
+
+    def floats(self, n_expected: int, what: str, nonneg: bool = False) -> np.ndarray:
+        n = self.u64(f"{what} length")
+        if n != n_expected:
+            raise CheckpointError(f"{what} length {n}, expected {n_expected}")
+        a = np.frombuffer(self.take(4 * n, what), dtype="<f4").astype(np.float32)
+        if not np.all(np.isfinite(a)):
+            raise CheckpointError(f"non-finite {what}")
+        if nonneg and np.any(a < 0):
+            raise CheckpointError(f"negative {what}")
+        return a
+
+    def usizes(self, n_expected: int, what: str) -> np.ndarray:
+        n = self.u64(f"{what} length")
+        if n != n_expected:
+            raise CheckpointError(f"{what} length {n}, expected {n_expected}")
+        return np.frombuffer(self.take(8 * n, what), dtype="<u8").astype(np.uint64)
+
+    def matrix(self, n: int, what: str) -> np.ndarray:
+        data = self.floats(n, what)
+        self.floats(n, f"{what}.grad")
+        self.floats(n, f"{what}.m")
+        self.floats(n, f"{what}.v", nonneg=True)
+        return data
+
+
+@dataclasses.dataclass
+class LoadedCheckpoint:
+    version: int
+    weights: ModelWeights
+    carry: np.ndarray  # [depth, d*s] h_persistent per block
+    step_counter: int
+    rng_state: int
+    vocabulary: list[str]
+    hyper: dict
+
+
+def _config(r: _Reader):
+    dims = [r.u64(n) for n in ("d_vocab", "d_latent", "d_state", "d_mem_key", "mem_capacity", "chunk_len")]
+    hyper = {n: r.f32(n) for n in ("lr", "beta1", "beta2", "weight_decay", "eps", "tau_mem", "ema_alpha")}
+    return dims, hyper
+
+
+def _vocab(r: _Reader, d_vocab: int) -> list[str]:
+    n = r.u64("vocabulary count")
+    if n not in (0, d_vocab):
+        raise CheckpointError("vocabulary count must be zero or d_vocab")
+    return [r.take(r.u64("vocabulary token length"), "vocabulary token").decode("utf-8") for _ in range(n)]
+
+
+def _block(r: _Reader, w: ModelWeights, l: int, carry: np.ndarray, embed_first: bool) -> None:
+    c = w.cfg
+    d, s, k, C = c.d_latent, c.d_state, c.d_mem_key, c.mem_capacity
+    b = w.blocks[l]
+    if embed_first:
+        w.embed[:] = r.matrix(c.d_vocab * d, "embed_w").reshape(c.d_vocab, d)
+    order = [("a_raw", d * s), ("w_delta", d * d), ("w_b", s * d), ("w_c", s * d), ("w_qx", k * d),
+             ("w_qh", k * d), ("w_gate", d * d), ("w_proj", d * d), ("mlp_w1", 2 * d * d),
+             ("mlp_w2", 2 * d * d)]
+    for name, n in order:
+        getattr(b, name)[...] = r.matrix(n, name).reshape(getattr(b, name).shape)
+    if embed_first:
+        w.unembed[:] = r.matrix(c.d_vocab * d, "unembed_w").reshape(c.d_vocab, d)
+    b.norm_gamma[:] = r.matrix(d, "norm_gamma")
+    b.norm_beta[:] = r.matrix(d, "norm_beta")
+    carry[l] = r.floats(d * s, "h_persistent")
+    b.mem_count = r.u64("memory count")
+    b.mem_write_head = r.u64("memory write_head")
+    if b.mem_count > C or b.mem_write_head >= C or (b.mem_count < C and b.mem_write_head != 0):
+        raise CheckpointError("memory count/write head invalid")
+    b.mem_keys[...] = r.floats(C * k, "memory keys").reshape(C, k)
+    b.mem_values[...] = r.floats(C * d, "memory values").reshape(C, d)
+    b.mem_norm_sq[:] = r.floats(C, "memory norm_sq", nonneg=True)
+    b.mem_confidence[:] = r.floats(C, "memory confidence", nonneg=True)
+    b.mem_last_seen[:] = r.usizes(C, "memory last_seen_step")
+    b.adapter_down[...] = r.matrix(ADAPTER_RANK * d, "adapter.down").reshape(ADAPTER_RANK, d)
+    b.adapter_up[...] = r.matrix(d * ADAPTER_RANK, "adapter.up").reshape(d, ADAPTER_RANK)
+    b.adapter_slow[...] = r.floats(d * ADAPTER_RANK, "adapter.consolidated_up").reshape(d, ADAPTER_RANK)
+
+
+def load_bytes(data: bytes, verify_checksum: bool = True) -> LoadedCheckpoint:
+    if len(data) < HEADER_LEN or data[:4] != b"PSSA":
+        raise CheckpointError("not a PSSA checkpoint")
+    version = struct.unpack("<H", data[4:6])[0]
+    plen, checksum = struct.unpack("<QQ", data[6:22])
+    if len(data) != HEADER_LEN + plen:
+        raise CheckpointError("payload length does not match file")
+    payload = data[HEADER_LEN:]
+    if verify_checksum and fnv1a64(payload) != checksum:
+        raise CheckpointError("payload checksum mismatch")
+    if version not in (6, 7, 8):
+        raise CheckpointError(f"unsupported checkpoint version {version}")
+    r = _Reader(payload)
+    (V, d, s, k, C, _chunk), hyper = _config(r)
+    depth = 1
+    if version == 8:
+        depth = r.u64("depth")
+        n_scales = r.u64("residual scales length")
+        r.take(4 * n_scales, "residual scales")
+    cfg = PSSAConfig(depth=depth, d_vocab=V, d_latent=d, d_state=s, d_mem_key=k, mem_capacity=C,
+                     tau_mem=hyper["tau_mem"])
+    w = ModelWeights(cfg)
+    carry = np.zeros((depth, d * s), dtype=np.float32)
+    step = r.u64("step_counter")
+    rng = r.u64("rng state")
+    vocab = _vocab(r, V)
+    if version == 8:
+        w.embed[:] = r.matrix(V * d, "embed_w").reshape(V, d)
+        w.unembed[:] = r.matrix(V * d, "unembed_w").reshape(V, d)
+        for l in range(depth):
+            _block(r, w, l, carry, embed_first=False)
+    else:
+        _block(r, w, 0, carry, embed_first=True)
+    r.usizes(V, "embed_row_marks")
+    # The tokenizer / schedule tail (V7/V8) is not needed by the forward path.
+    w.rng_state = rng
+    return LoadedCheckpoint(version, w, carry, step, rng, vocab, hyper)
+
+
+def load(path: str, verify_checksum: bool = True) -> LoadedCheckpoint:
+    with open(path, "rb") as f:
+        return load_bytes(f.read(), verify_checksum)

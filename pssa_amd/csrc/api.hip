@@ -1,0 +1,718 @@
+// C ABI of libpssa_hip (include/pssa_hip.h).  Validation happens before any
+// allocation or launch; device failures after a launch are reported as
+// PSSA_HIP_EDEVICE (fatal).
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <memory>
+
+#include "gemm.h"
+#include "memory.h"
+#include "model.h"
+#include "ssm.h"
+
+namespace pssa {
+Status launch_dense_scan(hipStream_t stream, const float* A, const float* B, const float* H0, float* H,
+                         int batch, int L, int s);
+}
+
+using pssa::DevBuf;
+using pssa::Status;
+
+namespace {
+
+Status upload(DevBuf& dst, const void* src, size_t bytes, hipStream_t st) {
+  PSSA_RETURN_IF(dst.alloc(bytes));
+  if (bytes) PSSA_HIP_TRY(hipMemcpyAsync(dst.p, src, bytes, hipMemcpyHostToDevice, st));
+  return Status::Ok();
+}
+
+Status download(void* dst, const DevBuf& src, size_t bytes, hipStream_t st) {
+  if (bytes) PSSA_HIP_TRY(hipMemcpyAsync(dst, src.p, bytes, hipMemcpyDeviceToHost, st));
+  return Status::Ok();
+}
+
+uint16_t bf16_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Weight upload in the model's storage type.
+Status upload_weight(DevBuf& dst, const float* src, size_t n, int dtype, hipStream_t st) {
+  if (dtype == PSSA_HIP_F32) return upload(dst, src, n * 4, st);
+  std::vector<uint16_t> tmp(n);
+  for (size_t i = 0; i < n; ++i) tmp[i] = bf16_bits(src[i]);
+  PSSA_RETURN_IF(upload(dst, tmp.data(), n * 2, st));
+  PSSA_HIP_TRY(hipStreamSynchronize(st));  // tmp must outlive the copy
+  return Status::Ok();
+}
+
+Status sync(pssa_hip_ctx* ctx) {
+  PSSA_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return Status::Ok();
+}
+
+Status need(bool cond, const char* msg) { return cond ? Status::Ok() : Status::Invalid(msg); }
+
+Status check_ctx(pssa_hip_ctx* ctx) { return ctx ? Status::Ok() : Status::Invalid("null context"); }
+
+Status check_config(const pssa_hip_config& c) {
+  if (c.depth < 1 || c.depth > 32) return Status::Invalid("depth must be in 1..=32");
+  if (!c.d_vocab || !c.d_latent || !c.d_state || !c.d_mem_key || !c.mem_capacity || !c.adapter_rank)
+    return Status::Invalid("model dimensions and memory capacity must be positive");
+  if (!(std::isfinite(c.tau_mem) && c.tau_mem > 0.0f))
+    return Status::Invalid("tau_mem must be finite and positive");
+  if (c.d_latent > 16384 || c.d_state > 4096 || c.d_mem_key > 4096 || c.mem_capacity > 8192 ||
+      c.d_vocab > (1u << 24) || c.adapter_rank > 256)
+    return Status::Invalid("model dimensions exceed the supported range");
+  return Status::Ok();
+}
+
+float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+Status stage_ids_locked(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T) {
+  PSSA_RETURN_IF(need(ids != nullptr, "null ids"));
+  PSSA_RETURN_IF(need(T > 0, "prefill requires at least one token"));
+  PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
+  PSSA_RETURN_IF(need(n_lanes * T <= L->max_tokens, "n_lanes*seq_len exceeds max_tokens"));
+  const uint32_t V = (uint32_t)L->model->cfg.d_vocab;
+  for (size_t i = 0; i < n_lanes * T; ++i)
+    if (ids[i] >= V)
+      return Status::Invalid("prompt ID " + std::to_string(ids[i]) + " outside model vocabulary");
+  PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids, n_lanes * T * 4, hipMemcpyHostToDevice, L->ctx->stream));
+  L->staged_lanes = n_lanes;
+  L->staged_len = T;
+  return Status::Ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int pssa_hip_abi_version(void) { return PSSA_HIP_ABI_VERSION; }
+
+int pssa_hip_is_fatal(int code) { return code == PSSA_HIP_EDEVICE ? 1 : 0; }
+
+int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    if (!out) return Status::Invalid("null output handle");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+      (void)hipGetLastError();
+      return Status::NoDev("no HIP device visible");
+    }
+    if (device < 0 || device >= n) return Status::NoDev("device index out of range");
+    hipDeviceProp_t prop;
+    PSSA_HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      return Status::NoDev(std::string("device is ") + prop.gcnArchName + ", this build targets gfx950");
+    PSSA_HIP_TRY(hipSetDevice(device));
+    auto ctx = std::make_unique<pssa_hip_ctx>();
+    ctx->device = device;
+    ctx->name = prop.name;
+    ctx->cu_count = prop.multiProcessorCount;
+    PSSA_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    *out = ctx.release();
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+void pssa_hip_destroy(pssa_hip_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+}
+
+int pssa_hip_device_name(const pssa_hip_ctx* ctx, char* out, size_t out_len) {
+  if (!ctx || !out || !out_len) return PSSA_HIP_EINVAL;
+  std::snprintf(out, out_len, "hip:%s (gfx950, %d CUs)", ctx->name.c_str(), ctx->cu_count);
+  return PSSA_HIP_OK;
+}
+
+int pssa_hip_synchronize(pssa_hip_ctx* ctx, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+// ------------------------------------------------------------------- GEMM
+int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const void* w, size_t w_len,
+                      int w_dtype, size_t m, size_t n, size_t k, size_t batch, float* y,
+                      size_t y_len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(x && w && y, "gemm: null buffer"));
+    PSSA_RETURN_IF(need(m && n && k && batch, "GEMM dimensions must be positive"));
+    PSSA_RETURN_IF(need(w_dtype == PSSA_HIP_F32 || w_dtype == PSSA_HIP_BF16, "gemm: unknown dtype"));
+    size_t rows = 0, xin = 0, win = 0, yout = 0;
+    PSSA_RETURN_IF(pssa::checked_count({m, batch}, &rows, "gemm rows"));
+    PSSA_RETURN_IF(pssa::checked_count({rows, k}, &xin, "gemm input"));
+    PSSA_RETURN_IF(pssa::checked_count({n, k}, &win, "gemm weights"));
+    PSSA_RETURN_IF(pssa::checked_count({rows, n}, &yout, "gemm output"));
+    if (x_len != xin || w_len != win)
+      return Status::Invalid("GEMM operand lengths must be " + std::to_string(xin) + " and " +
+                             std::to_string(win) + ", got " + std::to_string(x_len) + " and " +
+                             std::to_string(w_len));
+    if (y_len != yout) return Status::Invalid("GEMM output length mismatch");
+    if (rows > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return Status::Invalid("gemm: too large");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    DevBuf dx, dw, dy;
+    PSSA_RETURN_IF(upload(dx, x, xin * 4, ctx->stream));
+    PSSA_RETURN_IF(upload(dw, w, win * (w_dtype == PSSA_HIP_BF16 ? 2 : 4), ctx->stream));
+    PSSA_RETURN_IF(dy.alloc(yout * 4));
+    PSSA_RETURN_IF(pssa::launch_gemm_xwt(ctx->stream, dx.as<float>(), (int)k, dw.p, (int)k, w_dtype,
+                                         dy.as<float>(), (int)n, (int)rows, (int)n, (int)k,
+                                         pssa::EpiParams{}));
+    PSSA_RETURN_IF(download(y, dy, yout * 4, ctx->stream));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_softplus_in_place(pssa_hip_ctx* ctx, float* values, size_t len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(values || len == 0, "softplus: null buffer"));
+    if (len == 0) return Status::Ok();
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    DevBuf dv;
+    PSSA_RETURN_IF(upload(dv, values, len * 4, ctx->stream));
+    PSSA_RETURN_IF(pssa::launch_softplus(ctx->stream, dv.as<float>(), len));
+    PSSA_RETURN_IF(download(values, dv, len * 4, ctx->stream));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+// -------------------------------------------------------------- SSM stage
+int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len,
+                         const float* delta_raw, const float* b_proj, size_t b_len,
+                         const float* x_norm, size_t x_len, const float* rates, size_t rates_len,
+                         const float* rate_deriv, const float* c_proj, size_t c_len,
+                         const float* initial, size_t initial_len, size_t seq_len, size_t d_m,
+                         size_t d_s, float* bar_a, float* bar_b, float* states, float* y_ssm,
+                         size_t y_len, float* final_state, char* err, size_t err_len) {
+  (void)delta_raw;
+  (void)rate_deriv;
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(seq_len && d_m && d_s, "ssm: dimensions must be positive"));
+    PSSA_RETURN_IF(need(delta && b_proj && x_norm && rates && c_proj && initial && y_ssm, "ssm: null input"));
+    PSSA_RETURN_IF(need((bar_a == nullptr) == (bar_b == nullptr) && (bar_a == nullptr) == (states == nullptr),
+                        "ssm: bar_a, bar_b and states are materialised together"));
+    size_t ld = 0, ls = 0, w = 0, lw = 0, lw1 = 0;
+    PSSA_RETURN_IF(pssa::checked_count({seq_len, d_m}, &ld, "ssm"));
+    PSSA_RETURN_IF(pssa::checked_count({seq_len, d_s}, &ls, "ssm"));
+    PSSA_RETURN_IF(pssa::checked_count({d_m, d_s}, &w, "ssm"));
+    PSSA_RETURN_IF(pssa::checked_count({seq_len, w}, &lw, "ssm"));
+    PSSA_RETURN_IF(pssa::checked_count({seq_len + 1, w}, &lw1, "ssm"));
+    if (delta_len != ld || x_len != ld || y_len != ld) return Status::Invalid("ssm: delta/x_norm/y_ssm must be seq_len*d_m");
+    if (b_len != ls || c_len != ls) return Status::Invalid("ssm: b_proj/c_proj must be seq_len*d_s");
+    if (rates_len != w || initial_len != w) return Status::Invalid("ssm: rates/initial must be d_m*d_s");
+    if (seq_len > INT32_MAX || d_m > INT32_MAX || d_s > INT32_MAX) return Status::Invalid("ssm: too large");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = ctx->stream;
+    DevBuf dd, db, dx, dr, dc, dh, dy, da, dbb, dsx;
+    PSSA_RETURN_IF(upload(dd, delta, ld * 4, st));
+    PSSA_RETURN_IF(upload(db, b_proj, ls * 4, st));
+    PSSA_RETURN_IF(upload(dx, x_norm, ld * 4, st));
+    PSSA_RETURN_IF(upload(dr, rates, w * 4, st));
+    PSSA_RETURN_IF(upload(dc, c_proj, ls * 4, st));
+    PSSA_RETURN_IF(upload(dh, initial, w * 4, st));
+    PSSA_RETURN_IF(dy.alloc(ld * 4));
+    PSSA_RETURN_IF(pssa::launch_scale(st, dr.as<float>(), dr.as<float>(), w, 1.4426950408889634f));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(st, dy.as<float>(), ld));
+    pssa::SsmArgs a;
+    a.delta = dd.as<float>();
+    a.ld_delta = (int)d_m;
+    a.bproj = db.as<float>();
+    a.ld_b = (int)d_s;
+    a.cproj = dc.as<float>();
+    a.ld_c = (int)d_s;
+    a.xn = dx.as<float>();
+    a.ld_x = (int)d_m;
+    a.rates2 = dr.as<float>();
+    a.carry = dh.as<float>();
+    a.carry_stride = (long)w;
+    a.y = dy.as<float>();
+    a.ld_y = (int)d_m;
+    a.T = (int)seq_len;
+    a.d = (int)d_m;
+    a.s = (int)d_s;
+    a.lanes = 1;
+    if (bar_a) {
+      PSSA_RETURN_IF(da.alloc(lw * 4));
+      PSSA_RETURN_IF(dbb.alloc(lw * 4));
+      PSSA_RETURN_IF(dsx.alloc(lw1 * 4));
+      a.bar_a = da.as<float>();
+      a.bar_b = dbb.as<float>();
+      a.states = dsx.as<float>();
+    }
+    PSSA_RETURN_IF(pssa::launch_ssm_scan(st, a));
+    PSSA_RETURN_IF(download(y_ssm, dy, ld * 4, st));
+    if (final_state) PSSA_RETURN_IF(download(final_state, dh, w * 4, st));
+    if (bar_a) {
+      PSSA_RETURN_IF(download(bar_a, da, lw * 4, st));
+      PSSA_RETURN_IF(download(bar_b, dbb, lw * 4, st));
+      PSSA_RETURN_IF(download(states, dsx, lw1 * 4, st));
+    }
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+// ----------------------------------------------------------- memory stage
+int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float* y_ssm,
+                            const float* w_qx, const float* w_qh, const float* w_gate,
+                            const float* w_proj, const float* keys, const float* norm_sq,
+                            const float* values, size_t seq_len, size_t d_m, size_t d_k,
+                            size_t d_val, size_t capacity, size_t count, float tau, size_t top_k,
+                            float* q_euc, float* q_pnc, float* q_norm, float* weights,
+                            float* m_val, float* g_mem, float* m_proj, float* m_inj, char* err,
+                            size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(seq_len && d_m && d_k && d_val && capacity, "memory: dimensions must be positive"));
+    PSSA_RETURN_IF(need(d_val == d_m, "memory: the model path reads values of width d_latent"));
+    PSSA_RETURN_IF(need(count <= capacity, "memory: count exceeds capacity"));
+    PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "memory: top_k must be at most 64"));
+    PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
+    PSSA_RETURN_IF(need(x_norm && y_ssm && w_qx && w_qh && w_gate && w_proj && keys && norm_sq &&
+                            values && m_inj,
+                        "memory: null input"));
+    if (seq_len > INT32_MAX / 4 || d_m > 16384 || d_k > 4096 || capacity > 8192)
+      return Status::Invalid("memory: shape exceeds the supported range");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = ctx->stream;
+    const int L = (int)seq_len, d = (int)d_m, k = (int)d_k, C = (int)capacity;
+    DevBuf dx, dy, dwqx, dwqh, dwg, dwp, dk_, dn, dv, dvt, qx, qe, qp, qn, wts, mv, gm, mp, mi;
+    PSSA_RETURN_IF(upload(dx, x_norm, (size_t)L * d * 4, st));
+    PSSA_RETURN_IF(upload(dy, y_ssm, (size_t)L * d * 4, st));
+    PSSA_RETURN_IF(upload(dwqx, w_qx, (size_t)k * d * 4, st));
+    PSSA_RETURN_IF(upload(dwqh, w_qh, (size_t)k * d * 4, st));
+    PSSA_RETURN_IF(upload(dwg, w_gate, (size_t)d * d * 4, st));
+    PSSA_RETURN_IF(upload(dwp, w_proj, (size_t)d * d * 4, st));
+    PSSA_RETURN_IF(upload(dk_, keys, (size_t)C * k * 4, st));
+    PSSA_RETURN_IF(upload(dn, norm_sq, (size_t)C * 4, st));
+    PSSA_RETURN_IF(upload(dv, values, (size_t)C * d * 4, st));
+    std::vector<float> vt((size_t)d * C);
+    for (int s2 = 0; s2 < C; ++s2)
+      for (int j = 0; j < d; ++j) vt[(size_t)j * C + s2] = values[(size_t)s2 * d + j];
+    PSSA_RETURN_IF(upload(dvt, vt.data(), vt.size() * 4, st));
+    for (DevBuf* b : {&qx, &qe, &qp}) PSSA_RETURN_IF(b->alloc((size_t)L * k * 4));
+    PSSA_RETURN_IF(qn.alloc((size_t)L * 4));
+    PSSA_RETURN_IF(wts.alloc((size_t)L * C * 4));
+    for (DevBuf* b : {&mv, &gm, &mp, &mi}) PSSA_RETURN_IF(b->alloc((size_t)L * d * 4));
+    // q_euc = x W_qx^T + y W_qh^T, as dot(row_x, x) + dot(row_h, y) (src/pssa.rs:1147-1152).
+    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dx.as<float>(), d, dwqx.p, d, PSSA_HIP_F32, qx.as<float>(), k, L, k, d, pssa::EpiParams{}));
+    pssa::EpiParams eq;
+    eq.kind = pssa::EPI_ADD_AUX;
+    eq.aux = qx.as<float>();
+    eq.ld_aux = k;
+    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dy.as<float>(), d, dwqh.p, d, PSSA_HIP_F32, qe.as<float>(), k, L, k, d, eq));
+    pssa::RetrieveArgs ra;
+    ra.q = qe.as<float>();
+    ra.ld_q = k;
+    ra.project = 1;
+    ra.q_pnc = qp.as<float>();
+    ra.q_norm = qn.as<float>();
+    ra.keys = dk_.as<float>();
+    ra.norm_sq = dn.as<float>();
+    ra.values = dv.as<float>();
+    ra.n = L;
+    ra.dk = k;
+    ra.dv = d;
+    ra.capacity = C;
+    ra.count = (int)count;
+    ra.tau = tau;
+    ra.top_k = (int)top_k;
+    ra.weights = wts.as<float>();
+    const bool sparse = top_k > 0 && top_k < count;
+    if (sparse) ra.out_val = mv.as<float>();
+    PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
+    if (!sparse) {
+      if (count > 0)
+        PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, wts.as<float>(), C, dvt.p, C, PSSA_HIP_F32, mv.as<float>(), d, L, d, (int)count, pssa::EpiParams{}));
+      else
+        PSSA_RETURN_IF(pssa::launch_fill_zero(st, mv.as<float>(), (size_t)L * d));
+    }
+    pssa::EpiParams eg;
+    eg.kind = pssa::EPI_SEGMENTS;
+    eg.seg[0] = 0;
+    eg.seg[1] = 0;
+    eg.seg[2] = d;
+    eg.seg[3] = d;
+    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dx.as<float>(), d, dwg.p, d, PSSA_HIP_F32, gm.as<float>(), d, L, d, d, eg));
+    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, mv.as<float>(), d, dwp.p, d, PSSA_HIP_F32, mp.as<float>(), d, L, d, d, pssa::EpiParams{}));
+    PSSA_RETURN_IF(pssa::launch_mul(st, gm.as<float>(), mp.as<float>(), mi.as<float>(), (size_t)L * d));
+    if (q_euc) PSSA_RETURN_IF(download(q_euc, qe, (size_t)L * k * 4, st));
+    if (q_pnc) PSSA_RETURN_IF(download(q_pnc, qp, (size_t)L * k * 4, st));
+    if (q_norm) PSSA_RETURN_IF(download(q_norm, qn, (size_t)L * 4, st));
+    if (weights) PSSA_RETURN_IF(download(weights, wts, (size_t)L * C * 4, st));
+    if (m_val) PSSA_RETURN_IF(download(m_val, mv, (size_t)L * d * 4, st));
+    if (g_mem) PSSA_RETURN_IF(download(g_mem, gm, (size_t)L * d * 4, st));
+    if (m_proj) PSSA_RETURN_IF(download(m_proj, mp, (size_t)L * d * 4, st));
+    PSSA_RETURN_IF(download(m_inj, mi, (size_t)L * d * 4, st));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                      const float* norm_sq, const float* values, size_t capacity, size_t count,
+                      size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
+                      float* out_min, uint32_t* out_idx, float* out_weights, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(n_q && d_key && d_val && capacity, "retrieve: dimensions must be positive"));
+    PSSA_RETURN_IF(need(count <= capacity, "retrieve: count exceeds capacity"));
+    PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "retrieve: top_k must be at most 64"));
+    PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
+    PSSA_RETURN_IF(need(q_pnc && keys && norm_sq && values && out_val, "retrieve: null buffer"));
+    PSSA_RETURN_IF(need(!out_idx || top_k > 0, "retrieve: indices need top_k > 0"));
+    if (n_q > INT32_MAX / 4 || d_key > 4096 || d_val > 65536 || capacity > 8192)
+      return Status::Invalid("retrieve: shape exceeds the supported range");
+    // The query must lie in the open ball (retrieve_soft_into's assertion).
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = ctx->stream;
+    DevBuf dq, dk_, dn, dv, dval, dmin, didx, dw;
+    PSSA_RETURN_IF(upload(dq, q_pnc, n_q * d_key * 4, st));
+    PSSA_RETURN_IF(upload(dk_, keys, capacity * d_key * 4, st));
+    PSSA_RETURN_IF(upload(dn, norm_sq, capacity * 4, st));
+    PSSA_RETURN_IF(upload(dv, values, capacity * d_val * 4, st));
+    PSSA_RETURN_IF(dval.alloc(n_q * d_val * 4));
+    if (out_min) PSSA_RETURN_IF(dmin.alloc(n_q * 4));
+    if (out_idx) PSSA_RETURN_IF(didx.alloc(n_q * top_k * 4));
+    if (out_weights) PSSA_RETURN_IF(dw.alloc(n_q * capacity * 4));
+    pssa::RetrieveArgs ra;
+    ra.q = dq.as<float>();
+    ra.ld_q = (int)d_key;
+    ra.project = 0;
+    ra.keys = dk_.as<float>();
+    ra.norm_sq = dn.as<float>();
+    ra.values = dv.as<float>();
+    ra.n = (int)n_q;
+    ra.dk = (int)d_key;
+    ra.dv = (int)d_val;
+    ra.capacity = (int)capacity;
+    ra.count = (int)count;
+    ra.tau = tau;
+    ra.top_k = (int)top_k;
+    ra.weights = out_weights ? dw.as<float>() : nullptr;
+    ra.out_val = dval.as<float>();
+    ra.out_min = out_min ? dmin.as<float>() : nullptr;
+    ra.out_idx = out_idx ? didx.as<uint32_t>() : nullptr;
+    PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
+    PSSA_RETURN_IF(download(out_val, dval, n_q * d_val * 4, st));
+    if (out_min) PSSA_RETURN_IF(download(out_min, dmin, n_q * 4, st));
+    if (out_idx) PSSA_RETURN_IF(download(out_idx, didx, n_q * top_k * 4, st));
+    if (out_weights) PSSA_RETURN_IF(download(out_weights, dw, n_q * capacity * 4, st));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+// ------------------------------------------------------------------ model
+int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight_dtype,
+                        pssa_hip_model** out, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(out != nullptr, "null output handle"));
+    *out = nullptr;
+    PSSA_RETURN_IF(need(w && w->embed && w->unembed && w->blocks, "weights: null pointer"));
+    PSSA_RETURN_IF(need(weight_dtype == PSSA_HIP_F32 || weight_dtype == PSSA_HIP_BF16, "unknown weight dtype"));
+    const pssa_hip_config& c = w->cfg;
+    PSSA_RETURN_IF(check_config(c));
+    const size_t V = c.d_vocab, d = c.d_latent, s = c.d_state, k = c.d_mem_key, C = c.mem_capacity,
+                 r = c.adapter_rank;
+    for (size_t l = 0; l < c.depth; ++l) {
+      const pssa_hip_block& b = w->blocks[l];
+      PSSA_RETURN_IF(need(b.norm_gamma && b.norm_beta && b.a_raw && b.w_delta && b.w_b && b.w_c &&
+                              b.w_qx && b.w_qh && b.w_gate && b.w_proj && b.adapter_down &&
+                              b.adapter_up && b.adapter_slow && b.mlp_w1 && b.mlp_w2 && b.mem_keys &&
+                              b.mem_values && b.mem_norm_sq,
+                          "weights: null block tensor"));
+      PSSA_RETURN_IF(need(b.mem_count <= C, "memory count exceeds capacity"));
+      for (size_t q = 0; q < b.mem_count; ++q)
+        PSSA_RETURN_IF(need(std::isfinite(b.mem_norm_sq[q]) && b.mem_norm_sq[q] >= 0.0f && b.mem_norm_sq[q] < 1.0f,
+                            "memory key norms must lie in [0, 1)"));
+    }
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = ctx->stream;
+    auto m = std::make_unique<pssa_hip_model>();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->dtype = weight_dtype;
+    m->n_in = 2 * d + 2 * s + k + r;
+    PSSA_RETURN_IF(upload(m->embed, w->embed, V * d * 4, st));
+    PSSA_RETURN_IF(upload_weight(m->unembed, w->unembed, V * d, weight_dtype, st));
+    m->blocks.resize(c.depth);
+    std::vector<float> tmp;
+    for (size_t l = 0; l < c.depth; ++l) {
+      const pssa_hip_block& b = w->blocks[l];
+      pssa::DevBlock& B = m->blocks[l];
+      // Fused input projection rows: W_delta | W_B | W_C | W_qx | W_gate | D.
+      tmp.assign(m->n_in * d, 0.0f);
+      float* p = tmp.data();
+      auto put = [&](const float* src, size_t rows) {
+        std::memcpy(p, src, rows * d * 4);
+        p += rows * d;
+      };
+      put(b.w_delta, d);
+      put(b.w_b, s);
+      put(b.w_c, s);
+      put(b.w_qx, k);
+      put(b.w_gate, d);
+      put(b.adapter_down, r);
+      PSSA_RETURN_IF(upload_weight(B.w_in, tmp.data(), tmp.size(), weight_dtype, st));
+      PSSA_RETURN_IF(upload_weight(B.w_qh, b.w_qh, k * d, weight_dtype, st));
+      PSSA_RETURN_IF(upload_weight(B.w_proj, b.w_proj, d * d, weight_dtype, st));
+      PSSA_RETURN_IF(upload_weight(B.mlp_w1, b.mlp_w1, 2 * d * d, weight_dtype, st));
+      PSSA_RETURN_IF(upload_weight(B.mlp_w2, b.mlp_w2, d * 2 * d, weight_dtype, st));
+      std::vector<float> ueff(d * r), rates(d * s), vt(d * C);
+      for (size_t i = 0; i < d * r; ++i) ueff[i] = b.adapter_up[i] + b.adapter_slow[i];
+      for (size_t i = 0; i < d * s; ++i) rates[i] = -softplus_host(b.a_raw[i]) * 1.4426950408889634f;
+      for (size_t q = 0; q < C; ++q)
+        for (size_t j = 0; j < d; ++j) vt[j * C + q] = b.mem_values[q * d + j];
+      PSSA_RETURN_IF(upload(B.u_eff, ueff.data(), ueff.size() * 4, st));
+      PSSA_RETURN_IF(upload(B.rates2, rates.data(), rates.size() * 4, st));
+      PSSA_RETURN_IF(upload(B.gamma, b.norm_gamma, d * 4, st));
+      PSSA_RETURN_IF(upload(B.beta, b.norm_beta, d * 4, st));
+      PSSA_RETURN_IF(upload(B.keys, b.mem_keys, C * k * 4, st));
+      PSSA_RETURN_IF(upload(B.norm_sq, b.mem_norm_sq, C * 4, st));
+      PSSA_RETURN_IF(upload(B.values, b.mem_values, C * d * 4, st));
+      PSSA_RETURN_IF(upload_weight(B.values_t, vt.data(), vt.size(), weight_dtype, st));
+      B.count = b.mem_count;
+      PSSA_RETURN_IF(sync(ctx));  // host staging vectors are reused
+    }
+    *out = m.release();
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+void pssa_hip_model_free(pssa_hip_model* model) {
+  if (!model) return;
+  (void)hipSetDevice(model->ctx->device);
+  (void)hipStreamSynchronize(model->ctx->stream);
+  delete model;
+}
+
+int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t lanes,
+                          size_t max_tokens, pssa_hip_lanes** out, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(model && out, "null model or output handle"));
+    *out = nullptr;
+    PSSA_RETURN_IF(need(lanes > 0 && max_tokens >= lanes, "lanes must be positive and max_tokens >= lanes"));
+    PSSA_RETURN_IF(need(max_tokens <= (1u << 24), "max_tokens exceeds 2^24"));
+    const pssa_hip_config& c = model->cfg;
+    const size_t d = c.d_latent, s = c.d_state, k = c.d_mem_key, C = c.mem_capacity;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    auto L = std::make_unique<pssa_hip_lanes>();
+    L->ctx = ctx;
+    L->model = model;
+    L->lanes = lanes;
+    L->max_tokens = max_tokens;
+    const size_t n = max_tokens;
+    PSSA_RETURN_IF(L->carry.alloc(lanes * c.depth * d * s * 4));
+    PSSA_RETURN_IF(L->ids.alloc(n * 4));
+    PSSA_RETURN_IF(L->X.alloc(n * d * 4));
+    PSSA_RETURN_IF(L->XN.alloc(n * d * 4));
+    PSSA_RETURN_IF(L->P.alloc(n * model->n_in * 4));
+    PSSA_RETURN_IF(L->Y.alloc(n * d * 4));
+    PSSA_RETURN_IF(L->Q.alloc(n * k * 4));
+    PSSA_RETURN_IF(L->Wm.alloc(n * C * 4));
+    PSSA_RETURN_IF(L->Mval.alloc(n * d * 4));
+    PSSA_RETURN_IF(L->Zraw.alloc(n * d * 4));
+    PSSA_RETURN_IF(L->H1.alloc(n * 2 * d * 4));
+    PSSA_RETURN_IF(L->logits.alloc(lanes * c.d_vocab * 4));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(ctx->stream, L->carry.as<float>(), lanes * c.depth * d * s));
+    PSSA_RETURN_IF(sync(ctx));
+    *out = L.release();
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+void pssa_hip_lanes_free(pssa_hip_lanes* lanes) {
+  if (!lanes) return;
+  (void)hipSetDevice(lanes->ctx->device);
+  (void)hipStreamSynchronize(lanes->ctx->stream);
+  delete lanes;
+}
+
+int pssa_hip_lanes_reset(pssa_hip_lanes* L, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const pssa_hip_config& c = L->model->cfg;
+    PSSA_RETURN_IF(pssa::launch_fill_zero(L->ctx->stream, L->carry.as<float>(),
+                                          L->lanes * c.depth * c.d_latent * c.d_state));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_get_carry(pssa_hip_lanes* L, float* out, size_t len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L && out, "null argument"));
+    const pssa_hip_config& c = L->model->cfg;
+    const size_t n = L->lanes * c.depth * c.d_latent * c.d_state;
+    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_RETURN_IF(download(out, L->carry, n * 4, L->ctx->stream));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_set_carry(pssa_hip_lanes* L, const float* in, size_t len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L && in, "null argument"));
+    const pssa_hip_config& c = L->model->cfg;
+    const size_t n = L->lanes * c.depth * c.d_latent * c.d_state;
+    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_HIP_TRY(hipMemcpyAsync(L->carry.p, in, n * 4, hipMemcpyHostToDevice, L->ctx->stream));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+
+int pssa_hip_prefill(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
+                     float* logits_last, size_t logits_len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    const size_t V = L->model->cfg.d_vocab;
+    if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_RETURN_IF(stage_ids_locked(L, ids, n_lanes, seq_len));
+    PSSA_RETURN_IF(pssa::run_prefill(L, n_lanes, seq_len));
+    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_forward_inference(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, float* logits,
+                               size_t logits_len, char* err, size_t err_len) {
+  return pssa_hip_prefill(L, ids, n_lanes, 1, logits, logits_len, err, err_len);
+}
+
+int pssa_hip_lanes_stage_ids(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
+                             char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_RETURN_IF(stage_ids_locked(L, ids, n_lanes, seq_len));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* L, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    PSSA_RETURN_IF(need(L->staged_len > 0, "no ids staged"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    return pssa::run_prefill(L, L->staged_lanes, L->staged_len);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_read_logits(pssa_hip_lanes* L, float* out, size_t len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L && out, "null argument"));
+    const size_t n = L->staged_lanes * L->model->cfg.d_vocab;
+    PSSA_RETURN_IF(need(n > 0 && len == n, "logits length must be staged_lanes*d_vocab"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_RETURN_IF(download(out, L->logits, n * 4, L->ctx->stream));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_stage_times(pssa_hip_lanes* L, int enable, const char** names, float* ms, size_t cap) {
+  if (!L) return PSSA_HIP_EINVAL;
+  if (enable >= 0) L->timing = enable != 0;
+  size_t n = 0;
+  for (int s2 = 0; s2 < pssa::ST_COUNT && n < cap; ++s2) {
+    if (names) names[n] = pssa::kStageNames[s2];
+    if (ms) ms[n] = L->stage_ms[s2];
+    ++n;
+  }
+  return (int)n;
+}
+
+int pssa_hip_dense_scan(pssa_hip_ctx* ctx, const float* a, const float* b, const float* h0,
+                        size_t batch, size_t seq_len, size_t d_state, float* h, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(a && b && h, "dense scan: null buffer"));
+    PSSA_RETURN_IF(need(batch && seq_len && d_state, "dense scan: dimensions must be positive"));
+    PSSA_RETURN_IF(need(d_state <= 64, "dense scan: d_state above 64 is not supported"));
+    size_t na = 0, nb = 0;
+    PSSA_RETURN_IF(pssa::checked_count({batch, seq_len, d_state, d_state}, &na, "dense scan"));
+    PSSA_RETURN_IF(pssa::checked_count({batch, seq_len, d_state}, &nb, "dense scan"));
+    if (batch > INT32_MAX || seq_len > INT32_MAX) return Status::Invalid("dense scan: too large");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipStream_t st = ctx->stream;
+    DevBuf da, db, dh0, dh;
+    PSSA_RETURN_IF(upload(da, a, na * 4, st));
+    PSSA_RETURN_IF(upload(db, b, nb * 4, st));
+    if (h0) PSSA_RETURN_IF(upload(dh0, h0, batch * d_state * 4, st));
+    PSSA_RETURN_IF(dh.alloc(nb * 4));
+    PSSA_RETURN_IF(pssa::launch_dense_scan(st, da.as<float>(), db.as<float>(), h0 ? dh0.as<float>() : nullptr,
+                                           dh.as<float>(), (int)batch, (int)seq_len, (int)d_state));
+    PSSA_RETURN_IF(download(h, dh, nb * 4, st));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_dense_scan_resident(pssa_hip_ctx* ctx, const float* d_a, const float* d_b,
+                                 const float* d_h0, size_t batch, size_t seq_len, size_t d_state,
+                                 float* d_h, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(d_a && d_b && d_h, "dense scan: null buffer"));
+    PSSA_RETURN_IF(need(batch && seq_len && d_state, "dense scan: dimensions must be positive"));
+    PSSA_RETURN_IF(need(d_state <= 64, "dense scan: d_state above 64 is not supported"));
+    if (batch > INT32_MAX || seq_len > INT32_MAX) return Status::Invalid("dense scan: too large");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    return pssa::launch_dense_scan(ctx->stream, d_a, d_b, d_h0, d_h, (int)batch, (int)seq_len, (int)d_state);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+}  // extern "C"

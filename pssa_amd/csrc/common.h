@@ -1,0 +1,131 @@
+// Shared host/device helpers for libpssa_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/pssa_hip.h"
+
+namespace pssa {
+
+// Error carrier used inside the library; converted to (code, message) at the
+// C boundary.
+struct Status {
+  int code = PSSA_HIP_OK;
+  std::string msg;
+  bool ok() const { return code == PSSA_HIP_OK; }
+  static Status Ok() { return {}; }
+  static Status Invalid(const std::string& m) { return {PSSA_HIP_EINVAL, m}; }
+  static Status Device(const std::string& m) { return {PSSA_HIP_EDEVICE, m}; }
+  static Status NoMem(const std::string& m) { return {PSSA_HIP_ENOMEM, m}; }
+  static Status NoDev(const std::string& m) { return {PSSA_HIP_ENODEV, m}; }
+};
+
+inline int finish(const Status& s, char* err, size_t err_len) {
+  if (err && err_len) {
+    if (s.ok()) {
+      err[0] = 0;
+    } else {
+      std::snprintf(err, err_len, "%s", s.msg.c_str());
+    }
+  }
+  return s.code;
+}
+
+#define PSSA_RETURN_IF(st) \
+  do {                     \
+    Status _s = (st);      \
+    if (!_s.ok()) return _s; \
+  } while (0)
+
+#define PSSA_HIP_TRY(expr)                                                              \
+  do {                                                                                  \
+    hipError_t _e = (expr);                                                             \
+    if (_e != hipSuccess)                                                               \
+      return Status::Device(std::string(#expr) + ": " + hipGetErrorString(_e));          \
+  } while (0)
+
+// Launch check: a failed launch configuration is reported at the call site.
+#define PSSA_LAUNCH_CHECK(name)                                                         \
+  do {                                                                                  \
+    hipError_t _e = hipGetLastError();                                                  \
+    if (_e != hipSuccess)                                                               \
+      return Status::Device(std::string("launch ") + (name) + ": " + hipGetErrorString(_e)); \
+  } while (0)
+
+inline bool mul_ok(size_t a, size_t b, size_t* out) {
+  if (a != 0 && b > SIZE_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+inline Status checked_count(std::initializer_list<size_t> dims, size_t* out, const char* what) {
+  size_t n = 1;
+  for (size_t d : dims)
+    if (!mul_ok(n, d, &n)) return Status::Invalid(std::string(what) + ": element count overflow");
+  if (n > ((size_t)1 << 40)) return Status::Invalid(std::string(what) + ": too large");
+  *out = n;
+  return Status::Ok();
+}
+
+// Device buffer owned by RAII.
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  DevBuf(DevBuf&& o) noexcept : p(o.p), bytes(o.bytes) {
+    o.p = nullptr;
+    o.bytes = 0;
+  }
+  DevBuf& operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+      release();
+      p = o.p;
+      bytes = o.bytes;
+      o.p = nullptr;
+      o.bytes = 0;
+    }
+    return *this;
+  }
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  Status alloc(size_t n) {
+    release();
+    if (n == 0) n = 16;
+    hipError_t e = hipMalloc(&p, n);
+    if (e != hipSuccess) {
+      p = nullptr;
+      (void)hipGetLastError();
+      return Status::NoMem("hipMalloc(" + std::to_string(n) + "): " + hipGetErrorString(e));
+    }
+    bytes = n;
+    return Status::Ok();
+  }
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+}  // namespace pssa
+
+// The opaque context handed out through the C ABI.
+struct pssa_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name;
+  int cu_count = 0;
+  std::mutex mu;
+};

@@ -1,0 +1,29 @@
+// Poincare-ball episodic memory read (HyperbolicEpisodicBankV2, src/memory.rs).
+#pragma once
+#include "common.h"
+
+namespace pssa {
+
+struct RetrieveArgs {
+  const float* q = nullptr;     // queries [n, ld_q]: Euclidean (project=1) or already in the ball
+  int ld_q = 0;
+  int project = 1;
+  float* q_pnc = nullptr;       // optional [n, dk] projected queries
+  float* q_norm = nullptr;      // optional [n] ||q_euc|| (diffeomorphic_project's return)
+  const float* keys = nullptr;  // [capacity, dk]
+  const float* norm_sq = nullptr;  // [capacity]
+  const float* values = nullptr;   // [capacity, dv] (needed when top_k > 0)
+  int n = 0, dk = 0, dv = 0, capacity = 0, count = 0;
+  float tau = 0.1f;
+  int top_k = 0;                // 0: full soft read -> weights only (readout is a GEMM)
+  float* weights = nullptr;     // [n, capacity]; required for the full read, optional for top-k
+  float* out_val = nullptr;     // [n, dv] (top-k readout)
+  float* out_min = nullptr;     // optional [n]
+  uint32_t* out_idx = nullptr;  // optional [n, top_k], ascending slot order
+};
+
+Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a);
+
+constexpr int kMaxTopK = 64;
+
+}  // namespace pssa

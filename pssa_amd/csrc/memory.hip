@@ -1,0 +1,240 @@
+// Poincare-ball memory read for gfx950.
+//
+// One wave per query, one lane per group of slots.  Everything that decides
+// which slots are read -- the projection into the ball, the squared norms and
+// the distances -- is computed in f64 in the reference's own order
+// (sequential sums, no fused multiply-add, Rust's asinh formula), so the f32
+// distances, and with them the top-k indices, agree with the reference
+// (src/memory.rs:181-262).  The softmax weights and the value mix are fp32.
+#include "memory.h"
+
+#include <cfloat>
+
+namespace pssa {
+
+__device__ __forceinline__ double rust_asinh(double x) {
+  // Rust std f64::asinh: ln_1p(|x| + |x| / (hypot(1, 1/|x|) + 1/|x|)), sign of x.
+  const double ax = fabs(x);
+  const double ix = 1.0 / ax;
+  return copysign(log1p(ax + (ax / (hypot(1.0, ix) + ix))), x);
+}
+
+// Sequential f64 sum of squares (squared_norm_f64, src/memory.rs:188-192).
+__device__ __forceinline__ double sumsq_f64(const float* p, int n) {
+#pragma clang fp contract(off)
+  double acc = 0.0;
+  for (int i = 0; i < n; ++i) {
+    const double v = (double)p[i];
+    acc = acc + v * v;
+  }
+  return acc;
+}
+
+__device__ __forceinline__ float bank_norm_sq(const float* p, int n) {
+  const double v = sumsq_f64(p, n);
+  if (v < 1.0 && (float)v == 1.0f) return __uint_as_float(0x3f7fffffu);
+  return (float)v;
+}
+
+// poincare_distance (src/memory.rs:242-262).
+__device__ __forceinline__ float poincare_dist(const float* __restrict__ q, float q_sq,
+                                               const float* __restrict__ key, float k_sq, int n) {
+#pragma clang fp contract(off)
+  double sq = 0.0;
+  int i = 0;
+  if (((uintptr_t)key & 15) == 0) {
+    for (; i + 4 <= n; i += 4) {
+      const float4 kv = *reinterpret_cast<const float4*>(key + i);
+      double t;
+      t = (double)q[i] - (double)kv.x;
+      sq = sq + t * t;
+      t = (double)q[i + 1] - (double)kv.y;
+      sq = sq + t * t;
+      t = (double)q[i + 2] - (double)kv.z;
+      sq = sq + t * t;
+      t = (double)q[i + 3] - (double)kv.w;
+      sq = sq + t * t;
+    }
+  }
+  for (; i < n; ++i) {
+    const double t = (double)q[i] - (double)key[i];
+    sq = sq + t * t;
+  }
+  const double den = (1.0 - (double)q_sq) * (1.0 - (double)k_sq);
+  return (float)(2.0 * rust_asinh(sqrt(sq / den)));
+}
+
+// Orders this wave's LDS writes before its subsequent LDS reads.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+constexpr double kMaxRadius = 1.0 - 8.0 * (double)FLT_EPSILON;  // src/memory.rs:173
+
+__global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
+  extern __shared__ float smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dk_pad = (a.dk + 3) & ~3;
+  float* sq = smem + wave * (dk_pad + a.capacity);  // this wave's query, then distances
+  float* sdist = sq + dk_pad;
+  __shared__ uint32_t ssel[4][kMaxTopK];
+
+  for (int n = blockIdx.x * 4 + wave; n < a.n; n += gridDim.x * 4) {
+    const float* qrow = a.q + (size_t)n * a.ld_q;
+    for (int i = lane; i < a.dk; i += 64) sq[i] = qrow[i];
+    wave_sync();
+    // ---- diffeomorphic_project (src/memory.rs:194-211) ----
+    if (a.project) {
+      const double r = sqrt(sumsq_f64(sq, a.dk));
+      const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+      wave_sync();
+      for (int i = lane; i < a.dk; i += 64) sq[i] = (float)((double)sq[i] * scale);
+      if (a.q_norm && lane == 0) a.q_norm[n] = (float)fmin(r, (double)FLT_MAX);
+      wave_sync();
+    }
+    if (a.q_pnc)
+      for (int i = lane; i < a.dk; i += 64) a.q_pnc[(size_t)n * a.dk + i] = sq[i];
+    const float q_sq = bank_norm_sq(sq, a.dk);
+
+    if (a.count == 0) {
+      if (a.weights)
+        for (int s = lane; s < a.capacity; s += 64) a.weights[(size_t)n * a.capacity + s] = 0.0f;
+      if (a.out_val)
+        for (int j = lane; j < a.dv; j += 64) a.out_val[(size_t)n * a.dv + j] = 0.0f;
+      if (a.out_min && lane == 0) a.out_min[n] = 0.0f;
+      if (a.out_idx)
+        for (int r = lane; r < a.top_k; r += 64) a.out_idx[(size_t)n * a.top_k + r] = 0xFFFFFFFFu;
+      wave_sync();
+      continue;
+    }
+    // ---- distances ----
+    float local_min = FLT_MAX;
+    for (int s = lane; s < a.count; s += 64) {
+      const float dist = poincare_dist(sq, q_sq, a.keys + (size_t)s * a.dk, a.norm_sq[s], a.dk);
+      sdist[s] = dist;
+      local_min = fminf(local_min, dist);
+    }
+    const float min_dist = wave_min(local_min);
+    wave_sync();
+    if (a.out_min && lane == 0) a.out_min[n] = min_dist;
+
+    if (a.top_k > 0 && a.top_k < a.count) {
+      // ---- exact top-k by (distance bits, slot) (src/memory.rs:380-392) ----
+      const int k = a.top_k;
+      for (int r = 0; r < k; ++r) {
+        unsigned long long best = ~0ull;
+        for (int s = lane; s < a.count; s += 64) {
+          const uint32_t bits = __float_as_uint(sdist[s]);
+          const unsigned long long key = ((unsigned long long)bits << 32) | (unsigned)s;
+          bool taken = false;
+          for (int p = 0; p < r; ++p) taken |= ssel[wave][p] == (uint32_t)s;
+          if (!taken && key < best) best = key;
+        }
+        best = wave_min_u64(best);
+        if (lane == 0) ssel[wave][r] = (uint32_t)(best & 0xFFFFFFFFu);
+        wave_sync();
+      }
+      if (lane == 0) {  // ascending slot order
+        for (int x = 1; x < k; ++x) {
+          const uint32_t v = ssel[wave][x];
+          int y = x - 1;
+          while (y >= 0 && ssel[wave][y] > v) {
+            ssel[wave][y + 1] = ssel[wave][y];
+            --y;
+          }
+          ssel[wave][y + 1] = v;
+        }
+      }
+      wave_sync();
+      float sum = 0.0f;
+      for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[wave][r]]) / a.tau);
+      if (a.weights) {
+        for (int s = lane; s < a.capacity; s += 64) {
+          bool chosen = false;
+          for (int r = 0; r < k; ++r) chosen |= ssel[wave][r] == (uint32_t)s;
+          a.weights[(size_t)n * a.capacity + s] =
+              chosen ? expf((min_dist - sdist[s]) / a.tau) / sum : 0.0f;
+        }
+      }
+      if (a.out_idx)
+        for (int r = lane; r < k; r += 64) a.out_idx[(size_t)n * k + r] = ssel[wave][r];
+      if (a.out_val) {
+        for (int j = lane; j < a.dv; j += 64) {
+#pragma clang fp contract(off)
+          float acc = 0.0f;
+          for (int r = 0; r < k; ++r) {
+            const uint32_t s = ssel[wave][r];
+            const float w = expf((min_dist - sdist[s]) / a.tau) / sum;
+            acc = acc + w * a.values[(size_t)s * a.dv + j];
+          }
+          a.out_val[(size_t)n * a.dv + j] = acc;
+        }
+      }
+    } else {
+      // ---- full soft read (src/memory.rs:409-425) ----
+      float part = 0.0f;
+      for (int s = lane; s < a.count; s += 64) {
+        const float e = expf((min_dist - sdist[s]) / a.tau);
+        sdist[s] = e;
+        part += e;
+      }
+      const float sum = wave_sum(part);
+      wave_sync();
+      for (int s = lane; s < a.capacity; s += 64) {
+        const float w = s < a.count ? sdist[s] / sum : 0.0f;
+        if (s < a.count) sdist[s] = w;
+        if (a.weights) a.weights[(size_t)n * a.capacity + s] = w;
+      }
+      wave_sync();
+      if (a.out_val) {
+        for (int j = lane; j < a.dv; j += 64) {
+          float acc = 0.0f;
+          for (int s = 0; s < a.count; ++s) acc = fmaf(sdist[s], a.values[(size_t)s * a.dv + j], acc);
+          a.out_val[(size_t)n * a.dv + j] = acc;
+        }
+      }
+      if (a.out_idx)
+        for (int r = lane; r < a.top_k; r += 64)
+          a.out_idx[(size_t)n * a.top_k + r] = r < a.count ? (uint32_t)r : 0xFFFFFFFFu;
+    }
+    wave_sync();
+  }
+}
+
+Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
+  if (a.n <= 0) return Status::Ok();
+  if (a.dk <= 0 || a.capacity <= 0 || a.count < 0 || a.count > a.capacity)
+    return Status::Invalid("retrieve: bad bank shape");
+  if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
+  if (a.top_k == 0 && !a.weights && !a.out_val) return Status::Invalid("retrieve: no output");
+  const int dk_pad = (a.dk + 3) & ~3;
+  const size_t lds = (size_t)4 * (dk_pad + a.capacity) * sizeof(float);
+  if (lds > 128 * 1024) return Status::Invalid("retrieve: d_key + capacity too large for LDS");
+  int blocks = (a.n + 3) / 4;
+  if (blocks > 4096) blocks = 4096;
+  retrieve_kernel<<<blocks, 256, lds, stream>>>(a);
+  PSSA_LAUNCH_CHECK("retrieve");
+  return Status::Ok();
+}
+
+}  // namespace pssa

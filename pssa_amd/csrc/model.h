@@ -1,0 +1,82 @@
+// Device-resident PSSA model and per-lane prefill/decode state.
+#pragma once
+#include <array>
+
+#include "common.h"
+
+namespace pssa {
+
+struct DevBlock {
+  DevBuf w_in;     // [n_in, d]: W_delta; W_B; W_C; W_qx; W_gate; adapter D  (weight dtype)
+  DevBuf w_qh;     // [k, d]
+  DevBuf w_proj;   // [d, d]
+  DevBuf mlp_w1;   // [2d, d]
+  DevBuf mlp_w2;   // [d, 2d]
+  DevBuf u_eff;    // [d, r] f32: adapter up + consolidated (refresh_adapter_up_effective)
+  DevBuf gamma;    // [d] f32
+  DevBuf beta;     // [d] f32
+  DevBuf rates2;   // [d*s] f32: -softplus(a_raw) * log2(e)
+  DevBuf keys;     // [C, k] f32
+  DevBuf norm_sq;  // [C] f32
+  DevBuf values;   // [C, d] f32 (top-k readout)
+  DevBuf values_t; // [d, C] weight dtype (soft-read readout GEMM operand)
+  size_t count = 0;
+};
+
+// Stage ids used for per-kernel timing.
+enum Stage : int {
+  ST_EMBED = 0,
+  ST_NORM,
+  ST_GEMM_IN,
+  ST_SSM,
+  ST_GEMM_QH,
+  ST_RETRIEVE,
+  ST_GEMM_READ,
+  ST_GEMM_PROJ,
+  ST_GEMM_MLP1,
+  ST_GEMM_MLP2,
+  ST_HEAD,
+  ST_COUNT
+};
+extern const char* const kStageNames[ST_COUNT];
+
+}  // namespace pssa
+
+struct pssa_hip_model {
+  pssa_hip_ctx* ctx = nullptr;
+  pssa_hip_config cfg{};
+  int dtype = PSSA_HIP_F32;
+  size_t n_in = 0;  // width of the fused input projection
+  pssa::DevBuf embed;    // [V, d] f32 (row gather)
+  pssa::DevBuf unembed;  // [V, d] weight dtype
+  std::vector<pssa::DevBlock> blocks;
+};
+
+struct pssa_hip_lanes {
+  pssa_hip_ctx* ctx = nullptr;
+  const pssa_hip_model* model = nullptr;
+  size_t lanes = 0, max_tokens = 0;
+  pssa::DevBuf carry;  // [lanes, depth, d*s]
+  pssa::DevBuf ids;    // [max_tokens] u32
+  pssa::DevBuf X, XN, P, Y, Q, Wm, Mval, Zraw, H1, logits;
+  size_t staged_lanes = 0, staged_len = 0;
+  bool timing = false;
+  std::array<float, pssa::ST_COUNT> stage_ms{};
+  std::array<int, pssa::ST_COUNT> stage_calls{};
+  std::vector<hipEvent_t> events;
+  std::vector<int> event_stage;
+  ~pssa_hip_lanes() {
+    for (hipEvent_t e : events) (void)hipEventDestroy(e);
+  }
+};
+
+namespace pssa {
+// Runs prefill for `n_lanes` lanes of `T` tokens whose ids are already in
+// lanes->ids (row-major [n_lanes, T]); last-token logits land in lanes->logits.
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T);
+Status launch_fill_zero(hipStream_t stream, float* p, size_t n);
+Status launch_mul(hipStream_t stream, const float* a, const float* b, float* out, size_t n);
+Status launch_softplus(hipStream_t stream, float* p, size_t n);
+Status launch_sigmoid(hipStream_t stream, float* p, size_t n);
+Status launch_check_ids(hipStream_t stream, const uint32_t* ids, size_t n, uint32_t vocab, int* bad);
+}  // namespace pssa

@@ -1,0 +1,296 @@
+// PSSA layer prefill on gfx950: the reference's per-token forward
+// (forward_continuous_inference, src/pssa.rs:1072-1209) evaluated for all
+// tokens of all lanes at once, stage by stage, following the batched stage
+// decomposition of src/gpu_batch.rs:445-1255:
+//
+//   norm        x = RMSNorm(h)                                  (one wave/row)
+//   gemm_in     [delta|B|C|q_x|gate|ad] = x W_in^T, epilogue softplus/sigmoid/SiLU
+//   ssm         fused diagonal scan -> y, carry
+//   gemm_qh     q_euc = y W_qh^T + q_x
+//   retrieve    project, f64 Poincare distances, softmax weights
+//   gemm_read   m_val = weights values
+//   gemm_proj   z_raw = y/sqrt(s) + gate * (m_val W_proj^T) + U_eff act
+//   gemm_mlp1   a = SiLU(z_raw W1^T)
+//   gemm_mlp2   h = z_raw + a W2^T   (layer 0)  /  h += (z_raw + a W2^T)/sqrt(depth)
+//   head        logits = h_last U^T / sqrt(d)   (last token of each lane only)
+#include "model.h"
+
+#include <cmath>
+
+#include "gemm.h"
+#include "memory.h"
+#include "ssm.h"
+
+namespace pssa {
+
+const char* const kStageNames[ST_COUNT] = {"embed",     "rmsnorm",    "gemm_in",   "ssm_scan",
+                                           "gemm_qh",   "retrieve",   "gemm_read", "gemm_proj",
+                                           "gemm_mlp1", "gemm_mlp2",  "head"};
+
+__global__ void embed_kernel(const uint32_t* __restrict__ ids, const float* __restrict__ embed,
+                             float* __restrict__ X, int d, size_t rows) {
+  const size_t r = blockIdx.x;
+  if (r >= rows) return;
+  const float* src = embed + (size_t)ids[r] * d;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) X[r * d + i] = src[i];
+}
+
+// Affine RMSNorm with epsilon inside the root (src/pssa.rs:1080-1086).  One
+// wave per row.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta,
+                                                      float* __restrict__ XN, int d, size_t rows) {
+  const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;
+  const float* x = X + r * d;
+  float ss = 0.0f;
+  for (int i = lane; i < d; i += 64) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  const float inv = 1.0f / sqrtf(ss / (float)d + 1e-5f);
+  for (int i = lane; i < d; i += 64) XN[r * d + i] = gamma[i] * (x[i] * inv) + beta[i];
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = 0.0f;
+}
+__global__ void mul_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                           float* __restrict__ out, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = a[i] * b[i];
+}
+__global__ void softplus_kernel(float* __restrict__ p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const float x = p[i];
+    p[i] = x > 20.0f ? x : log1pf(expf(x));
+  }
+}
+__global__ void sigmoid_kernel(float* __restrict__ p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 1.0f / (1.0f + expf(-p[i]));
+}
+__global__ void check_ids_kernel(const uint32_t* __restrict__ ids, size_t n, uint32_t vocab,
+                                 int* __restrict__ bad) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n && ids[i] >= vocab) atomicOr(bad, 1);
+}
+
+static unsigned grid1d(size_t n, unsigned cap = 65535u * 4) {
+  size_t g = (n + 255) / 256;
+  if (g == 0) g = 1;
+  return (unsigned)(g > cap ? cap : g);
+}
+
+Status launch_fill_zero(hipStream_t stream, float* p, size_t n) {
+  if (!n) return Status::Ok();
+  fill_zero_kernel<<<grid1d(n, 8192), 256, 0, stream>>>(p, n);
+  PSSA_LAUNCH_CHECK("fill_zero");
+  return Status::Ok();
+}
+Status launch_mul(hipStream_t stream, const float* a, const float* b, float* out, size_t n) {
+  if (!n) return Status::Ok();
+  mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(a, b, out, n);
+  PSSA_LAUNCH_CHECK("mul");
+  return Status::Ok();
+}
+Status launch_softplus(hipStream_t stream, float* p, size_t n) {
+  if (!n) return Status::Ok();
+  softplus_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(p, n);
+  PSSA_LAUNCH_CHECK("softplus");
+  return Status::Ok();
+}
+Status launch_sigmoid(hipStream_t stream, float* p, size_t n) {
+  if (!n) return Status::Ok();
+  sigmoid_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(p, n);
+  PSSA_LAUNCH_CHECK("sigmoid");
+  return Status::Ok();
+}
+Status launch_check_ids(hipStream_t stream, const uint32_t* ids, size_t n, uint32_t vocab, int* bad) {
+  if (!n) return Status::Ok();
+  check_ids_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(ids, n, vocab, bad);
+  PSSA_LAUNCH_CHECK("check_ids");
+  return Status::Ok();
+}
+
+namespace {
+
+struct Timer {
+  pssa_hip_lanes* L;
+  hipStream_t s;
+  size_t next = 0;
+  Status mark(int stage) {
+    if (!L->timing) return Status::Ok();
+    if (next == L->events.size()) {
+      hipEvent_t e;
+      PSSA_HIP_TRY(hipEventCreate(&e));
+      L->events.push_back(e);
+      L->event_stage.push_back(0);
+    }
+    L->event_stage[next] = stage;
+    PSSA_HIP_TRY(hipEventRecord(L->events[next], s));
+    ++next;
+    return Status::Ok();
+  }
+  // Closes the last interval and folds all intervals into per-stage totals.
+  Status finish() {
+    if (!L->timing) return Status::Ok();
+    PSSA_RETURN_IF(mark(-1));
+    PSSA_HIP_TRY(hipEventSynchronize(L->events[next - 1]));
+    L->stage_ms.fill(0.0f);
+    L->stage_calls.fill(0);
+    for (size_t i = 0; i + 1 < next; ++i) {
+      float ms = 0.0f;
+      PSSA_HIP_TRY(hipEventElapsedTime(&ms, L->events[i], L->events[i + 1]));
+      const int st = L->event_stage[i];
+      if (st >= 0) {
+        L->stage_ms[st] += ms;
+        L->stage_calls[st] += 1;
+      }
+    }
+    return Status::Ok();
+  }
+};
+
+}  // namespace
+
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
+  const pssa_hip_model* M = L->model;
+  const pssa_hip_config& c = M->cfg;
+  const hipStream_t st = L->ctx->stream;
+  const int d = (int)c.d_latent, s = (int)c.d_state, k = (int)c.d_mem_key;
+  const int C = (int)c.mem_capacity, r = (int)c.adapter_rank, V = (int)c.d_vocab;
+  const int n_in = (int)M->n_in;
+  const size_t rows = n_lanes * T;
+  const int m = (int)rows;
+  const int dt = M->dtype;
+  const float ssm_scale = 1.0f / sqrtf((float)s);
+  const float depth_scale = 1.0f / sqrtf((float)c.depth);
+  const float logit_scale = 1.0f / sqrtf((float)d);
+  // Column offsets inside the fused projection output P.
+  const int o_b = d, o_c = d + s, o_qx = d + 2 * s, o_gate = d + 2 * s + k, o_act = 2 * d + 2 * s + k;
+
+  float* X = L->X.as<float>();
+  float* XN = L->XN.as<float>();
+  float* P = L->P.as<float>();
+  float* Y = L->Y.as<float>();
+  float* Q = L->Q.as<float>();
+  float* Wm = L->Wm.as<float>();
+  float* Mv = L->Mval.as<float>();
+  float* Zr = L->Zraw.as<float>();
+  float* H1 = L->H1.as<float>();
+
+  Timer tm{L, st};
+  PSSA_RETURN_IF(tm.mark(ST_EMBED));
+  embed_kernel<<<(unsigned)rows, 256, 0, st>>>(L->ids.as<uint32_t>(), M->embed.as<float>(), X, d, rows);
+  PSSA_LAUNCH_CHECK("embed");
+
+  for (size_t l = 0; l < c.depth; ++l) {
+    const DevBlock& B = M->blocks[l];
+    PSSA_RETURN_IF(tm.mark(ST_NORM));
+    rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(X, B.gamma.as<float>(), B.beta.as<float>(), XN, d, rows);
+    PSSA_LAUNCH_CHECK("rmsnorm");
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_IN));
+    EpiParams e_in;
+    e_in.kind = EPI_SEGMENTS;
+    e_in.seg[0] = d;
+    e_in.seg[1] = o_gate;
+    e_in.seg[2] = o_act;
+    e_in.seg[3] = n_in;
+    PSSA_RETURN_IF(launch_gemm_xwt(st, XN, d, B.w_in.p, d, dt, P, n_in, m, n_in, d, e_in));
+
+    PSSA_RETURN_IF(tm.mark(ST_SSM));
+    if (ssm_needs_zeroed_y(s)) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
+    SsmArgs sa;
+    sa.delta = P;
+    sa.ld_delta = n_in;
+    sa.bproj = P + o_b;
+    sa.ld_b = n_in;
+    sa.cproj = P + o_c;
+    sa.ld_c = n_in;
+    sa.xn = XN;
+    sa.ld_x = d;
+    sa.rates2 = B.rates2.as<float>();
+    sa.carry = L->carry.as<float>() + l * (size_t)d * s;
+    sa.carry_stride = (long)(c.depth * (size_t)d * s);
+    sa.y = Y;
+    sa.ld_y = d;
+    sa.T = (int)T;
+    sa.d = d;
+    sa.s = s;
+    sa.lanes = (int)n_lanes;
+    PSSA_RETURN_IF(launch_ssm_scan(st, sa));
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));
+    EpiParams e_q;
+    e_q.kind = EPI_ADD_AUX;
+    e_q.aux = P + o_qx;
+    e_q.ld_aux = n_in;
+    PSSA_RETURN_IF(launch_gemm_xwt(st, Y, d, B.w_qh.p, d, dt, Q, k, m, k, d, e_q));
+
+    PSSA_RETURN_IF(tm.mark(ST_RETRIEVE));
+    RetrieveArgs ra;
+    ra.q = Q;
+    ra.ld_q = k;
+    ra.project = 1;
+    ra.keys = B.keys.as<float>();
+    ra.norm_sq = B.norm_sq.as<float>();
+    ra.n = m;
+    ra.dk = k;
+    ra.dv = d;
+    ra.capacity = C;
+    ra.count = (int)B.count;
+    ra.tau = c.tau_mem;
+    ra.weights = Wm;
+    PSSA_RETURN_IF(launch_retrieve(st, ra));
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_READ));
+    if (B.count > 0) {
+      PSSA_RETURN_IF(launch_gemm_xwt(st, Wm, C, B.values_t.p, C, dt, Mv, d, m, d, (int)B.count, EpiParams{}));
+    } else {
+      PSSA_RETURN_IF(launch_fill_zero(st, Mv, rows * d));
+    }
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_PROJ));
+    EpiParams e_z;
+    e_z.kind = EPI_ZRAW;
+    e_z.y = Y;
+    e_z.ld_y = d;
+    e_z.g = P + o_gate;
+    e_z.ld_g = n_in;
+    e_z.act = P + o_act;
+    e_z.ld_act = n_in;
+    e_z.U = B.u_eff.as<float>();
+    e_z.rank = r;
+    e_z.scale = ssm_scale;
+    PSSA_RETURN_IF(launch_gemm_xwt(st, Mv, d, B.w_proj.p, d, dt, Zr, d, m, d, d, e_z));
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP1));
+    EpiParams e_s;
+    e_s.kind = EPI_SILU;
+    PSSA_RETURN_IF(launch_gemm_xwt(st, Zr, d, B.mlp_w1.p, d, dt, H1, 2 * d, m, 2 * d, d, e_s));
+
+    PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP2));
+    EpiParams e_r;
+    e_r.kind = EPI_RESIDUAL;
+    e_r.zraw = Zr;
+    e_r.ld_zraw = d;
+    e_r.first = l == 0 ? 1 : 0;
+    e_r.scale = depth_scale;
+    PSSA_RETURN_IF(launch_gemm_xwt(st, H1, 2 * d, B.mlp_w2.p, 2 * d, dt, X, d, m, d, 2 * d, e_r));
+  }
+
+  PSSA_RETURN_IF(tm.mark(ST_HEAD));
+  EpiParams e_h;
+  e_h.kind = EPI_SCALE;
+  e_h.scale = logit_scale;
+  PSSA_RETURN_IF(launch_gemm_xwt(st, X + (T - 1) * (size_t)d, (int)(T * d), M->unembed.p, d, dt,
+                                 L->logits.as<float>(), V, (int)n_lanes, V, d, e_h));
+  return tm.finish();
+}
+
+}  // namespace pssa

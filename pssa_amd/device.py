@@ -1,0 +1,244 @@
+"""Host-side mirror of the reference's device surface, backed by libpssa_hip.
+
+`HipDevice` plays the role of `GpuDispatch::Hip` next to the reference's
+`GpuDispatch::{Wgpu, Cuda}` (src/backend.rs:1025-1446): same method names,
+argument meaning and error behaviour (shape errors raise before anything runs;
+device failures are fatal and never fall back to the CPU).
+
+`PSSALayer` carries the model-level inference entry points of PSSALayerV2
+(`forward_inference`, `prefill_inference`, `reset_recurrent_state`,
+src/pssa.rs:2245-2442) for a batch of independent lanes
+(SequenceBatch, src/sequence_batch.rs:21-78).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _abi
+from .weights import ModelWeights
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class HipDevice:
+    """Device context (CudaContext peer, src/cuda.rs:158-192)."""
+
+    def __init__(self, device: int = 0):
+        self._lib = _abi.lib()
+        h = C.c_void_p()
+        _abi.call(self._lib.pssa_hip_init, device, C.byref(h))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            self._lib.pssa_hip_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def backend_label(self) -> str:
+        buf = C.create_string_buffer(256)
+        self._lib.pssa_hip_device_name(self.handle, buf, 256)
+        return buf.value.decode()
+
+    def synchronize(self) -> None:
+        _abi.call(self._lib.pssa_hip_synchronize, self.handle)
+
+    # -- GpuDispatch::try_dispatch_gemm_into (src/backend.rs:1049-1085) -------
+    def try_dispatch_gemm(self, x, w, m: int, n: int, k: int, batch: int = 1,
+                          w_dtype: str = "f32") -> np.ndarray:
+        x = _f32(x).ravel()
+        if w_dtype == "f32":
+            wb = _f32(w).ravel()
+            code, wlen = _abi.F32, wb.size
+        elif w_dtype == "bf16":
+            wb = np.ascontiguousarray(w, dtype=np.uint16).ravel()
+            code, wlen = _abi.BF16, wb.size
+        else:
+            raise ValueError("w_dtype must be 'f32' or 'bf16'")
+        y = np.empty(batch * m * n, dtype=np.float32)
+        _abi.call(self._lib.pssa_hip_gemm_xwt, self.handle, _abi.ptr(x), x.size,
+                  wb.ctypes.data_as(C.c_void_p), wlen, code, m, n, k, batch, _abi.ptr(y), y.size)
+        return y
+
+    def softplus_in_place(self, values: np.ndarray) -> None:
+        assert values.dtype == np.float32 and values.flags.c_contiguous
+        _abi.call(self._lib.pssa_hip_softplus_in_place, self.handle, _abi.ptr(values), values.size)
+
+    # -- GpuDispatch::ssm_forward (src/backend.rs:1213-1244) -------------------
+    def ssm_forward(self, delta, b_proj, x_norm, rates, c_proj, initial, seq_len: int, d_m: int,
+                    d_s: int, materialize: bool = True):
+        """Returns (bar_a, bar_b, states, y_ssm, final_state); the first three are
+        None when materialize is False."""
+        delta, b_proj, x_norm = _f32(delta).ravel(), _f32(b_proj).ravel(), _f32(x_norm).ravel()
+        rates, c_proj, initial = _f32(rates).ravel(), _f32(c_proj).ravel(), _f32(initial).ravel()
+        w = d_m * d_s
+        y = np.empty(seq_len * d_m, np.float32)
+        fin = np.empty(w, np.float32)
+        bar_a = np.empty(seq_len * w, np.float32) if materialize else None
+        bar_b = np.empty(seq_len * w, np.float32) if materialize else None
+        states = np.empty((seq_len + 1) * w, np.float32) if materialize else None
+        _abi.call(self._lib.pssa_hip_ssm_forward, self.handle, _abi.ptr(delta), delta.size, None,
+                  _abi.ptr(b_proj), b_proj.size, _abi.ptr(x_norm), x_norm.size, _abi.ptr(rates),
+                  rates.size, None, _abi.ptr(c_proj), c_proj.size, _abi.ptr(initial), initial.size,
+                  seq_len, d_m, d_s, _abi.ptr(bar_a), _abi.ptr(bar_b), _abi.ptr(states), _abi.ptr(y),
+                  y.size, _abi.ptr(fin))
+        return bar_a, bar_b, states, y, fin
+
+    # -- GpuDispatch::memory_forward (src/backend.rs:1345-1385) ----------------
+    def memory_forward(self, x_norm, y_ssm, w_qx, w_qh, w_gate, w_proj, keys, norm_sq, values,
+                       seq_len: int, d_m: int, d_k: int, d_val: int, capacity: int, count: int,
+                       tau: float, top_k: int = 0) -> dict:
+        args = [_f32(a).ravel() for a in (x_norm, y_ssm, w_qx, w_qh, w_gate, w_proj, keys, norm_sq, values)]
+        out = {
+            "q_euc": np.empty(seq_len * d_k, np.float32),
+            "q_pnc": np.empty(seq_len * d_k, np.float32),
+            "q_norm": np.empty(seq_len, np.float32),
+            "weights": np.empty(seq_len * capacity, np.float32),
+            "m_val": np.empty(seq_len * d_val, np.float32),
+            "g_mem": np.empty(seq_len * d_val, np.float32),
+            "m_proj": np.empty(seq_len * d_val, np.float32),
+            "m_inj": np.empty(seq_len * d_val, np.float32),
+        }
+        _abi.call(self._lib.pssa_hip_memory_forward, self.handle, *[_abi.ptr(a) for a in args],
+                  seq_len, d_m, d_k, d_val, capacity, count, tau, top_k,
+                  *[_abi.ptr(out[k]) for k in ("q_euc", "q_pnc", "q_norm", "weights", "m_val",
+                                              "g_mem", "m_proj", "m_inj")])
+        return out
+
+    # -- batched retrieve_soft_into (src/memory.rs:344-426) --------------------
+    def retrieve(self, q_pnc, keys, norm_sq, values, count: int, tau: float, top_k: int = 0,
+                 want_weights: bool = False):
+        q_pnc, keys, norm_sq, values = (_f32(a) for a in (q_pnc, keys, norm_sq, values))
+        n_q, d_key = q_pnc.shape
+        capacity, d_val = values.shape
+        out_val = np.empty((n_q, d_val), np.float32)
+        out_min = np.empty(n_q, np.float32)
+        out_idx = np.empty((n_q, top_k), np.uint32) if top_k > 0 else None
+        out_w = np.empty((n_q, capacity), np.float32) if want_weights else None
+        _abi.call(self._lib.pssa_hip_retrieve, self.handle, _abi.ptr(q_pnc), n_q, _abi.ptr(keys),
+                  _abi.ptr(norm_sq), _abi.ptr(values), capacity, count, d_key, d_val, tau, top_k,
+                  _abi.ptr(out_val), _abi.ptr(out_min),
+                  None if out_idx is None else _abi.ptr(out_idx, C.c_uint32), _abi.ptr(out_w))
+        return out_val, out_min, out_idx, out_w
+
+    def dense_scan(self, a, b, h0=None):
+        a, b = _f32(a), _f32(b)
+        batch, L, s = b.shape
+        assert a.shape == (batch, L, s, s)
+        h = np.empty((batch, L, s), np.float32)
+        h0p = None if h0 is None else _abi.ptr(_f32(h0))
+        _abi.call(self._lib.pssa_hip_dense_scan, self.handle, _abi.ptr(a), _abi.ptr(b), h0p, batch, L, s,
+                  _abi.ptr(h))
+        return h
+
+    def dense_scan_resident(self, a_ptr: int, b_ptr: int, h0_ptr: int | None, batch: int, L: int, s: int,
+                            h_ptr: int) -> None:
+        _abi.call(self._lib.pssa_hip_dense_scan_resident, self.handle, C.c_void_p(a_ptr), C.c_void_p(b_ptr),
+                  C.c_void_p(h0_ptr) if h0_ptr else None, batch, L, s, C.c_void_p(h_ptr))
+
+
+class PSSALayer:
+    """Device-resident PSSA model with `lanes` independent recurrent carries."""
+
+    def __init__(self, device: HipDevice, weights: ModelWeights, lanes: int = 1,
+                 max_tokens: int | None = None, weight_dtype: str = "f32"):
+        self.device = device
+        self.cfg = weights.cfg
+        self.lanes = lanes
+        self.max_tokens = max_tokens or lanes
+        lib = device._lib
+        self._lib = lib
+        w, keep = weights.c_view()
+        m = C.c_void_p()
+        code = _abi.F32 if weight_dtype == "f32" else _abi.BF16
+        _abi.call(lib.pssa_hip_model_load, device.handle, C.byref(w), code, C.byref(m))
+        self.model = m
+        del keep
+        ln = C.c_void_p()
+        try:
+            _abi.call(lib.pssa_hip_lanes_create, device.handle, m, lanes, self.max_tokens, C.byref(ln))
+        except Exception:
+            lib.pssa_hip_model_free(m)
+            raise
+        self.handle = ln
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self._lib.pssa_hip_lanes_free(self.handle)
+            self.handle = None
+        if getattr(self, "model", None):
+            self._lib.pssa_hip_model_free(self.model)
+            self.model = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset_recurrent_state(self) -> None:
+        _abi.call(self._lib.pssa_hip_lanes_reset, self.handle)
+
+    def carry_shape(self):
+        return (self.lanes, self.cfg.depth, self.cfg.d_latent * self.cfg.d_state)
+
+    def get_carry(self) -> np.ndarray:
+        out = np.empty(self.carry_shape(), np.float32)
+        _abi.call(self._lib.pssa_hip_lanes_get_carry, self.handle, _abi.ptr(out), out.size)
+        return out
+
+    def set_carry(self, carry) -> None:
+        carry = _f32(carry)
+        assert carry.shape == self.carry_shape()
+        _abi.call(self._lib.pssa_hip_lanes_set_carry, self.handle, _abi.ptr(carry), carry.size)
+
+    def prefill_inference(self, token_ids, want_logits: bool = True):
+        """token_ids [n_lanes, T] (or [T] for one lane).  Returns the last
+        token's logits [n_lanes, V] (None when want_logits is False)."""
+        ids = np.ascontiguousarray(np.atleast_2d(np.asarray(token_ids)), dtype=np.uint32)
+        n_lanes, T = ids.shape
+        logits = np.empty((n_lanes, self.cfg.d_vocab), np.float32) if want_logits else None
+        _abi.call(self._lib.pssa_hip_prefill, self.handle, _abi.ptr(ids, C.c_uint32), n_lanes, T,
+                  _abi.ptr(logits), 0 if logits is None else logits.size)
+        return logits
+
+    def forward_inference(self, ids):
+        """One token per lane; returns logits [n_lanes, V]."""
+        ids = np.ascontiguousarray(np.atleast_1d(np.asarray(ids)), dtype=np.uint32)
+        logits = np.empty((ids.size, self.cfg.d_vocab), np.float32)
+        _abi.call(self._lib.pssa_hip_forward_inference, self.handle, _abi.ptr(ids, C.c_uint32), ids.size,
+                  _abi.ptr(logits), logits.size)
+        return logits
+
+    # -- device-resident measurement path ------------------------------------
+    def stage_ids(self, token_ids) -> None:
+        ids = np.ascontiguousarray(np.atleast_2d(np.asarray(token_ids)), dtype=np.uint32)
+        _abi.call(self._lib.pssa_hip_lanes_stage_ids, self.handle, _abi.ptr(ids, C.c_uint32), *ids.shape)
+        self._staged = ids.shape
+
+    def prefill_staged(self) -> None:
+        _abi.call(self._lib.pssa_hip_lanes_prefill_staged, self.handle)
+
+    def read_logits(self) -> np.ndarray:
+        n_lanes = self._staged[0]
+        out = np.empty((n_lanes, self.cfg.d_vocab), np.float32)
+        _abi.call(self._lib.pssa_hip_lanes_read_logits, self.handle, _abi.ptr(out), out.size)
+        return out
+
+    def set_stage_timing(self, enable: bool) -> None:
+        self._lib.pssa_hip_lanes_stage_times(self.handle, 1 if enable else 0, None, None, 0)
+
+    def stage_times(self) -> dict:
+        names = (C.c_char_p * 32)()
+        ms = (C.c_float * 32)()
+        n = self._lib.pssa_hip_lanes_stage_times(self.handle, -1, names, ms, 32)
+        return {names[i].decode(): float(ms[i]) for i in range(n)}

@@ -1,0 +1,219 @@
+"""Kernel-level parity on the GPU, through the C ABI, against the CPU oracle.
+
+Gates: fp32 max normwise relative error 1e-4, bf16 weights 2e-2; retrieved
+slot indices bit-exact.  Small shapes run first."""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from oracle import oracle as O
+from pssa_amd import bf16_round
+from test_oracle_closed_forms import F32_MIN_SUB, bank, cuda_ssm_fixture
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+# ------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (7, 5, 3), (33, 17, 9), (128, 128, 64), (130, 257, 768),
+                                   (300, 2096, 768)])
+def test_gemm_f32_matches_oracle(hip, m, n, k):
+    say("gemm f32", m, n, k)
+    rng = np.random.default_rng(m * 1000 + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    y = hip.try_dispatch_gemm(x, w, m, n, k).reshape(m, n)
+    assert rel_err(y, O.gemm_xwt(x, w)) < 1e-5
+
+
+@pytest.mark.parametrize("m,n,k,batch", [(5, 9, 8, 1), (64, 130, 776, 2), (257, 96, 768, 1), (31, 3, 20, 3)])
+def test_gemm_bf16_weights(hip, m, n, k, batch):
+    say("gemm bf16", m, n, k, batch)
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((batch * m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    wb = bf16_round(w)
+    wbits = (wb.view(np.uint32) >> 16).astype(np.uint16)
+    y = hip.try_dispatch_gemm(x, wbits, m, n, k, batch, w_dtype="bf16").reshape(batch * m, n)
+    # Exact products of bf16 operands, fp32 accumulation.
+    exact = bf16_round(x).astype(np.float64) @ wb.astype(np.float64).T
+    assert rel_err(y, exact) < 1e-5
+    assert rel_err(y, O.gemm_xwt(x, w)) < 2e-2
+
+
+def test_gemm_shape_errors_leave_output_untouched(hip):
+    from pssa_amd._abi import HipError
+
+    with pytest.raises(HipError, match="GEMM operand lengths"):
+        hip.try_dispatch_gemm(np.ones(5, np.float32), np.ones(6, np.float32), 2, 3, 2)
+
+
+# -------------------------------------------------------------------- SSM
+def test_ssm_reference_fixture(hip):
+    """tests/backend_cuda.rs:97-160 (L=7, d=3, s=2) with every tape output."""
+    say("ssm fixture 7x3x2")
+    L, dm, ds, delta, b, x, rates, c, init = cuda_ssm_fixture()
+    bar_a, bar_b, states, y, fin = hip.ssm_forward(delta, b, x, rates, c, init, L, dm, ds)
+    ra, rb, rs, ry = O.ssm_forward(delta, b, x, rates, c, init, L, dm, ds)
+    assert rel_err(bar_a, ra) < 1e-6
+    assert rel_err(bar_b, rb) < 1e-6
+    assert rel_err(states, rs) < 1e-5
+    assert rel_err(y, ry) < 1e-5
+    np.testing.assert_array_equal(states[: dm * ds], init)
+    assert rel_err(fin, rs[L * dm * ds:]) < 1e-5
+
+
+def test_ssm_len64_stride4096_covers_all_channels(hip):
+    """tests/backend_cuda.rs:262-340: patterned L=64, d=256, s=16."""
+    say("ssm patterned 64x256x16")
+    L, dm, ds = 64, 256, 16
+    i = np.arange(L * dm)
+    delta = np.float32(0.01 + (i % 19) * 0.001)
+    b = np.float32((np.arange(L * ds) % 13) * 0.002 - 0.01)
+    x = np.float32((i % 23) * 0.01 - 0.1)
+    rates = np.float32(-0.01 - (np.arange(dm * ds) % 7) * 0.001)
+    c = np.float32((np.arange(L * ds) % 11) * 0.003 - 0.01)
+    init = np.float32((np.arange(dm * ds) % 17) * 0.001 - 0.008)
+    bar_a, bar_b, states, y, fin = hip.ssm_forward(delta, b, x, rates, c, init, L, dm, ds)
+    ra, rb, rs, ry = O.ssm_forward(delta, b, x, rates, c, init, L, dm, ds)
+    assert rel_err(y, ry) < 1e-5 and rel_err(states, rs) < 1e-5
+    assert states[0] == init[0]
+    stride = dm * ds
+    assert abs(states[L * stride + stride - 1] - rs[L * stride + stride - 1]) < 1e-6
+
+
+@pytest.mark.parametrize("L,dm,ds", [(1, 1, 1), (17, 5, 3), (300, 100, 256), (33, 130, 64), (40, 64, 300)])
+def test_ssm_random_shapes(hip, L, dm, ds):
+    say("ssm random", L, dm, ds)
+    rng = np.random.default_rng(L + dm + ds)
+    delta = np.float32(np.log1p(np.exp(rng.standard_normal(L * dm))))
+    b = rng.standard_normal(L * ds).astype(np.float32) * 0.3
+    x = rng.standard_normal(L * dm).astype(np.float32)
+    rates = -np.float32(np.log1p(np.exp(rng.standard_normal(dm * ds))))
+    c = rng.standard_normal(L * ds).astype(np.float32) * 0.3
+    init = rng.standard_normal(dm * ds).astype(np.float32) * 0.1
+    _, _, _, y, fin = hip.ssm_forward(delta, b, x, rates, c, init, L, dm, ds, materialize=False)
+    ra, rb, rs, ry = O.ssm_forward(delta, b, x, rates, c, init, L, dm, ds)
+    assert rel_err(y, ry) < 1e-5
+    assert rel_err(fin, rs[L * dm * ds:]) < 1e-5
+
+
+def test_ssm_softplus_and_rate_tails(hip):
+    """tests/numeric_recurrence.rs:48-137: tiny delta from the softplus tail and a
+    huge delta against a tiny rate keep the state finite and exact to ~1e-6."""
+    say("ssm tails")
+    for raw in (-17.0, -20.0):
+        delta = np.float32([np.log1p(np.exp(np.float64(raw)))] * 2)
+        _, _, _, y, fin = hip.ssm_forward(delta, np.float32([1.0, 1.0]), np.float32([1.0, 1.0]),
+                                          np.float32([-0.5]), np.float32([1.0, 1.0]), np.float32([0.0]), 2, 1, 1,
+                                          materialize=False)
+        assert fin[0] > 0 and abs(fin[0] / (2 * float(delta[0])) - 1) < 2e-6
+    for raw in (-17.0, -20.0):
+        rate = -np.float32(np.log1p(np.exp(np.float64(raw))))
+        delta = np.float32([1e7, 1e7])
+        _, _, _, y, fin = hip.ssm_forward(delta, np.float32([0.0, 0.0]), np.float32([1.0, 1.0]),
+                                          np.float32([rate]), np.float32([1.0, 1.0]), np.float32([1.0]), 2, 1, 1,
+                                          materialize=False)
+        expected = np.exp(-1e7 * np.float64(-rate)) ** 2
+        assert abs(fin[0] - expected) < 2e-6
+
+
+# --------------------------------------------------------------- retrieval
+def ball(rng, n, dim, rmax=0.9):
+    d = rng.standard_normal((n, dim))
+    return (d / np.linalg.norm(d, axis=1, keepdims=True) * rng.uniform(0, rmax, (n, 1))).astype(np.float32)
+
+
+def test_retrieve_closed_forms(hip):
+    """tests/memory_expansion.rs:53-93 and tests/memory_projection.rs:40-54."""
+    say("retrieve closed forms")
+    K, N, V, count = bank(5, [[0.0], [0.1], [0.6]], [[2.0], [4.0], [100.0]])
+    out, mn, idx, w = hip.retrieve(np.float32([[0.0]]), K, N, V, count, 1.0, top_k=1, want_weights=True)
+    assert out[0, 0] == 2.0 and idx[0, 0] == 0
+    np.testing.assert_array_equal(w[0], np.float32([1, 0, 0, 0, 0]))
+    full, _, _, wf = hip.retrieve(np.float32([[0.0]]), K, N, V, count, 1.0, top_k=0, want_weights=True)
+    for k in (3, 9):
+        out, _, _, w = hip.retrieve(np.float32([[0.0]]), K, N, V, count, 1.0, top_k=k, want_weights=True)
+        assert rel_err(out, full) < 1e-6 and rel_err(w, wf) < 1e-6
+    K, N, V, count = bank(4, [[0.2], [-0.2]], [[1.0], [2.0]])
+    out, _, idx, w = hip.retrieve(np.float32([[0.0]]), K, N, V, count, F32_MIN_SUB, top_k=1, want_weights=True)
+    assert out[0, 0] == 1.0 and idx[0, 0] == 0  # exact tie -> lower slot
+    K, N, V, count = bank(3, [[0.5], [-0.5], [0.75]], [[1.0, 2.0], [3.0, -2.0], [100.0, 100.0]])
+    out, _, _, w = hip.retrieve(np.float32([[0.0]]), K, N, V, count, F32_MIN_SUB, top_k=0, want_weights=True)
+    np.testing.assert_array_equal(w[0], np.float32([0.5, 0.5, 0.0]))
+    np.testing.assert_array_equal(out[0], np.float32([2.0, 0.0]))
+    K, N, V, count = bank(4, np.zeros((0, 1)), np.zeros((0, 1)))
+    out, mn, idx, w = hip.retrieve(np.float32([[0.0]]), K, N, V, 0, 0.5, top_k=1, want_weights=True)
+    assert out[0, 0] == 0.0 and not w.any() and idx[0, 0] == 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("n_q,C,dk,dv,k", [(1, 3, 2, 4, 2), (500, 512, 32, 48, 8), (300, 512, 768, 96, 8),
+                                           (257, 100, 7, 5, 1)])
+def test_retrieve_top_k_indices_bit_exact(hip, n_q, C, dk, dv, k):
+    say("retrieve top-k", n_q, C, dk, dv, k)
+    rng = np.random.default_rng(C + dk)
+    keys = ball(rng, C, dk)
+    vals = ball(rng, C, dv)
+    q = ball(rng, n_q, dk)
+    q[0] = keys[min(3, C - 1)]  # exact hit: distance 0
+    K, N, V, count = bank(C, keys, vals)
+    out, mn, idx, _ = hip.retrieve(q, K, N, V, count, 0.1, top_k=k)
+    r_out, r_min, r_idx = O.retrieve_batch(K, N, V, count, q, 0.1, k, threads=8)
+    np.testing.assert_array_equal(idx, r_idx)
+    np.testing.assert_array_equal(mn.view(np.uint32), r_min.view(np.uint32))
+    assert rel_err(out, r_out) < 1e-5
+
+
+def test_retrieve_full_soft_read(hip):
+    say("retrieve full soft read")
+    rng = np.random.default_rng(11)
+    keys, vals, q = ball(rng, 200, 16), ball(rng, 200, 24), ball(rng, 64, 16)
+    K, N, V, count = bank(256, keys, vals)
+    out, mn, _, w = hip.retrieve(q, K, N, V, count, 0.1, top_k=0, want_weights=True)
+    r_out, r_min, _ = O.retrieve_batch(K, N, V, count, q, 0.1, 0)
+    assert rel_err(out, r_out) < 1e-5
+    np.testing.assert_array_equal(mn.view(np.uint32), r_min.view(np.uint32))
+    assert not w[:, count:].any()
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_memory_forward_stage_matches_oracle(hip):
+    """GpuDispatch::memory_forward composition against the oracle's per-token
+    steps (src/pssa.rs:1147-1172)."""
+    say("memory_forward stage")
+    rng = np.random.default_rng(12)
+    L, d, k, C, count = 40, 24, 6, 16, 12
+    xn = rng.standard_normal((L, d)).astype(np.float32)
+    y = rng.standard_normal((L, d)).astype(np.float32) * 0.3
+    wqx, wqh = (rng.standard_normal((k, d)) * 0.1).astype(np.float32), (rng.standard_normal((k, d)) * 0.1).astype(np.float32)
+    wg, wp = (rng.standard_normal((d, d)) * 0.1).astype(np.float32), (rng.standard_normal((d, d)) * 0.1).astype(np.float32)
+    K, N, V, count = bank(C, ball(rng, count, k), ball(rng, count, d))
+    for top_k in (0, 4):
+        out = hip.memory_forward(xn, y, wqx, wqh, wg, wp, K, N, V, L, d, k, d, C, count, 0.1, top_k)
+        qe = O.gemm_xwt(xn, wqx) + O.gemm_xwt(y, wqh)
+        assert rel_err(out["q_euc"].reshape(L, k), qe) < 1e-5
+        qp = np.stack([O.project(r)[0] for r in qe])
+        assert rel_err(out["q_pnc"].reshape(L, k), qp) < 1e-5
+        mv = np.stack([O.retrieve(K, N, V, count, qp[t], 0.1, top_k)[0] for t in range(L)])
+        assert rel_err(out["m_val"].reshape(L, d), mv) < 1e-4
+        g = 1 / (1 + np.exp(-O.gemm_xwt(xn, wg).astype(np.float64)))
+        assert rel_err(out["g_mem"].reshape(L, d), g) < 1e-5
+        mp = mv.astype(np.float64) @ wp.T.astype(np.float64)
+        assert rel_err(out["m_inj"].reshape(L, d), g * mp) < 1e-4
+
+
+# -------------------------------------------------------------- dense scan
+@pytest.mark.parametrize("B,L,s", [(1, 1, 1), (3, 100, 5), (2, 257, 16), (4, 300, 33), (5, 200, 64)])
+def test_dense_scan_matches_oracle(hip, B, L, s):
+    say("dense scan", B, L, s)
+    rng = np.random.default_rng(B * L + s)
+    q, _ = np.linalg.qr(rng.standard_normal((B, L, s, s)))
+    a = (q * rng.uniform(0.8, 0.99, (B, L, 1, s))).astype(np.float32)
+    b = rng.standard_normal((B, L, s)).astype(np.float32)
+    h0 = rng.standard_normal((B, s)).astype(np.float32)
+    h = hip.dense_scan(a, b, h0)
+    ref = O.dense_scan(a, b, h0, threads=4)
+    assert rel_err(h, ref) < 1e-4

@@ -1,0 +1,171 @@
+"""Model-level parity on the GPU: prefill_inference / forward_inference through
+the C ABI against the CPU oracle on the same seeded weights and ids.
+
+Gates: fp32 weights 1e-4 and bf16 weights 2e-2 max normwise relative error on
+the last-token logits and on every lane's carry."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_err
+from oracle import oracle as O
+from pssa_amd import ModelWeights, PSSAConfig, PSSALayer, checkpoint
+from pssa_amd._abi import HipError
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def oracle_prefill(w, ids, carry=None, threads=8):
+    om = O.OracleModel(w)
+    lanes = ids.shape[0]
+    states = om.zero_state(lanes) if carry is None else carry.copy()
+    logits = om.prefill_lanes(states, ids, threads=threads)
+    return logits, states
+
+
+def test_golden_fixture_model(hip):
+    """The reference's depth-one fixture model (tests/golden/*_initial.pssa) with
+    its populated bank, nonzero carry and adapter, run through the HIP path."""
+    say("golden fixture model")
+    ck = checkpoint.load(os.path.join(GOLDEN, "depth_one_main85d9d33_initial.pssa"))
+    w = ck.weights
+    layer = PSSALayer(hip, w, lanes=1, max_tokens=8)
+    layer.set_carry(ck.carry[None])
+    got = layer.prefill_inference([[1, 2, 1]])
+    ref, st = oracle_prefill(w, np.array([[1, 2, 1]], np.uint32), ck.carry[None])
+    assert rel_err(got, ref) < 1e-5
+    assert rel_err(layer.get_carry(), st) < 1e-5
+    for tok in (4, 3, 2):
+        g = layer.forward_inference([tok])
+        r = O.OracleModel(w).forward_inference(st[0], tok)
+        assert rel_err(g[0], r) < 1e-5
+    layer.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_prefill_matches_oracle_small(hip, dtype):
+    say("prefill small", dtype)
+    cfg = PSSAConfig(depth=3, d_vocab=301, d_latent=64, d_state=24, d_mem_key=8, mem_capacity=40)
+    w = ModelWeights.init(cfg, 7, "baseline")
+    w.populate_banks(8, count=33)
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, cfg.d_vocab, (3, 37), dtype=np.uint32)
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=3 * 37, weight_dtype=dtype)
+    got = layer.prefill_inference(ids)
+    ref_w = w if dtype == "f32" else w.to_bf16_values()
+    ref, st = oracle_prefill(ref_w, ids)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    assert rel_err(got, ref) < tol
+    assert rel_err(layer.get_carry(), st) < tol
+    layer.close()
+
+
+def test_config1_shape_fp32_and_bf16(hip):
+    """Config 1 (d=128, s=64, depth 2, V=8192, 512-slot bank of dim 128),
+    B=1, T=512, reference initialisation plus a populated bank."""
+    cfg = PSSAConfig(depth=2, d_vocab=8192, d_latent=128, d_state=64, d_mem_key=128, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "reference")
+    w.populate_banks(1)
+    ids = np.random.default_rng(0).integers(0, cfg.d_vocab, (1, 512), dtype=np.uint32)
+    ref, st = oracle_prefill(w, ids)
+    ref_bf, st_bf = oracle_prefill(w.to_bf16_values(), ids)
+    for dtype, r, s, tol in (("f32", ref, st, 1e-4), ("bf16", ref_bf, st_bf, 2e-2)):
+        say("config1", dtype)
+        layer = PSSALayer(hip, w, lanes=1, max_tokens=512, weight_dtype=dtype)
+        got = layer.prefill_inference(ids)
+        assert rel_err(got, r) < tol
+        assert rel_err(layer.get_carry(), s) < tol
+        assert int(np.argmax(got[0, 1:])) == int(np.argmax(r[0, 1:]))
+        layer.close()
+
+
+def test_token_loop_equals_prefill_bitwise(hip):
+    """forward_inference token by token reproduces prefill bit for bit
+    (the reference's prefill/decode identity, src/inference.rs:1069-1113)."""
+    say("token loop == prefill")
+    cfg = PSSAConfig(depth=2, d_vocab=97, d_latent=48, d_state=32, d_mem_key=8, mem_capacity=24)
+    w = ModelWeights.init(cfg, 3, "baseline")
+    w.populate_banks(2, count=20)
+    ids = np.random.default_rng(1).integers(0, cfg.d_vocab, (2, 19), dtype=np.uint32)
+    a = PSSALayer(hip, w, lanes=2, max_tokens=64)
+    b = PSSALayer(hip, w, lanes=2, max_tokens=64)
+    la = a.prefill_inference(ids)
+    for t in range(ids.shape[1]):
+        lb = b.forward_inference(ids[:, t])
+    np.testing.assert_array_equal(la, lb)
+    np.testing.assert_array_equal(a.get_carry(), b.get_carry())
+    # Split prefill continues the carry exactly.
+    c = PSSALayer(hip, w, lanes=2, max_tokens=64)
+    c.prefill_inference(ids[:, :7], want_logits=False)
+    lc = c.prefill_inference(ids[:, 7:])
+    np.testing.assert_array_equal(la, lc)
+    for layer in (a, b, c):
+        layer.close()
+
+
+def test_invalid_ids_fail_before_anything_runs(hip):
+    say("invalid ids")
+    cfg = PSSAConfig(depth=1, d_vocab=10, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=4)
+    w = ModelWeights.init(cfg, 1, "baseline")
+    layer = PSSALayer(hip, w, lanes=1, max_tokens=8)
+    layer.prefill_inference([[1, 2]])
+    before = layer.get_carry()
+    with pytest.raises(HipError, match="outside model vocabulary"):
+        layer.prefill_inference([[3, 10]])
+    np.testing.assert_array_equal(layer.get_carry(), before)
+    with pytest.raises(HipError, match="at least one token"):
+        layer.prefill_inference(np.zeros((1, 0), np.uint32))
+    with pytest.raises(HipError, match="max_tokens"):
+        layer.prefill_inference(np.ones((1, 9), np.uint32))
+    layer.reset_recurrent_state()
+    assert not layer.get_carry().any()
+    layer.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_config3_full_model_prefix_against_oracle(hip, dtype):
+    """The 105M-scale model (d=768, s=256, 12 layers, V=16384, k=32, 512-slot
+    banks) at its real per-layer shape: 32 lanes x 64 tokens on the GPU, four of
+    the lanes replayed by the oracle."""
+    say("config3 prefix", dtype)
+    cfg = PSSAConfig(depth=12, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    ids = np.random.default_rng(2).integers(0, cfg.d_vocab, (32, 64), dtype=np.uint32)
+    layer = PSSALayer(hip, w, lanes=32, max_tokens=32 * 64, weight_dtype=dtype)
+    got = layer.prefill_inference(ids)
+    carry = layer.get_carry()
+    ref_w = w if dtype == "f32" else w.to_bf16_values()
+    ref, st = oracle_prefill(ref_w, ids[:4], threads=4)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    assert rel_err(got[:4], ref) < tol
+    assert rel_err(carry[:4], st) < tol
+    layer.close()
+
+
+def test_config3_full_length_properties(hip):
+    """Full benchmark shape (32 x 1024, bf16): finite, deterministic, and a
+    512 + 512 split prefill equals the single 1024-token prefill bit for bit."""
+    say("config3 full length")
+    cfg = PSSAConfig(depth=12, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    ids = np.random.default_rng(3).integers(0, cfg.d_vocab, (32, 1024), dtype=np.uint32)
+    layer = PSSALayer(hip, w, lanes=32, max_tokens=32 * 1024, weight_dtype="bf16")
+    a = layer.prefill_inference(ids)
+    ca = layer.get_carry()
+    assert np.all(np.isfinite(a)) and np.all(np.isfinite(ca))
+    layer.reset_recurrent_state()
+    b = layer.prefill_inference(ids)
+    np.testing.assert_array_equal(a, b)
+    layer.reset_recurrent_state()
+    layer.prefill_inference(ids[:, :512], want_logits=False)
+    c = layer.prefill_inference(ids[:, 512:])
+    np.testing.assert_array_equal(a, c)
+    np.testing.assert_array_equal(layer.get_carry(), ca)
+    layer.close()

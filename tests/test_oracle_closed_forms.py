@@ -1,0 +1,326 @@
+"""Closed-form and brute-force pins for the oracle functions the golden
+fixtures leave open: retrieval (top-k, ties, temperature extremes, projection),
+the SSM recurrence, the dense scan, depth>1 residuals, the refractory gate and
+the Hebbian fast-weight rule.  Each check is chosen so that a plausible slip
+(wrong index, sign, dropped term, transposed operand) fails it."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from pssa_amd import ModelWeights, PSSAConfig
+
+F32_MIN_SUB = np.float32(np.frombuffer(np.uint32(1).tobytes(), np.float32)[0])
+
+
+def bank(capacity, keys, values):
+    keys = np.float32(keys)
+    values = np.float32(values)
+    dk, dv = keys.shape[1], values.shape[1]
+    K = np.zeros((capacity, dk), np.float32)
+    V = np.zeros((capacity, dv), np.float32)
+    N = np.zeros(capacity, np.float32)
+    K[: len(keys)] = keys
+    V[: len(values)] = values
+    for i, k in enumerate(keys):
+        N[i] = O.squared_norm(k)
+    return K, N, V, len(keys)
+
+
+# ---- tests/memory_expansion.rs:53-78 ------------------------------------------
+def test_nearest_read_masks_other_slots_and_full_k_is_exact():
+    K, N, V, count = bank(5, [[0.0], [0.1], [0.6]], [[2.0], [4.0], [100.0]])
+    q = np.float32([0.0])
+    full_out, full_w, _ = O.retrieve(K, N, V, count, q, 1.0, 0)
+    for k in (3, 9):
+        out, w, _ = O.retrieve(K, N, V, count, q, 1.0, k)
+        np.testing.assert_array_equal(out, full_out)
+        np.testing.assert_array_equal(w, full_w)
+    out, w, _ = O.retrieve(K, N, V, count, q, 1.0, 1)
+    assert out[0] == 2.0
+    np.testing.assert_array_equal(w, np.float32([1, 0, 0, 0, 0]))
+    out, w, _ = O.retrieve(K, N, V, count, q, 1.0, 2)
+    assert 2.0 < out[0] < 4.0
+    assert abs(w.sum() - 1.0) < 1e-6 and w[2] == 0.0
+
+
+# ---- tests/memory_expansion.rs:80-93 ------------------------------------------
+def test_nearest_ties_tiny_temperature_and_empty_are_stable():
+    K, N, V, count = bank(4, np.zeros((0, 1)), np.zeros((0, 1)))
+    out, w, _ = O.retrieve(K, N, V, 0, np.float32([0.0]), F32_MIN_SUB, 1)
+    assert out[0] == 0.0 and not w.any()
+    K, N, V, count = bank(4, [[0.2], [-0.2]], [[1.0], [2.0]])
+    out, w, _ = O.retrieve(K, N, V, count, np.float32([0.0]), F32_MIN_SUB, 1)
+    assert out[0] == 1.0  # exact tie: the lower slot wins
+    np.testing.assert_array_equal(w, np.float32([1, 0, 0, 0]))
+
+
+# ---- tests/memory_projection.rs:4-54 ------------------------------------------
+@pytest.mark.parametrize("q", [
+    [0.0], [16_777_216.0], [-3.4028235e38], [3.4028235e38, -3.4028235e38, 3.4028235e38],
+    [3.4028235e38] * 4096, [1e-45, -1e-45],
+])
+def test_extreme_queries_project_strictly_inside_the_ball(q):
+    q = np.float32(q)
+    p, norm = O.project(q)
+    assert np.isfinite(norm) and np.all(np.isfinite(p))
+    assert O.squared_norm(p) < 1.0
+    if np.any(np.abs(q) > 1.0):
+        assert O.squared_norm(p) > 0.99
+    K, N, V, count = bank(1, [p], [[2.0, -3.0]])
+    out, w, _ = O.retrieve(K, N, V, count, p, F32_MIN_SUB, 0)
+    np.testing.assert_array_equal(out, np.float32([2.0, -3.0]))
+    assert w[0] == 1.0
+
+
+def test_tiny_temperature_keeps_nearest_entries_and_ties_finite():
+    K, N, V, count = bank(3, [[0.5]], [[1.0, 2.0]])
+    for tau in (1e-40, F32_MIN_SUB):
+        out, w, _ = O.retrieve(K, N, V, count, np.float32([0.0]), np.float32(tau), 0)
+        np.testing.assert_array_equal(out, np.float32([1.0, 2.0]))
+        assert w[0] == 1.0
+    K, N, V, count = bank(3, [[0.5], [-0.5], [0.75]], [[1.0, 2.0], [3.0, -2.0], [100.0, 100.0]])
+    out, w, _ = O.retrieve(K, N, V, count, np.float32([0.0]), F32_MIN_SUB, 0)
+    np.testing.assert_array_equal(w, np.float32([0.5, 0.5, 0.0]))
+    np.testing.assert_array_equal(out, np.float32([2.0, 0.0]))
+
+
+def test_projection_matches_closed_form():
+    rng = np.random.default_rng(1)
+    for n in (1, 2, 32, 768):
+        q = rng.standard_normal(n).astype(np.float32) * 3
+        p, norm = O.project(q)
+        r = np.sqrt(np.sum(q.astype(np.float64) ** 2))
+        np.testing.assert_allclose(p, q * (min(r / (1 + r), 1 - 8 * 2.0 ** -23) / r), rtol=2e-7)
+        assert abs(norm - r) <= 1e-6 * r
+
+
+def test_poincare_distance_matches_arccosh_form():
+    rng = np.random.default_rng(2)
+    for n in (1, 3, 32, 768):
+        for _ in range(20):
+            u = rng.standard_normal(n)
+            v = rng.standard_normal(n)
+            u = (u / np.linalg.norm(u) * rng.uniform(0, 0.9)).astype(np.float32)
+            v = (v / np.linalg.norm(v) * rng.uniform(0, 0.9)).astype(np.float32)
+            uu, vv = u.astype(np.float64), v.astype(np.float64)
+            su, sv = np.sum(uu ** 2), np.sum(vv ** 2)
+            ref = np.arccosh(1 + 2 * np.sum((uu - vv) ** 2) / ((1 - su) * (1 - sv)))
+            assert abs(float(O.poincare_distance(u, v)) - ref) <= 1e-6 * max(ref, 1e-3)
+    # Rust's asinh formula: exact zero, odd symmetry, agreement with arcsinh.
+    assert O.lib().oracle_rust_asinh(0.0) == 0.0
+    for x in (1e-300, 1e-8, 0.3, 1.0, 7.5, 1e10, 1e300):
+        a = O.lib().oracle_rust_asinh(x)
+        assert a == -O.lib().oracle_rust_asinh(-x)
+        assert abs(a - np.arcsinh(x)) <= 4e-16 * abs(np.arcsinh(x))
+
+
+def test_retrieve_top_k_matches_brute_sort():
+    rng = np.random.default_rng(5)
+    C, dk, dv, k = 64, 8, 5, 8
+    dirs = rng.standard_normal((C, dk))
+    keys = (dirs / np.linalg.norm(dirs, axis=1, keepdims=True) * rng.uniform(0, 0.9, (C, 1))).astype(np.float32)
+    keys[10] = keys[3]  # an exact tie: slot 3 must win over slot 10
+    vals = rng.standard_normal((C, dv)).astype(np.float32)
+    K, N, V, count = bank(C, keys, vals)
+    for t in range(30):
+        q = keys[3] if t == 0 else (rng.standard_normal(dk) * 0.05).astype(np.float32)
+        out, w, mn = O.retrieve(K, N, V, count, q, 0.1, k)
+        d = np.float32([O.poincare_distance(q, keys[s]) for s in range(C)])
+        order = sorted(range(C), key=lambda s: (d[s].view(np.uint32), s))[:k]
+        assert set(np.nonzero(w)[0]) == set(order)
+        e = np.exp((np.float64(d.min()) - d[order]) / 0.1)
+        np.testing.assert_allclose(w[sorted(order)], (e / e.sum())[np.argsort(order)], rtol=1e-5)
+        np.testing.assert_allclose(out, (e / e.sum()) @ vals[order], rtol=1e-5, atol=1e-6)
+        assert mn == d.min()
+        if t == 0:
+            assert 3 in order and (10 not in order or k > 1)
+
+
+def test_full_soft_read_matches_float64_softmax():
+    rng = np.random.default_rng(6)
+    C, dk, dv = 100, 6, 9
+    dirs = rng.standard_normal((C, dk))
+    keys = (dirs / np.linalg.norm(dirs, axis=1, keepdims=True) * rng.uniform(0, 0.9, (C, 1))).astype(np.float32)
+    vals = rng.standard_normal((C, dv)).astype(np.float32)
+    K, N, V, count = bank(128, keys, vals)
+    q = (rng.standard_normal(dk) * 0.1).astype(np.float32)
+    out, w, _ = O.retrieve(K, N, V, count, q, 0.1, 0)
+    d = np.float64([O.poincare_distance(q, keys[s]) for s in range(C)])
+    e = np.exp((d.min() - d) / 0.1)
+    np.testing.assert_allclose(w[:C], e / e.sum(), rtol=1e-5, atol=1e-9)
+    assert not w[C:].any()
+    np.testing.assert_allclose(out, (e / e.sum()) @ vals, rtol=1e-5, atol=1e-6)
+
+
+# ---- SSM recurrence vs float64 closed form (tests/backend_cuda.rs:97-140 fixture)
+def cuda_ssm_fixture():
+    L, dm, ds = 7, 3, 2
+    delta = np.float32([0.2, 0.4, 0.3, 0.5, 0.25, 0.6, 0.35, 0.45, 0.55, 0.3, 0.7, 0.2, 0.5, 0.4, 0.65,
+                        0.25, 0.35, 0.8, 0.45, 0.3, 0.6])
+    b_proj = np.float32([0.03 * (i - 4.0) for i in range(L * ds)])
+    x_norm = np.float32([0.1 + 0.02 * i for i in range(L * dm)])
+    rates = np.float32([-0.2, -0.35, -0.25, -0.45, -0.3, -0.15])
+    c_proj = np.float32([-0.04 + 0.01 * i for i in range(L * ds)])
+    initial = np.float32([0.01, -0.02, 0.03, -0.04, 0.02, -0.01])
+    return L, dm, ds, delta, b_proj, x_norm, rates, c_proj, initial
+
+
+def ssm_f64(L, dm, ds, delta, b_proj, x_norm, rates, c_proj, initial):
+    h = initial.astype(np.float64).reshape(dm, ds).copy()
+    ys, states = [], [h.copy()]
+    D = delta.reshape(L, dm).astype(np.float64)
+    B = b_proj.reshape(L, ds).astype(np.float64)
+    X = x_norm.reshape(L, dm).astype(np.float64)
+    Cc = c_proj.reshape(L, ds).astype(np.float64)
+    R = rates.reshape(dm, ds).astype(np.float64)
+    for t in range(L):
+        a = np.exp(D[t][:, None] * R)
+        h = a * h + (D[t][:, None] * B[t][None, :]) * X[t][:, None]
+        states.append(h.copy())
+        ys.append(h @ Cc[t])
+    return np.array(ys).ravel(), np.array(states).ravel()
+
+
+def test_ssm_oracle_matches_closed_form_on_reference_fixture():
+    args = cuda_ssm_fixture()
+    bar_a, bar_b, states, y = O.ssm_forward(*args[3:], *args[:3])
+    y64, s64 = ssm_f64(*args)
+    # f32 rounding of values ~1e-2 over seven steps: absolute error ~1e-9.
+    np.testing.assert_allclose(y, y64, rtol=2e-6, atol=1e-8)
+    np.testing.assert_allclose(states, s64, rtol=2e-6, atol=1e-8)
+    L, dm, ds = args[:3]
+    assert np.all(states[: dm * ds] == args[-1])
+
+
+def test_dense_scan_oracle_matches_float64_and_reduces_to_diagonal():
+    rng = np.random.default_rng(9)
+    B, L, s = 2, 50, 6
+    q, _ = np.linalg.qr(rng.standard_normal((B, L, s, s)))
+    a = (q * rng.uniform(0.8, 0.99, (B, L, 1, s))).astype(np.float32)
+    b = rng.standard_normal((B, L, s)).astype(np.float32)
+    h = O.dense_scan(a, b)
+    ref = np.zeros((B, L, s))
+    for i in range(B):
+        cur = np.zeros(s)
+        for t in range(L):
+            cur = a[i, t].astype(np.float64) @ cur + b[i, t]
+            ref[i, t] = cur
+    np.testing.assert_allclose(h, ref, rtol=1e-5, atol=1e-5)
+    # A diagonal A_t makes it the diagonal recurrence h = a*h + b (f32 state,
+    # products exact in f64, one rounding per step).
+    diag = rng.uniform(0.5, 0.99, (B, L, s)).astype(np.float32)
+    A = np.zeros((B, L, s, s), np.float32)
+    idx = np.arange(s)
+    A[:, :, idx, idx] = diag
+    h2 = O.dense_scan(A, b)
+    cur = np.zeros((B, s), np.float32)
+    for t in range(L):
+        cur = np.float32(diag[:, t].astype(np.float64) * cur + b[:, t])
+        np.testing.assert_array_equal(h2[:, t], cur)
+
+
+# ---- depth > 1: a second block whose output is forced to zero ------------------
+def test_depth_two_with_silent_second_block_equals_depth_one():
+    c1 = PSSAConfig(depth=1, d_vocab=11, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=8)
+    c2 = PSSAConfig(depth=2, d_vocab=11, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=8)
+    w1 = ModelWeights(c1)
+    O.OracleModel(w1).init_baseline(11)
+    w2 = ModelWeights(c2)
+    O.OracleModel(w2).init_baseline(11)
+    w2.embed[:] = w1.embed
+    w2.unembed[:] = w1.unembed
+    for name in w1.blocks[0].SHAPES:
+        getattr(w2.blocks[0], name)[...] = getattr(w1.blocks[0], name)
+    # Block 1: C = 0 (y = 0), W_proj = 0, adapter up = 0, W2 = 0 -> z_final = 0.
+    b = w2.blocks[1]
+    for name in ("w_c", "w_proj", "adapter_up", "adapter_slow", "mlp_w2"):
+        getattr(b, name)[...] = 0
+    o1, o2 = O.OracleModel(w1), O.OracleModel(w2)
+    s1, s2 = o1.zero_state(), o2.zero_state()
+    ids = [1, 5, 3, 9, 2]
+    l1 = o1.prefill(s1, ids)
+    l2 = o2.prefill(s2, ids)
+    np.testing.assert_array_equal(l1, l2)
+    # ... and a second block with a live readout does change them.
+    w2.blocks[1].w_c[...] = 0.05
+    o2 = O.OracleModel(w2)
+    f1 = o1.features(o1.zero_state(), 4)
+    f2 = o2.features(o2.zero_state(), 4)
+    assert np.max(np.abs(f1 - f2)) > 1e-3
+
+
+# ---- src/feature_benchmark.rs:446-500 refractory protocol ------------------------
+def test_refractory_protocol_closed_form():
+    import ctypes as C
+
+    from pssa_amd import _abi
+
+    cfg = PSSAConfig(depth=1, d_vocab=2, d_latent=1, d_state=1, d_mem_key=1, mem_capacity=1)
+    w = ModelWeights(cfg)
+    view, blocks = w.c_view()
+    blk = C.cast(C.pointer(blocks[0]), C.c_void_p)
+    key, _ = O.project(np.float32([0.4]))
+    contra, _ = O.project(np.float32([-0.4]))
+    assert O.lib().oracle_bank_insert(blk, 1, 1, 1, O.ptr(key), O.ptr(np.float32([1.0]))) == 0
+    defended = 0
+    for step in range(1, 257):
+        r = O.lib().oracle_bank_insert_protected(blk, 1, 1, 1, O.ptr(contra), O.ptr(np.float32([-1.0])), 2.5, step)
+        defended += r < 0
+    w.sync_from_c(blocks)
+    assert defended == 256
+    assert w.blocks[0].mem_values[0, 0] == 1.0
+    # gain = max((1 - e^(-1/60))^2, 0.005) = 0.005; damage = 0.08 * 2.5 * 0.005 per step.
+    assert O.lib().oracle_refractory_gain(1, 60.0) == np.float32(0.005)
+    assert abs(float(w.blocks[0].mem_confidence[0]) - (1 - 256 * 0.001)) < 1e-5
+    # A long quiet interval rebuilds full damage and the slot is overwritten.
+    assert O.lib().oracle_bank_insert_protected(blk, 1, 1, 1, O.ptr(contra), O.ptr(np.float32([-1.0])), 20.0, 10_000) == 0
+    w.sync_from_c(blocks)
+    assert w.blocks[0].mem_values[0, 0] == -1.0 and w.blocks[0].mem_confidence[0] == 1.0
+    del _abi
+
+
+def test_hebbian_rule_closed_form():
+    d, r = 3, 2
+    up = np.zeros((d, r), np.float32)
+    target = np.float32([3.0, 4.0, 0.0])  # ||v|| = 5 -> rate = 0.02 / 6
+    current = np.float32([1.0, -10.0, 0.5])
+    act = np.float32([0.5, -2.0])
+    O.lib().oracle_hebbian_update(O.ptr(up), O.ptr(target), O.ptr(current), O.ptr(act), d, r)
+    rate = np.float32(0.02) / np.float32(6.0)
+    err = np.float32([2.0, 4.0, -0.5])  # 14 is clamped to 4
+    np.testing.assert_allclose(up, (rate * err)[:, None] * act[None, :], rtol=1e-6)
+
+
+def test_oracle_prefill_equals_token_loop_and_lanes():
+    cfg = PSSAConfig(depth=2, d_vocab=50, d_latent=24, d_state=8, d_mem_key=4, mem_capacity=16)
+    w = ModelWeights.init(cfg, 21, "baseline")
+    w.populate_banks(4, 10)
+    om = O.OracleModel(w)
+    ids = np.array([[3, 7, 1, 49, 0, 22], [5, 5, 5, 1, 2, 3]], np.uint32)
+    states = om.zero_state(2)
+    lanes_logits = om.prefill_lanes(states, ids, threads=2)
+    for lane in range(2):
+        st = om.zero_state()
+        for t in ids[lane][:-1]:
+            om.forward_inference(st, int(t), logits=False)
+        last = om.forward_inference(st, int(ids[lane][-1]))
+        np.testing.assert_array_equal(last, lanes_logits[lane])
+        np.testing.assert_array_equal(st, states[lane])
+    with pytest.raises(ValueError):
+        om.prefill(om.zero_state(), [1, 50])
+
+
+def test_product_baseline_init_matches_oracle():
+    cfg = PSSAConfig(depth=2, d_vocab=30, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=8)
+    p = ModelWeights.init(cfg, 5, "baseline")
+    p.populate_banks(6, 5)
+    o = ModelWeights(cfg)
+    om = O.OracleModel(o)
+    assert om.init_baseline(5) == p.rng_state
+    om.populate_banks(6, 5)
+    np.testing.assert_array_equal(p.embed, o.embed)
+    for bp, bo in zip(p.blocks, o.blocks):
+        for name in bp.SHAPES:
+            np.testing.assert_array_equal(getattr(bp, name), getattr(bo, name), err_msg=name)
+        assert bp.mem_count == bo.mem_count == 5
+    assert np.all(p.blocks[0].mem_norm_sq[:5] < 0.9 ** 2)

@@ -169,13 +169,21 @@ int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const voi
     if (rows > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return Status::Invalid("gemm: too large");
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
-    DevBuf dx, dw, dy;
+    DevBuf dx, dxh, dw, dy;
     PSSA_RETURN_IF(upload(dx, x, xin * 4, ctx->stream));
     PSSA_RETURN_IF(upload(dw, w, win * (w_dtype == PSSA_HIP_BF16 ? 2 : 4), ctx->stream));
     PSSA_RETURN_IF(dy.alloc(yout * 4));
-    PSSA_RETURN_IF(pssa::launch_gemm_xwt(ctx->stream, dx.as<float>(), (int)k, dw.p, (int)k, w_dtype,
-                                         dy.as<float>(), (int)n, (int)rows, (int)n, (int)k,
-                                         pssa::EpiParams{}));
+    const void* a = dx.p;
+    if (w_dtype == PSSA_HIP_BF16) {
+      // bf16 weights multiply bf16-rounded activations (fp32 accumulation).
+      PSSA_RETURN_IF(dxh.alloc(xin * 2));
+      PSSA_RETURN_IF(pssa::launch_to_bf16(ctx->stream, dx.as<float>(), (int)k, dxh.as<uint16_t>(), (int)k, rows, (int)k));
+      a = dxh.p;
+    }
+    pssa::EpiParams ep;
+    ep.out32 = dy.as<float>();
+    ep.ld32 = (int)n;
+    PSSA_RETURN_IF(pssa::launch_gemm(ctx->stream, w_dtype, a, (int)k, dw.p, (int)k, (int)rows, (int)n, (int)k, ep));
     PSSA_RETURN_IF(download(y, dy, yout * 4, ctx->stream));
     return sync(ctx);
   };
@@ -320,12 +328,17 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
     PSSA_RETURN_IF(wts.alloc((size_t)L * C * 4));
     for (DevBuf* b : {&mv, &gm, &mp, &mi}) PSSA_RETURN_IF(b->alloc((size_t)L * d * 4));
     // q_euc = x W_qx^T + y W_qh^T, as dot(row_x, x) + dot(row_h, y) (src/pssa.rs:1147-1152).
-    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dx.as<float>(), d, dwqx.p, d, PSSA_HIP_F32, qx.as<float>(), k, L, k, d, pssa::EpiParams{}));
+    pssa::EpiParams ex;
+    ex.out32 = qx.as<float>();
+    ex.ld32 = k;
+    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwqx.p, d, L, k, d, ex));
     pssa::EpiParams eq;
     eq.kind = pssa::EPI_ADD_AUX;
     eq.aux = qx.as<float>();
     eq.ld_aux = k;
-    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dy.as<float>(), d, dwqh.p, d, PSSA_HIP_F32, qe.as<float>(), k, L, k, d, eq));
+    eq.out32 = qe.as<float>();
+    eq.ld32 = k;
+    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dy.p, d, dwqh.p, d, L, k, d, eq));
     pssa::RetrieveArgs ra;
     ra.q = qe.as<float>();
     ra.ld_q = k;
@@ -348,7 +361,12 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
     PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
     if (!sparse) {
       if (count > 0)
-        PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, wts.as<float>(), C, dvt.p, C, PSSA_HIP_F32, mv.as<float>(), d, L, d, (int)count, pssa::EpiParams{}));
+      {
+        pssa::EpiParams em;
+        em.out32 = mv.as<float>();
+        em.ld32 = d;
+        PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, wts.p, C, dvt.p, C, L, d, (int)count, em));
+      }
       else
         PSSA_RETURN_IF(pssa::launch_fill_zero(st, mv.as<float>(), (size_t)L * d));
     }
@@ -358,8 +376,13 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
     eg.seg[1] = 0;
     eg.seg[2] = d;
     eg.seg[3] = d;
-    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, dx.as<float>(), d, dwg.p, d, PSSA_HIP_F32, gm.as<float>(), d, L, d, d, eg));
-    PSSA_RETURN_IF(pssa::launch_gemm_xwt(st, mv.as<float>(), d, dwp.p, d, PSSA_HIP_F32, mp.as<float>(), d, L, d, d, pssa::EpiParams{}));
+    eg.out32 = gm.as<float>();
+    eg.ld32 = d;
+    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwg.p, d, L, d, d, eg));
+    pssa::EpiParams ep2;
+    ep2.out32 = mp.as<float>();
+    ep2.ld32 = d;
+    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, mv.p, d, dwp.p, d, L, d, d, ep2));
     PSSA_RETURN_IF(pssa::launch_mul(st, gm.as<float>(), mp.as<float>(), mi.as<float>(), (size_t)L * d));
     if (q_euc) PSSA_RETURN_IF(download(q_euc, qe, (size_t)L * k * 4, st));
     if (q_pnc) PSSA_RETURN_IF(download(q_pnc, qp, (size_t)L * k * 4, st));
@@ -492,7 +515,7 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       for (size_t i = 0; i < d * s; ++i) rates[i] = -softplus_host(b.a_raw[i]) * 1.4426950408889634f;
       for (size_t q = 0; q < C; ++q)
         for (size_t j = 0; j < d; ++j) vt[j * C + q] = b.mem_values[q * d + j];
-      PSSA_RETURN_IF(upload(B.u_eff, ueff.data(), ueff.size() * 4, st));
+      PSSA_RETURN_IF(upload_weight(B.u_eff, ueff.data(), ueff.size(), weight_dtype, st));
       PSSA_RETURN_IF(upload(B.rates2, rates.data(), rates.size() * 4, st));
       PSSA_RETURN_IF(upload(B.gamma, b.norm_gamma, d * 4, st));
       PSSA_RETURN_IF(upload(B.beta, b.norm_beta, d * 4, st));
@@ -536,15 +559,21 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     const size_t n = max_tokens;
     PSSA_RETURN_IF(L->carry.alloc(lanes * c.depth * d * s * 4));
     PSSA_RETURN_IF(L->ids.alloc(n * 4));
+    const size_t es = model->dtype == PSSA_HIP_BF16 ? 2 : 4;  // operand element size
     PSSA_RETURN_IF(L->X.alloc(n * d * 4));
     PSSA_RETURN_IF(L->XN.alloc(n * d * 4));
     PSSA_RETURN_IF(L->P.alloc(n * model->n_in * 4));
     PSSA_RETURN_IF(L->Y.alloc(n * d * 4));
     PSSA_RETURN_IF(L->Q.alloc(n * k * 4));
-    PSSA_RETURN_IF(L->Wm.alloc(n * C * 4));
-    PSSA_RETURN_IF(L->Mval.alloc(n * d * 4));
     PSSA_RETURN_IF(L->Zraw.alloc(n * d * 4));
-    PSSA_RETURN_IF(L->H1.alloc(n * 2 * d * 4));
+    if (es == 2) {
+      PSSA_RETURN_IF(L->XNh.alloc(n * d * 2));
+      PSSA_RETURN_IF(L->Yh.alloc(n * d * 2));
+      PSSA_RETURN_IF(L->Zrawh.alloc(n * d * 2));
+    }
+    PSSA_RETURN_IF(L->Wm.alloc(n * C * es));
+    PSSA_RETURN_IF(L->Mval.alloc(n * d * es));
+    PSSA_RETURN_IF(L->H1.alloc(n * 2 * d * es));
     PSSA_RETURN_IF(L->logits.alloc(lanes * c.d_vocab * 4));
     PSSA_RETURN_IF(pssa::launch_fill_zero(ctx->stream, L->carry.as<float>(), lanes * c.depth * d * s));
     PSSA_RETURN_IF(sync(ctx));

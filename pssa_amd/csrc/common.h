@@ -103,7 +103,8 @@ struct DevBuf {
   }
   Status alloc(size_t n) {
     release();
-    if (n == 0) n = 16;
+    n = (n + 255) & ~(size_t)255;  // whole 256-byte granules: fills may round up to a vector
+    if (n == 0) n = 256;
     hipError_t e = hipMalloc(&p, n);
     if (e != hipSuccess) {
       p = nullptr;

@@ -5,37 +5,49 @@
 namespace pssa {
 
 enum EpiKind : int {
-  EPI_STORE = 0,     // C = acc
+  EPI_STORE = 0,     // r = acc
   EPI_SEGMENTS = 1,  // column ranges: [0,seg0) softplus, [seg0,seg1) identity,
                      // [seg1,seg2) sigmoid, [seg2,seg3) SiLU, rest identity
-  EPI_ADD_AUX = 2,   // C = acc + aux[row, col]
-  EPI_ZRAW = 3,      // C = y*scale + g*acc + sum_r U[col,r]*act[row,r]
-  EPI_SILU = 4,      // C = SiLU(acc)
-  EPI_RESIDUAL = 5,  // zf = zraw + acc; C = first ? zf : C + scale*zf
-  EPI_SCALE = 6,     // C = acc * scale
+  EPI_ADD_AUX = 2,   // r = acc + aux[row, col]
+  EPI_ZRAW = 3,      // r = (y*scale + g*acc) + sum_q U[col,q]*act[row,q]
+  EPI_SILU = 4,      // r = SiLU(acc)
+  EPI_RESIDUAL = 5,  // zf = aux + acc; r = first ? zf : out32 + scale*zf
+  EPI_SCALE = 6,     // r = acc * scale
+  EPI_KINDS = 7,
 };
 
+// Every GEMM writes r to out32 (fp32) and/or out16 (the operand type of the
+// GEMM: bf16 bits for bf16 GEMMs, fp32 for fp32 GEMMs); either may be null.
 struct EpiParams {
   int kind = EPI_STORE;
   int seg[4] = {0, 0, 0, 0};
-  const float* aux = nullptr;
+  const float* aux = nullptr;  // ADD_AUX operand, RESIDUAL's z_raw
   int ld_aux = 0;
-  const float* y = nullptr;
+  const float* y = nullptr;    // ZRAW: SSM readout
   int ld_y = 0;
-  const float* g = nullptr;
+  const float* g = nullptr;    // ZRAW: memory gate
   int ld_g = 0;
-  const float* act = nullptr;
+  const float* act = nullptr;  // ZRAW: adapter activations [rows, rank] (fp32)
   int ld_act = 0;
-  const float* U = nullptr;
+  const void* U = nullptr;     // ZRAW: adapter up-projection [N, rank] in the operand type
   int rank = 0;
   float scale = 1.0f;
-  const float* zraw = nullptr;
-  int ld_zraw = 0;
   int first = 1;
+  float* out32 = nullptr;
+  int ld32 = 0;
+  void* out16 = nullptr;
+  int ld16 = 0;
 };
 
-// A: fp32 [M, lda]; B: [N, ldb] fp32 or bf16 bits (b_dtype); C: fp32 [M, ldc].
-Status launch_gemm_xwt(hipStream_t stream, const float* A, int lda, const void* B, int ldb,
-                       int b_dtype, float* C, int ldc, int M, int N, int K, const EpiParams& ep);
+// A: activations [M, lda], B: weights [N, ldb], both K-contiguous and of the
+// same type (dtype PSSA_HIP_BF16: bf16 bit patterns; PSSA_HIP_F32: fp32).
+// Accumulation is fp32.
+Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const void* B, int ldb,
+                   int M, int N, int K, const EpiParams& ep);
+
+// fp32 -> bf16 (round to nearest even) copy of a [rows, cols] matrix with
+// leading dimensions ld_in / ld_out.
+Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* out, int ld_out,
+                      size_t rows, int cols);
 
 }  // namespace pssa

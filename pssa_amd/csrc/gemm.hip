@@ -1,15 +1,21 @@
 // MFMA GEMM for gfx950: C[M,N] = epilogue(A[M,K] * B[N,K]^T).
 //
-// A holds fp32 activations.  B holds weights, fp32 or bf16:
-//   bf16 weights -> v_mfma_f32_32x32x16_bf16 (A is rounded to bf16 as it is
-//                   staged in LDS), fp32 accumulation;
-//   fp32 weights -> v_mfma_f32_32x32x2_f32, exact fp32 products.
-// One 256-thread workgroup computes a 128x128 tile; each of its four waves
-// owns a 64x64 quadrant (2x2 MFMA 32x32 tiles, 64 accumulators per lane).
-// K advances in LDS-staged slabs, with the next slab prefetched into
-// registers while the current one feeds the matrix cores.  Tiles are handed
-// out so that each XCD (eight per device, each with its own L2) walks a
-// contiguous run of the output, keeping the activation row-panel in one L2.
+// A holds activations (token rows), B holds weights; both are K-contiguous
+// and share one operand type:
+//   bf16 -> v_mfma_f32_32x32x16_bf16, fp32 accumulation;
+//   fp32 -> v_mfma_f32_32x32x2_f32, exact fp32 products.
+//
+// A 128-thread workgroup (two waves) computes a 128x128 tile; each wave owns
+// 64 token rows x 128 weight rows (2x4 MFMA 32x32 tiles, 128 accumulators
+// per lane).  The weights are the MFMA's first operand, so the accumulator
+// holds the tile transposed: a lane keeps one token row and runs of four
+// consecutive output columns, which the epilogue reads and writes as 16-byte
+// vectors.  K advances in LDS-staged slabs; the next slab is prefetched into
+// registers while the current one feeds the matrix cores.  Rows are padded
+// to an odd multiple of 16 bytes so the fragment reads are bank-conflict
+// free.  Tiles are handed out so that each XCD (eight per device, each with
+// its own L2) walks a contiguous run of tiles in token-row-major order,
+// keeping the activation row panel in one L2.
 #include "gemm.h"
 
 namespace pssa {
@@ -17,16 +23,30 @@ namespace pssa {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// softplus(x) = x > 20 ? x : ln(1 + e^x) (src/linalg.rs:548-551).  ln(1+t) is
+// evaluated as ln(u) * t / (u - 1) with u = 1 + t, which cancels the rounding
+// of u (relative error a few ulp), and as t - t^2/2 for t < 2^-12.
+__device__ __forceinline__ float softplus_f(float x) {
+  if (x > 20.0f) return x;
+  const float t = __expf(x);
+  if (t < 2.44140625e-4f) return t - 0.5f * t * t;
+  const float u = 1.0f + t;
+  return __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.0f));
+}
+// sigmoid(x) = 1 / (1 + e^-x) (src/linalg.rs:553-555), with the hardware
+// reciprocal (1 ulp).
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
-// Maps the hardware block id to a tile so that the blocks an XCD receives
+// Maps the hardware block id to a tile so that the blocks one XCD receives
 // (block ids congruent mod 8) cover one contiguous range of tiles.
 __device__ __forceinline__ int xcd_tile(int bid, int total) {
   const int per = total / 8, rem = total % 8;
@@ -34,246 +54,223 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
   return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
 }
 
-__device__ __forceinline__ float apply_epilogue(const EpiParams& ep, float acc, int row, int col,
-                                                float* __restrict__ C, int ldc) {
-  switch (ep.kind) {
-    case EPI_STORE:
-      return acc;
-    case EPI_SCALE:
-      return acc * ep.scale;
-    case EPI_SEGMENTS: {
-      if (col < ep.seg[0]) return softplus_f(acc);
-      if (col < ep.seg[1]) return acc;
-      if (col < ep.seg[2]) return sigmoid_f(acc);
-      if (col < ep.seg[3]) return acc * sigmoid_f(acc);
-      return acc;
-    }
-    case EPI_ADD_AUX:
-      return acc + ep.aux[(size_t)row * ep.ld_aux + col];
-    case EPI_SILU:
-      return acc * sigmoid_f(acc);
-    case EPI_ZRAW: {
-      // z_raw = (y * ssm_scale) + (g * m_proj) + adapter, in the reference's
-      // left-to-right order (src/pssa.rs:1190-1192).
-      const float* act = ep.act + (size_t)row * ep.ld_act;
-      const float* u = ep.U + (size_t)col * ep.rank;
-      float ad = 0.0f;
-      for (int r = 0; r < ep.rank; ++r) ad = fmaf(u[r], act[r], ad);
-      const float yv = ep.y[(size_t)row * ep.ld_y + col];
-      const float gv = ep.g[(size_t)row * ep.ld_g + col];
-      return (yv * ep.scale + gv * acc) + ad;
-    }
-    case EPI_RESIDUAL: {
-      // z_final = z_raw + mlp_out; layer 0 publishes it, deeper layers add
-      // it with the 1/sqrt(depth) residual scale (src/pssa.rs:2332-2337).
-      const float zf = ep.zraw[(size_t)row * ep.ld_zraw + col] + acc;
-      if (ep.first) return zf;
-      return C[(size_t)row * ldc + col] + ep.scale * zf;
-    }
-    default:
-      return acc;
+template <typename T>
+struct Op;
+template <>
+struct Op<uint16_t> {
+  static constexpr int BK = 32;  // K per slab
+  static constexpr int LD = 40;  // LDS row pitch (elements): 80 bytes
+  static constexpr int VE = 8;   // elements per 16-byte vector
+};
+template <>
+struct Op<float> {
+  static constexpr int BK = 16;
+  static constexpr int LD = 20;
+  static constexpr int VE = 4;
+};
+
+constexpr int BM = 128, BN = 128, NT = 128;
+
+// One output element's epilogue (fp32 result before the stores).
+template <int KIND>
+__device__ __forceinline__ float epi_value(const EpiParams& ep, float acc, int row, int col, float ad) {
+  if constexpr (KIND == EPI_STORE) {
+    return acc;
+  } else if constexpr (KIND == EPI_SCALE) {
+    return acc * ep.scale;
+  } else if constexpr (KIND == EPI_SEGMENTS) {
+    if (col < ep.seg[0]) return softplus_f(acc);
+    if (col < ep.seg[1]) return acc;
+    if (col < ep.seg[2]) return sigmoid_f(acc);
+    if (col < ep.seg[3]) return acc * sigmoid_f(acc);
+    return acc;
+  } else if constexpr (KIND == EPI_ADD_AUX) {
+    return acc + ep.aux[(size_t)row * ep.ld_aux + col];
+  } else if constexpr (KIND == EPI_SILU) {
+    return acc * sigmoid_f(acc);
+  } else if constexpr (KIND == EPI_ZRAW) {
+    // z_raw = (y * ssm_scale) + (g * m_proj) + adapter, left to right
+    // (src/pssa.rs:1190-1192).
+    const float yv = ep.y[(size_t)row * ep.ld_y + col];
+    const float gv = ep.g[(size_t)row * ep.ld_g + col];
+    return (yv * ep.scale + gv * acc) + ad;
+  } else {  // EPI_RESIDUAL
+    // z_final = z_raw + mlp_out; layer 0 publishes it, deeper layers add it
+    // with the 1/sqrt(depth) residual scale (src/pssa.rs:2332-2337).
+    const float zf = ep.aux[(size_t)row * ep.ld_aux + col] + acc;
+    if (ep.first) return zf;
+    return ep.out32[(size_t)row * ep.ld32 + col] + ep.scale * zf;
   }
 }
 
-constexpr int BM = 128, BN = 128;
+template <typename T>
+__device__ __forceinline__ void store_one(const EpiParams& ep, int row, int col, float r) {
+  if (ep.out32) ep.out32[(size_t)row * ep.ld32 + col] = r;
+  if (ep.out16) {
+    if constexpr (sizeof(T) == 2)
+      static_cast<uint16_t*>(ep.out16)[(size_t)row * ep.ld16 + col] = (uint16_t)f32_to_bf16_bits(r);
+    else
+      static_cast<float*>(ep.out16)[(size_t)row * ep.ld16 + col] = r;
+  }
+}
 
-template <bool BF16>
-struct Cfg;
-template <>
-struct Cfg<true> {
-  static constexpr int BK = 64;
-  static constexpr int LDS_LD = BK + 8;  // bf16 elements; 144-byte rows keep b128 reads conflict-free
-  using elem = uint16_t;
-};
-template <>
-struct Cfg<false> {
-  static constexpr int BK = 32;
-  static constexpr int LDS_LD = BK + 4;  // floats; 144-byte rows
-  using elem = float;
-};
+// Four consecutive columns col..col+3 of one row.  `vec`: all four are in
+// range and every operand row is 16-byte aligned at col.
+template <typename T, int KIND>
+__device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, int N, bool vec,
+                                         const float (&acc)[4], const float (&ad)[4]) {
+  if (vec) {
+    float r[4];
+    if constexpr (KIND == EPI_ZRAW) {
+      const float4 yv = *reinterpret_cast<const float4*>(ep.y + (size_t)row * ep.ld_y + col);
+      const float4 gv = *reinterpret_cast<const float4*>(ep.g + (size_t)row * ep.ld_g + col);
+      r[0] = (yv.x * ep.scale + gv.x * acc[0]) + ad[0];
+      r[1] = (yv.y * ep.scale + gv.y * acc[1]) + ad[1];
+      r[2] = (yv.z * ep.scale + gv.z * acc[2]) + ad[2];
+      r[3] = (yv.w * ep.scale + gv.w * acc[3]) + ad[3];
+    } else if constexpr (KIND == EPI_ADD_AUX || KIND == EPI_RESIDUAL) {
+      const float4 av = *reinterpret_cast<const float4*>(ep.aux + (size_t)row * ep.ld_aux + col);
+      const float a4[4] = {av.x, av.y, av.z, av.w};
+      if constexpr (KIND == EPI_ADD_AUX) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = acc[e] + a4[e];
+      } else {
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+        if (!ep.first) {
+          const float4 ov = *reinterpret_cast<const float4*>(ep.out32 + (size_t)row * ep.ld32 + col);
+          o4[0] = ov.x, o4[1] = ov.y, o4[2] = ov.z, o4[3] = ov.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float zf = a4[e] + acc[e];
+          r[e] = ep.first ? zf : o4[e] + ep.scale * zf;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = epi_value<KIND>(ep, acc[e], row, col + e, 0.0f);
+    }
+    if (ep.out32)
+      *reinterpret_cast<float4*>(ep.out32 + (size_t)row * ep.ld32 + col) = make_float4(r[0], r[1], r[2], r[3]);
+    if (ep.out16) {
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ep.out16) + (size_t)row * ep.ld16 + col) =
+            make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+      } else {
+        *reinterpret_cast<float4*>(static_cast<float*>(ep.out16) + (size_t)row * ep.ld16 + col) =
+            make_float4(r[0], r[1], r[2], r[3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (col + e < N) store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
+  }
+}
 
-// VEC: K, lda, ldb are multiples of the vector width and pointers are
-// 16-byte aligned, so slabs move as 16-byte vectors.  Otherwise every
-// element is loaded with its own bounds check (small or ragged shapes).
-template <bool BF16, bool VEC>
-__global__ __launch_bounds__(256) void gemm_xwt_kernel(const float* __restrict__ A, int lda,
-                                                       const void* __restrict__ Bv, int ldb,
-                                                       float* __restrict__ C, int ldc, int M,
-                                                       int N, int K, EpiParams ep) {
-  using CF = Cfg<BF16>;
-  using elem = typename CF::elem;
-  constexpr int BK = CF::BK, LD = CF::LDS_LD;
-  __shared__ __attribute__((aligned(16))) elem sA[BM * LD];
-  __shared__ __attribute__((aligned(16))) elem sB[BN * LD];
+template <typename T, int KIND>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const T* __restrict__ A, int lda,
+                                                  const T* __restrict__ B, int ldb, int M, int N,
+                                                  int K, int vec_load, int vec_epi, EpiParams ep) {
+  constexpr int BK = Op<T>::BK, LD = Op<T>::LD, VE = Op<T>::VE;
+  constexpr int CPR = BK / VE;         // 16-byte chunks per slab row
+  constexpr int NV = BM * CPR / NT;    // chunks per thread per operand
+  static_assert(BM == BN, "both operands share the staging map");
+  __shared__ __attribute__((aligned(16))) T sA[BM * LD];
+  __shared__ __attribute__((aligned(16))) T sB[BN * LD];
 
   const int tilesN = (N + BN - 1) / BN, tilesM = (M + BM - 1) / BM;
   const int tile = xcd_tile(blockIdx.x, tilesM * tilesN);
   const int m0 = (tile / tilesN) * BM, n0 = (tile % tilesN) * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int half = lane >> 5, l32 = lane & 31;
 
-  // ---- register prefetch of one slab ------------------------------------
-  // fp32 A slab: BM x BK floats = BM*BK/4 float4; bf16 mode uses BK=64 so
-  // A needs 8 float4 per thread, fp32 mode 4.
-  constexpr int A_VEC = BM * BK / 4 / 256;
-  constexpr int B_VEC = BF16 ? (BN * BK / 8 / 256) : (BN * BK / 4 / 256);
-  float4 ra[A_VEC];
-  float4 rb[B_VEC];  // bf16: 8 bf16 bit patterns per float4
-
+  float4 ra[NV], rb[NV];
   auto load_slab = [&](int k0) {
-    if constexpr (VEC) {
 #pragma unroll
-      for (int i = 0; i < A_VEC; ++i) {
-        const int v = tid + 256 * i;
-        const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-        const int gr = m0 + r, gk = k0 + c;
-        ra[i] = (gr < M && gk < K) ? *reinterpret_cast<const float4*>(A + (size_t)gr * lda + gk)
+    for (int i = 0; i < NV; ++i) {
+      const int v = tid + NT * i;
+      const int r = v / CPR, c = (v % CPR) * VE;
+      const int gk = k0 + c;
+      const int gm = m0 + r, gn = n0 + r;
+      if (vec_load) {
+        ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const float4*>(A + (size_t)gm * lda + gk)
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+        rb[i] = (gn < N && gk < K) ? *reinterpret_cast<const float4*>(B + (size_t)gn * ldb + gk)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        T ta[VE], tb[VE];
 #pragma unroll
-      for (int i = 0; i < B_VEC; ++i) {
-        const int v = tid + 256 * i;
-        if constexpr (BF16) {
-          const int r = v / (BK / 8), c = (v % (BK / 8)) * 8;
-          const int gn = n0 + r, gk = k0 + c;
-          const uint16_t* B = static_cast<const uint16_t*>(Bv);
-          rb[i] = (gn < N && gk < K) ? *reinterpret_cast<const float4*>(B + (size_t)gn * ldb + gk)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
-        } else {
-          const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-          const int gn = n0 + r, gk = k0 + c;
-          const float* B = static_cast<const float*>(Bv);
-          rb[i] = (gn < N && gk < K) ? *reinterpret_cast<const float4*>(B + (size_t)gn * ldb + gk)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int q = 0; q < VE; ++q) {
+          const bool kin = gk + q < K;
+          ta[q] = (gm < M && kin) ? A[(size_t)gm * lda + gk + q] : T(0);
+          tb[q] = (gn < N && kin) ? B[(size_t)gn * ldb + gk + q] : T(0);
         }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < A_VEC; ++i) {
-        const int v = tid + 256 * i;
-        const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-        const int gr = m0 + r;
-        float t[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int gk = k0 + c + q;
-          t[q] = (gr < M && gk < K) ? A[(size_t)gr * lda + gk] : 0.0f;
-        }
-        ra[i] = make_float4(t[0], t[1], t[2], t[3]);
-      }
-#pragma unroll
-      for (int i = 0; i < B_VEC; ++i) {
-        const int v = tid + 256 * i;
-        if constexpr (BF16) {
-          const int r = v / (BK / 8), c = (v % (BK / 8)) * 8;
-          const int gn = n0 + r;
-          const uint16_t* B = static_cast<const uint16_t*>(Bv);
-          uint16_t t[8];
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int gk = k0 + c + q;
-            t[q] = (gn < N && gk < K) ? B[(size_t)gn * ldb + gk] : (uint16_t)0;
-          }
-          uint32_t w[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) w[q] = (uint32_t)t[2 * q] | ((uint32_t)t[2 * q + 1] << 16);
-          rb[i] = make_float4(__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]),
-                              __uint_as_float(w[3]));
-        } else {
-          const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-          const int gn = n0 + r;
-          const float* B = static_cast<const float*>(Bv);
-          float t[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int gk = k0 + c + q;
-            t[q] = (gn < N && gk < K) ? B[(size_t)gn * ldb + gk] : 0.0f;
-          }
-          rb[i] = make_float4(t[0], t[1], t[2], t[3]);
-        }
+        __builtin_memcpy(&ra[i], ta, 16);
+        __builtin_memcpy(&rb[i], tb, 16);
       }
     }
   };
-
   auto store_slab = [&]() {
 #pragma unroll
-    for (int i = 0; i < A_VEC; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-      if constexpr (BF16) {
-        const uint32_t lo = (uint32_t)f32_to_bf16_bits(ra[i].x) | ((uint32_t)f32_to_bf16_bits(ra[i].y) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16_bits(ra[i].z) | ((uint32_t)f32_to_bf16_bits(ra[i].w) << 16);
-        *reinterpret_cast<uint2*>(&sA[r * LD + c]) = make_uint2(lo, hi);
-      } else {
-        *reinterpret_cast<float4*>(&sA[r * LD + c]) = ra[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < B_VEC; ++i) {
-      const int v = tid + 256 * i;
-      if constexpr (BF16) {
-        const int r = v / (BK / 8), c = (v % (BK / 8)) * 8;
-        *reinterpret_cast<float4*>(&sB[r * LD + c]) = rb[i];
-      } else {
-        const int r = v / (BK / 4), c = (v % (BK / 4)) * 4;
-        *reinterpret_cast<float4*>(&sB[r * LD + c]) = rb[i];
-      }
+    for (int i = 0; i < NV; ++i) {
+      const int v = tid + NT * i;
+      const int r = v / CPR, c = (v % CPR) * VE;
+      *reinterpret_cast<float4*>(&sA[r * LD + c]) = ra[i];
+      *reinterpret_cast<float4*>(&sB[r * LD + c]) = rb[i];
     }
   };
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[2][4];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+      for (int i = 0; i < 16; ++i) acc[t][u][i] = 0.0f;
 
   const int nk = (K + BK - 1) / BK;
   load_slab(0);
   store_slab();
   __syncthreads();
-  const int half = lane >> 5, l32 = lane & 31;
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + 1 < nk) load_slab((kt + 1) * BK);
-    if constexpr (BF16) {
+    if constexpr (sizeof(T) == 2) {
 #pragma unroll
       for (int kk = 0; kk < BK / 16; ++kk) {
-        bf16x8_t af[2], bf[2];
+        bf16x8_t fa[2], fb[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int ar = wm * 64 + t * 32 + l32;
-          const int br = wn * 64 + t * 32 + l32;
-          af[t] = *reinterpret_cast<const bf16x8_t*>(&sA[ar * LD + kk * 16 + half * 8]);
-          bf[t] = *reinterpret_cast<const bf16x8_t*>(&sB[br * LD + kk * 16 + half * 8]);
-        }
+        for (int t = 0; t < 2; ++t)
+          fa[t] = *reinterpret_cast<const bf16x8_t*>(&sA[(wave * 64 + t * 32 + l32) * LD + kk * 16 + half * 8]);
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int u = 0; u < 4; ++u)
+          fb[u] = *reinterpret_cast<const bf16x8_t*>(&sB[(u * 32 + l32) * LD + kk * 16 + half * 8]);
 #pragma unroll
-          for (int b = 0; b < 2; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bf[b], acc[a][b], 0, 0, 0);
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[u], fa[t], acc[t][u], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int kk = 0; kk < BK / 8; ++kk) {
-        float4 af[2], bf[2];
+        float4 fa[2], fb[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int ar = wm * 64 + t * 32 + l32;
-          const int br = wn * 64 + t * 32 + l32;
-          af[t] = *reinterpret_cast<const float4*>(&sA[ar * LD + kk * 8 + half * 4]);
-          bf[t] = *reinterpret_cast<const float4*>(&sB[br * LD + kk * 8 + half * 4]);
-        }
-        // Lane half h contributes k = kk*8 + 4h + q to the q-th product; A and
-        // B use the same assignment, so the sum over k is complete.
+        for (int t = 0; t < 2; ++t)
+          fa[t] = *reinterpret_cast<const float4*>(&sA[(wave * 64 + t * 32 + l32) * LD + kk * 8 + half * 4]);
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int u = 0; u < 4; ++u)
+          fb[u] = *reinterpret_cast<const float4*>(&sB[(u * 32 + l32) * LD + kk * 8 + half * 4]);
+        // MFMA q reads k = kk*8 + 4*half + q from lane half `half` of both
+        // operands, so the four products cover k = kk*8 .. kk*8+7.
 #pragma unroll
-          for (int b = 0; b < 2; ++b) {
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].x, bf[b].x, acc[a][b], 0, 0, 0);
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].y, bf[b].y, acc[a][b], 0, 0, 0);
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].z, bf[b].z, acc[a][b], 0, 0, 0);
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a].w, bf[b].w, acc[a][b], 0, 0, 0);
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u].x, fa[t].x, acc[t][u], 0, 0, 0);
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u].y, fa[t].y, acc[t][u], 0, 0, 0);
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u].z, fa[t].z, acc[t][u], 0, 0, 0);
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u].w, fa[t].w, acc[t][u], 0, 0, 0);
           }
       }
     }
@@ -284,46 +281,141 @@ __global__ __launch_bounds__(256) void gemm_xwt_kernel(const float* __restrict__
     }
   }
 
-  // ---- epilogue: 32x32 accumulator layout, lane l holds column l%32 and
-  // rows 8*(i/4) + 4*(l/32) + i%4 of its tile. ------------------------------
+  // ---- epilogue.  Accumulator layout of a 32x32 tile (weights as the first
+  // operand): lane l holds token row l%32 and output columns
+  // 8*(i/4) + 4*(l/32) + i%4 for i = 0..15. ----------------------------------
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int t = 0; t < 2; ++t) {
+    const int row = m0 + wave * 64 + t * 32 + l32;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int col = n0 + wn * 64 + b * 32 + l32;
-      if (col >= N) continue;
+    for (int u = 0; u < 4; ++u) {
+      const int nb = n0 + u * 32 + half * 4;
+      f32x16_t adv;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = m0 + wm * 64 + a * 32 + (i >> 2) * 8 + half * 4 + (i & 3);
-        if (row < M) {
-          const float v = apply_epilogue(ep, acc[a][b][i], row, col, C, ldc);
-          C[(size_t)row * ldc + col] = v;
+      for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
+      if constexpr (KIND == EPI_ZRAW) {
+        // Adapter up-projection sum_q U[col,q] * act[row,q] on the matrix
+        // cores, in the same accumulator layout as the main product.
+        const int urow = n0 + u * 32 + l32;
+        if constexpr (sizeof(T) == 2) {
+          const uint16_t* U = static_cast<const uint16_t*>(ep.U);
+          for (int q0 = 0; q0 < ep.rank; q0 += 16) {
+            uint32_t wa[4], wu[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const int q = q0 + half * 8 + 2 * p;
+              const float a0 = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
+              const float a1 = (row < M && q + 1 < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q + 1] : 0.0f;
+              wa[p] = pack_bf16x2(a0, a1);
+              const uint32_t u0 = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0u;
+              const uint32_t u1 = (urow < N && q + 1 < ep.rank) ? U[(size_t)urow * ep.rank + q + 1] : 0u;
+              wu[p] = u0 | (u1 << 16);
+            }
+            bf16x8_t fa, fu;
+            __builtin_memcpy(&fa, wa, 16);
+            __builtin_memcpy(&fu, wu, 16);
+            adv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, fa, adv, 0, 0, 0);
+          }
+        } else {
+          const float* U = static_cast<const float*>(ep.U);
+          for (int q0 = 0; q0 < ep.rank; q0 += 2) {
+            const int q = q0 + half;
+            const float a = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
+            const float w = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0.0f;
+            adv = __builtin_amdgcn_mfma_f32_32x32x2f32(w, a, adv, 0, 0, 0);
+          }
+        }
+      }
+      if (row < M) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = nb + g * 8;
+          if (col < N) {
+            const float a4[4] = {acc[t][u][g * 4 + 0], acc[t][u][g * 4 + 1], acc[t][u][g * 4 + 2],
+                                 acc[t][u][g * 4 + 3]};
+            const float d4[4] = {adv[g * 4 + 0], adv[g * 4 + 1], adv[g * 4 + 2], adv[g * 4 + 3]};
+            epi_quad<T, KIND>(ep, row, col, N, vec_epi && col + 3 < N, a4, d4);
+          }
         }
       }
     }
+  }
 }
 
-Status launch_gemm_xwt(hipStream_t stream, const float* A, int lda, const void* B, int ldb,
-                       int b_dtype, float* C, int ldc, int M, int N, int K, const EpiParams& ep) {
-  if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
-  const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const bool bf16 = b_dtype == PSSA_HIP_BF16;
-  const int vw = bf16 ? 8 : 4;
-  const bool vec = (K % vw == 0) && (lda % 4 == 0) && (ldb % vw == 0) &&
-                   ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0);
-  dim3 grid(tiles), block(256);
-  if (bf16) {
-    if (vec)
-      gemm_xwt_kernel<true, true><<<grid, block, 0, stream>>>(A, lda, B, ldb, C, ldc, M, N, K, ep);
-    else
-      gemm_xwt_kernel<true, false><<<grid, block, 0, stream>>>(A, lda, B, ldb, C, ldc, M, N, K, ep);
-  } else {
-    if (vec)
-      gemm_xwt_kernel<false, true><<<grid, block, 0, stream>>>(A, lda, B, ldb, C, ldc, M, N, K, ep);
-    else
-      gemm_xwt_kernel<false, false><<<grid, block, 0, stream>>>(A, lda, B, ldb, C, ldc, M, N, K, ep);
+template <typename T>
+static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int lda, const T* B,
+                        int ldb, int M, int N, int K, int vl, int ve, const EpiParams& ep) {
+#define PSSA_GEMM_CASE(KD)                                                                   \
+  case KD:                                                                                   \
+    gemm_kernel<T, KD><<<grid, NT, 0, stream>>>(A, lda, B, ldb, M, N, K, vl, ve, ep); \
+    break;
+  switch (kind) {
+    PSSA_GEMM_CASE(EPI_STORE)
+    PSSA_GEMM_CASE(EPI_SEGMENTS)
+    PSSA_GEMM_CASE(EPI_ADD_AUX)
+    PSSA_GEMM_CASE(EPI_ZRAW)
+    PSSA_GEMM_CASE(EPI_SILU)
+    PSSA_GEMM_CASE(EPI_RESIDUAL)
+    PSSA_GEMM_CASE(EPI_SCALE)
+    default:
+      break;
   }
-  PSSA_LAUNCH_CHECK("gemm_xwt");
+#undef PSSA_GEMM_CASE
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const void* B, int ldb,
+                   int M, int N, int K, const EpiParams& ep) {
+  if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
+  if (ep.kind < 0 || ep.kind >= EPI_KINDS) return Status::Invalid("gemm: unknown epilogue");
+  if (!ep.out32 && !ep.out16) return Status::Invalid("gemm: no output");
+  if (ep.kind == EPI_RESIDUAL && !ep.out32) return Status::Invalid("gemm: residual needs the fp32 output");
+  if (ep.kind == EPI_ZRAW && (!ep.y || !ep.g || (ep.rank > 0 && (!ep.act || !ep.U))))
+    return Status::Invalid("gemm: z_raw epilogue operands missing");
+  const bool bf16 = dtype == PSSA_HIP_BF16;
+  const int ve = bf16 ? 8 : 4;
+  const int vec_load = (K % ve == 0) && (lda % ve == 0) && (ldb % ve == 0) && al16(A) && al16(B);
+  // Epilogue vectors: every row operand 16-byte aligned at multiples of 4 columns.
+  bool vec_epi = true;
+  auto chk32 = [&](const float* p, int ld) {
+    if (p) vec_epi = vec_epi && al16(p) && ld % 4 == 0;
+  };
+  chk32(ep.out32, ep.ld32);
+  chk32(ep.aux, ep.ld_aux);
+  chk32(ep.y, ep.ld_y);
+  chk32(ep.g, ep.ld_g);
+  if (ep.out16) vec_epi = vec_epi && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
+  const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (tiles > INT32_MAX) return Status::Invalid("gemm: too many tiles");
+  dim3 grid((unsigned)tiles);
+  if (bf16)
+    launch_kind<uint16_t>(stream, ep.kind, grid, static_cast<const uint16_t*>(A), lda,
+                          static_cast<const uint16_t*>(B), ldb, M, N, K, vec_load, vec_epi, ep);
+  else
+    launch_kind<float>(stream, ep.kind, grid, static_cast<const float*>(A), lda,
+                       static_cast<const float*>(B), ldb, M, N, K, vec_load, vec_epi, ep);
+  PSSA_LAUNCH_CHECK("gemm");
+  return Status::Ok();
+}
+
+__global__ void to_bf16_kernel(const float* __restrict__ in, int ld_in, uint16_t* __restrict__ out,
+                               int ld_out, size_t rows, int cols) {
+  const size_t n = rows * (size_t)cols;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = i / cols, c = i % cols;
+    out[r * ld_out + c] = (uint16_t)f32_to_bf16_bits(in[r * ld_in + c]);
+  }
+}
+
+Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* out, int ld_out,
+                      size_t rows, int cols) {
+  const size_t n = rows * (size_t)cols;
+  if (!n) return Status::Ok();
+  size_t g = (n + 255) / 256;
+  if (g > 16384) g = 16384;
+  to_bf16_kernel<<<(unsigned)g, 256, 0, stream>>>(in, ld_in, out, ld_out, rows, cols);
+  PSSA_LAUNCH_CHECK("to_bf16");
   return Status::Ok();
 }
 

@@ -16,7 +16,8 @@ struct RetrieveArgs {
   int n = 0, dk = 0, dv = 0, capacity = 0, count = 0;
   float tau = 0.1f;
   int top_k = 0;                // 0: full soft read -> weights only (readout is a GEMM)
-  float* weights = nullptr;     // [n, capacity]; required for the full read, optional for top-k
+  float* weights = nullptr;     // [n, capacity]; optional
+  uint16_t* weights16 = nullptr;  // [n, capacity] bf16 bits; optional (operand of a bf16 readout)
   float* out_val = nullptr;     // [n, dv] (top-k readout)
   float* out_min = nullptr;     // optional [n]
   uint32_t* out_idx = nullptr;  // optional [n, top_k], ascending slot order

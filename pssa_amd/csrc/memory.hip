@@ -89,6 +89,18 @@ __device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v)
   return v;
 }
 
+__device__ __forceinline__ uint16_t bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ void put_weight(const RetrieveArgs& a, int n, int s, float w) {
+  const size_t o = (size_t)n * a.capacity + s;
+  if (a.weights) a.weights[o] = w;
+  if (a.weights16) a.weights16[o] = bf16_bits(w);
+}
+
 constexpr double kMaxRadius = 1.0 - 8.0 * (double)FLT_EPSILON;  // src/memory.rs:173
 
 __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
@@ -117,8 +129,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
     const float q_sq = bank_norm_sq(sq, a.dk);
 
     if (a.count == 0) {
-      if (a.weights)
-        for (int s = lane; s < a.capacity; s += 64) a.weights[(size_t)n * a.capacity + s] = 0.0f;
+      for (int s = lane; s < a.capacity; s += 64) put_weight(a, n, s, 0.0f);
       if (a.out_val)
         for (int j = lane; j < a.dv; j += 64) a.out_val[(size_t)n * a.dv + j] = 0.0f;
       if (a.out_min && lane == 0) a.out_min[n] = 0.0f;
@@ -168,12 +179,11 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
       wave_sync();
       float sum = 0.0f;
       for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[wave][r]]) / a.tau);
-      if (a.weights) {
+      if (a.weights || a.weights16) {
         for (int s = lane; s < a.capacity; s += 64) {
           bool chosen = false;
           for (int r = 0; r < k; ++r) chosen |= ssel[wave][r] == (uint32_t)s;
-          a.weights[(size_t)n * a.capacity + s] =
-              chosen ? expf((min_dist - sdist[s]) / a.tau) / sum : 0.0f;
+          put_weight(a, n, s, chosen ? expf((min_dist - sdist[s]) / a.tau) / sum : 0.0f);
         }
       }
       if (a.out_idx)
@@ -203,7 +213,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
       for (int s = lane; s < a.capacity; s += 64) {
         const float w = s < a.count ? sdist[s] / sum : 0.0f;
         if (s < a.count) sdist[s] = w;
-        if (a.weights) a.weights[(size_t)n * a.capacity + s] = w;
+        put_weight(a, n, s, w);
       }
       wave_sync();
       if (a.out_val) {
@@ -226,7 +236,7 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.dk <= 0 || a.capacity <= 0 || a.count < 0 || a.count > a.capacity)
     return Status::Invalid("retrieve: bad bank shape");
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
-  if (a.top_k == 0 && !a.weights && !a.out_val) return Status::Invalid("retrieve: no output");
+  if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
   const int dk_pad = (a.dk + 3) & ~3;
   const size_t lds = (size_t)4 * (dk_pad + a.capacity) * sizeof(float);
   if (lds > 128 * 1024) return Status::Invalid("retrieve: d_key + capacity too large for LDS");

@@ -58,7 +58,13 @@ struct pssa_hip_lanes {
   size_t lanes = 0, max_tokens = 0;
   pssa::DevBuf carry;  // [lanes, depth, d*s]
   pssa::DevBuf ids;    // [max_tokens] u32
-  pssa::DevBuf X, XN, P, Y, Q, Wm, Mval, Zraw, H1, logits;
+  // Activations for max_tokens rows.  fp32: X residual stream [n,d], XN norm
+  // output [n,d], P fused input projection [n,n_in], Y SSM readout [n,d],
+  // Q memory query [n,k], Zraw [n,d].  Operand type of the model (bf16 or
+  // fp32): XNh, Yh, Zrawh (bf16 copies, aliases of the fp32 buffers in an
+  // fp32 model), Wm soft-read weights [n,C], Mval read values [n,d],
+  // H1 MLP hidden [n,2d].
+  pssa::DevBuf X, XN, XNh, P, Y, Yh, Q, Wm, Mval, Zraw, Zrawh, H1, logits;
   size_t staged_lanes = 0, staged_len = 0;
   bool timing = false;
   std::array<float, pssa::ST_COUNT> stage_ms{};

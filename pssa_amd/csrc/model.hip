@@ -37,10 +37,17 @@ __global__ void embed_kernel(const uint32_t* __restrict__ ids, const float* __re
 
 // Affine RMSNorm with epsilon inside the root (src/pssa.rs:1080-1086).  One
 // wave per row.
+__device__ __forceinline__ uint16_t bf16_of(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta,
-                                                      float* __restrict__ XN, int d, size_t rows) {
+                                                      float* __restrict__ XN,
+                                                      uint16_t* __restrict__ XNh, int d, size_t rows) {
   const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
@@ -50,7 +57,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
   const float inv = 1.0f / sqrtf(ss / (float)d + 1e-5f);
-  for (int i = lane; i < d; i += 64) XN[r * d + i] = gamma[i] * (x[i] * inv) + beta[i];
+  for (int i = lane; i < d; i += 64) {
+    const float v = gamma[i] * (x[i] * inv) + beta[i];
+    XN[r * d + i] = v;
+    if (XNh) XNh[r * d + i] = bf16_of(v);
+  }
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ p, size_t n) {
@@ -167,6 +178,7 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
   const size_t rows = n_lanes * T;
   const int m = (int)rows;
   const int dt = M->dtype;
+  const bool bf16 = dt == PSSA_HIP_BF16;
   const float ssm_scale = 1.0f / sqrtf((float)s);
   const float depth_scale = 1.0f / sqrtf((float)c.depth);
   const float logit_scale = 1.0f / sqrtf((float)d);
@@ -178,10 +190,15 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
   float* P = L->P.as<float>();
   float* Y = L->Y.as<float>();
   float* Q = L->Q.as<float>();
-  float* Wm = L->Wm.as<float>();
-  float* Mv = L->Mval.as<float>();
   float* Zr = L->Zraw.as<float>();
-  float* H1 = L->H1.as<float>();
+  // GEMM operands in the model's operand type (aliases of the fp32 buffers
+  // in an fp32 model).
+  void* XNh = bf16 ? L->XNh.p : (void*)XN;
+  void* Yh = bf16 ? L->Yh.p : (void*)Y;
+  void* Zrh = bf16 ? L->Zrawh.p : (void*)Zr;
+  void* Wm = L->Wm.p;
+  void* Mv = L->Mval.p;
+  void* H1 = L->H1.p;
 
   Timer tm{L, st};
   PSSA_RETURN_IF(tm.mark(ST_EMBED));
@@ -191,9 +208,12 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
   for (size_t l = 0; l < c.depth; ++l) {
     const DevBlock& B = M->blocks[l];
     PSSA_RETURN_IF(tm.mark(ST_NORM));
-    rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(X, B.gamma.as<float>(), B.beta.as<float>(), XN, d, rows);
+    rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
+        X, B.gamma.as<float>(), B.beta.as<float>(), XN, bf16 ? L->XNh.as<uint16_t>() : nullptr, d, rows);
     PSSA_LAUNCH_CHECK("rmsnorm");
 
+    // [delta | B | C | q_x | gate | adapter act] = x W_in^T with softplus,
+    // sigmoid and SiLU applied per column segment.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_IN));
     EpiParams e_in;
     e_in.kind = EPI_SEGMENTS;
@@ -201,7 +221,9 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_in.seg[1] = o_gate;
     e_in.seg[2] = o_act;
     e_in.seg[3] = n_in;
-    PSSA_RETURN_IF(launch_gemm_xwt(st, XN, d, B.w_in.p, d, dt, P, n_in, m, n_in, d, e_in));
+    e_in.out32 = P;
+    e_in.ld32 = n_in;
+    PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
 
     PSSA_RETURN_IF(tm.mark(ST_SSM));
     if (ssm_needs_zeroed_y(s)) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
@@ -224,13 +246,17 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     sa.s = s;
     sa.lanes = (int)n_lanes;
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
+    if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, L->Yh.as<uint16_t>(), d, rows, d));
 
+    // q_euc = y W_qh^T + q_x.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));
     EpiParams e_q;
     e_q.kind = EPI_ADD_AUX;
     e_q.aux = P + o_qx;
     e_q.ld_aux = n_in;
-    PSSA_RETURN_IF(launch_gemm_xwt(st, Y, d, B.w_qh.p, d, dt, Q, k, m, k, d, e_q));
+    e_q.out32 = Q;
+    e_q.ld32 = k;
+    PSSA_RETURN_IF(launch_gemm(st, dt, Yh, d, B.w_qh.p, d, m, k, d, e_q));
 
     PSSA_RETURN_IF(tm.mark(ST_RETRIEVE));
     RetrieveArgs ra;
@@ -245,16 +271,24 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     ra.capacity = C;
     ra.count = (int)B.count;
     ra.tau = c.tau_mem;
-    ra.weights = Wm;
+    if (bf16)
+      ra.weights16 = static_cast<uint16_t*>(Wm);
+    else
+      ra.weights = static_cast<float*>(Wm);
     PSSA_RETURN_IF(launch_retrieve(st, ra));
 
+    // m_val = weights values (soft read readout).
     PSSA_RETURN_IF(tm.mark(ST_GEMM_READ));
     if (B.count > 0) {
-      PSSA_RETURN_IF(launch_gemm_xwt(st, Wm, C, B.values_t.p, C, dt, Mv, d, m, d, (int)B.count, EpiParams{}));
+      EpiParams e_m;
+      e_m.out16 = Mv;
+      e_m.ld16 = d;
+      PSSA_RETURN_IF(launch_gemm(st, dt, Wm, C, B.values_t.p, C, m, d, (int)B.count, e_m));
     } else {
-      PSSA_RETURN_IF(launch_fill_zero(st, Mv, rows * d));
+      PSSA_RETURN_IF(launch_fill_zero(st, static_cast<float*>(Mv), (rows * d * (bf16 ? 2 : 4) + 3) / 4));
     }
 
+    // z_raw = y/sqrt(s) + gate * (m_val W_proj^T) + U_eff act.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_PROJ));
     EpiParams e_z;
     e_z.kind = EPI_ZRAW;
@@ -264,32 +298,54 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_z.ld_g = n_in;
     e_z.act = P + o_act;
     e_z.ld_act = n_in;
-    e_z.U = B.u_eff.as<float>();
+    e_z.U = B.u_eff.p;
     e_z.rank = r;
     e_z.scale = ssm_scale;
-    PSSA_RETURN_IF(launch_gemm_xwt(st, Mv, d, B.w_proj.p, d, dt, Zr, d, m, d, d, e_z));
+    e_z.out32 = Zr;
+    e_z.ld32 = d;
+    if (bf16) {
+      e_z.out16 = Zrh;
+      e_z.ld16 = d;
+    }
+    PSSA_RETURN_IF(launch_gemm(st, dt, Mv, d, B.w_proj.p, d, m, d, d, e_z));
 
+    // a = SiLU(z_raw W1^T).
     PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP1));
     EpiParams e_s;
     e_s.kind = EPI_SILU;
-    PSSA_RETURN_IF(launch_gemm_xwt(st, Zr, d, B.mlp_w1.p, d, dt, H1, 2 * d, m, 2 * d, d, e_s));
+    e_s.out16 = H1;
+    e_s.ld16 = 2 * d;
+    PSSA_RETURN_IF(launch_gemm(st, dt, Zrh, d, B.mlp_w1.p, d, m, 2 * d, d, e_s));
 
+    // h = z_raw + a W2^T (layer 0), h += (z_raw + a W2^T) / sqrt(depth).
     PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP2));
     EpiParams e_r;
     e_r.kind = EPI_RESIDUAL;
-    e_r.zraw = Zr;
-    e_r.ld_zraw = d;
+    e_r.aux = Zr;
+    e_r.ld_aux = d;
     e_r.first = l == 0 ? 1 : 0;
     e_r.scale = depth_scale;
-    PSSA_RETURN_IF(launch_gemm_xwt(st, H1, 2 * d, B.mlp_w2.p, 2 * d, dt, X, d, m, d, 2 * d, e_r));
+    e_r.out32 = X;
+    e_r.ld32 = d;
+    PSSA_RETURN_IF(launch_gemm(st, dt, H1, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r));
   }
 
+  // Head on the last token of every lane.
   PSSA_RETURN_IF(tm.mark(ST_HEAD));
+  const float* xlast = X + (T - 1) * (size_t)d;
+  const void* hin = xlast;
+  int ld_h = (int)(T * d);
+  if (bf16) {
+    PSSA_RETURN_IF(launch_to_bf16(st, xlast, (int)(T * d), L->XNh.as<uint16_t>(), d, n_lanes, d));
+    hin = L->XNh.p;
+    ld_h = d;
+  }
   EpiParams e_h;
   e_h.kind = EPI_SCALE;
   e_h.scale = logit_scale;
-  PSSA_RETURN_IF(launch_gemm_xwt(st, X + (T - 1) * (size_t)d, (int)(T * d), M->unembed.p, d, dt,
-                                 L->logits.as<float>(), V, (int)n_lanes, V, d, e_h));
+  e_h.out32 = L->logits.as<float>();
+  e_h.ld32 = V;
+  PSSA_RETURN_IF(launch_gemm(st, dt, hin, ld_h, M->unembed.p, d, (int)n_lanes, V, d, e_h));
   return tm.finish();
 }
 

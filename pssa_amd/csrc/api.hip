@@ -263,6 +263,12 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
     a.d = (int)d_m;
     a.s = (int)d_s;
     a.lanes = 1;
+    DevBuf dpart;
+    const int nz = pssa::ssm_state_blocks((int)d_s);
+    if (!bar_a && nz > 2) {
+      PSSA_RETURN_IF(dpart.alloc((size_t)nz * ld * 4));
+      a.y_part = dpart.as<float>();
+    }
     if (bar_a) {
       PSSA_RETURN_IF(da.alloc(lw * 4));
       PSSA_RETURN_IF(dbb.alloc(lw * 4));
@@ -575,6 +581,8 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     PSSA_RETURN_IF(L->Mval.alloc(n * d * es));
     PSSA_RETURN_IF(L->H1.alloc(n * 2 * d * es));
     PSSA_RETURN_IF(L->logits.alloc(lanes * c.d_vocab * 4));
+    const int nz = pssa::ssm_state_blocks((int)s);
+    if (nz > 2) PSSA_RETURN_IF(L->Ypart.alloc((size_t)nz * n * d * 4));
     PSSA_RETURN_IF(pssa::launch_fill_zero(ctx->stream, L->carry.as<float>(), lanes * c.depth * d * s));
     PSSA_RETURN_IF(sync(ctx));
     *out = L.release();

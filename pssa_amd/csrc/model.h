@@ -65,6 +65,7 @@ struct pssa_hip_lanes {
   // fp32 model), Wm soft-read weights [n,C], Mval read values [n,d],
   // H1 MLP hidden [n,2d].
   pssa::DevBuf X, XN, XNh, P, Y, Yh, Q, Wm, Mval, Zraw, Zrawh, H1, logits;
+  pssa::DevBuf Ypart;  // SSM partial readouts when d_state needs more than two state blocks
   size_t staged_lanes = 0, staged_len = 0;
   bool timing = false;
   std::array<float, pssa::ST_COUNT> stage_ms{};

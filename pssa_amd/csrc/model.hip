@@ -245,6 +245,7 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     sa.d = d;
     sa.s = s;
     sa.lanes = (int)n_lanes;
+    sa.y_part = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
     if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, L->Yh.as<uint16_t>(), d, rows, d));
 

@@ -25,11 +25,18 @@ struct SsmArgs {
   float* bar_a = nullptr;
   float* bar_b = nullptr;
   float* states = nullptr;
+  // Partial readouts [state blocks, lanes*T, d], required when
+  // ssm_state_blocks(s) > 2 (the blocks are then summed in a fixed order).
+  float* y_part = nullptr;
+  size_t rows = 0;  // set by launch_ssm_scan
 };
 
-// Rows of lane b are b*T .. b*T+T-1.  y must be zero-filled by the caller
-// when s exceeds one workgroup's j-range (several workgroups then add their
-// partial sums); ssm_needs_zeroed_y() says when.
+// Rows of lane b are b*T .. b*T+T-1.  The states of a channel are split into
+// ssm_state_blocks(s) workgroups.  With two blocks both add their partial
+// readouts into y, which the caller zero-fills first (ssm_needs_zeroed_y; two
+// addends onto zero give the same sum in either order); with more, the
+// caller provides y_part and the blocks are summed in a fixed order.
+int ssm_state_blocks(int s);
 bool ssm_needs_zeroed_y(int s);
 Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a);
 

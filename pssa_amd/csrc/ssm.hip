@@ -18,25 +18,29 @@
 
 namespace pssa {
 
-constexpr int SSM_TC = 16;  // time steps staged per chunk
+// ---------------------------------------------------------------------------
+// Materialising variant (stage API): also writes bar_a, bar_b and every
+// state h_t.  Used for small diagnostic shapes only.
+constexpr int MAT_TC = 16;
 
-template <int J, bool MAT>
-__global__ __launch_bounds__(256) void ssm_scan_kernel(SsmArgs a) {
-  __shared__ float sD[SSM_TC][64];
-  __shared__ float sX[SSM_TC][64];
-  __shared__ __attribute__((aligned(16))) float sB[SSM_TC][4 * J];
-  __shared__ __attribute__((aligned(16))) float sC[SSM_TC][4 * J];
-  __shared__ float sY[4][SSM_TC][64];
+template <int J>
+__global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
+  __shared__ float sD[MAT_TC][64];
+  __shared__ float sX[MAT_TC][64];
+  __shared__ float sB[MAT_TC][4 * J];
+  __shared__ float sC[MAT_TC][4 * J];
+  __shared__ float sY[4][MAT_TC][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i0 = blockIdx.x * 64;
   const int b = blockIdx.y;
   const int jb = blockIdx.z * 4 * J;
   const int i = i0 + lane;
-  const int jw = jb + wave * J;  // first state of this wave
+  const int jw = jb + wave * J;
   const bool ivalid = i < a.d;
   const int T = a.T, d = a.d, s = a.s;
   const size_t row0 = (size_t)b * T;
+  const size_t ds = (size_t)d * s;
 
   float h[J], r2[J];
   float* carry = a.carry + (size_t)b * a.carry_stride;
@@ -47,17 +51,11 @@ __global__ __launch_bounds__(256) void ssm_scan_kernel(SsmArgs a) {
     h[q] = ok ? carry[(size_t)i * s + j] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)i * s + j] : 0.0f;
   }
-  if constexpr (MAT) {
-    if (blockIdx.z == 0 && wave == 0) {
-      // states[0] = h0 for this lane's channels (all j of row i).
-      for (int j = 0; j < s && ivalid; ++j)
-        a.states[(size_t)b * (T + 1) * d * s + (size_t)i * s + j] = carry[(size_t)i * s + j];
-    }
-  }
+  if (blockIdx.z == 0 && wave == 0 && ivalid)
+    for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[(size_t)i * s + j];
 
-  for (int t0 = 0; t0 < T; t0 += SSM_TC) {
-    // ---- stage the chunk ----
-    for (int e = tid; e < SSM_TC * 64; e += 256) {
+  for (int t0 = 0; t0 < T; t0 += MAT_TC) {
+    for (int e = tid; e < MAT_TC * 64; e += 256) {
       const int tt = e >> 6, ii = e & 63;
       const int t = t0 + tt, gi = i0 + ii;
       const bool ok = t < T && gi < d;
@@ -65,7 +63,7 @@ __global__ __launch_bounds__(256) void ssm_scan_kernel(SsmArgs a) {
       sD[tt][ii] = ok ? a.delta[r * a.ld_delta + gi] : 0.0f;
       sX[tt][ii] = ok ? a.xn[r * a.ld_x + gi] : 0.0f;
     }
-    for (int e = tid; e < SSM_TC * 4 * J; e += 256) {
+    for (int e = tid; e < MAT_TC * 4 * J; e += 256) {
       const int tt = e / (4 * J), jj = e % (4 * J);
       const int t = t0 + tt, gj = jb + jj;
       const bool ok = t < T && gj < s;
@@ -74,34 +72,29 @@ __global__ __launch_bounds__(256) void ssm_scan_kernel(SsmArgs a) {
       sC[tt][jj] = ok ? a.cproj[r * a.ld_c + gj] : 0.0f;
     }
     __syncthreads();
-    // ---- recurrence over the chunk ----
-    const int steps = min(SSM_TC, T - t0);
+    const int steps = min(MAT_TC, T - t0);
     for (int tt = 0; tt < steps; ++tt) {
       const float dl = sD[tt][lane];
       const float u = dl * sX[tt][lane];
-      const float* bt = &sB[tt][wave * J];
-      const float* ct = &sC[tt][wave * J];
       float yp = 0.0f;
 #pragma unroll
       for (int q = 0; q < J; ++q) {
+        const float bq = sB[tt][wave * J + q];
         const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
-        h[q] = fmaf(ab, h[q], u * bt[q]);
-        yp = fmaf(h[q], ct[q], yp);
-        if constexpr (MAT) {
-          const int j = jw + q;
-          if (ivalid && j < s) {
-            const size_t c = (size_t)i * s + j;
-            const size_t base = (size_t)b * T * d * s + (size_t)(t0 + tt) * d * s;
-            a.bar_a[base + c] = ab;
-            a.bar_b[base + c] = dl * bt[q];
-            a.states[(size_t)b * (T + 1) * d * s + (size_t)(t0 + tt + 1) * d * s + c] = h[q];
-          }
+        h[q] = fmaf(ab, h[q], u * bq);
+        yp = fmaf(h[q], sC[tt][wave * J + q], yp);
+        const int j = jw + q;
+        if (ivalid && j < s) {
+          const size_t c = (size_t)i * s + j;
+          const size_t base = (size_t)b * T * ds + (size_t)(t0 + tt) * ds;
+          a.bar_a[base + c] = ab;
+          a.bar_b[base + c] = dl * bq;
+          a.states[(size_t)b * (T + 1) * ds + (size_t)(t0 + tt + 1) * ds + c] = h[q];
         }
       }
       sY[wave][tt][lane] = yp;
     }
     __syncthreads();
-    // ---- combine the four waves' partial sums over j ----
     for (int e = tid; e < steps * 64; e += 256) {
       const int tt = e >> 6, ii = e & 63;
       const int gi = i0 + ii;
@@ -123,25 +116,180 @@ __global__ __launch_bounds__(256) void ssm_scan_kernel(SsmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Production scan.  The next TC time steps' inputs are fetched into registers
+// while the current TC steps run out of LDS, so the global-memory latency of
+// the staging hides behind the recurrence.  Time steps past the end of a lane
+// read delta = x = 0: the update is then h <- exp2(0) h + 0 = h, so whole
+// chunks run unguarded and only the stores check t < T.  Per state the inner
+// loop batches G independent exponentials before the dependent FMAs, and the
+// readout sum over a wave's states runs as four interleaved partial sums.
+constexpr int SSM_TC = 4;
+
+template <int J>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void ssm_scan_kernel(SsmArgs a) {
+  constexpr int TC = SSM_TC;
+  constexpr int G = J < 16 ? J : 16;
+  constexpr int NDX = TC * 64 / 256;        // delta/x values staged per thread
+  constexpr int NBC = (TC * 4 * J + 255) / 256;  // B/C values staged per thread
+  static_assert(NDX >= 1, "chunk too short");
+  __shared__ float sD[TC][64];
+  __shared__ float sX[TC][64];
+  __shared__ __attribute__((aligned(16))) float sB[TC][4 * J];
+  __shared__ __attribute__((aligned(16))) float sC[TC][4 * J];
+  __shared__ float sY[4][TC][64];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i0 = blockIdx.x * 64;
+  const int b = blockIdx.y;
+  const int jb = blockIdx.z * 4 * J;
+  const int i = i0 + lane;
+  const int jw = jb + wave * J;
+  const bool ivalid = i < a.d;
+  const int T = a.T, d = a.d, s = a.s;
+  const size_t row0 = (size_t)b * T;
+
+  float h[J], r2[J];
+  float* carry = a.carry + (size_t)b * a.carry_stride;
+#pragma unroll
+  for (int q = 0; q < J; ++q) {
+    const int j = jw + q;
+    const bool ok = ivalid && j < s;
+    h[q] = ok ? carry[(size_t)i * s + j] : 0.0f;
+    r2[q] = ok ? a.rates2[(size_t)i * s + j] : 0.0f;
+  }
+
+  float pd[NDX], px[NDX], pb[NBC], pc[NBC];
+  auto load = [&](int t0) {
+#pragma unroll
+    for (int k = 0; k < NDX; ++k) {
+      const int e = tid + 256 * k;
+      const int t = t0 + (e >> 6), gi = i0 + (e & 63);
+      const bool ok = t < T && gi < d;
+      const size_t r = row0 + t;
+      pd[k] = ok ? a.delta[r * a.ld_delta + gi] : 0.0f;
+      px[k] = ok ? a.xn[r * a.ld_x + gi] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < NBC; ++k) {
+      const int e = tid + 256 * k;
+      const int t = t0 + e / (4 * J), gj = jb + e % (4 * J);
+      const bool ok = e < TC * 4 * J && t < T && gj < s;
+      const size_t r = row0 + t;
+      pb[k] = ok ? a.bproj[r * a.ld_b + gj] : 0.0f;
+      pc[k] = ok ? a.cproj[r * a.ld_c + gj] : 0.0f;
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int k = 0; k < NDX; ++k) {
+      const int e = tid + 256 * k;
+      sD[e >> 6][e & 63] = pd[k];
+      sX[e >> 6][e & 63] = px[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NBC; ++k) {
+      const int e = tid + 256 * k;
+      if (e < TC * 4 * J) {
+        sB[e / (4 * J)][e % (4 * J)] = pb[k];
+        sC[e / (4 * J)][e % (4 * J)] = pc[k];
+      }
+    }
+  };
+
+  load(0);
+  store();
+  __syncthreads();
+  for (int t0 = 0; t0 < T; t0 += TC) {
+    if (t0 + TC < T) load(t0 + TC);
+    for (int tt = 0; tt < TC; ++tt) {
+      const float dl = sD[tt][lane];
+      const float u = dl * sX[tt][lane];
+      const float* bt = &sB[tt][wave * J];
+      const float* ct = &sC[tt][wave * J];
+      float yp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int g0 = 0; g0 < J; g0 += G) {
+        float ab[G];
+#pragma unroll
+        for (int q = 0; q < G; ++q) ab[q] = dl * r2[g0 + q];
+#pragma unroll
+        for (int q = 0; q < G; ++q) ab[q] = __builtin_amdgcn_exp2f(ab[q]);
+#pragma unroll
+        for (int q = 0; q < G; ++q) h[g0 + q] = fmaf(ab[q], h[g0 + q], u * bt[g0 + q]);
+#pragma unroll
+        for (int q = 0; q < G; ++q) yp[q & 3] = fmaf(h[g0 + q], ct[g0 + q], yp[q & 3]);
+      }
+      sY[wave][tt][lane] = (yp[0] + yp[1]) + (yp[2] + yp[3]);
+    }
+    __syncthreads();
+    // Four waves' partial sums over j, added in a fixed order.
+#pragma unroll
+    for (int k = 0; k < NDX; ++k) {
+      const int e = tid + 256 * k;
+      const int tt = e >> 6, gi = i0 + (e & 63);
+      const int t = t0 + tt;
+      if (t < T && gi < d) {
+        const float v = ((sY[0][tt][e & 63] + sY[1][tt][e & 63]) + sY[2][tt][e & 63]) + sY[3][tt][e & 63];
+        const size_t r = row0 + t;
+        if (a.y_part)
+          a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + gi] = v;
+        else if (gridDim.z > 1)
+          atomicAdd(a.y + r * a.ld_y + gi, v);
+        else
+          a.y[r * a.ld_y + gi] = v;
+      }
+    }
+    if (t0 + TC < T) store();
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < J; ++q) {
+    const int j = jw + q;
+    if (ivalid && j < s) carry[(size_t)i * s + j] = h[q];
+  }
+}
+
+// y = sum over state blocks of the partial readouts, in block order.
+__global__ void ssm_reduce_kernel(const float* __restrict__ part, int nz, size_t rows, int d,
+                                  float* __restrict__ y, int ld_y) {
+  const size_t n = rows * (size_t)d;
+  for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
+    float v = part[e];
+    for (int z = 1; z < nz; ++z) v += part[(size_t)z * n + e];
+    y[(e / d) * ld_y + e % d] = v;
+  }
+}
+
 static int pick_j(int s) { return s >= 128 ? 32 : (s >= 32 ? 8 : 2); }
 
-bool ssm_needs_zeroed_y(int s) {
+int ssm_state_blocks(int s) {
   const int J = pick_j(s);
-  return s > 4 * J;
+  return (s + 4 * J - 1) / (4 * J);
 }
+
+bool ssm_needs_zeroed_y(int s) { return ssm_state_blocks(s) == 2; }
 
 template <int J>
 static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   dim3 grid((a.d + 63) / 64, a.lanes, (a.s + 4 * J - 1) / (4 * J));
   if (mat)
-    ssm_scan_kernel<J, true><<<grid, 256, 0, stream>>>(a);
+    ssm_materialize_kernel<J><<<grid, 256, 0, stream>>>(a);
   else
-    ssm_scan_kernel<J, false><<<grid, 256, 0, stream>>>(a);
+    ssm_scan_kernel<J><<<grid, 256, 0, stream>>>(a);
 }
 
-Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a) {
+Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a_in) {
+  SsmArgs a = a_in;
   if (a.T <= 0 || a.d <= 0 || a.s <= 0 || a.lanes <= 0) return Status::Invalid("ssm: empty shape");
   const bool mat = a.bar_a && a.bar_b && a.states;
+  const int nz = ssm_state_blocks(a.s);
+  a.rows = (size_t)a.lanes * a.T;
+  if (mat || nz <= 2) {
+    a.y_part = nullptr;
+  } else if (!a.y_part) {
+    return Status::Invalid("ssm: more than two state blocks need a partial-sum buffer");
+  }
   switch (pick_j(a.s)) {
     case 32:
       launch_j<32>(stream, a, mat);
@@ -154,6 +302,13 @@ Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a) {
       break;
   }
   PSSA_LAUNCH_CHECK("ssm_scan");
+  if (a.y_part) {
+    const size_t n = a.rows * (size_t)a.d;
+    size_t g = (n + 255) / 256;
+    if (g > 16384) g = 16384;
+    ssm_reduce_kernel<<<(unsigned)g, 256, 0, stream>>>(a.y_part, nz, a.rows, a.d, a.y, a.ld_y);
+    PSSA_LAUNCH_CHECK("ssm_reduce");
+  }
   return Status::Ok();
 }
 

@@ -168,6 +168,65 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
   }
 }
 
+
+// Epilogue of one 32x32 accumulator tile whose weight rows start at column
+// n32.  Accumulator layout (weights as the MFMA's first operand): lane l
+// holds token row `row` (= tile row + l%32) and output columns
+// n32 + 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.
+template <typename T, int KIND>
+__device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16_t& acc, int row,
+                                               int n32, int M, int N, int vec_epi, int half,
+                                               int l32) {
+  f32x16_t adv;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
+  if constexpr (KIND == EPI_ZRAW) {
+    // Adapter up-projection sum_q U[col,q] * act[row,q] on the matrix cores,
+    // in the same accumulator layout as the main product.
+    const int urow = n32 + l32;
+    if constexpr (sizeof(T) == 2) {
+      const uint16_t* U = static_cast<const uint16_t*>(ep.U);
+      for (int q0 = 0; q0 < ep.rank; q0 += 16) {
+        uint32_t wa[4], wu[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const int q = q0 + half * 8 + 2 * p;
+          const float a0 = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
+          const float a1 = (row < M && q + 1 < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q + 1] : 0.0f;
+          wa[p] = pack_bf16x2(a0, a1);
+          const uint32_t u0 = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0u;
+          const uint32_t u1 = (urow < N && q + 1 < ep.rank) ? U[(size_t)urow * ep.rank + q + 1] : 0u;
+          wu[p] = u0 | (u1 << 16);
+        }
+        bf16x8_t fa, fu;
+        __builtin_memcpy(&fa, wa, 16);
+        __builtin_memcpy(&fu, wu, 16);
+        adv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, fa, adv, 0, 0, 0);
+      }
+    } else {
+      const float* U = static_cast<const float*>(ep.U);
+      for (int q0 = 0; q0 < ep.rank; q0 += 2) {
+        const int q = q0 + half;
+        const float a = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
+        const float w = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0.0f;
+        adv = __builtin_amdgcn_mfma_f32_32x32x2f32(w, a, adv, 0, 0, 0);
+      }
+    }
+  }
+  if (row < M) {
+    const int nb = n32 + half * 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = nb + g * 8;
+      if (col < N) {
+        const float a4[4] = {acc[g * 4 + 0], acc[g * 4 + 1], acc[g * 4 + 2], acc[g * 4 + 3]};
+        const float d4[4] = {adv[g * 4 + 0], adv[g * 4 + 1], adv[g * 4 + 2], adv[g * 4 + 3]};
+        epi_quad<T, KIND>(ep, row, col, N, vec_epi && col + 3 < N, a4, d4);
+      }
+    }
+  }
+}
+
 template <typename T, int KIND>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_kernel(const T* __restrict__ A, int lda,
                                                   const T* __restrict__ B, int ldb, int M, int N,
@@ -281,65 +340,120 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2))) void ge
     }
   }
 
-  // ---- epilogue.  Accumulator layout of a 32x32 tile (weights as the first
-  // operand): lane l holds token row l%32 and output columns
-  // 8*(i/4) + 4*(l/32) + i%4 for i = 0..15. ----------------------------------
+  // ---- epilogue ----
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int row = m0 + wave * 64 + t * 32 + l32;
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int nb = n0 + u * 32 + half * 4;
-      f32x16_t adv;
+    for (int u = 0; u < 4; ++u)
+      epilogue_32x32<T, KIND>(ep, acc[t][u], m0 + wave * 64 + t * 32 + l32, n0 + u * 32, M, N, vec_epi,
+                              half, l32);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 GEMM with a direct-to-LDS pipeline (the production path for the model).
+//
+// A 256-thread workgroup (2x2 waves) computes a 128 x (64*NW) tile; each wave
+// owns 64 token rows x 32*NW weight rows.  Operand slabs of 32 K-elements
+// move global -> LDS with global_load_lds_dwordx4 (no register staging)
+// through a ring of LDS_STAGES slabs, so two slabs are in flight while a
+// third feeds the matrix cores.  Slab rows are 64 bytes with the 16-byte
+// chunk index XOR-swizzled by ((r>>1) ^ (r>>3)) & 3 (r = row mod 16), which
+// keeps the fragment reads bank-conflict free.  Each wave waits for its own
+// loads of the slab it is about to read (s_waitcnt vmcnt) and the workgroup
+// then meets at a plain s_barrier; the slot refilled next was last read
+// before that barrier.  Rows past M or N load a clamped in-range row and
+// their results are discarded; K must be a multiple of 32.
+constexpr int LDS_BK = 32, LDS_STAGES = 3;
+
+__device__ __forceinline__ int slab_swizzle(int r) { return (((r & 15) >> 1) ^ ((r & 15) >> 3)) & 3; }
+
+template <int KIND, int NW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_lds_kernel(
+    const uint16_t* __restrict__ A, int lda, const uint16_t* __restrict__ B, int ldb, int M, int N,
+    int K, int vec_epi, EpiParams ep) {
+  constexpr int BK = LDS_BK, S = LDS_STAGES;
+  constexpr int MT = 2;                 // 32-row MFMA tiles per wave along M
+  constexpr int BMt = 64 * MT, BNt = 64 * NW, R = BMt + BNt;
+  constexpr int RPI = 16;               // slab rows per DMA instruction (64 lanes x 16 B)
+  constexpr int BPW = R / RPI / 4;      // DMA instructions per wave per slab
+  static_assert((R / RPI) % 4 == 0, "slab rows must split over four waves");
+  __shared__ __attribute__((aligned(1024))) uint16_t sm[S][R * BK];
+
+  const int tilesN = (N + BNt - 1) / BNt, tilesM = (M + BMt - 1) / BMt;
+  const int tile = xcd_tile(blockIdx.x, tilesM * tilesN);
+  const int m0 = (tile / tilesN) * BMt, n0 = (tile % tilesN) * BNt;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Source rows of this wave's DMA instructions (row-major slab: A rows then B rows).
+  const int lr = lane >> 2, pc = lane & 3;
+  const uint16_t* src[BPW];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
-      if constexpr (KIND == EPI_ZRAW) {
-        // Adapter up-projection sum_q U[col,q] * act[row,q] on the matrix
-        // cores, in the same accumulator layout as the main product.
-        const int urow = n0 + u * 32 + l32;
-        if constexpr (sizeof(T) == 2) {
-          const uint16_t* U = static_cast<const uint16_t*>(ep.U);
-          for (int q0 = 0; q0 < ep.rank; q0 += 16) {
-            uint32_t wa[4], wu[4];
+  for (int i = 0; i < BPW; ++i) {
+    const int row = (wave + 4 * i) * RPI + lr;
+    const int lc = pc ^ slab_swizzle(row);
+    if (row < BMt)
+      src[i] = A + (size_t)min(m0 + row, M - 1) * lda + lc * 8;
+    else
+      src[i] = B + (size_t)min(n0 + row - BMt, N - 1) * ldb + lc * 8;
+  }
+  auto issue = [&](int slot, int k0) {
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-              const int q = q0 + half * 8 + 2 * p;
-              const float a0 = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
-              const float a1 = (row < M && q + 1 < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q + 1] : 0.0f;
-              wa[p] = pack_bf16x2(a0, a1);
-              const uint32_t u0 = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0u;
-              const uint32_t u1 = (urow < N && q + 1 < ep.rank) ? U[(size_t)urow * ep.rank + q + 1] : 0u;
-              wu[p] = u0 | (u1 << 16);
-            }
-            bf16x8_t fa, fu;
-            __builtin_memcpy(&fa, wa, 16);
-            __builtin_memcpy(&fu, wu, 16);
-            adv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fu, fa, adv, 0, 0, 0);
-          }
-        } else {
-          const float* U = static_cast<const float*>(ep.U);
-          for (int q0 = 0; q0 < ep.rank; q0 += 2) {
-            const int q = q0 + half;
-            const float a = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
-            const float w = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0.0f;
-            adv = __builtin_amdgcn_mfma_f32_32x32x2f32(w, a, adv, 0, 0, 0);
-          }
-        }
-      }
-      if (row < M) {
+    for (int i = 0; i < BPW; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(src[i] + k0),
+          (__attribute__((address_space(3))) void*)(&sm[slot][((wave + 4 * i) * RPI) * BK]), 16, 0, 0);
+  };
+
+  f32x16_t acc[MT][NW];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int col = nb + g * 8;
-          if (col < N) {
-            const float a4[4] = {acc[t][u][g * 4 + 0], acc[t][u][g * 4 + 1], acc[t][u][g * 4 + 2],
-                                 acc[t][u][g * 4 + 3]};
-            const float d4[4] = {adv[g * 4 + 0], adv[g * 4 + 1], adv[g * 4 + 2], adv[g * 4 + 3]};
-            epi_quad<T, KIND>(ep, row, col, N, vec_epi && col + 3 < N, a4, d4);
-          }
-        }
-      }
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int u = 0; u < NW; ++u)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[t][u][i] = 0.0f;
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st * BK);
+  const int fr = slab_swizzle(l32);
+  for (int kt = 0; kt < nk; ++kt) {
+    // Slab kt is complete once at most the slabs issued after it are in flight.
+    static_assert(S == 3, "the wait below assumes one slab issued after the current one");
+    if (kt + 1 < nk)
+      __builtin_amdgcn_s_waitcnt(BPW | (0x7 << 4) | (0xF << 8));  // vmcnt(BPW)
+    else
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));        // vmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + S - 1 < nk) issue((kt + S - 1) % S, (kt + S - 1) * BK);
+    const uint16_t* a = sm[kt % S];
+    const uint16_t* b = sm[kt % S] + BMt * BK;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int ch = (kk * 2 + half) ^ fr;
+      bf16x8_t fa[MT], fb[NW];
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        fa[t] = *reinterpret_cast<const bf16x8_t*>(a + (wm * MT * 32 + t * 32 + l32) * BK + ch * 8);
+#pragma unroll
+      for (int u = 0; u < NW; ++u)
+        fb[u] = *reinterpret_cast<const bf16x8_t*>(b + (wn * NW * 32 + u * 32 + l32) * BK + ch * 8);
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int u = 0; u < NW; ++u)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[u], fa[t], acc[t][u], 0, 0, 0);
     }
   }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int u = 0; u < NW; ++u)
+      epilogue_32x32<uint16_t, KIND>(ep, acc[t][u], m0 + wm * MT * 32 + t * 32 + l32,
+                                     n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half, l32);
 }
 
 template <typename T>
@@ -361,6 +475,28 @@ static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int
       break;
   }
 #undef PSSA_GEMM_CASE
+}
+
+template <int NW>
+static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint16_t* A, int lda,
+                            const uint16_t* B, int ldb, int M, int N, int K, int ve,
+                            const EpiParams& ep) {
+#define PSSA_GEMM_LDS_CASE(KD)                                                               \
+  case KD:                                                                                   \
+    gemm_lds_kernel<KD, NW><<<grid, 256, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+    break;
+  switch (kind) {
+    PSSA_GEMM_LDS_CASE(EPI_STORE)
+    PSSA_GEMM_LDS_CASE(EPI_SEGMENTS)
+    PSSA_GEMM_LDS_CASE(EPI_ADD_AUX)
+    PSSA_GEMM_LDS_CASE(EPI_ZRAW)
+    PSSA_GEMM_LDS_CASE(EPI_SILU)
+    PSSA_GEMM_LDS_CASE(EPI_RESIDUAL)
+    PSSA_GEMM_LDS_CASE(EPI_SCALE)
+    default:
+      break;
+  }
+#undef PSSA_GEMM_LDS_CASE
 }
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -386,6 +522,20 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   chk32(ep.y, ep.ld_y);
   chk32(ep.g, ep.ld_g);
   if (ep.out16) vec_epi = vec_epi && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
+  if (bf16 && K % LDS_BK == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B)) {
+    // Direct-to-LDS pipeline; narrow outputs use 64-column tiles.
+    const int nw = N <= 64 ? 1 : 4;
+    const long tiles = (long)((M + 127) / 128) * ((N + 64 * nw - 1) / (64 * nw));
+    if (tiles > INT32_MAX) return Status::Invalid("gemm: too many tiles");
+    const auto* a16 = static_cast<const uint16_t*>(A);
+    const auto* b16 = static_cast<const uint16_t*>(B);
+    if (nw == 1)
+      launch_lds_kind<1>(stream, ep.kind, dim3((unsigned)tiles), a16, lda, b16, ldb, M, N, K, vec_epi, ep);
+    else
+      launch_lds_kind<4>(stream, ep.kind, dim3((unsigned)tiles), a16, lda, b16, ldb, M, N, K, vec_epi, ep);
+    PSSA_LAUNCH_CHECK("gemm_lds");
+    return Status::Ok();
+  }
   const long tiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > INT32_MAX) return Status::Invalid("gemm: too many tiles");
   dim3 grid((unsigned)tiles);

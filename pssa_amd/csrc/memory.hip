@@ -231,12 +231,145 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Full soft read for the model path (no top-k, small banks): the bank's keys
+// stay in LDS for the whole launch, transposed so that lane j of a wave reads
+// slot j + 64q of key dimension i at consecutive addresses, next to
+// 1/(1 - |k|^2) per slot in f64.  One wave per query, up to SOFT_SPL slots
+// per lane, eight waves per workgroup.  The projection and the query norm
+// follow the reference's sequential f64 order exactly; the squared distance
+// sum runs in f64, and x = sum / ((1-|q|^2)(1-|k|^2)) is formed with the two
+// reciprocals.  Only the soft weights depend on the result (no ranking), so
+// 2 asinh(sqrt(x)) is then evaluated in f32 (relative error a few 1e-7, far
+// inside the 1e-4 parity gate), followed by the reference's f32 softmax
+// whose two sums over slots run as wave reductions.  Writes the
+// [n, capacity] weights; the value readout is a GEMM.
+constexpr int SOFT_SPL = 8;            // slots per lane: capacity <= 512
+constexpr int SOFT_MAX_KEYS = 16384;   // dk * capacity floats held in LDS (64 KiB)
+constexpr int SOFT_MAX_DK = 64;
+constexpr int SOFT_WAVES = 8;
+
+__device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
+  return (((size_t)dk * cap + 1) & ~(size_t)1);  // keep the f64 arrays 8-byte aligned
+}
+
+__global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs a) {
+  extern __shared__ float smem[];
+  const int cap = a.capacity, dk = a.dk, cnt = a.count;
+  float* keyT = smem;                                                  // [dk][cap]
+  double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]
+  double* pq = rk + cap;                                               // [waves][SOFT_MAX_DK]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < cnt * dk; e += 64 * SOFT_WAVES) {
+    const int i = e / cnt, sl = e - i * cnt;
+    keyT[i * cap + sl] = a.keys[(size_t)sl * dk + i];
+  }
+  for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
+  __syncthreads();
+  double* p = pq + wave * SOFT_MAX_DK;
+
+  for (int n = blockIdx.x * SOFT_WAVES + wave; n < a.n; n += gridDim.x * SOFT_WAVES) {
+    const float* qrow = a.q + (size_t)n * a.ld_q;
+    // diffeomorphic_project (src/memory.rs:194-211): sequential f64 norm.
+    const float qv = lane < dk ? qrow[lane] : 0.0f;
+    p[lane] = (double)qv;
+    wave_sync();
+    double r2 = 0.0;
+    {
+#pragma clang fp contract(off)
+      for (int i = 0; i < dk; ++i) r2 = r2 + p[i] * p[i];
+    }
+    const double r = sqrt(r2);
+    const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+    const float pv = (float)((double)qv * scale);
+    wave_sync();
+    p[lane] = (double)pv;
+    wave_sync();
+    // squared_norm of the projected query (src/memory.rs:181-192).
+    double qs = 0.0;
+    {
+#pragma clang fp contract(off)
+      for (int i = 0; i < dk; ++i) qs = qs + p[i] * p[i];
+    }
+    float q_sq = (float)qs;
+    if (qs < 1.0 && q_sq == 1.0f) q_sq = __uint_as_float(0x3f7fffffu);
+    const double rq = 1.0 / (1.0 - (double)q_sq);
+
+    float dist[SOFT_SPL];
+    float local_min = FLT_MAX;
+    if (cnt > 0) {
+      double sq[SOFT_SPL];
+#pragma unroll
+      for (int j = 0; j < SOFT_SPL; ++j) sq[j] = 0.0;
+      for (int i = 0; i < dk; ++i) {
+        const double pi = p[i];
+        const float* kr = keyT + i * cap;
+#pragma unroll
+        for (int j = 0; j < SOFT_SPL; ++j) {
+          const int sl = lane + 64 * j;
+          const double t = pi - (double)(sl < cnt ? kr[sl] : 0.0f);
+          sq[j] = fma(t, t, sq[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SOFT_SPL; ++j) {
+        const int sl = lane + 64 * j;
+        if (sl < cnt) {
+          const float x = (float)(sq[j] * rq * rk[sl]);
+          const float y = sqrtf(x);
+          // asinh(y) = log1p(y + y^2 / (1 + sqrt(1 + y^2))), y^2 = x.
+          dist[j] = 2.0f * log1pf(y + x / (1.0f + sqrtf(1.0f + x)));
+          local_min = fminf(local_min, dist[j]);
+        } else {
+          dist[j] = 0.0f;
+        }
+      }
+    }
+    const float min_dist = wave_min(local_min);
+    float e[SOFT_SPL];
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SOFT_SPL; ++j) {
+      const int sl = lane + 64 * j;
+      e[j] = sl < cnt ? expf((min_dist - dist[j]) / a.tau) : 0.0f;
+      part += e[j];
+    }
+    const float sum = wave_sum(part);
+#pragma unroll
+    for (int j = 0; j < SOFT_SPL; ++j) {
+      const int sl = lane + 64 * j;
+      if (sl < cap) put_weight(a, n, sl, sl < cnt ? e[j] / sum : 0.0f);
+    }
+    wave_sync();
+  }
+}
+
+static bool soft_read_fits(const RetrieveArgs& a) {
+  return (a.top_k == 0 || a.top_k >= a.count) && a.project && !a.q_pnc && !a.q_norm && !a.out_val &&
+         !a.out_min && !a.out_idx && a.dk <= SOFT_MAX_DK && a.capacity <= 64 * SOFT_SPL &&
+         (long)a.dk * a.capacity <= SOFT_MAX_KEYS;
+}
+
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.n <= 0) return Status::Ok();
   if (a.dk <= 0 || a.capacity <= 0 || a.count < 0 || a.count > a.capacity)
     return Status::Invalid("retrieve: bad bank shape");
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
   if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
+  if (soft_read_fits(a)) {
+    const size_t lds = (((size_t)a.dk * a.capacity + 1) & ~(size_t)1) * sizeof(float) +
+                       ((size_t)a.capacity + (size_t)SOFT_WAVES * SOFT_MAX_DK) * sizeof(double);
+    if (lds > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&soft_read_kernel),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return Status::Device(std::string("soft_read LDS attribute: ") + hipGetErrorString(e));
+    }
+    int blocks = (a.n + SOFT_WAVES - 1) / SOFT_WAVES;
+    if (blocks > 512) blocks = 512;
+    soft_read_kernel<<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);
+    PSSA_LAUNCH_CHECK("soft_read");
+    return Status::Ok();
+  }
   const int dk_pad = (a.dk + 3) & ~3;
   const size_t lds = (size_t)4 * (dk_pad + a.capacity) * sizeof(float);
   if (lds > 128 * 1024) return Status::Invalid("retrieve: d_key + capacity too large for LDS");

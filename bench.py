@@ -28,6 +28,15 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_TFLOPS = 2500.0
 FP32_TFLOPS = 157.3
+# VALU issue slots per second: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz (one
+# non-packed fp32 op per lane-slot; v_exp_f32 occupies two on gfx950).
+VALU_SLOTS_PER_S = 256 * 4 * 16 * 2.4e9
+# Issue slots per SSM element: v_mul (exponent), v_exp_f32 (2), v_mul (u*B),
+# v_fma (state), v_fma (readout).
+SSM_SLOTS_PER_ELEM = 6
+# Algorithmic fp32 flops per SSM element (the exponential not counted).
+SSM_FLOPS_PER_ELEM = 6
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "ssm_scan_105m_prefill_pmc.md")
 
 
 def model_config(args):
@@ -47,12 +56,25 @@ def stage_work(cfg, lanes, T):
     return {
         "gemm_flops": 2.0 * gemm_mac_tok * N * L + 2.0 * lanes * V * d,
         "ssm_elems": float(N) * d * s * L,
-        # per element: v_mul (exponent), v_exp, v_mul (B x), fma (h), fma (y)
-        "ssm_flops": 7.0 * N * d * s * L,
-        # HBM bytes the scan must move once: delta, x, y (fp32 [N,d]) and B, C ([N,s]) per layer
-        "ssm_bytes": (3.0 * N * d + 2.0 * N * s) * 4 * L,
+        "ssm_flops": float(SSM_FLOPS_PER_ELEM) * N * d * s * L,
+        # HBM bytes one scan launch must move: delta, x, y (fp32 [N,d]), B, C
+        # ([N,s]), and the carry read and written ([lanes,d,s]).
+        "ssm_bytes_per_launch": (3.0 * N * d + 2.0 * N * s + 2.0 * lanes * d * s) * 4,
         "dist_pairs": float(N) * C * L,
     }
+
+
+def pmc_traffic():
+    """HBM bytes per ssm_scan launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by a copy kernel of known size)."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(weights, ids, budget_s: float):
@@ -161,21 +183,33 @@ def main():
 
     work = stage_work(cfg, args.lanes, args.seq)
     ssm_ms = stages.get("ssm_scan", 0.0)
-    ssm_launch_ms = ssm_ms / cfg.depth
-    ssm_tflops = work["ssm_flops"] / (ssm_ms * 1e-3) / 1e12 if ssm_ms else 0.0
+    ssm_launch_s = ssm_ms / cfg.depth * 1e-3
+    ssm_tflops = work["ssm_flops"] / cfg.depth / ssm_launch_s / 1e12 if ssm_ms else 0.0
     gemm_ms = sum(v for k_, v in stages.items() if k_.startswith("gemm") or k_ == "head")
+    gemm_tflops = work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    # Whole-pass floor: GEMMs at the bf16 MFMA peak,
+    # the scan at the VALU issue peak; everything else is left out.
+    floor_s = work["gemm_flops"] / (BF16_MFMA_TFLOPS * 1e12) + \
+        work["ssm_elems"] * SSM_SLOTS_PER_ELEM / VALU_SLOTS_PER_S
     roofline = {
+        # The dominant kernel is the diagonal scan: 7.7e10 exponentials per
+        # pass with no matrix form, bound by VALU issue (neither HBM nor MFMA).
         "kernel": "ssm_scan",
         "bound": "valu",
         "achieved": round(ssm_tflops, 3),
         "peak": FP32_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(ssm_tflops / FP32_TFLOPS, 4),
-        "traffic": None,
-        "launch_ms": round(ssm_launch_ms, 4),
+        "traffic": pmc_traffic(),
+        "launch_ms": round(ssm_launch_s * 1e3, 4),
         "flops_per_launch": work["ssm_flops"] / cfg.depth,
-        "gemm_tflops": round(work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None,
-        "gemm_frac_bf16": round(work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12 / BF16_MFMA_TFLOPS, 4) if gemm_ms else None,
+        "algorithmic_bytes_per_launch": work["ssm_bytes_per_launch"],
+        "valu_issue_frac": round(work["ssm_elems"] / cfg.depth * SSM_SLOTS_PER_ELEM / ssm_launch_s /
+                                 VALU_SLOTS_PER_S, 4) if ssm_ms else None,
+        "gemm": {"bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": BF16_MFMA_TFLOPS,
+                 "unit": "TFLOP/s", "frac": round(gemm_tflops / BF16_MFMA_TFLOPS, 4)},
+        "pipeline_floor_ms": round(floor_s * 1e3, 3),
+        "pipeline_frac": round(floor_s / (elapsed / args.steps), 4),
     }
     cpu = None
     if not args.no_cpu_baseline:

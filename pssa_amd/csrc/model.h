@@ -29,6 +29,7 @@ enum Stage : int {
   ST_NORM,
   ST_GEMM_IN,
   ST_SSM,
+  ST_SSM_AUX,
   ST_GEMM_QH,
   ST_RETRIEVE,
   ST_GEMM_READ,

@@ -23,9 +23,9 @@
 
 namespace pssa {
 
-const char* const kStageNames[ST_COUNT] = {"embed",     "rmsnorm",    "gemm_in",   "ssm_scan",
-                                           "gemm_qh",   "retrieve",   "gemm_read", "gemm_proj",
-                                           "gemm_mlp1", "gemm_mlp2",  "head"};
+const char* const kStageNames[ST_COUNT] = {"embed",     "rmsnorm",   "gemm_in",   "ssm_scan",
+                                           "ssm_aux",   "gemm_qh",   "retrieve",  "gemm_read",
+                                           "gemm_proj", "gemm_mlp1", "gemm_mlp2", "head"};
 
 __global__ void embed_kernel(const uint32_t* __restrict__ ids, const float* __restrict__ embed,
                              float* __restrict__ X, int d, size_t rows) {
@@ -225,8 +225,9 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_in.ld32 = n_in;
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
 
-    PSSA_RETURN_IF(tm.mark(ST_SSM));
+    PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
     if (ssm_needs_zeroed_y(s)) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
+    PSSA_RETURN_IF(tm.mark(ST_SSM));
     SsmArgs sa;
     sa.delta = P;
     sa.ld_delta = n_in;
@@ -247,6 +248,7 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     sa.lanes = (int)n_lanes;
     sa.y_part = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
+    PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
     if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, L->Yh.as<uint16_t>(), d, rows, d));
 
     // q_euc = y W_qh^T + q_x.

@@ -253,6 +253,45 @@ int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* lanes, char* err, size_t err_l
 int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, char* err,
                                size_t err_len);
 
+/* ----------------------------------------------------------------- decode */
+
+#define PSSA_HIP_DECODE_PLASTIC 1 /* apply the plastic write rules after every step */
+#define PSSA_HIP_DECODE_GRAPH 2   /* replay one hipGraph-captured step */
+
+/* Greedy decode of `steps` tokens on lanes 0..n_lanes-1, each continuing its
+ * carry: every step is forward_inference (src/pssa.rs:2387-2391) on the
+ * lane's current token followed by the greedy choice over ids 1..V-1 in
+ * f32::total_cmp order, ties to the lower id (sample() at temperature 0,
+ * src/inference.rs:123-127).  first_ids [n_lanes] are the tokens fed to the
+ * first step; NULL feeds the greedy choice from the last prefill's logits
+ * (which must have covered the same n_lanes lanes).  out_ids [steps, n_lanes]
+ * receives the generated ids; logits_last [n_lanes, V] (may be NULL) the last
+ * step's logits.
+ *
+ * PSSA_HIP_DECODE_PLASTIC adds, after each step and block by block in lane
+ * order, the refractory-protected bank write of the lane's projected query and
+ * block output when the surprise -log softmax(logits)[chosen] exceeds 3.5
+ * (insert_protected, src/memory.rs:305-342; write rule of
+ * insert_training_memory_at, src/pssa.rs:3705-3736), and the Hebbian update of
+ * the adapter's fast weights toward the block output (dream_replay_value,
+ * src/pssa.rs:1814-1832).  The reference applies neither during inference;
+ * this composition is an extension of its decode step.  The model's banks and
+ * fast weights change; its step counter advances by one per step.
+ * PSSA_HIP_DECODE_GRAPH captures one step into a hipGraph (once per lane
+ * count and flag set) and replays it; results equal the eager steps. */
+int pssa_hip_decode(pssa_hip_lanes* lanes, const uint32_t* first_ids, size_t n_lanes,
+                    size_t steps, int flags, uint32_t* out_ids, size_t out_len,
+                    float* logits_last, size_t logits_len, char* err, size_t err_len);
+
+/* Reads one block's plastic state back from the device: adapter fast
+ * weights [d,r], bank keys [C,k], values [C,d], norm_sq [C], confidence [C],
+ * last_seen [C], count, write_head, and the model's step counter.  Any
+ * pointer may be NULL. */
+int pssa_hip_model_get_plastic(pssa_hip_model* model, size_t layer, float* adapter_up, float* keys,
+                               float* values, float* norm_sq, float* confidence,
+                               uint64_t* last_seen, uint64_t* count, uint64_t* write_head,
+                               uint64_t* step, char* err, size_t err_len);
+
 /* Per-stage kernel time (ms, summed over layers) of the most recent prefill,
  * recorded with HIP events on the stream the kernels run on.  enable = 1 turns
  * recording on for later calls, 0 off, -1 leaves it unchanged.  names/ms

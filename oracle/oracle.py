@@ -69,6 +69,9 @@ def lib() -> C.CDLL:
         "oracle_greedy": ([fp, C.c_size_t], C.c_uint32),
         "oracle_dense_scan": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_int], None),
         "oracle_hebbian_update": ([fp, fp, fp, fp, C.c_size_t, C.c_size_t], None),
+        "oracle_forward_taps": ([vp, fp, C.c_uint32, fp, fp, fp, fp, fp], None),
+        "oracle_decode": ([vp, fp, u32p, C.c_size_t, C.c_size_t, C.c_int, C.c_uint64, u32p, fp, fp, C.c_int],
+                          C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -161,6 +164,34 @@ class OracleModel:
         loss = lib().oracle_train_chunk_forward(self.ref, ptr(state), ptr(ids, C.c_uint32),
                                                 ptr(tg, C.c_uint32), ids.size, ptr(logits))
         return np.float32(loss), logits
+
+    def forward_taps(self, state: np.ndarray, token: int):
+        """forward_inference with per-block (q_pnc, z_final, adapter out, adapter act) and logits."""
+        c = self.cfg
+        q = np.empty((c.depth, c.d_mem_key), np.float32)
+        z = np.empty((c.depth, c.d_latent), np.float32)
+        a = np.empty((c.depth, c.d_latent), np.float32)
+        act = np.empty((c.depth, c.adapter_rank), np.float32)
+        lg = np.empty(c.d_vocab, np.float32)
+        lib().oracle_forward_taps(self.ref, ptr(state), token, ptr(q), ptr(z), ptr(a), ptr(act), ptr(lg))
+        return q, z, a, act, lg
+
+    def decode(self, states: np.ndarray, first_ids, steps: int, plastic: bool = False, step_base: int = 0,
+               threads: int = 1):
+        """Greedy decode of every lane for `steps` steps (oracle_decode).  Returns
+        (ids [steps, lanes], last logits [lanes, V], last surprise [lanes]).
+        With plastic set the banks and adapter_up of the weights change in place."""
+        ids = np.ascontiguousarray(first_ids, dtype=np.uint32).copy()
+        lanes = ids.size
+        out = np.empty((steps, lanes), np.uint32)
+        lg = np.empty((lanes, self.cfg.d_vocab), np.float32)
+        sp = np.empty(lanes, np.float32)
+        rc = lib().oracle_decode(self.ref, ptr(states), ptr(ids, C.c_uint32), lanes, steps, 1 if plastic else 0,
+                                 step_base, ptr(out, C.c_uint32), ptr(lg), ptr(sp), threads)
+        if rc:
+            raise ValueError(f"oracle decode rejected the ids ({rc})")
+        self.sync()
+        return out, lg, sp
 
     def features(self, state: np.ndarray, token: int) -> np.ndarray:
         out = np.empty(self.cfg.d_latent, np.float32)

@@ -18,6 +18,7 @@
 #include <cfloat>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <thread>
 #include <utility>
 #include <vector>
@@ -698,10 +699,19 @@ float oracle_train_chunk_forward(const oracle_model* m, float* state, const uint
   return total / (float)n;
 }
 
+// f32::total_cmp order key: larger key = larger in IEEE total order.
+static int32_t total_order_key(float f) {
+  int32_t b;
+  std::memcpy(&b, &f, 4);
+  return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
+}
+
+// sample() with temperature 0 (src/inference.rs:123-127): max_by over ids
+// 1..V-1 of total_cmp, ties broken toward the lower id.
 uint32_t oracle_greedy(const float* logits, size_t v) {
   uint32_t best = 1;
   for (uint32_t i = 2; i < v; i++)
-    if (logits[i] > logits[best]) best = i;
+    if (total_order_key(logits[i]) > total_order_key(logits[best])) best = i;
   return best;
 }
 
@@ -732,6 +742,101 @@ void oracle_hebbian_update(float* up, const float* target, const float* current,
     float err = std::min(std::max(target[i] - current[i], -4.0f), 4.0f);
     for (size_t q = 0; q < r; q++) up[i * r + q] += rate * err * act[q];
   }
+}
+
+// forward_inference (src/pssa.rs:2387-2391) that also returns, per block,
+// the projected query, the block output z_final, the adapter output and the
+// adapter activations: the operands of the plastic decode rules.
+void oracle_forward_taps(const oracle_model* m, float* state, uint32_t id, float* q_pnc,
+                         float* z_final, float* ad_out, float* act, float* logits) {
+  const oracle_config& c = m->cfg;
+  const size_t d = c.d_latent, ds = c.d_latent * c.d_state, k = c.d_mem_key, r = c.adapter_rank;
+  Runner run(m);
+  const float scale = 1.0f / sqrtf((float)c.depth);
+  for (size_t l = 0; l < c.depth; l++) {
+    float* z = l == 0 ? run.feat.data() : run.out.data();
+    const float* in = l == 0 ? m->embed + (size_t)id * d : run.feat.data();
+    block_forward(m->blocks[l], c, run.sc[l], state + l * ds, in, z);
+    std::memcpy(q_pnc + l * k, run.sc[l].qp.data(), k * 4);
+    std::memcpy(z_final + l * d, z, d * 4);
+    std::memcpy(ad_out + l * d, run.sc[l].adout.data(), d * 4);
+    std::memcpy(act + l * r, run.sc[l].act.data(), r * 4);
+    if (l > 0)
+      for (size_t i = 0; i < d; i++) run.feat[i] += scale * run.out[i];
+  }
+  if (logits) run.logits(logits);
+}
+
+// Greedy decode over `lanes` independent streams sharing one model
+// (forward_inference per stream, src/pssa.rs:2387-2391; greedy sample,
+// src/inference.rs:123-127).  With `plastic` set, every step then applies,
+// block by block and in lane order, (a) the refractory-protected bank write of
+// the stream's projected query and block output when its surprise
+// -log softmax(logits)[chosen] exceeds 3.5 (insert_protected,
+// src/memory.rs:305-342; the write rule of insert_training_memory_at,
+// src/pssa.rs:3705-3736), and (b) the Hebbian fast-weight rule of
+// dream_replay_value (src/pssa.rs:1814-1832) with the block output as the
+// target and the adapter output as the prediction.  The step counter that the
+// refractory gate reads advances by one per step; step k uses step_base + k.
+int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, size_t steps,
+                  int plastic, uint64_t step_base, uint32_t* out_ids, float* logits_last,
+                  float* surprise_last, int threads) {
+  const oracle_config& c = m->cfg;
+  const size_t d = c.d_latent, ds = c.d_latent * c.d_state, V = c.d_vocab, k = c.d_mem_key,
+               r = c.adapter_rank, depth = c.depth;
+  for (size_t i = 0; i < lanes; i++)
+    if (ids[i] >= V) return -1;
+  std::vector<float> lg(lanes * V), surprise(lanes);
+  std::vector<float> tq(lanes * depth * k), tz(lanes * depth * d), ta(lanes * depth * d),
+      tact(lanes * depth * r);
+  // The rate cache does not change during decode (only banks and the fast
+  // adapter do), so each stream keeps one runner.
+  std::vector<std::unique_ptr<Runner>> runners(lanes);
+  parallel_for(lanes, threads, [&](size_t ln) { runners[ln].reset(new Runner(m)); });
+  for (size_t step = 0; step < steps; step++) {
+    parallel_for(lanes, threads, [&](size_t ln) {
+      Runner& run = *runners[ln];
+      float* st = states + ln * depth * ds;
+      const float scale = 1.0f / sqrtf((float)depth);
+      for (size_t l = 0; l < depth; l++) {
+        float* z = l == 0 ? run.feat.data() : run.out.data();
+        const float* in = l == 0 ? m->embed + (size_t)ids[ln] * d : run.feat.data();
+        block_forward(m->blocks[l], c, run.sc[l], st + l * ds, in, z);
+        std::memcpy(&tq[(ln * depth + l) * k], run.sc[l].qp.data(), k * 4);
+        std::memcpy(&tz[(ln * depth + l) * d], z, d * 4);
+        std::memcpy(&ta[(ln * depth + l) * d], run.sc[l].adout.data(), d * 4);
+        std::memcpy(&tact[(ln * depth + l) * r], run.sc[l].act.data(), r * 4);
+        if (l > 0)
+          for (size_t i = 0; i < d; i++) run.feat[i] += scale * run.out[i];
+      }
+      float* lgl = &lg[ln * V];
+      run.logits(lgl);
+      const uint32_t next = oracle_greedy(lgl, V);
+      float mx = -INFINITY;
+      for (size_t v = 0; v < V; v++) mx = std::fmax(mx, lgl[v]);
+      float sum = 0.0f;
+      for (size_t v = 0; v < V; v++) sum += expf(lgl[v] - mx);
+      surprise[ln] = (mx + logf(sum)) - lgl[next];
+      out_ids[step * lanes + ln] = next;
+    });
+    if (plastic) {
+      const uint64_t cur = step_base + step + 1;
+      for (size_t l = 0; l < depth; l++) {
+        oracle_block* b = &m->blocks[l];
+        for (size_t ln = 0; ln < lanes; ln++)
+          if (surprise[ln] > 3.5f)
+            oracle_bank_insert_protected(b, c.mem_capacity, k, d, &tq[(ln * depth + l) * k],
+                                         &tz[(ln * depth + l) * d], surprise[ln], cur);
+        for (size_t ln = 0; ln < lanes; ln++)
+          oracle_hebbian_update(b->adapter_up, &tz[(ln * depth + l) * d], &ta[(ln * depth + l) * d],
+                                &tact[(ln * depth + l) * r], d, r);
+      }
+    }
+    for (size_t ln = 0; ln < lanes; ln++) ids[ln] = out_ids[step * lanes + ln];
+  }
+  if (logits_last) std::memcpy(logits_last, lg.data(), lanes * V * 4);
+  if (surprise_last) std::memcpy(surprise_last, surprise.data(), lanes * 4);
+  return 0;
 }
 
 }  // extern "C"

@@ -26,6 +26,11 @@
  *   dense scan ........................ pinned: closed form (orthogonal-scaled
  *                                        transitions, diagonal case == diagonal scan)
  *   refractory gate ................... pinned: closed form (feature_benchmark.rs:446-500)
+ *   greedy sample ..................... pinned: total_cmp order and tie rule, closed
+ *                                        cases (src/inference.rs:123-127)
+ *   decode composition (oracle_decode)  parity unpinned as a whole: it composes the
+ *                                        pinned forward, greedy, insert_protected and
+ *                                        Hebbian rules; the reference has no such step
  */
 #ifndef PSSA_ORACLE_H
 #define PSSA_ORACLE_H
@@ -152,7 +157,8 @@ float oracle_train_chunk_forward(const oracle_model* m, float* state, const uint
                                  const uint32_t* targets, size_t n, float* logits);
 /* Per-token features of the last block (z after residual), for tests. */
 void oracle_forward_features(const oracle_model* m, float* state, uint32_t id, float* features);
-/* Greedy argmax over ids 1..V-1, ties to the lower id (src/inference.rs:123-127). */
+/* Greedy argmax over ids 1..V-1 in f32::total_cmp order, ties to the lower
+ * id (src/inference.rs:123-127). */
 uint32_t oracle_greedy(const float* logits, size_t v);
 
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t, sequential. */
@@ -162,6 +168,21 @@ void oracle_dense_scan(const float* a, const float* b, const float* h0, size_t b
 /* Hebbian fast-weight rule of dream replay (src/pssa.rs:1814-1832). */
 void oracle_hebbian_update(float* up_fast, const float* target, const float* current,
                            const float* act, size_t d, size_t r);
+
+/* forward_inference plus per-block taps: q_pnc [depth,k], z_final [depth,d],
+ * ad_out [depth,d] (adapter output), act [depth,r] (adapter activations). */
+void oracle_forward_taps(const oracle_model* m, float* state, uint32_t id, float* q_pnc,
+                         float* z_final, float* ad_out, float* act, float* logits);
+
+/* Greedy decode of `lanes` streams for `steps` steps from ids[lanes] (updated
+ * to the last generated ids); out_ids [steps, lanes].  plastic != 0 adds the
+ * per-step lane-ordered protected bank write and Hebbian adapter update;
+ * the model's banks and adapter_up are modified in place.  logits_last and
+ * surprise_last (may be NULL) receive the last step's [lanes, V] logits and
+ * [lanes] surprise.  Returns -1 on an id outside the vocabulary. */
+int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, size_t steps,
+                  int plastic, uint64_t step_base, uint32_t* out_ids, float* logits_last,
+                  float* surprise_last, int threads);
 
 #ifdef __cplusplus
 }

@@ -22,6 +22,8 @@ F32 = 0
 BF16 = 1
 INIT_REFERENCE = 0
 INIT_BASELINE = 1
+DECODE_PLASTIC = 1
+DECODE_GRAPH = 2
 
 fp = C.POINTER(C.c_float)
 u64p = C.POINTER(C.c_uint64)
@@ -123,6 +125,8 @@ def lib() -> C.CDLL:
         "pssa_hip_lanes_prefill_staged": ([vp, err_t, sz], C.c_int),
         "pssa_hip_lanes_read_logits": ([vp, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_times": ([vp, C.c_int, C.POINTER(C.c_char_p), fp, sz], C.c_int),
+        "pssa_hip_decode": ([vp, u32p, sz, sz, C.c_int, u32p, sz, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_model_get_plastic": ([vp, sz, fp, fp, fp, fp, fp, u64p, u64p, u64p, u64p, err_t, sz], C.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpssa_hip.so")
 
-HIP_SOURCES = ["api.hip", "gemm.hip", "ssm.hip", "memory.hip", "model.hip", "dense_scan.hip"]
+HIP_SOURCES = ["api.hip", "gemm.hip", "ssm.hip", "memory.hip", "model.hip", "decode.hip", "dense_scan.hip"]
 HOST_SOURCES = ["host_weights.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -115,6 +115,7 @@ int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
     ctx->name = prop.name;
     ctx->cu_count = prop.multiProcessorCount;
     PSSA_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    PSSA_RETURN_IF(pssa::init_retrieve_attributes());
     *out = ctx.release();
     return Status::Ok();
   };
@@ -522,6 +523,17 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       for (size_t q = 0; q < C; ++q)
         for (size_t j = 0; j < d; ++j) vt[j * C + q] = b.mem_values[q * d + j];
       PSSA_RETURN_IF(upload_weight(B.u_eff, ueff.data(), ueff.size(), weight_dtype, st));
+      PSSA_RETURN_IF(upload(B.u_fast, b.adapter_up, d * r * 4, st));
+      PSSA_RETURN_IF(upload(B.u_slow, b.adapter_slow, d * r * 4, st));
+      std::vector<float> conf(C, 1.0f);
+      std::vector<unsigned long long> last(C, 0ull);
+      if (b.mem_confidence) std::memcpy(conf.data(), b.mem_confidence, C * 4);
+      if (b.mem_last_seen)
+        for (size_t q = 0; q < C; ++q) last[q] = b.mem_last_seen[q];
+      const int meta[2] = {(int)b.mem_count, (int)(b.mem_write_head % C)};
+      PSSA_RETURN_IF(upload(B.conf, conf.data(), C * 4, st));
+      PSSA_RETURN_IF(upload(B.last_seen, last.data(), C * 8, st));
+      PSSA_RETURN_IF(upload(B.meta, meta, sizeof(meta), st));
       PSSA_RETURN_IF(upload(B.rates2, rates.data(), rates.size() * 4, st));
       PSSA_RETURN_IF(upload(B.gamma, b.norm_gamma, d * 4, st));
       PSSA_RETURN_IF(upload(B.beta, b.norm_beta, d * 4, st));
@@ -529,9 +541,11 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       PSSA_RETURN_IF(upload(B.norm_sq, b.mem_norm_sq, C * 4, st));
       PSSA_RETURN_IF(upload(B.values, b.mem_values, C * d * 4, st));
       PSSA_RETURN_IF(upload_weight(B.values_t, vt.data(), vt.size(), weight_dtype, st));
-      B.count = b.mem_count;
       PSSA_RETURN_IF(sync(ctx));  // host staging vectors are reused
     }
+    const unsigned long long step0 = 0;
+    PSSA_RETURN_IF(upload(m->step, &step0, 8, st));
+    PSSA_RETURN_IF(sync(ctx));
     *out = m.release();
     return Status::Ok();
   };
@@ -707,6 +721,145 @@ int pssa_hip_lanes_stage_times(pssa_hip_lanes* L, int enable, const char** names
     ++n;
   }
   return (int)n;
+}
+
+int pssa_hip_model_get_plastic(pssa_hip_model* M, size_t layer, float* adapter_up, float* keys,
+                               float* values, float* norm_sq, float* confidence, uint64_t* last_seen,
+                               uint64_t* count, uint64_t* write_head, uint64_t* step, char* err,
+                               size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(M != nullptr, "null model"));
+    const pssa_hip_config& c = M->cfg;
+    PSSA_RETURN_IF(need(layer < c.depth, "layer out of range"));
+    std::lock_guard<std::mutex> g(M->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(M->ctx->device));
+    const hipStream_t st = M->ctx->stream;
+    const pssa::DevBlock& B = M->blocks[layer];
+    const size_t d = c.d_latent, k = c.d_mem_key, C = c.mem_capacity, r = c.adapter_rank;
+    if (adapter_up) PSSA_RETURN_IF(download(adapter_up, B.u_fast, d * r * 4, st));
+    if (keys) PSSA_RETURN_IF(download(keys, B.keys, C * k * 4, st));
+    if (values) PSSA_RETURN_IF(download(values, B.values, C * d * 4, st));
+    if (norm_sq) PSSA_RETURN_IF(download(norm_sq, B.norm_sq, C * 4, st));
+    if (confidence) PSSA_RETURN_IF(download(confidence, B.conf, C * 4, st));
+    std::vector<unsigned long long> last(C);
+    if (last_seen) PSSA_RETURN_IF(download(last.data(), B.last_seen, C * 8, st));
+    int meta[2] = {0, 0};
+    PSSA_RETURN_IF(download(meta, B.meta, sizeof(meta), st));
+    unsigned long long stp = 0;
+    PSSA_RETURN_IF(download(&stp, M->step, 8, st));
+    PSSA_RETURN_IF(sync(M->ctx));
+    if (last_seen)
+      for (size_t q = 0; q < C; ++q) last_seen[q] = last[q];
+    if (count) *count = (uint64_t)meta[0];
+    if (write_head) *write_head = (uint64_t)meta[1];
+    if (step) *step = stp;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+}  // extern "C"
+
+namespace {
+
+Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
+  const pssa_hip_config& c = L->model->cfg;
+  if (L->dec_lanes < L->lanes) {
+    const size_t n = L->lanes, D = c.depth;
+    PSSA_RETURN_IF(L->tap_q.alloc(D * n * c.d_mem_key * 4));
+    PSSA_RETURN_IF(L->tap_z.alloc(D * n * c.d_latent * 4));
+    PSSA_RETURN_IF(L->tap_a.alloc(D * n * c.d_latent * 4));
+    PSSA_RETURN_IF(L->tap_act.alloc(D * n * c.adapter_rank * 4));
+    PSSA_RETURN_IF(L->surprise.alloc(n * 4));
+    PSSA_RETURN_IF(L->hebb_rate.alloc(n * 4));
+    PSSA_RETURN_IF(L->gen_pos.alloc(4));
+    L->dec_lanes = n;
+  }
+  if (L->gen_cap < steps) {
+    const size_t cap = std::max<size_t>(steps, 128);
+    PSSA_RETURN_IF(L->gen_ids.alloc(cap * L->lanes * 4));
+    L->gen_cap = cap;
+    // The captured step holds the old buffer's address.
+    if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
+    if (L->graph) (void)hipGraphDestroy(L->graph);
+    L->graph_exec = nullptr;
+    L->graph = nullptr;
+    L->graph_lanes = 0;
+  }
+  (void)n_lanes;
+  return Status::Ok();
+}
+
+Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
+  if (L->graph_exec && L->graph_lanes == n_lanes && L->graph_plastic == (plastic ? 1 : 0))
+    return Status::Ok();
+  if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
+  if (L->graph) (void)hipGraphDestroy(L->graph);
+  L->graph_exec = nullptr;
+  L->graph = nullptr;
+  const hipStream_t st = L->ctx->stream;
+  const bool timing = L->timing;
+  L->timing = false;  // no event records inside the graph
+  PSSA_HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  Status s = pssa::run_decode_step(L, n_lanes, plastic);
+  hipGraph_t graph = nullptr;
+  const hipError_t e = hipStreamEndCapture(st, &graph);
+  L->timing = timing;
+  PSSA_RETURN_IF(s);
+  if (e != hipSuccess) return Status::Device(std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+  L->graph = graph;
+  PSSA_HIP_TRY(hipGraphInstantiate(&L->graph_exec, graph, nullptr, nullptr, 0));
+  L->graph_lanes = n_lanes;
+  L->graph_plastic = plastic ? 1 : 0;
+  return Status::Ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes, size_t steps,
+                    int flags, uint32_t* out_ids, size_t out_len, float* logits_last,
+                    size_t logits_len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    PSSA_RETURN_IF(need((flags & ~(PSSA_HIP_DECODE_PLASTIC | PSSA_HIP_DECODE_GRAPH)) == 0, "unknown decode flags"));
+    PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
+    PSSA_RETURN_IF(need(steps > 0 && steps <= (1u << 20), "steps must be in 1..=2^20"));
+    PSSA_RETURN_IF(need(out_ids != nullptr && out_len == steps * n_lanes, "out_ids length must be steps*n_lanes"));
+    const size_t V = L->model->cfg.d_vocab;
+    if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
+    if (first_ids) {
+      for (size_t i = 0; i < n_lanes; ++i)
+        if (first_ids[i] >= V)
+          return Status::Invalid("prompt ID " + std::to_string(first_ids[i]) + " outside model vocabulary");
+    } else {
+      PSSA_RETURN_IF(need(L->staged_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
+    }
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
+    PSSA_RETURN_IF(ensure_decode_buffers(L, n_lanes, steps));
+    if (first_ids)
+      PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, first_ids, n_lanes * 4, hipMemcpyHostToDevice, st));
+    else
+      PSSA_RETURN_IF(pssa::run_greedy_from_logits(L, n_lanes));
+    const int zero = 0;
+    PSSA_HIP_TRY(hipMemcpyAsync(L->gen_pos.p, &zero, 4, hipMemcpyHostToDevice, st));
+    if (flags & PSSA_HIP_DECODE_GRAPH) {
+      PSSA_RETURN_IF(capture_decode_step(L, n_lanes, plastic));
+      for (size_t t = 0; t < steps; ++t) PSSA_HIP_TRY(hipGraphLaunch(L->graph_exec, st));
+    } else {
+      for (size_t t = 0; t < steps; ++t) PSSA_RETURN_IF(pssa::run_decode_step(L, n_lanes, plastic));
+    }
+    PSSA_RETURN_IF(download(out_ids, L->gen_ids, steps * n_lanes * 4, st));
+    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
+    L->staged_lanes = n_lanes;
+    L->staged_len = 1;
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
 }
 
 int pssa_hip_dense_scan(pssa_hip_ctx* ctx, const float* a, const float* b, const float* h0,

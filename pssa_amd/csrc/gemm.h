@@ -37,6 +37,10 @@ struct EpiParams {
   int ld32 = 0;
   void* out16 = nullptr;
   int ld16 = 0;
+  // Optional fp32 tap: ZRAW writes the adapter output, RESIDUAL writes
+  // z_final (before the residual scaling).
+  float* tap = nullptr;
+  int ld_tap = 0;
 };
 
 // A: activations [M, lda], B: weights [N, ldb], both K-contiguous and of the

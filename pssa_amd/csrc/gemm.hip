@@ -120,7 +120,7 @@ template <typename T, int KIND>
 __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, int N, bool vec,
                                          const float (&acc)[4], const float (&ad)[4]) {
   if (vec) {
-    float r[4];
+    float r[4], tp[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (KIND == EPI_ZRAW) {
       const float4 yv = *reinterpret_cast<const float4*>(ep.y + (size_t)row * ep.ld_y + col);
       const float4 gv = *reinterpret_cast<const float4*>(ep.g + (size_t)row * ep.ld_g + col);
@@ -128,6 +128,8 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
       r[1] = (yv.y * ep.scale + gv.y * acc[1]) + ad[1];
       r[2] = (yv.z * ep.scale + gv.z * acc[2]) + ad[2];
       r[3] = (yv.w * ep.scale + gv.w * acc[3]) + ad[3];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tp[e] = ad[e];
     } else if constexpr (KIND == EPI_ADD_AUX || KIND == EPI_RESIDUAL) {
       const float4 av = *reinterpret_cast<const float4*>(ep.aux + (size_t)row * ep.ld_aux + col);
       const float a4[4] = {av.x, av.y, av.z, av.w};
@@ -143,12 +145,17 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float zf = a4[e] + acc[e];
+          tp[e] = zf;
           r[e] = ep.first ? zf : o4[e] + ep.scale * zf;
         }
       }
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e) r[e] = epi_value<KIND>(ep, acc[e], row, col + e, 0.0f);
+    }
+    if constexpr (KIND == EPI_ZRAW || KIND == EPI_RESIDUAL) {
+      if (ep.tap)
+        *reinterpret_cast<float4*>(ep.tap + (size_t)row * ep.ld_tap + col) = make_float4(tp[0], tp[1], tp[2], tp[3]);
     }
     if (ep.out32)
       *reinterpret_cast<float4*>(ep.out32 + (size_t)row * ep.ld32 + col) = make_float4(r[0], r[1], r[2], r[3]);
@@ -164,7 +171,14 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
   } else {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (col + e < N) store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
+      if (col + e < N) {
+        store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
+        if constexpr (KIND == EPI_ZRAW) {
+          if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ad[e];
+        } else if constexpr (KIND == EPI_RESIDUAL) {
+          if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ep.aux[(size_t)row * ep.ld_aux + col + e] + acc[e];
+        }
+      }
   }
 }
 
@@ -521,6 +535,7 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   chk32(ep.aux, ep.ld_aux);
   chk32(ep.y, ep.ld_y);
   chk32(ep.g, ep.ld_g);
+  chk32(ep.tap, ep.ld_tap);
   if (ep.out16) vec_epi = vec_epi && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
   if (bf16 && K % LDS_BK == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B)) {
     // Direct-to-LDS pipeline; narrow outputs use 64-column tiles.

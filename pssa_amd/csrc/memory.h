@@ -14,6 +14,7 @@ struct RetrieveArgs {
   const float* norm_sq = nullptr;  // [capacity]
   const float* values = nullptr;   // [capacity, dv] (needed when top_k > 0)
   int n = 0, dk = 0, dv = 0, capacity = 0, count = 0;
+  const int* count_dev = nullptr;  // when set, the occupied-slot count is read from device memory
   float tau = 0.1f;
   int top_k = 0;                // 0: full soft read -> weights only (readout is a GEMM)
   float* weights = nullptr;     // [n, capacity]; optional
@@ -24,6 +25,12 @@ struct RetrieveArgs {
 };
 
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a);
+// One-time per-device set-up a later launch_retrieve with these arguments
+// needs (call it outside graph capture).
+Status prepare_retrieve(const RetrieveArgs& a);
+// Per-device kernel attributes (large dynamic LDS), set at context creation
+// so that no attribute call happens during graph capture.
+Status init_retrieve_attributes();
 
 constexpr int kMaxTopK = 64;
 

@@ -110,6 +110,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
   float* sq = smem + wave * (dk_pad + a.capacity);  // this wave's query, then distances
   float* sdist = sq + dk_pad;
   __shared__ uint32_t ssel[4][kMaxTopK];
+  const int cnt = a.count_dev ? a.count_dev[0] : a.count;
 
   for (int n = blockIdx.x * 4 + wave; n < a.n; n += gridDim.x * 4) {
     const float* qrow = a.q + (size_t)n * a.ld_q;
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
       for (int i = lane; i < a.dk; i += 64) a.q_pnc[(size_t)n * a.dk + i] = sq[i];
     const float q_sq = bank_norm_sq(sq, a.dk);
 
-    if (a.count == 0) {
+    if (cnt == 0) {
       for (int s = lane; s < a.capacity; s += 64) put_weight(a, n, s, 0.0f);
       if (a.out_val)
         for (int j = lane; j < a.dv; j += 64) a.out_val[(size_t)n * a.dv + j] = 0.0f;
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
     }
     // ---- distances ----
     float local_min = FLT_MAX;
-    for (int s = lane; s < a.count; s += 64) {
+    for (int s = lane; s < cnt; s += 64) {
       const float dist = poincare_dist(sq, q_sq, a.keys + (size_t)s * a.dk, a.norm_sq[s], a.dk);
       sdist[s] = dist;
       local_min = fminf(local_min, dist);
@@ -149,12 +150,12 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
     wave_sync();
     if (a.out_min && lane == 0) a.out_min[n] = min_dist;
 
-    if (a.top_k > 0 && a.top_k < a.count) {
+    if (a.top_k > 0 && a.top_k < cnt) {
       // ---- exact top-k by (distance bits, slot) (src/memory.rs:380-392) ----
       const int k = a.top_k;
       for (int r = 0; r < k; ++r) {
         unsigned long long best = ~0ull;
-        for (int s = lane; s < a.count; s += 64) {
+        for (int s = lane; s < cnt; s += 64) {
           const uint32_t bits = __float_as_uint(sdist[s]);
           const unsigned long long key = ((unsigned long long)bits << 32) | (unsigned)s;
           bool taken = false;
@@ -203,7 +204,7 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
     } else {
       // ---- full soft read (src/memory.rs:409-425) ----
       float part = 0.0f;
-      for (int s = lane; s < a.count; s += 64) {
+      for (int s = lane; s < cnt; s += 64) {
         const float e = expf((min_dist - sdist[s]) / a.tau);
         sdist[s] = e;
         part += e;
@@ -211,21 +212,21 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
       const float sum = wave_sum(part);
       wave_sync();
       for (int s = lane; s < a.capacity; s += 64) {
-        const float w = s < a.count ? sdist[s] / sum : 0.0f;
-        if (s < a.count) sdist[s] = w;
+        const float w = s < cnt ? sdist[s] / sum : 0.0f;
+        if (s < cnt) sdist[s] = w;
         put_weight(a, n, s, w);
       }
       wave_sync();
       if (a.out_val) {
         for (int j = lane; j < a.dv; j += 64) {
           float acc = 0.0f;
-          for (int s = 0; s < a.count; ++s) acc = fmaf(sdist[s], a.values[(size_t)s * a.dv + j], acc);
+          for (int s = 0; s < cnt; ++s) acc = fmaf(sdist[s], a.values[(size_t)s * a.dv + j], acc);
           a.out_val[(size_t)n * a.dv + j] = acc;
         }
       }
       if (a.out_idx)
         for (int r = lane; r < a.top_k; r += 64)
-          a.out_idx[(size_t)n * a.top_k + r] = r < a.count ? (uint32_t)r : 0xFFFFFFFFu;
+          a.out_idx[(size_t)n * a.top_k + r] = r < cnt ? (uint32_t)r : 0xFFFFFFFFu;
     }
     wave_sync();
   }
@@ -255,7 +256,7 @@ __device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
 
 __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs a) {
   extern __shared__ float smem[];
-  const int cap = a.capacity, dk = a.dk, cnt = a.count;
+  const int cap = a.capacity, dk = a.dk, cnt = a.count_dev ? a.count_dev[0] : a.count;
   float* keyT = smem;                                                  // [dk][cap]
   double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]
   double* pq = rk + cap;                                               // [waves][SOFT_MAX_DK]
@@ -282,6 +283,7 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
     const double r = sqrt(r2);
     const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
     const float pv = (float)((double)qv * scale);
+    if (a.q_pnc && lane < dk) a.q_pnc[(size_t)n * dk + lane] = pv;
     wave_sync();
     p[lane] = (double)pv;
     wave_sync();
@@ -345,10 +347,33 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
 }
 
 static bool soft_read_fits(const RetrieveArgs& a) {
-  return (a.top_k == 0 || a.top_k >= a.count) && a.project && !a.q_pnc && !a.q_norm && !a.out_val &&
+  return (a.top_k == 0 || (!a.count_dev && a.top_k >= a.count)) && a.project && !a.q_norm && !a.out_val &&
          !a.out_min && !a.out_idx && a.dk <= SOFT_MAX_DK && a.capacity <= 64 * SOFT_SPL &&
          (long)a.dk * a.capacity <= SOFT_MAX_KEYS;
 }
+
+// Raises the kernel's dynamic-LDS limit to the device maximum once per
+// device, before any launch that could be captured into a graph.
+static Status allow_large_lds() {
+  static std::mutex mu;
+  static bool done[64] = {};
+  int dev = 0;
+  PSSA_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> g(mu);
+  if (dev >= 0 && dev < 64 && done[dev]) return Status::Ok();
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&soft_read_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  if (dev >= 0 && dev < 64) done[dev] = true;
+  return Status::Ok();
+}
+
+Status init_retrieve_attributes() { return allow_large_lds(); }
+
+Status prepare_retrieve(const RetrieveArgs& a) {
+  if (soft_read_fits(a)) return allow_large_lds();
+  return Status::Ok();
+}
+
 
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.n <= 0) return Status::Ok();
@@ -359,11 +384,7 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (soft_read_fits(a)) {
     const size_t lds = (((size_t)a.dk * a.capacity + 1) & ~(size_t)1) * sizeof(float) +
                        ((size_t)a.capacity + (size_t)SOFT_WAVES * SOFT_MAX_DK) * sizeof(double);
-    if (lds > 64 * 1024) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&soft_read_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return Status::Device(std::string("soft_read LDS attribute: ") + hipGetErrorString(e));
-    }
+    if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     int blocks = (a.n + SOFT_WAVES - 1) / SOFT_WAVES;
     if (blocks > 512) blocks = 512;
     soft_read_kernel<<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);

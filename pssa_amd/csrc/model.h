@@ -12,7 +12,9 @@ struct DevBlock {
   DevBuf w_proj;   // [d, d]
   DevBuf mlp_w1;   // [2d, d]
   DevBuf mlp_w2;   // [d, 2d]
-  DevBuf u_eff;    // [d, r] f32: adapter up + consolidated (refresh_adapter_up_effective)
+  DevBuf u_eff;    // [d, r] weight dtype: adapter fast + consolidated weights (the GEMM operand)
+  DevBuf u_fast;   // [d, r] f32: adapters[0].up_proj, updated by plastic decode
+  DevBuf u_slow;   // [d, r] f32: adapters[0].consolidated_up
   DevBuf gamma;    // [d] f32
   DevBuf beta;     // [d] f32
   DevBuf rates2;   // [d*s] f32: -softplus(a_raw) * log2(e)
@@ -20,7 +22,9 @@ struct DevBlock {
   DevBuf norm_sq;  // [C] f32
   DevBuf values;   // [C, d] f32 (top-k readout)
   DevBuf values_t; // [d, C] weight dtype (soft-read readout GEMM operand)
-  size_t count = 0;
+  DevBuf conf;     // [C] f32 memory.confidence
+  DevBuf last_seen;  // [C] u64 memory.last_seen_step
+  DevBuf meta;     // int32 [2]: memory.count, memory.write_head
 };
 
 // Stage ids used for per-kernel timing.
@@ -51,6 +55,7 @@ struct pssa_hip_model {
   pssa::DevBuf embed;    // [V, d] f32 (row gather)
   pssa::DevBuf unembed;  // [V, d] weight dtype
   std::vector<pssa::DevBlock> blocks;
+  pssa::DevBuf step;     // u64: step counter read by the refractory gate in plastic decode
 };
 
 struct pssa_hip_lanes {
@@ -67,6 +72,17 @@ struct pssa_hip_lanes {
   // H1 MLP hidden [n,2d].
   pssa::DevBuf X, XN, XNh, P, Y, Yh, Q, Wm, Mval, Zraw, Zrawh, H1, logits;
   pssa::DevBuf Ypart;  // SSM partial readouts when d_state needs more than two state blocks
+  // Decode state (allocated on the first decode call): per-block taps of the
+  // last step [depth, lanes, *], the surprise of each lane's greedy choice,
+  // 1/(1+|z_final|) rates, the generated ids [gen_cap, lanes] and the
+  // generation position.
+  pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
+  size_t dec_lanes = 0, gen_cap = 0;
+  // Captured decode step (one per lane count and plasticity setting).
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  size_t graph_lanes = 0;
+  int graph_plastic = -1;
   size_t staged_lanes = 0, staged_len = 0;
   bool timing = false;
   std::array<float, pssa::ST_COUNT> stage_ms{};
@@ -75,14 +91,28 @@ struct pssa_hip_lanes {
   std::vector<int> event_stage;
   ~pssa_hip_lanes() {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
+    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+    if (graph) (void)hipGraphDestroy(graph);
   }
 };
 
 namespace pssa {
 // Runs prefill for `n_lanes` lanes of `T` tokens whose ids are already in
 // lanes->ids (row-major [n_lanes, T]); last-token logits land in lanes->logits.
-Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T);
+// With `taps` set (single-token decode) every block also records its
+// projected query, adapter output, z_final and adapter activations into the
+// lanes' tap buffers.
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps = false);
+// One greedy decode step for n_lanes lanes (ids in lanes->ids, replaced by
+// the chosen ids); plastic adds the lane-ordered protected bank writes and
+// the Hebbian adapter update.  Only kernel launches: safe to capture.
+Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic);
+// Greedy choice from lanes->logits without a forward step (first decode
+// token after a prefill).
+Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes);
 Status launch_fill_zero(hipStream_t stream, float* p, size_t n);
+Status launch_copy_cols(hipStream_t stream, const float* in, int ld_in, float* out, int ld_out,
+                        size_t rows, int cols);
 Status launch_mul(hipStream_t stream, const float* a, const float* b, float* out, size_t n);
 Status launch_softplus(hipStream_t stream, float* p, size_t n);
 Status launch_sigmoid(hipStream_t stream, float* p, size_t n);

@@ -90,6 +90,24 @@ __global__ void check_ids_kernel(const uint32_t* __restrict__ ids, size_t n, uin
   if (i < n && ids[i] >= vocab) atomicOr(bad, 1);
 }
 
+__global__ void copy_cols_kernel(const float* __restrict__ in, int ld_in, float* __restrict__ out,
+                                 int ld_out, size_t rows, int cols) {
+  const size_t n = rows * (size_t)cols;
+  for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x)
+    out[(e / cols) * ld_out + e % cols] = in[(e / cols) * ld_in + e % cols];
+}
+
+Status launch_copy_cols(hipStream_t stream, const float* in, int ld_in, float* out, int ld_out,
+                        size_t rows, int cols) {
+  const size_t n = rows * (size_t)cols;
+  if (!n) return Status::Ok();
+  size_t g = (n + 255) / 256;
+  if (g > 4096) g = 4096;
+  copy_cols_kernel<<<(unsigned)g, 256, 0, stream>>>(in, ld_in, out, ld_out, rows, cols);
+  PSSA_LAUNCH_CHECK("copy_cols");
+  return Status::Ok();
+}
+
 static unsigned grid1d(size_t n, unsigned cap = 65535u * 4) {
   size_t g = (n + 255) / 256;
   if (g == 0) g = 1;
@@ -168,7 +186,7 @@ struct Timer {
 
 }  // namespace
 
-Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   const pssa_hip_model* M = L->model;
   const pssa_hip_config& c = M->cfg;
   const hipStream_t st = L->ctx->stream;
@@ -224,6 +242,8 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_in.out32 = P;
     e_in.ld32 = n_in;
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
+    if (taps)
+      PSSA_RETURN_IF(launch_copy_cols(st, P + o_act, n_in, L->tap_act.as<float>() + l * rows * r, r, rows, r));
 
     PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
     if (ssm_needs_zeroed_y(s)) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
@@ -272,8 +292,10 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     ra.dk = k;
     ra.dv = d;
     ra.capacity = C;
-    ra.count = (int)B.count;
+    ra.count = C;  // upper bound; the live count is read on the device
+    ra.count_dev = B.meta.as<int>();
     ra.tau = c.tau_mem;
+    if (taps) ra.q_pnc = L->tap_q.as<float>() + l * rows * k;
     if (bf16)
       ra.weights16 = static_cast<uint16_t*>(Wm);
     else
@@ -282,13 +304,13 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
 
     // m_val = weights values (soft read readout).
     PSSA_RETURN_IF(tm.mark(ST_GEMM_READ));
-    if (B.count > 0) {
+    {
+      // Slots past the live count carry zero weight, so the product runs
+      // over the whole capacity.
       EpiParams e_m;
       e_m.out16 = Mv;
       e_m.ld16 = d;
-      PSSA_RETURN_IF(launch_gemm(st, dt, Wm, C, B.values_t.p, C, m, d, (int)B.count, e_m));
-    } else {
-      PSSA_RETURN_IF(launch_fill_zero(st, static_cast<float*>(Mv), (rows * d * (bf16 ? 2 : 4) + 3) / 4));
+      PSSA_RETURN_IF(launch_gemm(st, dt, Wm, C, B.values_t.p, C, m, d, C, e_m));
     }
 
     // z_raw = y/sqrt(s) + gate * (m_val W_proj^T) + U_eff act.
@@ -306,6 +328,10 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_z.scale = ssm_scale;
     e_z.out32 = Zr;
     e_z.ld32 = d;
+    if (taps) {
+      e_z.tap = L->tap_a.as<float>() + l * rows * d;
+      e_z.ld_tap = d;
+    }
     if (bf16) {
       e_z.out16 = Zrh;
       e_z.ld16 = d;
@@ -330,6 +356,10 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T) {
     e_r.scale = depth_scale;
     e_r.out32 = X;
     e_r.ld32 = d;
+    if (taps) {
+      e_r.tap = L->tap_z.as<float>() + l * rows * d;
+      e_r.ld_tap = d;
+    }
     PSSA_RETURN_IF(launch_gemm(st, dt, H1, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r));
   }
 

@@ -19,11 +19,13 @@
 namespace pssa {
 
 // ---------------------------------------------------------------------------
-// Materialising variant (stage API): also writes bar_a, bar_b and every
-// state h_t.  Used for small diagnostic shapes only.
+// Unpipelined variant: with MAT it also writes bar_a, bar_b and every state
+// h_t (stage API, small diagnostic shapes); without MAT it serves sequences
+// shorter than one pipelined chunk (single-token decode), where it runs
+// exactly T steps.
 constexpr int MAT_TC = 16;
 
-template <int J>
+template <int J, bool MAT>
 __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
   __shared__ float sD[MAT_TC][64];
   __shared__ float sX[MAT_TC][64];
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
     h[q] = ok ? carry[(size_t)i * s + j] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)i * s + j] : 0.0f;
   }
-  if (blockIdx.z == 0 && wave == 0 && ivalid)
+  if (MAT && blockIdx.z == 0 && wave == 0 && ivalid)
     for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[(size_t)i * s + j];
 
   for (int t0 = 0; t0 < T; t0 += MAT_TC) {
@@ -76,15 +78,18 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
     for (int tt = 0; tt < steps; ++tt) {
       const float dl = sD[tt][lane];
       const float u = dl * sX[tt][lane];
-      float yp = 0.0f;
+      // Readout as four partial sums over states j = p (mod 4), combined as
+      // (p0 + p1) + (p2 + p3): the production scan's order, so that a run of
+      // single-token steps equals one prefill bit for bit.
+      float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int q = 0; q < J; ++q) {
         const float bq = sB[tt][wave * J + q];
         const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
         h[q] = fmaf(ab, h[q], u * bq);
-        yp = fmaf(h[q], sC[tt][wave * J + q], yp);
+        yp4[q & 3] = fmaf(h[q], sC[tt][wave * J + q], yp4[q & 3]);
         const int j = jw + q;
-        if (ivalid && j < s) {
+        if (MAT && ivalid && j < s) {
           const size_t c = (size_t)i * s + j;
           const size_t base = (size_t)b * T * ds + (size_t)(t0 + tt) * ds;
           a.bar_a[base + c] = ab;
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
           a.states[(size_t)b * (T + 1) * ds + (size_t)(t0 + tt + 1) * ds + c] = h[q];
         }
       }
-      sY[wave][tt][lane] = yp;
+      sY[wave][tt][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }
     __syncthreads();
     for (int e = tid; e < steps * 64; e += 256) {
@@ -100,11 +105,13 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
       const int gi = i0 + ii;
       if (gi < d) {
         const float v = ((sY[0][tt][ii] + sY[1][tt][ii]) + sY[2][tt][ii]) + sY[3][tt][ii];
-        float* dst = a.y + (row0 + t0 + tt) * a.ld_y + gi;
-        if (gridDim.z > 1)
-          atomicAdd(dst, v);
+        const size_t r = row0 + t0 + tt;
+        if (!MAT && a.y_part)
+          a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + gi] = v;
+        else if (gridDim.z > 1)
+          atomicAdd(a.y + r * a.ld_y + gi, v);
         else
-          *dst = v;
+          a.y[r * a.ld_y + gi] = v;
       }
     }
     __syncthreads();
@@ -274,7 +281,9 @@ template <int J>
 static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   dim3 grid((a.d + 63) / 64, a.lanes, (a.s + 4 * J - 1) / (4 * J));
   if (mat)
-    ssm_materialize_kernel<J><<<grid, 256, 0, stream>>>(a);
+    ssm_materialize_kernel<J, true><<<grid, 256, 0, stream>>>(a);
+  else if (a.T < SSM_TC)
+    ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);
   else
     ssm_scan_kernel<J><<<grid, 256, 0, stream>>>(a);
 }

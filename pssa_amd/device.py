@@ -209,6 +209,7 @@ class PSSALayer:
         logits = np.empty((n_lanes, self.cfg.d_vocab), np.float32) if want_logits else None
         _abi.call(self._lib.pssa_hip_prefill, self.handle, _abi.ptr(ids, C.c_uint32), n_lanes, T,
                   _abi.ptr(logits), 0 if logits is None else logits.size)
+        self._staged = (n_lanes, T)
         return logits
 
     def forward_inference(self, ids):
@@ -218,6 +219,49 @@ class PSSALayer:
         _abi.call(self._lib.pssa_hip_forward_inference, self.handle, _abi.ptr(ids, C.c_uint32), ids.size,
                   _abi.ptr(logits), logits.size)
         return logits
+
+    # -- greedy decode (forward_inference + sample, src/pssa.rs:2387-2391,
+    #    src/inference.rs:123-127) ------------------------------------------
+    def decode(self, steps: int, first_ids=None, n_lanes: int | None = None, plastic: bool = False,
+               graph: bool = False, want_logits: bool = False):
+        """Generates `steps` greedy tokens on lanes 0..n_lanes-1.  first_ids=None
+        continues from the last prefill's logits.  Returns ids [steps, n_lanes]
+        (and the last step's logits [n_lanes, V] when want_logits)."""
+        if first_ids is not None:
+            first = np.ascontiguousarray(np.atleast_1d(np.asarray(first_ids)), dtype=np.uint32)
+            n_lanes = first.size
+            fp_ = _abi.ptr(first, C.c_uint32)
+        else:
+            if n_lanes is None:
+                n_lanes = self._staged[0] if getattr(self, "_staged", None) else self.lanes
+            fp_ = None
+        out = np.empty((steps, n_lanes), np.uint32)
+        logits = np.empty((n_lanes, self.cfg.d_vocab), np.float32) if want_logits else None
+        flags = (_abi.DECODE_PLASTIC if plastic else 0) | (_abi.DECODE_GRAPH if graph else 0)
+        _abi.call(self._lib.pssa_hip_decode, self.handle, fp_, n_lanes, steps, flags,
+                  _abi.ptr(out, C.c_uint32), out.size, _abi.ptr(logits), 0 if logits is None else logits.size)
+        self._staged = (n_lanes, 1)
+        return (out, logits) if want_logits else out
+
+    def get_plastic(self, layer: int) -> dict:
+        """One block's adapter fast weights and bank state as held on the device."""
+        c = self.cfg
+        d, k, C_, r = c.d_latent, c.d_mem_key, c.mem_capacity, c.adapter_rank
+        out = {
+            "adapter_up": np.empty((d, r), np.float32),
+            "mem_keys": np.empty((C_, k), np.float32),
+            "mem_values": np.empty((C_, d), np.float32),
+            "mem_norm_sq": np.empty(C_, np.float32),
+            "mem_confidence": np.empty(C_, np.float32),
+            "mem_last_seen": np.empty(C_, np.uint64),
+        }
+        cnt, head, step = C.c_uint64(), C.c_uint64(), C.c_uint64()
+        _abi.call(self._lib.pssa_hip_model_get_plastic, self.model, layer, _abi.ptr(out["adapter_up"]),
+                  _abi.ptr(out["mem_keys"]), _abi.ptr(out["mem_values"]), _abi.ptr(out["mem_norm_sq"]),
+                  _abi.ptr(out["mem_confidence"]), _abi.ptr(out["mem_last_seen"], C.c_uint64),
+                  C.byref(cnt), C.byref(head), C.byref(step))
+        out.update(mem_count=int(cnt.value), mem_write_head=int(head.value), step=int(step.value))
+        return out
 
     # -- device-resident measurement path ------------------------------------
     def stage_ids(self, token_ids) -> None:

@@ -1,0 +1,157 @@
+"""Greedy decode on the GPU through the C ABI against the CPU oracle.
+
+Plain decode is the reference's forward_inference + sample() at temperature 0
+(src/pssa.rs:2387-2391, src/inference.rs:123-127): generated ids must equal
+the oracle's, logits and carries within 1e-4 (fp32 weights).  Plastic decode
+adds the lane-ordered protected bank writes and Hebbian adapter updates
+(oracle_decode); the bank counters, ages and written slots must match, the
+fast weights within 1e-4.  Graph replay must equal eager stepping bit for bit.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from oracle import oracle as O
+from pssa_amd import ModelWeights, PSSAConfig, PSSALayer
+from pssa_amd._abi import HipError
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def small_model(seed=5, full_banks=True, depth=2):
+    cfg = PSSAConfig(depth=depth, d_vocab=97, d_latent=48, d_state=32, d_mem_key=8, mem_capacity=24)
+    w = ModelWeights.init(cfg, seed, "baseline")
+    w.populate_banks(seed + 1, count=cfg.mem_capacity if full_banks else 10)
+    return w
+
+
+def prefill_both(w, lanes, T, seed=0):
+    ids = np.random.default_rng(seed).integers(0, w.cfg.d_vocab, (lanes, T), dtype=np.uint32)
+    om = O.OracleModel(w)
+    st = om.zero_state(lanes)
+    lg = om.prefill_lanes(st, ids, threads=lanes)
+    return ids, st, lg
+
+
+def test_decode_matches_oracle_forward_loop(hip):
+    say("decode plain vs oracle")
+    w = small_model()
+    ids, st, lg = prefill_both(w, 3, 9)
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=64)
+    layer.prefill_inference(ids)
+    first = [O.greedy(lg[i]) for i in range(3)]
+    got, glog = layer.decode(6, want_logits=True)  # continues from the prefill logits
+    ref_w = ModelWeights.init(w.cfg, 5, "baseline")
+    ref_w.populate_banks(6, count=w.cfg.mem_capacity)
+    ref_ids, ref_lg, _ = O.OracleModel(ref_w).decode(st, first, steps=6)
+    np.testing.assert_array_equal(got, ref_ids)
+    assert rel_err(glog, ref_lg) < 1e-4
+    assert rel_err(layer.get_carry(), st) < 1e-4
+    layer.close()
+
+
+def test_decode_graph_replay_equals_eager(hip):
+    """Two lane sets from the same state: eager steps vs a captured step
+    replayed, with eager work on the same stream between the replays."""
+    say("decode graph == eager")
+    w = small_model(seed=8)
+    ids = np.random.default_rng(3).integers(0, w.cfg.d_vocab, (4, 7), dtype=np.uint32)
+    res = []
+    for graph in (False, True):
+        layer = PSSALayer(hip, w, lanes=4, max_tokens=64)
+        layer.prefill_inference(ids)
+        a = layer.decode(3, graph=graph)
+        layer.get_carry()  # eager traffic between replays
+        b, lg = layer.decode(5, first_ids=a[-1], graph=graph, want_logits=True)
+        res.append((a, b, lg, layer.get_carry()))
+        layer.close()
+    for x, y in zip(*res):
+        np.testing.assert_array_equal(x, y)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_plastic_decode_matches_oracle(hip, graph):
+    say("plastic decode vs oracle, graph", graph)
+    lanes, steps = 3, 4
+    w = small_model(seed=11)
+    for b in w.blocks:
+        b.adapter_up[:] = (np.random.default_rng(2).standard_normal(b.adapter_up.shape) * 0.05).astype(np.float32)
+    ids, st, lg = prefill_both(w, lanes, 6, seed=4)
+    layer = PSSALayer(hip, w, lanes=lanes, max_tokens=64)
+    layer.prefill_inference(ids)
+    first = [O.greedy(lg[i]) for i in range(lanes)]
+    got, glog = layer.decode(steps, first_ids=first, plastic=True, graph=graph, want_logits=True)
+    ref = ModelWeights.init(w.cfg, 11, "baseline")
+    ref.populate_banks(12, count=w.cfg.mem_capacity)
+    for b, b0 in zip(ref.blocks, w.blocks):
+        b.adapter_up[:] = b0.adapter_up
+    ref_ids, ref_lg, ref_sp = O.OracleModel(ref).decode(st, first, steps=steps, plastic=True)
+    np.testing.assert_array_equal(got, ref_ids)
+    assert rel_err(glog, ref_lg) < 1e-4
+    assert np.all(ref_sp > 3.5)  # every lane writes (small random model: flat logits)
+    for l in range(w.cfg.depth):
+        dev = layer.get_plastic(l)
+        rb = ref.blocks[l]
+        assert dev["mem_count"] == rb.mem_count and dev["mem_write_head"] == rb.mem_write_head
+        np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
+        assert dev["step"] == steps
+        np.testing.assert_allclose(dev["mem_confidence"], rb.mem_confidence, rtol=1e-5, atol=1e-6)
+        assert rel_err(dev["mem_keys"], rb.mem_keys) < 1e-4
+        assert rel_err(dev["mem_values"], rb.mem_values) < 1e-4
+        assert rel_err(dev["mem_norm_sq"], rb.mem_norm_sq) < 1e-4
+        assert rel_err(dev["adapter_up"], rb.adapter_up) < 1e-4
+        assert not np.array_equal(dev["adapter_up"], w.blocks[l].adapter_up)
+    layer.close()
+
+
+def test_plastic_decode_fills_free_slots_first(hip):
+    """A bank with free slots takes plain inserts at `count` before any
+    protected overwrite (insert_protected, src/memory.rs:318-322)."""
+    say("plastic decode free slots")
+    w = small_model(seed=13, full_banks=False, depth=1)
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    layer.prefill_inference([[1, 2, 3], [4, 5, 6]])
+    layer.decode(3, plastic=True)
+    dev = layer.get_plastic(0)
+    assert dev["mem_count"] == 10 + 6 and dev["mem_write_head"] == 0
+    assert set(dev["mem_last_seen"][10:16].tolist()) == {1, 2, 3}
+    assert np.all(dev["mem_confidence"][10:16] == 1.0)
+    assert np.all(dev["mem_norm_sq"][10:16] < 1.0)
+    layer.close()
+
+
+def test_decode_rejects_bad_arguments(hip):
+    say("decode validation")
+    w = small_model(seed=1, depth=1)
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    with pytest.raises(HipError, match="outside model vocabulary"):
+        layer.decode(2, first_ids=[1, 97])
+    with pytest.raises(HipError, match="n_lanes"):
+        layer.decode(2, first_ids=[1, 2, 3])
+    with pytest.raises(HipError, match="last prefill"):
+        layer.decode(2, n_lanes=1)
+    layer.close()
+
+
+def test_decode_at_105m_width_graph_equals_eager(hip):
+    """The config-5 model width (d=768, s=256, k=32, C=512, V=16384, bf16) on
+    8 lanes x 2 layers: plastic graph replay equals plastic eager steps."""
+    say("decode 105M width")
+    cfg = PSSAConfig(depth=2, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    ids = np.random.default_rng(9).integers(0, cfg.d_vocab, (8, 16), dtype=np.uint32)
+    outs = []
+    for graph in (False, True):
+        layer = PSSALayer(hip, w, lanes=8, max_tokens=128, weight_dtype="bf16")
+        layer.prefill_inference(ids)
+        g, lg = layer.decode(4, plastic=True, graph=graph, want_logits=True)
+        outs.append((g, lg, layer.get_carry(), layer.get_plastic(1)["adapter_up"]))
+        layer.close()
+    for x, y in zip(*outs):
+        np.testing.assert_array_equal(x, y)
+    assert np.all(np.isfinite(outs[0][1]))

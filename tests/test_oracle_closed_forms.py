@@ -324,3 +324,90 @@ def test_product_baseline_init_matches_oracle():
             np.testing.assert_array_equal(getattr(bp, name), getattr(bo, name), err_msg=name)
         assert bp.mem_count == bo.mem_count == 5
     assert np.all(p.blocks[0].mem_norm_sq[:5] < 0.9 ** 2)
+
+
+def test_greedy_follows_total_order_and_lower_id_ties():
+    """sample() at temperature 0 (src/inference.rs:123-127): id 0 never wins,
+    equal logits go to the lower id, and +0.0 ranks above -0.0 (total_cmp)."""
+    assert O.greedy(np.float32([9.0, 1.0, 3.0, 3.0, 2.0])) == 2
+    assert O.greedy(np.float32([0.0, -1.0, -0.0, 0.0, -0.5])) == 3
+    assert O.greedy(np.float32([5.0, -2.0])) == 1
+    rng = np.random.default_rng(5)
+    for _ in range(50):
+        lg = rng.integers(-3, 3, 40).astype(np.float32)
+        best = max(range(1, 40), key=lambda i: (lg[i], -i))
+        assert O.greedy(lg) == best
+
+
+def test_oracle_decode_without_plasticity_is_the_forward_inference_loop():
+    cfg = PSSAConfig(depth=2, d_vocab=60, d_latent=16, d_state=8, d_mem_key=4, mem_capacity=12)
+    w = ModelWeights.init(cfg, 4, "baseline")
+    w.populate_banks(3, 10)
+    om = O.OracleModel(w)
+    states = om.zero_state(3)
+    om.prefill_lanes(states, np.array([[1, 2, 3], [4, 5, 6], [7, 8, 9]], np.uint32), logits=False)
+    ref_states = states.copy()
+    ids, lg, _ = om.decode(states, [10, 11, 12], steps=4)
+    for lane, first in enumerate([10, 11, 12]):
+        st = ref_states[lane].copy()
+        tok = first
+        for step in range(4):
+            logits = om.forward_inference(st, tok)
+            tok = O.greedy(logits)
+            assert tok == ids[step, lane]
+        np.testing.assert_array_equal(st, states[lane])
+        np.testing.assert_array_equal(logits, lg[lane])
+
+
+def test_oracle_decode_plastic_steps_equal_the_composed_primitives():
+    """Each plastic step equals: forward every lane, greedy, then per block and
+    in lane order insert_protected(q_poincare, z_final, surprise, step) when the
+    surprise exceeds 3.5, then the Hebbian rule with z_final as the target.
+    Restated here from the separately pinned primitives and compared bit for bit."""
+    import ctypes as C
+
+    cfg = PSSAConfig(depth=2, d_vocab=40, d_latent=8, d_state=4, d_mem_key=3, mem_capacity=3)
+    w, w2 = (ModelWeights.init(cfg, 9, "baseline") for _ in range(2))
+    for m in (w, w2):
+        m.populate_banks(2, 3)
+        for b in m.blocks:
+            b.adapter_up[:] = np.float32(0.01) * np.arange(b.adapter_up.size, dtype=np.float32).reshape(b.adapter_up.shape)
+    om, om2 = O.OracleModel(w), O.OracleModel(w2)
+    states = om.zero_state(3)
+    first = [5, 6, 7]
+    steps = 3
+    ids, lg, sp = om.decode(states, first, steps=steps, plastic=True, step_base=100)
+    st2 = om2.zero_state(3)
+    blocks = [C.cast(C.pointer(om2.keep[l]), C.c_void_p) for l in range(cfg.depth)]
+    toks = list(first)
+    for step in range(steps):
+        taps, nxt, surprise = [], [], []
+        for lane in range(3):
+            q, z, a, act, logits = om2.forward_taps(st2[lane], toks[lane])
+            n = O.greedy(logits)
+            mx = np.float32(np.max(logits))
+            sm = np.float32(0)
+            for v in logits:
+                sm = np.float32(sm + np.float32(np.exp(np.float32(v - mx))))
+            surprise.append(np.float32(np.float32(mx + np.float32(np.log(sm))) - logits[n]))
+            taps.append((q, z, a, act))
+            nxt.append(n)
+        assert nxt == list(ids[step])
+        for l in range(cfg.depth):
+            for lane in range(3):
+                if surprise[lane] > 3.5:
+                    q, z = taps[lane][0][l], taps[lane][1][l]
+                    O.lib().oracle_bank_insert_protected(blocks[l], cfg.mem_capacity, cfg.d_mem_key, cfg.d_latent,
+                                                         O.ptr(q), O.ptr(z), float(surprise[lane]), 101 + step)
+            for lane in range(3):
+                q, z, a, act = (t[l] for t in taps[lane])
+                O.lib().oracle_hebbian_update(O.ptr(w2.blocks[l].adapter_up), O.ptr(z), O.ptr(a), O.ptr(act),
+                                              cfg.d_latent, cfg.adapter_rank)
+        toks = nxt
+    om2.sync()
+    for b, b2 in zip(w.blocks, w2.blocks):
+        for name in ("adapter_up", "mem_keys", "mem_values", "mem_norm_sq", "mem_confidence", "mem_last_seen"):
+            np.testing.assert_array_equal(getattr(b, name), getattr(b2, name), err_msg=name)
+        assert b.mem_write_head == b2.mem_write_head and b.mem_count == b2.mem_count
+    np.testing.assert_array_equal(states, st2)
+    assert w.blocks[0].mem_last_seen.max() >= 101  # the gate saw the protected writes

@@ -123,6 +123,16 @@ int pssa_hip_device_name(const pssa_hip_ctx* ctx, char* out, size_t out_len);
 int pssa_hip_is_fatal(int code);
 int pssa_hip_synchronize(pssa_hip_ctx* ctx, char* err, size_t err_len);
 
+/* Device buffers for the *_resident entry points, for callers without a HIP
+ * allocator of their own.  Copies are synchronous on the context stream. */
+#define PSSA_HIP_H2D 0
+#define PSSA_HIP_D2H 1
+#define PSSA_HIP_D2D 2
+int pssa_hip_device_alloc(pssa_hip_ctx* ctx, size_t bytes, void** out, char* err, size_t err_len);
+void pssa_hip_device_free(pssa_hip_ctx* ctx, void* ptr);
+int pssa_hip_memcpy(pssa_hip_ctx* ctx, void* dst, const void* src, size_t bytes, int kind, char* err,
+                    size_t err_len);
+
 /* ------------------------------------------------- host-side weight set-up
  * These run on the host only (no device needed). */
 
@@ -196,6 +206,14 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
                       size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
                       float* out_min, uint32_t* out_idx, float* out_weights, char* err,
                       size_t err_len);
+
+/* pssa_hip_retrieve on device-resident buffers (plain device pointers from
+ * any allocator); asynchronous on the context stream. */
+int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q,
+                               const float* d_keys, const float* d_norm_sq, const float* d_values,
+                               size_t capacity, size_t count, size_t d_key, size_t d_val, float tau,
+                               size_t top_k, float* d_out_val, float* d_out_min,
+                               uint32_t* d_out_idx, char* err, size_t err_len);
 
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t (no reference counterpart:
  * the reference's SSM is diagonal; this is the standalone dense kernel).

@@ -22,6 +22,7 @@ F32 = 0
 BF16 = 1
 INIT_REFERENCE = 0
 INIT_BASELINE = 1
+H2D, D2H, D2D = 0, 1, 2
 DECODE_PLASTIC = 1
 DECODE_GRAPH = 2
 
@@ -100,6 +101,9 @@ def lib() -> C.CDLL:
         "pssa_hip_device_name": ([vp, err_t, sz], C.c_int),
         "pssa_hip_is_fatal": ([C.c_int], C.c_int),
         "pssa_hip_synchronize": ([vp, err_t, sz], C.c_int),
+        "pssa_hip_device_alloc": ([vp, sz, pp, err_t, sz], C.c_int),
+        "pssa_hip_device_free": ([vp, vp], None),
+        "pssa_hip_memcpy": ([vp, vp, vp, sz, C.c_int, err_t, sz], C.c_int),
         "pssa_hip_weights_init": ([C.POINTER(Weights), C.c_uint64, C.c_int, u64p, err_t, sz], C.c_int),
         "pssa_hip_weights_populate_banks": ([C.POINTER(Weights), C.c_uint64, C.c_uint64, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_gemm_xwt": ([vp, fp, sz, vp, sz, C.c_int, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
@@ -110,6 +114,8 @@ def lib() -> C.CDLL:
                                      C.c_float, sz, fp, fp, fp, fp, fp, fp, fp, fp, err_t, sz], C.c_int),
         "pssa_hip_retrieve": ([vp, fp, sz, fp, fp, fp, sz, sz, sz, sz, C.c_float, sz, fp, fp, u32p, fp,
                                err_t, sz], C.c_int),
+        "pssa_hip_retrieve_resident": ([vp, vp, sz, vp, vp, vp, sz, sz, sz, sz, C.c_float, sz, vp, vp, vp,
+                                        err_t, sz], C.c_int),
         "pssa_hip_dense_scan": ([vp, fp, fp, fp, sz, sz, sz, fp, err_t, sz], C.c_int),
         "pssa_hip_dense_scan_resident": ([vp, vp, vp, vp, sz, sz, sz, vp, err_t, sz], C.c_int),
         "pssa_hip_model_load": ([vp, C.POINTER(Weights), C.c_int, pp, err_t, sz], C.c_int),

@@ -116,6 +116,7 @@ int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
     ctx->cu_count = prop.multiProcessorCount;
     PSSA_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     PSSA_RETURN_IF(pssa::init_retrieve_attributes());
+    PSSA_RETURN_IF(pssa::init_decode_attributes());
     *out = ctx.release();
     return Status::Ok();
   };
@@ -136,6 +137,52 @@ int pssa_hip_device_name(const pssa_hip_ctx* ctx, char* out, size_t out_len) {
   if (!ctx || !out || !out_len) return PSSA_HIP_EINVAL;
   std::snprintf(out, out_len, "hip:%s (gfx950, %d CUs)", ctx->name.c_str(), ctx->cu_count);
   return PSSA_HIP_OK;
+}
+
+int pssa_hip_device_alloc(pssa_hip_ctx* ctx, size_t bytes, void** out, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(out != nullptr, "null output handle"));
+    *out = nullptr;
+    PSSA_RETURN_IF(need(bytes > 0 && bytes <= ((size_t)1 << 40), "allocation size must be in 1..=2^40"));
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return Status::NoMem(std::string("hipMalloc: ") + hipGetErrorString(e));
+    }
+    *out = p;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+void pssa_hip_device_free(pssa_hip_ctx* ctx, void* p) {
+  if (!ctx || !p) return;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  (void)hipFree(p);
+}
+
+int pssa_hip_memcpy(pssa_hip_ctx* ctx, void* dst, const void* src, size_t bytes, int kind, char* err,
+                    size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(dst && src, "memcpy: null pointer"));
+    PSSA_RETURN_IF(need(kind == PSSA_HIP_H2D || kind == PSSA_HIP_D2H || kind == PSSA_HIP_D2D, "memcpy: unknown kind"));
+    if (bytes == 0) return Status::Ok();
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    const hipMemcpyKind k = kind == PSSA_HIP_H2D ? hipMemcpyHostToDevice
+                            : kind == PSSA_HIP_D2H ? hipMemcpyDeviceToHost
+                                                   : hipMemcpyDeviceToDevice;
+    PSSA_HIP_TRY(hipMemcpyAsync(dst, src, bytes, k, ctx->stream));
+    return sync(ctx);
+  };
+  return pssa::finish(body(), err, err_len);
 }
 
 int pssa_hip_synchronize(pssa_hip_ctx* ctx, char* err, size_t err_len) {
@@ -459,6 +506,45 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
   return pssa::finish(body(), err, err_len);
 }
 
+int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
+                               const float* d_norm_sq, const float* d_values, size_t capacity,
+                               size_t count, size_t d_key, size_t d_val, float tau, size_t top_k,
+                               float* d_out_val, float* d_out_min, uint32_t* d_out_idx,
+                               char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(n_q && d_key && d_val && capacity, "retrieve: dimensions must be positive"));
+    PSSA_RETURN_IF(need(count <= capacity, "retrieve: count exceeds capacity"));
+    PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "retrieve: top_k must be at most 64"));
+    PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
+    PSSA_RETURN_IF(need(d_q_pnc && d_keys && d_norm_sq && d_values && d_out_val, "retrieve: null buffer"));
+    PSSA_RETURN_IF(need(!d_out_idx || top_k > 0, "retrieve: indices need top_k > 0"));
+    if (n_q > INT32_MAX / 4 || d_key > 4096 || d_val > 65536 || capacity > 8192)
+      return Status::Invalid("retrieve: shape exceeds the supported range");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    pssa::RetrieveArgs ra;
+    ra.q = d_q_pnc;
+    ra.ld_q = (int)d_key;
+    ra.project = 0;
+    ra.keys = d_keys;
+    ra.norm_sq = d_norm_sq;
+    ra.values = d_values;
+    ra.n = (int)n_q;
+    ra.dk = (int)d_key;
+    ra.dv = (int)d_val;
+    ra.capacity = (int)capacity;
+    ra.count = (int)count;
+    ra.tau = tau;
+    ra.top_k = (int)top_k;
+    ra.out_val = d_out_val;
+    ra.out_min = d_out_min;
+    ra.out_idx = d_out_idx;
+    return pssa::launch_retrieve(ctx->stream, ra);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 // ------------------------------------------------------------------ model
 int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight_dtype,
                         pssa_hip_model** out, char* err, size_t err_len) {
@@ -771,7 +857,7 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
     PSSA_RETURN_IF(L->tap_a.alloc(D * n * c.d_latent * 4));
     PSSA_RETURN_IF(L->tap_act.alloc(D * n * c.adapter_rank * 4));
     PSSA_RETURN_IF(L->surprise.alloc(n * 4));
-    PSSA_RETURN_IF(L->hebb_rate.alloc(n * 4));
+    PSSA_RETURN_IF(L->hebb_rate.alloc(D * n * 4));  // [depth, lanes]
     PSSA_RETURN_IF(L->gen_pos.alloc(4));
     L->dec_lanes = n;
   }
@@ -836,10 +922,13 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     } else {
       PSSA_RETURN_IF(need(L->staged_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
     }
+    const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
+    if (plastic)
+      PSSA_RETURN_IF(need(pssa::bank_write_lds((int)L->model->cfg.mem_capacity, (int)n_lanes) <= 160 * 1024,
+                          "plastic decode: mem_capacity and n_lanes exceed the bank-write LDS budget"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
-    const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
     PSSA_RETURN_IF(ensure_decode_buffers(L, n_lanes, steps));
     if (first_ids)
       PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, first_ids, n_lanes * 4, hipMemcpyHostToDevice, st));

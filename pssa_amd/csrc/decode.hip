@@ -87,68 +87,104 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
   }
 }
 
-// 0.02 / (1 + |z_final|) per lane (the Hebbian rate of dream_replay_value;
-// the norm is a sequential f64 sum).
-__global__ void hebbian_rate_kernel(const float* __restrict__ z, int d, int n_lanes,
-                                    float* __restrict__ rate) {
-  const int ln = blockIdx.x * blockDim.x + threadIdx.x;
-  if (ln >= n_lanes) return;
-  const float* zr = z + (size_t)ln * d;
-  double acc = 0.0;
-  {
-#pragma clang fp contract(off)
-    for (int i = 0; i < d; ++i) acc = acc + (double)zr[i] * (double)zr[i];
-  }
-  const double tn = sqrt(acc);
-  rate[ln] = 0.02f / (1.0f + (float)fmin(tn, (double)FLT_MAX));
+// Per-layer operand pointers of the plastic write kernels (one launch covers
+// every block).
+struct PlasticArgs {
+  float* keys[kMaxDepth];
+  float* norm_sq[kMaxDepth];
+  float* values[kMaxDepth];
+  void* values_t[kMaxDepth];
+  float* conf[kMaxDepth];
+  unsigned long long* last_seen[kMaxDepth];
+  int* meta[kMaxDepth];
+  float* up[kMaxDepth];
+  const float* slow[kMaxDepth];
+  void* u_eff[kMaxDepth];
+  const float* tap_q;    // [depth, lanes, k]
+  const float* tap_z;    // [depth, lanes, d]
+  const float* tap_a;    // [depth, lanes, d]
+  const float* tap_act;  // [depth, lanes, r]
+  const float* surprise; // [lanes]
+  float* rate;           // [depth, lanes]
+  const unsigned long long* step;
+  int lanes, C, dk, d, r, wt_bf16;
+};
+
+__device__ __forceinline__ uint16_t to_bf16(float v) {
+  uint32_t b = __float_as_uint(v);
+  b += 0x7FFFu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
 }
 
 // up[i,q] += rate_l * clamp(z_l[i] - a_l[i], -4, 4) * act_l[q] for lanes l in
-// order, then the GEMM operand u_eff = up + slow in the weight type.
-__global__ void hebbian_kernel(float* __restrict__ up, const float* __restrict__ slow,
-                               void* __restrict__ u_eff, int ueff_bf16,
-                               const float* __restrict__ z, const float* __restrict__ a,
-                               const float* __restrict__ act, const float* __restrict__ rate,
-                               int n_lanes, int d, int r) {
+// order (rounded as the reference: (rate * err) * act, then the add), then
+// the GEMM operand u_eff = up + slow in the weight type.  blockIdx.y = block.
+__global__ void hebbian_kernel(PlasticArgs p) {
+  const int l = blockIdx.y;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= d * r) return;
-  const int i = e / r, q = e % r;
-  float u = up[e];
-  for (int ln = 0; ln < n_lanes; ++ln) {
-    const float err = fminf(fmaxf(z[(size_t)ln * d + i] - a[(size_t)ln * d + i], -4.0f), 4.0f);
-    u = __fadd_rn(u, __fmul_rn(__fmul_rn(rate[ln], err), act[(size_t)ln * r + q]));
+  if (e >= p.d * p.r) return;
+  const int i = e / p.r, q = e % p.r;
+  const size_t n = p.lanes;
+  const float* z = p.tap_z + (size_t)l * n * p.d;
+  const float* a = p.tap_a + (size_t)l * n * p.d;
+  const float* act = p.tap_act + (size_t)l * n * p.r;
+  const float* rate = p.rate + (size_t)l * n;
+  float u = p.up[l][e];
+  for (int ln = 0; ln < p.lanes; ++ln) {
+    const float err = fminf(fmaxf(z[(size_t)ln * p.d + i] - a[(size_t)ln * p.d + i], -4.0f), 4.0f);
+    u = __fadd_rn(u, __fmul_rn(__fmul_rn(rate[ln], err), act[(size_t)ln * p.r + q]));
   }
-  up[e] = u;
-  const float eff = u + slow[e];
-  if (ueff_bf16) {
-    uint32_t b = __float_as_uint(eff);
-    b += 0x7FFFu + ((b >> 16) & 1u);
-    static_cast<uint16_t*>(u_eff)[e] = (uint16_t)(b >> 16);
-  } else {
-    static_cast<float*>(u_eff)[e] = eff;
-  }
+  p.up[l][e] = u;
+  const float eff = u + p.slow[l][e];
+  if (p.wt_bf16)
+    static_cast<uint16_t*>(p.u_eff[l])[e] = to_bf16(eff);
+  else
+    static_cast<float*>(p.u_eff[l])[e] = eff;
 }
 
-// Protected writes of one block's bank for all lanes, in lane order.  The
-// accept/defend decisions depend only on the bank's counters, confidences and
-// ages, so thread 0 makes them sequentially; the slot contents are then
-// copied in parallel, each slot from the last lane in order that wrote it.
-__global__ __launch_bounds__(256) void bank_write_kernel(
-    float* __restrict__ keys, float* __restrict__ norm_sq, float* __restrict__ values,
-    void* __restrict__ values_t, int vt_bf16, float* __restrict__ conf,
-    unsigned long long* __restrict__ last_seen, int* __restrict__ meta,
-    const unsigned long long* __restrict__ step, const float* __restrict__ q,
-    const float* __restrict__ z, const float* __restrict__ surprise, int n_lanes, int C, int dk,
-    int d) {
-  extern __shared__ int writer[];  // [C]: last lane that wrote the slot this step, or -1
-  const int tid = threadIdx.x;
-  for (int c = tid; c < C; c += blockDim.x) writer[c] = -1;
+// 0.02 / (1 + |z_final|) per (block, lane): the Hebbian rate of
+// dream_replay_value, with the norm as a sequential f64 sum.
+__global__ void hebbian_rate_kernel(PlasticArgs p) {
+  const int l = blockIdx.y;
+  const int ln = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ln >= p.lanes) return;
+  const float* zr = p.tap_z + ((size_t)l * p.lanes + ln) * p.d;
+  double acc = 0.0;
+  {
+#pragma clang fp contract(off)
+    for (int i = 0; i < p.d; ++i) acc = acc + (double)zr[i] * (double)zr[i];
+  }
+  const double tn = sqrt(acc);
+  p.rate[(size_t)l * p.lanes + ln] = 0.02f / (1.0f + (float)fmin(tn, (double)FLT_MAX));
+}
+
+// Protected writes of every block's bank (blockIdx.x = block) for all lanes,
+// in lane order.  The accept/defend decisions depend only on the bank's
+// counters, confidences and ages: those are staged in LDS, thread 0 makes
+// the decisions sequentially, and the slot contents are then copied in
+// parallel, each slot from the last lane in order that wrote it.
+__global__ __launch_bounds__(256) void bank_write_kernel(PlasticArgs p) {
+  extern __shared__ unsigned char bw_smem[];
+  const int l = blockIdx.x, C = p.C, tid = threadIdx.x;
+  unsigned long long* s_last = reinterpret_cast<unsigned long long*>(bw_smem);  // [C]
+  float* s_conf = reinterpret_cast<float*>(s_last + C);                          // [C]
+  int* writer = reinterpret_cast<int*>(s_conf + C);                              // [C]
+  float* s_sp = reinterpret_cast<float*>(writer + C);                            // [lanes]
+  float* conf = p.conf[l];
+  unsigned long long* last_seen = p.last_seen[l];
+  for (int c = tid; c < C; c += blockDim.x) {
+    writer[c] = -1;
+    s_conf[c] = conf[c];
+    s_last[c] = last_seen[c];
+  }
+  for (int ln = tid; ln < p.lanes; ln += blockDim.x) s_sp[ln] = p.surprise[ln];
   __syncthreads();
   if (tid == 0) {
-    const unsigned long long cur = step[0] + 1;
+    const unsigned long long cur = p.step[0] + 1;
+    int* meta = p.meta[l];
     int count = meta[0], head = meta[1];
-    for (int ln = 0; ln < n_lanes; ++ln) {
-      const float sp = surprise[ln];
+    for (int ln = 0; ln < p.lanes; ++ln) {
+      const float sp = s_sp[ln];
       if (!(sp > 3.5f)) continue;
       int idx;
       if (count < C) {  // insert() into a free slot
@@ -156,54 +192,56 @@ __global__ __launch_bounds__(256) void bank_write_kernel(
       } else {
         idx = head;
         // RateLimiterGate::apply_refractory_overwrite (src/defense.rs:45-67).
-        const unsigned long long last = last_seen[idx];
+        const unsigned long long last = s_last[idx];
         const float dt = (float)(cur > last ? cur - last : 0ull);
         const float lin = 1.0f - expf(-dt / 60.0f);
         const float gain = fmaxf(lin * lin, 0.005f);
         const float damage = 0.08f * sp * gain;
-        if (conf[idx] > damage) {
-          conf[idx] -= damage;
-          last_seen[idx] = cur;
+        if (s_conf[idx] > damage) {
+          s_conf[idx] -= damage;
+          s_last[idx] = cur;
           continue;
         }
         head = (head + 1) % C;
       }
-      conf[idx] = 1.0f;
-      last_seen[idx] = cur;
+      s_conf[idx] = 1.0f;
+      s_last[idx] = cur;
       writer[idx] = ln;
     }
     meta[0] = count;
     meta[1] = head;
   }
   __syncthreads();
+  for (int c = tid; c < C; c += blockDim.x) {
+    conf[c] = s_conf[c];
+    last_seen[c] = s_last[c];
+  }
   const int wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+  const size_t n = p.lanes;
   for (int c = wave; c < C; c += nw) {
     const int ln = writer[c];
     if (ln < 0) continue;
-    const float* kq = q + (size_t)ln * dk;
-    const float* vz = z + (size_t)ln * d;
-    for (int j = lane; j < dk; j += 64) keys[(size_t)c * dk + j] = kq[j];
-    for (int j = lane; j < d; j += 64) {
+    const float* kq = p.tap_q + ((size_t)l * n + ln) * p.dk;
+    const float* vz = p.tap_z + ((size_t)l * n + ln) * p.d;
+    for (int j = lane; j < p.dk; j += 64) p.keys[l][(size_t)c * p.dk + j] = kq[j];
+    for (int j = lane; j < p.d; j += 64) {
       const float v = vz[j];
-      values[(size_t)c * d + j] = v;
-      if (vt_bf16) {
-        uint32_t b = __float_as_uint(v);
-        b += 0x7FFFu + ((b >> 16) & 1u);
-        static_cast<uint16_t*>(values_t)[(size_t)j * C + c] = (uint16_t)(b >> 16);
-      } else {
-        static_cast<float*>(values_t)[(size_t)j * C + c] = v;
-      }
+      p.values[l][(size_t)c * p.d + j] = v;
+      if (p.wt_bf16)
+        static_cast<uint16_t*>(p.values_t[l])[(size_t)j * C + c] = to_bf16(v);
+      else
+        static_cast<float*>(p.values_t[l])[(size_t)j * C + c] = v;
     }
     if (lane == 0) {
       // squared_norm (src/memory.rs:181-192): sequential f64 sum.
       double acc = 0.0;
       {
 #pragma clang fp contract(off)
-        for (int j = 0; j < dk; ++j) acc = acc + (double)kq[j] * (double)kq[j];
+        for (int j = 0; j < p.dk; ++j) acc = acc + (double)kq[j] * (double)kq[j];
       }
       float v = (float)acc;
       if (acc < 1.0 && v == 1.0f) v = __uint_as_float(0x3f7fffffu);
-      norm_sq[c] = v;
+      p.norm_sq[l][c] = v;
     }
   }
 }
@@ -220,6 +258,14 @@ __global__ void advance_pos_kernel(int* __restrict__ gen_pos) {
 }
 
 }  // namespace
+
+size_t bank_write_lds(int capacity, int lanes) { return (size_t)capacity * (8 + 4 + 4) + (size_t)lanes * 4; }
+
+Status init_decode_attributes() {
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&bank_write_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  return Status::Ok();
+}
 
 Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes) {
   const hipStream_t st = L->ctx->stream;
@@ -243,25 +289,40 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
                                              L->surprise.as<float>());
   PSSA_LAUNCH_CHECK("greedy");
   if (plastic) {
-    const bool vbf = M->dtype == PSSA_HIP_BF16;
+    PlasticArgs p{};
     for (size_t l = 0; l < c.depth; ++l) {
       const DevBlock& B = M->blocks[l];
-      const float* tq = L->tap_q.as<float>() + l * n * k;
-      const float* tz = L->tap_z.as<float>() + l * n * d;
-      const float* ta = L->tap_a.as<float>() + l * n * d;
-      const float* tact = L->tap_act.as<float>() + l * n * r;
-      bank_write_kernel<<<1, 256, (size_t)C * sizeof(int), st>>>(
-          B.keys.as<float>(), B.norm_sq.as<float>(), B.values.as<float>(), B.values_t.p, vbf ? 1 : 0,
-          B.conf.as<float>(), B.last_seen.as<unsigned long long>(), B.meta.as<int>(),
-          M->step.as<unsigned long long>(), tq, tz, L->surprise.as<float>(), (int)n, C, k, d);
-      PSSA_LAUNCH_CHECK("bank_write");
-      hebbian_rate_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(tz, d, (int)n, L->hebb_rate.as<float>());
-      PSSA_LAUNCH_CHECK("hebbian_rate");
-      hebbian_kernel<<<(unsigned)((d * r + 255) / 256), 256, 0, st>>>(
-          B.u_fast.as<float>(), B.u_slow.as<float>(), B.u_eff.p, vbf ? 1 : 0, tz, ta, tact,
-          L->hebb_rate.as<float>(), (int)n, d, r);
-      PSSA_LAUNCH_CHECK("hebbian");
+      p.keys[l] = B.keys.as<float>();
+      p.norm_sq[l] = B.norm_sq.as<float>();
+      p.values[l] = B.values.as<float>();
+      p.values_t[l] = B.values_t.p;
+      p.conf[l] = B.conf.as<float>();
+      p.last_seen[l] = B.last_seen.as<unsigned long long>();
+      p.meta[l] = B.meta.as<int>();
+      p.up[l] = B.u_fast.as<float>();
+      p.slow[l] = B.u_slow.as<float>();
+      p.u_eff[l] = B.u_eff.p;
     }
+    p.tap_q = L->tap_q.as<float>();
+    p.tap_z = L->tap_z.as<float>();
+    p.tap_a = L->tap_a.as<float>();
+    p.tap_act = L->tap_act.as<float>();
+    p.surprise = L->surprise.as<float>();
+    p.rate = L->hebb_rate.as<float>();
+    p.step = M->step.as<unsigned long long>();
+    p.lanes = (int)n;
+    p.C = C;
+    p.dk = k;
+    p.d = d;
+    p.r = r;
+    p.wt_bf16 = M->dtype == PSSA_HIP_BF16 ? 1 : 0;
+    const int depth = (int)c.depth;
+    bank_write_kernel<<<depth, 256, bank_write_lds(C, (int)n), st>>>(p);
+    PSSA_LAUNCH_CHECK("bank_write");
+    hebbian_rate_kernel<<<dim3((unsigned)((n + 255) / 256), depth), 256, 0, st>>>(p);
+    PSSA_LAUNCH_CHECK("hebbian_rate");
+    hebbian_kernel<<<dim3((unsigned)((d * r + 255) / 256), depth), 256, 0, st>>>(p);
+    PSSA_LAUNCH_CHECK("hebbian");
     advance_kernel<<<1, 64, 0, st>>>(M->step.as<unsigned long long>(), L->gen_pos.as<int>());
   } else {
     advance_pos_kernel<<<1, 64, 0, st>>>(L->gen_pos.as<int>());

@@ -6,6 +6,8 @@
 
 namespace pssa {
 
+constexpr int kMaxDepth = 32;  // PSSAConfigV2 depth limit enforced by check_config
+
 struct DevBlock {
   DevBuf w_in;     // [n_in, d]: W_delta; W_B; W_C; W_qx; W_gate; adapter D  (weight dtype)
   DevBuf w_qh;     // [k, d]
@@ -73,9 +75,9 @@ struct pssa_hip_lanes {
   pssa::DevBuf X, XN, XNh, P, Y, Yh, Q, Wm, Mval, Zraw, Zrawh, H1, logits;
   pssa::DevBuf Ypart;  // SSM partial readouts when d_state needs more than two state blocks
   // Decode state (allocated on the first decode call): per-block taps of the
-  // last step [depth, lanes, *], the surprise of each lane's greedy choice,
-  // 1/(1+|z_final|) rates, the generated ids [gen_cap, lanes] and the
-  // generation position.
+  // last step [depth, lanes, *], the surprise of each lane's greedy choice
+  // [lanes], the Hebbian rates 0.02/(1+|z_final|) [depth, lanes], the
+  // generated ids [gen_cap, lanes] and the generation position.
   pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
@@ -110,6 +112,9 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic);
 // Greedy choice from lanes->logits without a forward step (first decode
 // token after a prefill).
 Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes);
+// Dynamic LDS of the bank-write kernel and its per-device attribute set-up.
+size_t bank_write_lds(int capacity, int lanes);
+Status init_decode_attributes();
 Status launch_fill_zero(hipStream_t stream, float* p, size_t n);
 Status launch_copy_cols(hipStream_t stream, const float* in, int ld_in, float* out, int ld_out,
                         size_t rows, int cols);

@@ -52,6 +52,18 @@ class HipDevice:
     def synchronize(self) -> None:
         _abi.call(self._lib.pssa_hip_synchronize, self.handle)
 
+    # -- device buffers for the resident entry points ---------------------------
+    def upload(self, array: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(array)
+        buf = DeviceBuffer(self, a.nbytes, a.shape, a.dtype)
+        _abi.call(self._lib.pssa_hip_memcpy, self.handle, C.c_void_p(buf.ptr), a.ctypes.data_as(C.c_void_p),
+                  a.nbytes, _abi.H2D)
+        return buf
+
+    def empty(self, shape, dtype) -> "DeviceBuffer":
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        return DeviceBuffer(self, n, tuple(shape), np.dtype(dtype))
+
     # -- GpuDispatch::try_dispatch_gemm_into (src/backend.rs:1049-1085) -------
     def try_dispatch_gemm(self, x, w, m: int, n: int, k: int, batch: int = 1,
                           w_dtype: str = "f32") -> np.ndarray:
@@ -130,6 +142,15 @@ class HipDevice:
                   None if out_idx is None else _abi.ptr(out_idx, C.c_uint32), _abi.ptr(out_w))
         return out_val, out_min, out_idx, out_w
 
+    def retrieve_resident(self, q_ptr: int, n_q: int, keys_ptr: int, norm_sq_ptr: int, values_ptr: int,
+                          capacity: int, count: int, d_key: int, d_val: int, tau: float, top_k: int,
+                          out_val_ptr: int, out_min_ptr: int | None = None, out_idx_ptr: int | None = None) -> None:
+        """retrieve on device buffers (asynchronous on the context stream)."""
+        vp = C.c_void_p
+        _abi.call(self._lib.pssa_hip_retrieve_resident, self.handle, vp(q_ptr), n_q, vp(keys_ptr), vp(norm_sq_ptr),
+                  vp(values_ptr), capacity, count, d_key, d_val, tau, top_k, vp(out_val_ptr),
+                  vp(out_min_ptr) if out_min_ptr else None, vp(out_idx_ptr) if out_idx_ptr else None)
+
     def dense_scan(self, a, b, h0=None):
         a, b = _f32(a), _f32(b)
         batch, L, s = b.shape
@@ -144,6 +165,40 @@ class HipDevice:
                             h_ptr: int) -> None:
         _abi.call(self._lib.pssa_hip_dense_scan_resident, self.handle, C.c_void_p(a_ptr), C.c_void_p(b_ptr),
                   C.c_void_p(h0_ptr) if h0_ptr else None, batch, L, s, C.c_void_p(h_ptr))
+
+
+class DeviceBuffer:
+    """A device allocation made through the C ABI (freed on close/GC)."""
+
+    def __init__(self, device: HipDevice, nbytes: int, shape, dtype):
+        self.device = device
+        self.shape, self.dtype, self.nbytes = tuple(shape), np.dtype(dtype), nbytes
+        p = C.c_void_p()
+        _abi.call(device._lib.pssa_hip_device_alloc, device.handle, max(nbytes, 1), C.byref(p))
+        self.ptr = p.value
+
+    def to_host(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        _abi.call(self.device._lib.pssa_hip_memcpy, self.device.handle, out.ctypes.data_as(C.c_void_p),
+                  C.c_void_p(self.ptr), self.nbytes, _abi.D2H)
+        return out
+
+    def write(self, array: np.ndarray, offset_bytes: int = 0) -> None:
+        a = np.ascontiguousarray(array)
+        assert offset_bytes + a.nbytes <= self.nbytes
+        _abi.call(self.device._lib.pssa_hip_memcpy, self.device.handle, C.c_void_p(self.ptr + offset_bytes),
+                  a.ctypes.data_as(C.c_void_p), a.nbytes, _abi.H2D)
+
+    def close(self) -> None:
+        if self.ptr:
+            self.device._lib.pssa_hip_device_free(self.device.handle, C.c_void_p(self.ptr))
+            self.ptr = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class PSSALayer:

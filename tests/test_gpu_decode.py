@@ -155,3 +155,32 @@ def test_decode_at_105m_width_graph_equals_eager(hip):
     for x, y in zip(*outs):
         np.testing.assert_array_equal(x, y)
     assert np.all(np.isfinite(outs[0][1]))
+
+
+def test_plastic_decode_many_lanes_and_layers_matches_oracle(hip):
+    """64 lanes x 12 blocks: the per-(block, lane) Hebbian rates and the
+    per-block bank writes of one launch cover every block."""
+    say("plastic decode 64 lanes x 12 layers")
+    cfg = PSSAConfig(depth=12, d_vocab=61, d_latent=16, d_state=8, d_mem_key=4, mem_capacity=24)
+    w = ModelWeights.init(cfg, 21, "baseline")
+    w.populate_banks(22, count=24)
+    ref = ModelWeights.init(cfg, 21, "baseline")
+    ref.populate_banks(22, count=24)
+    lanes = 64
+    ids = np.random.default_rng(6).integers(0, cfg.d_vocab, (lanes, 3), dtype=np.uint32)
+    om = O.OracleModel(ref)
+    st = om.zero_state(lanes)
+    lg = om.prefill_lanes(st, ids, threads=8)
+    first = [O.greedy(lg[i]) for i in range(lanes)]
+    layer = PSSALayer(hip, w, lanes=lanes, max_tokens=lanes * 3)
+    layer.prefill_inference(ids)
+    got = layer.decode(2, plastic=True, graph=True)
+    ref_ids, _, _ = om.decode(st, first, steps=2, plastic=True, threads=8)
+    np.testing.assert_array_equal(got, ref_ids)
+    for l in (0, 5, 11):
+        dev = layer.get_plastic(l)
+        rb = ref.blocks[l]
+        np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
+        assert dev["mem_write_head"] == rb.mem_write_head
+        assert rel_err(dev["adapter_up"], rb.adapter_up) < 1e-4
+    layer.close()

@@ -72,6 +72,21 @@ Status check_config(const pssa_hip_config& c) {
 
 float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
+// Carries are [lanes, depth, d, s] at the ABI (h_persistent, src/pssa.rs) and
+// [lanes, depth, s, d] on the device (the scan's coalesced layout).
+Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_device) {
+  const pssa_hip_config& c = L->model->cfg;
+  const int d = (int)c.d_latent, s = (int)c.d_state;
+  const size_t mats = L->lanes * c.depth;
+  for (size_t m0 = 0; m0 < mats; m0 += 65535) {
+    const size_t cnt = std::min<size_t>(65535, mats - m0);
+    const size_t off = m0 * (size_t)d * s;
+    PSSA_RETURN_IF(pssa::launch_transpose(L->ctx->stream, in + off, out + off, cnt, to_device ? d : s,
+                                          to_device ? s : d, 1.0f));
+  }
+  return Status::Ok();
+}
+
 Status stage_ids_locked(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T) {
   PSSA_RETURN_IF(need(ids != nullptr, "null ids"));
   PSSA_RETURN_IF(need(T > 0, "prefill requires at least one token"));
@@ -291,7 +306,14 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
     PSSA_RETURN_IF(upload(dc, c_proj, ls * 4, st));
     PSSA_RETURN_IF(upload(dh, initial, w * 4, st));
     PSSA_RETURN_IF(dy.alloc(ld * 4));
-    PSSA_RETURN_IF(pssa::launch_scale(st, dr.as<float>(), dr.as<float>(), w, 1.4426950408889634f));
+    // The scan keeps states and rates state-major ([s, d]); the stage API
+    // speaks the reference's [d, s].
+    DevBuf dr2, dh2;
+    PSSA_RETURN_IF(dr2.alloc(w * 4));
+    PSSA_RETURN_IF(dh2.alloc(w * 4));
+    PSSA_RETURN_IF(pssa::launch_transpose(st, dr.as<float>(), dr2.as<float>(), 1, (int)d_m, (int)d_s,
+                                          1.4426950408889634f));
+    PSSA_RETURN_IF(pssa::launch_transpose(st, dh.as<float>(), dh2.as<float>(), 1, (int)d_m, (int)d_s, 1.0f));
     PSSA_RETURN_IF(pssa::launch_fill_zero(st, dy.as<float>(), ld));
     pssa::SsmArgs a;
     a.delta = dd.as<float>();
@@ -302,8 +324,8 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
     a.ld_c = (int)d_s;
     a.xn = dx.as<float>();
     a.ld_x = (int)d_m;
-    a.rates2 = dr.as<float>();
-    a.carry = dh.as<float>();
+    a.rates2 = dr2.as<float>();
+    a.carry = dh2.as<float>();
     a.carry_stride = (long)w;
     a.y = dy.as<float>();
     a.ld_y = (int)d_m;
@@ -327,7 +349,10 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
     }
     PSSA_RETURN_IF(pssa::launch_ssm_scan(st, a));
     PSSA_RETURN_IF(download(y_ssm, dy, ld * 4, st));
-    if (final_state) PSSA_RETURN_IF(download(final_state, dh, w * 4, st));
+    if (final_state) {
+      PSSA_RETURN_IF(pssa::launch_transpose(st, dh2.as<float>(), dh.as<float>(), 1, (int)d_s, (int)d_m, 1.0f));
+      PSSA_RETURN_IF(download(final_state, dh, w * 4, st));
+    }
     if (bar_a) {
       PSSA_RETURN_IF(download(bar_a, da, lw * 4, st));
       PSSA_RETURN_IF(download(bar_b, dbb, lw * 4, st));
@@ -605,7 +630,9 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       PSSA_RETURN_IF(upload_weight(B.mlp_w2, b.mlp_w2, d * 2 * d, weight_dtype, st));
       std::vector<float> ueff(d * r), rates(d * s), vt(d * C);
       for (size_t i = 0; i < d * r; ++i) ueff[i] = b.adapter_up[i] + b.adapter_slow[i];
-      for (size_t i = 0; i < d * s; ++i) rates[i] = -softplus_host(b.a_raw[i]) * 1.4426950408889634f;
+      // State-major [s, d] for the scan.
+      for (size_t i = 0; i < d; ++i)
+        for (size_t j = 0; j < s; ++j) rates[j * d + i] = -softplus_host(b.a_raw[i * s + j]) * 1.4426950408889634f;
       for (size_t q = 0; q < C; ++q)
         for (size_t j = 0; j < d; ++j) vt[j * C + q] = b.mem_values[q * d + j];
       PSSA_RETURN_IF(upload_weight(B.u_eff, ueff.data(), ueff.size(), weight_dtype, st));
@@ -719,7 +746,10 @@ int pssa_hip_lanes_get_carry(pssa_hip_lanes* L, float* out, size_t len, char* er
     PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
-    PSSA_RETURN_IF(download(out, L->carry, n * 4, L->ctx->stream));
+    DevBuf tmp;
+    PSSA_RETURN_IF(tmp.alloc(n * 4));
+    PSSA_RETURN_IF(carry_layout(L, L->carry.as<float>(), tmp.as<float>(), false));
+    PSSA_RETURN_IF(download(out, tmp, n * 4, L->ctx->stream));
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
@@ -733,12 +763,13 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* L, const float* in, size_t len, cha
     PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
-    PSSA_HIP_TRY(hipMemcpyAsync(L->carry.p, in, n * 4, hipMemcpyHostToDevice, L->ctx->stream));
+    DevBuf tmp;
+    PSSA_RETURN_IF(upload(tmp, in, n * 4, L->ctx->stream));
+    PSSA_RETURN_IF(carry_layout(L, tmp.as<float>(), L->carry.as<float>(), true));
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
 }
-
 
 int pssa_hip_prefill(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
                      float* logits_last, size_t logits_len, char* err, size_t err_len) {

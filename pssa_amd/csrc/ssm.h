@@ -13,8 +13,10 @@ struct SsmArgs {
   int ld_c = 0;
   const float* xn = nullptr;     // normalised input x_t, [rows, d]
   int ld_x = 0;
-  const float* rates2 = nullptr; // -softplus(a_raw) * log2(e), [d*s]
-  float* carry = nullptr;        // h, lane b at carry + b*carry_stride, [d*s]; read, then overwritten
+  // State-major layouts [s, d] (channel contiguous), so that the 64
+  // channels of a wave read and write 256 contiguous bytes per state.
+  const float* rates2 = nullptr; // -softplus(a_raw) * log2(e), [s, d]
+  float* carry = nullptr;        // h, lane b at carry + b*carry_stride, [s, d]; read, then overwritten
   long carry_stride = 0;
   float* y = nullptr;            // readout, [rows, d]
   int ld_y = 0;
@@ -42,5 +44,10 @@ Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a);
 
 // rates2[i] = rates[i] * log2(e) (stage API receives -softplus(a_raw)).
 Status launch_scale(hipStream_t stream, const float* in, float* out, size_t n, float scale);
+
+// out[c, r] = in[r, c] for `count` consecutive [rows, cols] matrices (the
+// reference's [d, s] state layout <-> the scan's [s, d]), scaled by `scale`.
+Status launch_transpose(hipStream_t stream, const float* in, float* out, size_t count, int rows,
+                        int cols, float scale);
 
 }  // namespace pssa

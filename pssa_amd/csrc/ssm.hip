@@ -50,11 +50,11 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[(size_t)i * s + j] : 0.0f;
-    r2[q] = ok ? a.rates2[(size_t)i * s + j] : 0.0f;
+    h[q] = ok ? carry[(size_t)j * d + i] : 0.0f;
+    r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
   if (MAT && blockIdx.z == 0 && wave == 0 && ivalid)
-    for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[(size_t)i * s + j];
+    for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[(size_t)j * d + i];
 
   for (int t0 = 0; t0 < T; t0 += MAT_TC) {
     for (int e = tid; e < MAT_TC * 64; e += 256) {
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[(size_t)i * s + j] = h[q];
+    if (ivalid && j < s) carry[(size_t)j * d + i] = h[q];
   }
 }
 
@@ -162,8 +162,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[(size_t)i * s + j] : 0.0f;
-    r2[q] = ok ? a.rates2[(size_t)i * s + j] : 0.0f;
+    h[q] = ok ? carry[(size_t)j * d + i] : 0.0f;
+    r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
 
   float pd[NDX], px[NDX], pb[NBC], pc[NBC];
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[(size_t)i * s + j] = h[q];
+    if (ivalid && j < s) carry[(size_t)j * d + i] = h[q];
   }
 }
 
@@ -325,6 +325,33 @@ __global__ void scale_kernel(const float* __restrict__ in, float* __restrict__ o
                              float scale) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = in[i] * scale;
+}
+
+// 32x32 tiles through LDS; blockIdx.z = matrix.
+__global__ void transpose_kernel(const float* __restrict__ in, float* __restrict__ out, int rows, int cols,
+                                 float scale) {
+  __shared__ float tile[32][33];
+  const size_t base = (size_t)blockIdx.z * rows * cols;
+  const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+  for (int k = threadIdx.y; k < 32; k += blockDim.y) {
+    const int r = r0 + k, c = c0 + threadIdx.x;
+    if (r < rows && c < cols) tile[k][threadIdx.x] = in[base + (size_t)r * cols + c];
+  }
+  __syncthreads();
+  for (int k = threadIdx.y; k < 32; k += blockDim.y) {
+    const int c = c0 + k, r = r0 + threadIdx.x;
+    if (r < rows && c < cols) out[base + (size_t)c * rows + r] = tile[threadIdx.x][k] * scale;
+  }
+}
+
+Status launch_transpose(hipStream_t stream, const float* in, float* out, size_t count, int rows,
+                        int cols, float scale) {
+  if (!count || rows <= 0 || cols <= 0) return Status::Ok();
+  if (count > 65535) return Status::Invalid("transpose: too many matrices");
+  dim3 grid((cols + 31) / 32, (rows + 31) / 32, (unsigned)count), block(32, 8);
+  transpose_kernel<<<grid, block, 0, stream>>>(in, out, rows, cols, scale);
+  PSSA_LAUNCH_CHECK("transpose");
+  return Status::Ok();
 }
 
 Status launch_scale(hipStream_t stream, const float* in, float* out, size_t n, float scale) {

@@ -91,10 +91,17 @@ struct pssa_hip_lanes {
   std::array<int, pssa::ST_COUNT> stage_calls{};
   std::vector<hipEvent_t> events;
   std::vector<int> event_stage;
+  // Second stream (default priority) for the concurrent lane group of a
+  // prefill, and the events that fork and join it.
+  hipStream_t aux_stream = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_first = nullptr, ev_join = nullptr;
   ~pssa_hip_lanes() {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
     if (graph) (void)hipGraphDestroy(graph);
+    for (hipEvent_t e : {ev_fork, ev_first, ev_join})
+      if (e) (void)hipEventDestroy(e);
+    if (aux_stream) (void)hipStreamDestroy(aux_stream);
   }
 };
 

@@ -152,7 +152,7 @@ struct Timer {
   hipStream_t s;
   size_t next = 0;
   Status mark(int stage) {
-    if (!L->timing) return Status::Ok();
+    if (!L || !L->timing) return Status::Ok();
     if (next == L->events.size()) {
       hipEvent_t e;
       PSSA_HIP_TRY(hipEventCreate(&e));
@@ -166,7 +166,7 @@ struct Timer {
   }
   // Closes the last interval and folds all intervals into per-stage totals.
   Status finish() {
-    if (!L->timing) return Status::Ok();
+    if (!L || !L->timing) return Status::Ok();
     PSSA_RETURN_IF(mark(-1));
     PSSA_HIP_TRY(hipEventSynchronize(L->events[next - 1]));
     L->stage_ms.fill(0.0f);
@@ -186,48 +186,59 @@ struct Timer {
 
 }  // namespace
 
-Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
+// Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`.  Every buffer
+// pointer is offset to the view's rows, so disjoint views can run
+// concurrently.  `first_in_done` (may be null) is recorded once layer 0's
+// input projection has been issued.
+static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T,
+                           bool taps, bool timing, hipEvent_t first_in_done, float* y_part) {
   const pssa_hip_model* M = L->model;
   const pssa_hip_config& c = M->cfg;
-  const hipStream_t st = L->ctx->stream;
   const int d = (int)c.d_latent, s = (int)c.d_state, k = (int)c.d_mem_key;
   const int C = (int)c.mem_capacity, r = (int)c.adapter_rank, V = (int)c.d_vocab;
   const int n_in = (int)M->n_in;
   const size_t rows = n_lanes * T;
+  const size_t row0 = lane0 * T;
   const int m = (int)rows;
   const int dt = M->dtype;
   const bool bf16 = dt == PSSA_HIP_BF16;
+  const size_t es = bf16 ? 2 : 4;
   const float ssm_scale = 1.0f / sqrtf((float)s);
   const float depth_scale = 1.0f / sqrtf((float)c.depth);
   const float logit_scale = 1.0f / sqrtf((float)d);
   // Column offsets inside the fused projection output P.
   const int o_b = d, o_c = d + s, o_qx = d + 2 * s, o_gate = d + 2 * s + k, o_act = 2 * d + 2 * s + k;
 
-  float* X = L->X.as<float>();
-  float* XN = L->XN.as<float>();
-  float* P = L->P.as<float>();
-  float* Y = L->Y.as<float>();
-  float* Q = L->Q.as<float>();
-  float* Zr = L->Zraw.as<float>();
+  float* X = L->X.as<float>() + row0 * d;
+  float* XN = L->XN.as<float>() + row0 * d;
+  float* P = L->P.as<float>() + row0 * n_in;
+  float* Y = L->Y.as<float>() + row0 * d;
+  float* Q = L->Q.as<float>() + row0 * k;
+  float* Zr = L->Zraw.as<float>() + row0 * d;
   // GEMM operands in the model's operand type (aliases of the fp32 buffers
   // in an fp32 model).
-  void* XNh = bf16 ? L->XNh.p : (void*)XN;
-  void* Yh = bf16 ? L->Yh.p : (void*)Y;
-  void* Zrh = bf16 ? L->Zrawh.p : (void*)Zr;
-  void* Wm = L->Wm.p;
-  void* Mv = L->Mval.p;
-  void* H1 = L->H1.p;
+  uint16_t* XNh16 = bf16 ? L->XNh.as<uint16_t>() + row0 * d : nullptr;
+  void* XNh = bf16 ? (void*)XNh16 : (void*)XN;
+  void* Yh = bf16 ? (void*)(L->Yh.as<uint16_t>() + row0 * d) : (void*)Y;
+  void* Zrh = bf16 ? (void*)(L->Zrawh.as<uint16_t>() + row0 * d) : (void*)Zr;
+  void* Wm = static_cast<char*>(L->Wm.p) + row0 * C * es;
+  void* Mv = static_cast<char*>(L->Mval.p) + row0 * d * es;
+  void* H1 = static_cast<char*>(L->H1.p) + row0 * 2 * d * es;
+  const uint32_t* ids = L->ids.as<uint32_t>() + row0;
+  float* carry = L->carry.as<float>() + lane0 * c.depth * (size_t)d * s;
+  float* logits = L->logits.as<float>() + lane0 * (size_t)V;
 
-  Timer tm{L, st};
+  pssa_hip_lanes* TL = timing ? L : nullptr;
+  Timer tm{TL, st};
   PSSA_RETURN_IF(tm.mark(ST_EMBED));
-  embed_kernel<<<(unsigned)rows, 256, 0, st>>>(L->ids.as<uint32_t>(), M->embed.as<float>(), X, d, rows);
+  embed_kernel<<<(unsigned)rows, 256, 0, st>>>(ids, M->embed.as<float>(), X, d, rows);
   PSSA_LAUNCH_CHECK("embed");
 
   for (size_t l = 0; l < c.depth; ++l) {
     const DevBlock& B = M->blocks[l];
     PSSA_RETURN_IF(tm.mark(ST_NORM));
     rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
-        X, B.gamma.as<float>(), B.beta.as<float>(), XN, bf16 ? L->XNh.as<uint16_t>() : nullptr, d, rows);
+        X, B.gamma.as<float>(), B.beta.as<float>(), XN, XNh16, d, rows);
     PSSA_LAUNCH_CHECK("rmsnorm");
 
     // [delta | B | C | q_x | gate | adapter act] = x W_in^T with softplus,
@@ -242,6 +253,7 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
     e_in.out32 = P;
     e_in.ld32 = n_in;
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
+    if (l == 0 && first_in_done) PSSA_HIP_TRY(hipEventRecord(first_in_done, st));
     if (taps)
       PSSA_RETURN_IF(launch_copy_cols(st, P + o_act, n_in, L->tap_act.as<float>() + l * rows * r, r, rows, r));
 
@@ -258,7 +270,7 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
     sa.xn = XN;
     sa.ld_x = d;
     sa.rates2 = B.rates2.as<float>();
-    sa.carry = L->carry.as<float>() + l * (size_t)d * s;
+    sa.carry = carry + l * (size_t)d * s;
     sa.carry_stride = (long)(c.depth * (size_t)d * s);
     sa.y = Y;
     sa.ld_y = d;
@@ -266,10 +278,10 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
     sa.d = d;
     sa.s = s;
     sa.lanes = (int)n_lanes;
-    sa.y_part = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
+    sa.y_part = y_part;
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
     PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
-    if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, L->Yh.as<uint16_t>(), d, rows, d));
+    if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
 
     // q_euc = y W_qh^T + q_x.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));
@@ -369,17 +381,40 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   const void* hin = xlast;
   int ld_h = (int)(T * d);
   if (bf16) {
-    PSSA_RETURN_IF(launch_to_bf16(st, xlast, (int)(T * d), L->XNh.as<uint16_t>(), d, n_lanes, d));
-    hin = L->XNh.p;
+    PSSA_RETURN_IF(launch_to_bf16(st, xlast, (int)(T * d), XNh16, d, n_lanes, d));
+    hin = XNh16;
     ld_h = d;
   }
   EpiParams e_h;
   e_h.kind = EPI_SCALE;
   e_h.scale = logit_scale;
-  e_h.out32 = L->logits.as<float>();
+  e_h.out32 = logits;
   e_h.ld32 = V;
   PSSA_RETURN_IF(launch_gemm(st, dt, hin, ld_h, M->unembed.p, d, (int)n_lanes, V, d, e_h));
   return tm.finish();
+}
+
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
+  const hipStream_t st = L->ctx->stream;
+  const pssa_hip_config& c = L->model->cfg;
+  const int nz = ssm_state_blocks((int)c.d_state);
+  float* ypart = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
+  // Two lane groups on two streams: the VALU-bound scan of one group runs
+  // beside the MFMA-bound GEMMs of the other.  Group 1 starts once group 0's
+  // first input projection is issued, which keeps the two a stage apart.
+  if (!taps && !L->timing && L->aux_stream && n_lanes >= 2 && T >= 64) {
+    const size_t g0 = n_lanes / 2, g1 = n_lanes - g0;
+    PSSA_HIP_TRY(hipEventRecord(L->ev_fork, st));
+    PSSA_HIP_TRY(hipStreamWaitEvent(L->aux_stream, L->ev_fork, 0));
+    PSSA_RETURN_IF(prefill_view(L, st, 0, g0, T, false, false, L->ev_first, ypart));
+    PSSA_HIP_TRY(hipStreamWaitEvent(L->aux_stream, L->ev_first, 0));
+    float* ypart1 = ypart ? ypart + (size_t)nz * g0 * T * c.d_latent : nullptr;
+    PSSA_RETURN_IF(prefill_view(L, L->aux_stream, g0, g1, T, false, false, nullptr, ypart1));
+    PSSA_HIP_TRY(hipEventRecord(L->ev_join, L->aux_stream));
+    PSSA_HIP_TRY(hipStreamWaitEvent(st, L->ev_join, 0));
+    return Status::Ok();
+  }
+  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart);
 }
 
 }  // namespace pssa

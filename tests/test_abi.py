@@ -25,8 +25,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_links_no_oracle_and_no_torch():
     out = subprocess.run(["ldd", _abi.LIB_PATH], capture_output=True, text=True).stdout
-    assert "oracle" not in out and "torch" not in out and "c10" not in out
-    assert "amdhip64" in out
+    # Library names only (the hex load addresses can contain any substring).
+    names = [line.split()[0] for line in out.splitlines() if line.strip()]
+    assert not any(("oracle" in n or "torch" in n or n.startswith("libc10")) for n in names), names
+    assert any("amdhip64" in n for n in names), names
 
 
 def test_init_rejects_a_missing_device():

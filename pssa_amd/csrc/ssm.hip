@@ -31,7 +31,9 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
   __shared__ float sX[MAT_TC][64];
   __shared__ float sB[MAT_TC][4 * J];
   __shared__ float sC[MAT_TC][4 * J];
-  __shared__ float sY[4][MAT_TC][64];
+  constexpr int GS = J < 16 ? J : 16;  // readout group, as in the production scan
+  constexpr int NG = J / GS;
+  __shared__ float sY[4 * NG][MAT_TC][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i0 = blockIdx.x * 64;
@@ -78,33 +80,39 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
     for (int tt = 0; tt < steps; ++tt) {
       const float dl = sD[tt][lane];
       const float u = dl * sX[tt][lane];
-      // Readout as four partial sums over states j = p (mod 4), combined as
-      // (p0 + p1) + (p2 + p3): the production scan's order, so that a run of
-      // single-token steps equals one prefill bit for bit.
-      float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      // Readout in the production scan's order (groups of GS states, four
+      // partial sums each), so that a run of single-token steps equals one
+      // prefill bit for bit.
 #pragma unroll
-      for (int q = 0; q < J; ++q) {
-        const float bq = sB[tt][wave * J + q];
-        const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
-        h[q] = fmaf(ab, h[q], u * bq);
-        yp4[q & 3] = fmaf(h[q], sC[tt][wave * J + q], yp4[q & 3]);
-        const int j = jw + q;
-        if (MAT && ivalid && j < s) {
-          const size_t c = (size_t)i * s + j;
-          const size_t base = (size_t)b * T * ds + (size_t)(t0 + tt) * ds;
-          a.bar_a[base + c] = ab;
-          a.bar_b[base + c] = dl * bq;
-          a.states[(size_t)b * (T + 1) * ds + (size_t)(t0 + tt + 1) * ds + c] = h[q];
+      for (int g = 0; g < NG; ++g) {
+        float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int qq = 0; qq < GS; ++qq) {
+          const int q = g * GS + qq;
+          const float bq = sB[tt][wave * J + q];
+          const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
+          h[q] = fmaf(ab, h[q], u * bq);
+          yp4[qq & 3] = fmaf(h[q], sC[tt][wave * J + q], yp4[qq & 3]);
+          const int j = jw + q;
+          if (MAT && ivalid && j < s) {
+            const size_t c = (size_t)i * s + j;
+            const size_t base = (size_t)b * T * ds + (size_t)(t0 + tt) * ds;
+            a.bar_a[base + c] = ab;
+            a.bar_b[base + c] = dl * bq;
+            a.states[(size_t)b * (T + 1) * ds + (size_t)(t0 + tt + 1) * ds + c] = h[q];
+          }
         }
+        sY[wave * NG + g][tt][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
       }
-      sY[wave][tt][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }
     __syncthreads();
     for (int e = tid; e < steps * 64; e += 256) {
       const int tt = e >> 6, ii = e & 63;
       const int gi = i0 + ii;
       if (gi < d) {
-        const float v = ((sY[0][tt][ii] + sY[1][tt][ii]) + sY[2][tt][ii]) + sY[3][tt][ii];
+        float v = sY[0][tt][ii];
+#pragma unroll
+        for (int g = 1; g < 4 * NG; ++g) v += sY[g][tt][ii];
         const size_t r = row0 + t0 + tt;
         if (!MAT && a.y_part)
           a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + gi] = v;
@@ -129,27 +137,36 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 // the staging hides behind the recurrence.  Time steps past the end of a lane
 // read delta = x = 0: the update is then h <- exp2(0) h + 0 = h, so whole
 // chunks run unguarded and only the stores check t < T.  Per state the inner
-// loop batches G independent exponentials before the dependent FMAs, and the
-// readout sum over a wave's states runs as four interleaved partial sums.
+// loop batches GS independent exponentials before the dependent FMAs.
+//
+// NW waves of J states each cover one state block of NW*J states (128 for
+// J >= 32 with four waves and J = 16 with eight).  Every variant sums the
+// readout in the same order (readout_group_size): per group of GS states four
+// partial sums over j = p (mod 4), combined as (p0 + p1) + (p2 + p3), then the
+// group sums of the block added one after another in state order.  The
+// variant can therefore be chosen by occupancy alone without changing a bit
+// of the result, and a run of single-token steps still equals one prefill.
 constexpr int SSM_TC = 4;
 
-template <int J>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void ssm_scan_kernel(SsmArgs a) {
+template <int J, int NW, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void ssm_scan_kernel(SsmArgs a) {
   constexpr int TC = SSM_TC;
-  constexpr int G = J < 16 ? J : 16;
-  constexpr int NDX = TC * 64 / 256;        // delta/x values staged per thread
-  constexpr int NBC = (TC * 4 * J + 255) / 256;  // B/C values staged per thread
-  static_assert(NDX >= 1, "chunk too short");
+  constexpr int NT = NW * 64;
+  constexpr int GS = J < 16 ? J : 16;        // states per readout group
+  constexpr int NG = J / GS;                 // readout groups per wave
+  constexpr int SB = NW * J;                 // states per block
+  constexpr int NDX = (TC * 64 + NT - 1) / NT;  // delta/x values staged per thread
+  constexpr int NBC = (TC * SB + NT - 1) / NT;  // B/C values staged per thread
   __shared__ float sD[TC][64];
   __shared__ float sX[TC][64];
-  __shared__ __attribute__((aligned(16))) float sB[TC][4 * J];
-  __shared__ __attribute__((aligned(16))) float sC[TC][4 * J];
-  __shared__ float sY[4][TC][64];
+  __shared__ __attribute__((aligned(16))) float sB[TC][SB];
+  __shared__ __attribute__((aligned(16))) float sC[TC][SB];
+  __shared__ float sY[NW * NG][TC][64];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i0 = blockIdx.x * 64;
   const int b = blockIdx.y;
-  const int jb = blockIdx.z * 4 * J;
+  const int jb = blockIdx.z * SB;
   const int i = i0 + lane;
   const int jw = jb + wave * J;
   const bool ivalid = i < a.d;
@@ -170,18 +187,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   auto load = [&](int t0) {
 #pragma unroll
     for (int k = 0; k < NDX; ++k) {
-      const int e = tid + 256 * k;
+      const int e = tid + NT * k;
       const int t = t0 + (e >> 6), gi = i0 + (e & 63);
-      const bool ok = t < T && gi < d;
+      const bool ok = e < TC * 64 && t < T && gi < d;
       const size_t r = row0 + t;
       pd[k] = ok ? a.delta[r * a.ld_delta + gi] : 0.0f;
       px[k] = ok ? a.xn[r * a.ld_x + gi] : 0.0f;
     }
 #pragma unroll
     for (int k = 0; k < NBC; ++k) {
-      const int e = tid + 256 * k;
-      const int t = t0 + e / (4 * J), gj = jb + e % (4 * J);
-      const bool ok = e < TC * 4 * J && t < T && gj < s;
+      const int e = tid + NT * k;
+      const int t = t0 + e / SB, gj = jb + e % SB;
+      const bool ok = e < TC * SB && t < T && gj < s;
       const size_t r = row0 + t;
       pb[k] = ok ? a.bproj[r * a.ld_b + gj] : 0.0f;
       pc[k] = ok ? a.cproj[r * a.ld_c + gj] : 0.0f;
@@ -190,16 +207,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   auto store = [&]() {
 #pragma unroll
     for (int k = 0; k < NDX; ++k) {
-      const int e = tid + 256 * k;
-      sD[e >> 6][e & 63] = pd[k];
-      sX[e >> 6][e & 63] = px[k];
+      const int e = tid + NT * k;
+      if (e < TC * 64) {
+        sD[e >> 6][e & 63] = pd[k];
+        sX[e >> 6][e & 63] = px[k];
+      }
     }
 #pragma unroll
     for (int k = 0; k < NBC; ++k) {
-      const int e = tid + 256 * k;
-      if (e < TC * 4 * J) {
-        sB[e / (4 * J)][e % (4 * J)] = pb[k];
-        sC[e / (4 * J)][e % (4 * J)] = pc[k];
+      const int e = tid + NT * k;
+      if (e < TC * SB) {
+        sB[e / SB][e % SB] = pb[k];
+        sC[e / SB][e % SB] = pc[k];
       }
     }
   };
@@ -214,30 +233,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
       const float u = dl * sX[tt][lane];
       const float* bt = &sB[tt][wave * J];
       const float* ct = &sC[tt][wave * J];
-      float yp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int g0 = 0; g0 < J; g0 += G) {
-        float ab[G];
+      for (int g = 0; g < NG; ++g) {
+        const int g0 = g * GS;
+        float ab[GS];
+        float yp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int q = 0; q < G; ++q) ab[q] = dl * r2[g0 + q];
+        for (int q = 0; q < GS; ++q) ab[q] = dl * r2[g0 + q];
 #pragma unroll
-        for (int q = 0; q < G; ++q) ab[q] = __builtin_amdgcn_exp2f(ab[q]);
+        for (int q = 0; q < GS; ++q) ab[q] = __builtin_amdgcn_exp2f(ab[q]);
 #pragma unroll
-        for (int q = 0; q < G; ++q) h[g0 + q] = fmaf(ab[q], h[g0 + q], u * bt[g0 + q]);
+        for (int q = 0; q < GS; ++q) h[g0 + q] = fmaf(ab[q], h[g0 + q], u * bt[g0 + q]);
 #pragma unroll
-        for (int q = 0; q < G; ++q) yp[q & 3] = fmaf(h[g0 + q], ct[g0 + q], yp[q & 3]);
+        for (int q = 0; q < GS; ++q) yp[q & 3] = fmaf(h[g0 + q], ct[g0 + q], yp[q & 3]);
+        sY[wave * NG + g][tt][lane] = (yp[0] + yp[1]) + (yp[2] + yp[3]);
       }
-      sY[wave][tt][lane] = (yp[0] + yp[1]) + (yp[2] + yp[3]);
     }
     __syncthreads();
-    // Four waves' partial sums over j, added in a fixed order.
 #pragma unroll
     for (int k = 0; k < NDX; ++k) {
-      const int e = tid + 256 * k;
+      const int e = tid + NT * k;
       const int tt = e >> 6, gi = i0 + (e & 63);
       const int t = t0 + tt;
-      if (t < T && gi < d) {
-        const float v = ((sY[0][tt][e & 63] + sY[1][tt][e & 63]) + sY[2][tt][e & 63]) + sY[3][tt][e & 63];
+      if (e < TC * 64 && t < T && gi < d) {
+        float v = sY[0][tt][e & 63];
+#pragma unroll
+        for (int g = 1; g < NW * NG; ++g) v += sY[g][tt][e & 63];
         const size_t r = row0 + t;
         if (a.y_part)
           a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + gi] = v;
@@ -277,15 +298,26 @@ int ssm_state_blocks(int s) {
 
 bool ssm_needs_zeroed_y(int s) { return ssm_state_blocks(s) == 2; }
 
+// Workgroups at which the four-wave J = 32 scan holds three waves per SIMD on
+// the 256 CUs; below that the eight-wave J = 16 variant (same state blocks,
+// twice the waves, half the registers per lane) keeps the SIMDs fed.
+constexpr long kScanFullGrid = 768;
+
 template <int J>
 static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   dim3 grid((a.d + 63) / 64, a.lanes, (a.s + 4 * J - 1) / (4 * J));
-  if (mat)
+  if (mat) {
     ssm_materialize_kernel<J, true><<<grid, 256, 0, stream>>>(a);
-  else if (a.T < SSM_TC)
+  } else if (a.T < SSM_TC) {
     ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);
-  else
-    ssm_scan_kernel<J><<<grid, 256, 0, stream>>>(a);
+  } else if constexpr (J == 32) {
+    if ((long)grid.x * grid.y * grid.z < kScanFullGrid)
+      ssm_scan_kernel<16, 8, 4><<<grid, 512, 0, stream>>>(a);
+    else
+      ssm_scan_kernel<32, 4, 3><<<grid, 256, 0, stream>>>(a);
+  } else {
+    ssm_scan_kernel<J, 4, 3><<<grid, 256, 0, stream>>>(a);
+  }
 }
 
 Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a_in) {

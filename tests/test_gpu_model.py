@@ -108,6 +108,32 @@ def test_token_loop_equals_prefill_bitwise(hip):
         layer.close()
 
 
+def test_scan_variants_keep_token_loop_identity(hip):
+    """d_state=256 at d_latent=768, 32 lanes: a 5-token prefill runs the
+    four-wave J=32 scan (one stream, 768 workgroups), a following 67-token
+    prefill the two lane groups with the eight-wave J=16 scan, and single
+    tokens the short kernel.  All three sum the readout in one order, so the
+    prefill/decode identity holds across them (src/inference.rs:1069-1113
+    checks lengths 1 .. 1024 without resets in between)."""
+    say("scan variants token loop == prefill")
+    cfg = PSSAConfig(depth=1, d_vocab=64, d_latent=768, d_state=256, d_mem_key=8, mem_capacity=16)
+    w = ModelWeights.init(cfg, 7, "baseline")
+    w.populate_banks(8, count=12)
+    lanes = 32
+    rng = np.random.default_rng(4)
+    a = PSSALayer(hip, w, lanes=lanes, max_tokens=lanes * 67)
+    b = PSSALayer(hip, w, lanes=lanes, max_tokens=lanes * 67)
+    for T in (5, 67, 1):
+        ids = rng.integers(0, cfg.d_vocab, (lanes, T), dtype=np.uint32)
+        la = a.prefill_inference(ids)
+        for t in range(T):
+            lb = b.forward_inference(ids[:, t])
+        np.testing.assert_array_equal(la, lb)
+        np.testing.assert_array_equal(a.get_carry(), b.get_carry())
+    a.close()
+    b.close()
+
+
 def test_invalid_ids_fail_before_anything_runs(hip):
     say("invalid ids")
     cfg = PSSAConfig(depth=1, d_vocab=10, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=4)

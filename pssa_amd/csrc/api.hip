@@ -145,6 +145,7 @@ void pssa_hip_destroy(pssa_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->stream);
   }
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
   delete ctx;
 }
 
@@ -476,6 +477,29 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
   return pssa::finish(body(), err, err_len);
 }
 
+}  // extern "C"
+
+// Points ra.scratch at the context's scratch, grown to what the launch needs.
+// Called with ctx->mu held; the previous buffer is released only once the
+// stream has drained.
+static Status bind_retrieve_scratch(pssa_hip_ctx* ctx, pssa::RetrieveArgs& ra) {
+  const size_t need_bytes = pssa::retrieve_scratch_bytes(ra);
+  if (!need_bytes) return Status::Ok();
+  if (ctx->scratch_bytes < need_bytes) {
+    PSSA_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->scratch) PSSA_HIP_TRY(hipFree(ctx->scratch));
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    PSSA_HIP_TRY(hipMalloc(&ctx->scratch, need_bytes));
+    ctx->scratch_bytes = need_bytes;
+  }
+  ra.scratch = ctx->scratch;
+  ra.scratch_bytes = ctx->scratch_bytes;
+  return Status::Ok();
+}
+
+extern "C" {
+
 int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
                       const float* norm_sq, const float* values, size_t capacity, size_t count,
                       size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
@@ -521,6 +545,7 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
     ra.out_val = dval.as<float>();
     ra.out_min = out_min ? dmin.as<float>() : nullptr;
     ra.out_idx = out_idx ? didx.as<uint32_t>() : nullptr;
+    PSSA_RETURN_IF(bind_retrieve_scratch(ctx, ra));
     PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
     PSSA_RETURN_IF(download(out_val, dval, n_q * d_val * 4, st));
     if (out_min) PSSA_RETURN_IF(download(out_min, dmin, n_q * 4, st));
@@ -565,6 +590,7 @@ int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n
     ra.out_val = d_out_val;
     ra.out_min = d_out_min;
     ra.out_idx = d_out_idx;
+    PSSA_RETURN_IF(bind_retrieve_scratch(ctx, ra));
     return pssa::launch_retrieve(ctx->stream, ra);
   };
   return pssa::finish(body(), err, err_len);

@@ -129,4 +129,8 @@ struct pssa_hip_ctx {
   std::string name;
   int cu_count = 0;
   std::mutex mu;
+  // Kernel scratch reused across calls (grown on demand, freed with the
+  // context); calls on one context are serialised by `mu` on one stream.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
 };

@@ -22,7 +22,14 @@ struct RetrieveArgs {
   float* out_val = nullptr;     // [n, dv] (top-k readout)
   float* out_min = nullptr;     // optional [n]
   uint32_t* out_idx = nullptr;  // optional [n, top_k], ascending slot order
+  // Device scratch for the ranked top-k path (retrieve_scratch_bytes); when
+  // absent or too small the general kernel runs instead.
+  void* scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
+
+// Scratch the ranked top-k path needs for these arguments (0: not taken).
+size_t retrieve_scratch_bytes(const RetrieveArgs& a);
 
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a);
 // One-time per-device set-up a later launch_retrieve with these arguments

@@ -8,6 +8,7 @@
 // (src/memory.rs:181-262).  The softmax weights and the value mix are fp32.
 #include "memory.h"
 
+#include <algorithm>
 #include <cfloat>
 
 namespace pssa {
@@ -346,6 +347,560 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Exact top-k read for wide keys: the search is pruned on the matrix cores
+// and decided in the reference's own f64 arithmetic.
+//
+// 1. ranked_dot_kernel: dot products q.k for all queries x occupied slots
+//    from bf16 MFMAs on split operands, x = x_hi + x_lo (x_hi = bf16(x),
+//    x_lo = bf16(x - x_hi), |x - x_hi - x_lo| <= 2^-18 |x|), summing
+//    hi*hi + lo*hi + hi*lo in fp32.  Their error is at most
+//    RK_DOT_ERR * |q| |k| (split remainder ~3 * 2^-18 plus fp32 accumulation
+//    of 3 * d_key products, ~(3 d_key + 48) * 2^-24 for d_key <= 1024, both
+//    doubled for margin).
+// 2. ranked_pick_kernel, per query: z_s = |q - k_s|^2 / (1 - |k_s|^2) orders
+//    the slots exactly like the reference's distance (2 asinh(sqrt(z_s /
+//    (1 - |q|^2))) is monotone in z_s; the f32 rounding of the distance can
+//    only merge neighbours).  From |q - k|^2 = |q|^2 + |k|^2 - 2 q.k the bound
+//    gives an interval [L_s, U_s] around z_s.  T is the top_k-th smallest of
+//    the 64 per-lane minima of U (each lane holds every 64th slot), so at
+//    least top_k slots have z <= T, and every slot of the exact top_k by
+//    (distance bits, slot) has L_s <= T (1 + RK_TIE) (the slack covers slots
+//    whose larger z rounds to the same f32 distance).  Those are the
+//    candidates -- about top_k + 1 per query at the benchmark shape.
+// 3. The candidates' distances are recomputed exactly as in
+//    poincare_distance (sequential f64 sum, no fused multiply-add, Rust's
+//    asinh), one job per thread, together with one sequential |q|^2 chain
+//    per query (squared_norm).  The workgroup's query rows and the distinct
+//    candidate keys pass through LDS in 32-dimension chunks.
+// 4. Selection by (distance bits, slot) through ranks counted over the
+//    candidates, softmax over the selected distances, and the value readout
+//    in ascending slot order, as retrieve_soft_into (src/memory.rs:344-407).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int RK_SLOTS = 512;            // occupied slots handled
+constexpr int RK_BK = 32;                // key dimensions per slab and per exact chunk
+constexpr int RK_MAX_DK = 1024;
+constexpr int RK_THREADS = 512;
+constexpr int RK_TQ = 256, RK_TS = 256;  // dot tile: queries x slots
+constexpr int RK_CHUNK = 32768;          // queries per dot/pick pass (scratch rows)
+constexpr double RK_DOT_ERR = 4e-4;
+constexpr double RK_TIE = 1.0 / 4096.0;
+
+__device__ __forceinline__ int rk_swizzle(int r) { return (((r & 15) >> 1) ^ ((r & 15) >> 3)) & 3; }
+__device__ __forceinline__ uint32_t rk_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+struct RankedScratch {
+  uint16_t* khi;  // [RK_SLOTS][dkp] bf16 hi parts (zero past count and past d_key)
+  uint16_t* klo;  // [RK_SLOTS][dkp] bf16 lo parts
+  double* kk;     // [RK_SLOTS] |k|^2 (any order)
+  double* kn;     // [RK_SLOTS] |k|
+  double* rk;     // [RK_SLOTS] 1 / (1 - norm_sq) with the stored f32 norm_sq
+  float* zdot;    // [RK_CHUNK][RK_SLOTS] approximate q.k
+  double* qq;     // [RK_CHUNK] |q|^2 (any order)
+};
+
+__host__ __device__ inline int ranked_dkp(int dk) { return (dk + RK_BK - 1) / RK_BK * RK_BK; }
+
+static size_t ranked_scratch_bytes(int dk) {
+  return (size_t)RK_SLOTS * ranked_dkp(dk) * 2 * sizeof(uint16_t) + 3 * RK_SLOTS * sizeof(double) +
+         (size_t)RK_CHUNK * RK_SLOTS * sizeof(float) + (size_t)RK_CHUNK * sizeof(double);
+}
+
+static RankedScratch ranked_scratch(void* base, int dk) {
+  const size_t row = (size_t)RK_SLOTS * ranked_dkp(dk);
+  RankedScratch s;
+  s.khi = static_cast<uint16_t*>(base);
+  s.klo = s.khi + row;
+  s.kk = reinterpret_cast<double*>(s.klo + row);
+  s.kn = s.kk + RK_SLOTS;
+  s.rk = s.kn + RK_SLOTS;
+  s.zdot = reinterpret_cast<float*>(s.rk + RK_SLOTS);
+  s.qq = reinterpret_cast<double*>(s.zdot + (size_t)RK_CHUNK * RK_SLOTS);
+  return s;
+}
+
+__global__ __launch_bounds__(256) void ranked_prep_kernel(RetrieveArgs a, RankedScratch sc) {
+  __shared__ double part[256];
+  const int s = blockIdx.x, dkp = ranked_dkp(a.dk);
+  const bool live = s < a.count;
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < dkp; i += 256) {
+    const float x = (live && i < a.dk) ? a.keys[(size_t)s * a.dk + i] : 0.0f;
+    const uint32_t hb = rk_bf16(x);
+    const float lo = x - __uint_as_float(hb << 16);
+    sc.khi[(size_t)s * dkp + i] = (uint16_t)hb;
+    sc.klo[(size_t)s * dkp + i] = (uint16_t)rk_bf16(lo);
+    acc += (double)x * (double)x;
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    sc.kk[s] = part[0];
+    sc.kn[s] = sqrt(part[0]);
+    sc.rk[s] = live ? 1.0 / (1.0 - (double)a.norm_sq[s]) : 0.0;
+  }
+}
+
+// ---- 1. approximate dot products ------------------------------------------
+// A 512-thread workgroup computes a 256-query x 256-slot tile; wave w owns
+// queries (w & 1) * 128 .. +128 and slots (w >> 1) * 64 .. +64 (4 x 2 MFMA
+// 32x32 tiles).  Key slabs (pre-split) move global -> LDS directly; query
+// slabs are loaded as fp32, split into hi/lo in registers and stored.  Two
+// slab stages; 64-byte slab rows with the 16-byte chunk index XOR-swizzled.
+constexpr int RD_A = RK_TQ * RK_BK * 2;          // bytes of one bf16 query slab (hi or lo)
+constexpr int RD_B = RK_TS * RK_BK * 2;          // bytes of one bf16 key slab
+constexpr int RD_STAGE = 2 * RD_A + 2 * RD_B;
+constexpr int RD_LDS = 2 * RD_STAGE;
+static_assert(RD_LDS <= 160 * 1024, "LDS budget");
+
+__global__ __launch_bounds__(RK_THREADS) void ranked_dot_kernel(RetrieveArgs a, RankedScratch sc, int q0, int nq) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char rd_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int wq = wave & 1, ws = wave >> 1;
+  const int qb = blockIdx.x * RK_TQ, sb = blockIdx.y * RK_TS;
+  const int dk = a.dk, dkp = ranked_dkp(dk);
+
+  // Query staging: thread -> rows tid/8 + 64p, four dimensions at (tid%8)*4.
+  const int ar = tid >> 3, ac = (tid & 7) * 4;
+  const float* qsrc[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) qsrc[p] = a.q + (size_t)(q0 + min(qb + ar + 64 * p, nq - 1)) * a.ld_q;
+  float4 qv[4];
+  double qpart[4] = {0.0, 0.0, 0.0, 0.0};
+  auto load_q = [&](int k0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      qv[p] = (k0 + ac < dk) ? *reinterpret_cast<const float4*>(qsrc[p] + k0 + ac) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto store_q = [&](int stage) {
+    uint16_t* ahi = reinterpret_cast<uint16_t*>(rd_smem + stage * RD_STAGE);
+    uint16_t* alo = reinterpret_cast<uint16_t*>(rd_smem + stage * RD_STAGE + RD_A);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float x[4] = {qv[p].x, qv[p].y, qv[p].z, qv[p].w};
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[e] = rk_bf16(x[e]);
+        l[e] = rk_bf16(x[e] - __uint_as_float(h[e] << 16));
+        qpart[p] += (double)x[e] * (double)x[e];
+      }
+      const int row = ar + 64 * p;
+      const int off = row * RK_BK + (((ac >> 3) ^ rk_swizzle(row)) << 3) + (ac & 7);
+      *reinterpret_cast<uint2*>(ahi + off) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      *reinterpret_cast<uint2*>(alo + off) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+    }
+  };
+  // Key slabs: 16 rows of 64 bytes per wave instruction, two per array.
+  const int lr = lane >> 2, pc = lane & 3;
+  auto issue_b = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < RK_TS / 16 / 8; ++i) {
+      const int row = (wave + 8 * i) * 16 + lr;
+      const int lc = pc ^ rk_swizzle(row);
+      const size_t src = (size_t)(sb + row) * dkp + k0 + lc * 8;
+      unsigned char* base = rd_smem + stage * RD_STAGE + 2 * RD_A + (wave + 8 * i) * 16 * RK_BK * 2;
+      __builtin_amdgcn_global_load_lds((const void*)(sc.khi + src),
+                                       (__attribute__((address_space(3))) void*)base, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(sc.klo + src),
+                                       (__attribute__((address_space(3))) void*)(base + RD_B), 16, 0, 0);
+    }
+  };
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[t][u][i] = 0.0f;
+
+  const int nk = dkp / RK_BK;
+  issue_b(0, 0);
+  load_q(0);
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0)
+  store_q(0);
+  const int fr = rk_swizzle(l32);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+    // This wave's slab loads and LDS stores are complete; meet the others.
+    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8));  // vmcnt(0) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + 1 < nk) {
+      issue_b(st ^ 1, (kt + 1) * RK_BK);
+      load_q((kt + 1) * RK_BK);
+    }
+    const uint16_t* ahi = reinterpret_cast<const uint16_t*>(rd_smem + st * RD_STAGE);
+    const uint16_t* alo = ahi + RK_TQ * RK_BK;
+    const uint16_t* bhi = alo + RK_TQ * RK_BK;
+    const uint16_t* blo = bhi + RK_TS * RK_BK;
+#pragma unroll
+    for (int kk = 0; kk < RK_BK / 16; ++kk) {
+      const int ch = (kk * 2 + half) ^ fr;
+      bf16x8_t fbh[2], fbl[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int brow = (ws * 64 + u * 32 + l32) * RK_BK + ch * 8;
+        fbh[u] = *reinterpret_cast<const bf16x8_t*>(bhi + brow);
+        fbl[u] = *reinterpret_cast<const bf16x8_t*>(blo + brow);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int arow = (wq * 128 + t * 32 + l32) * RK_BK + ch * 8;
+        const bf16x8_t fah = *reinterpret_cast<const bf16x8_t*>(ahi + arow);
+        const bf16x8_t fal = *reinterpret_cast<const bf16x8_t*>(alo + arow);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fbh[u], fah, acc[t][u], 0, 0, 0);
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fbl[u], fah, acc[t][u], 0, 0, 0);
+          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fbh[u], fal, acc[t][u], 0, 0, 0);
+        }
+      }
+    }
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));  // vmcnt(0): the query slab
+      store_q(st ^ 1);
+    }
+  }
+  // |q|^2 per row (the slot-half-0 workgroups): eight adjacent lanes per row.
+  if (blockIdx.y == 0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      double v = qpart[p];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      const int row = qb + ar + 64 * p;
+      if ((tid & 7) == 0 && row < nq) sc.qq[row] = v;
+    }
+  }
+  // Accumulator layout (keys as the first operand): lane l holds query
+  // tile row l%32 and slots 8*(i/4) + 4*(l/32) + i%4.
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int row = qb + wq * 128 + t * 32 + l32;
+    if (row < nq) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int slot = sb + ws * 64 + u * 32 + 8 * g + 4 * half;
+          *reinterpret_cast<float4*>(sc.zdot + (size_t)row * RK_SLOTS + slot) =
+              make_float4(acc[t][u][4 * g], acc[t][u][4 * g + 1], acc[t][u][4 * g + 2], acc[t][u][4 * g + 3]);
+        }
+    }
+  }
+}
+
+// ---- 2-4. candidates, exact distances, selection, readout -----------------
+// One wave per query, no workgroup-wide synchronisation.
+//  - Candidates: the bounds of every slot from the approximate dot product;
+//    T = the top_k-th smallest of the 64 per-lane minima of U.
+//  - Distances of the candidates: |q - k|^2 summed in f64 across the wave
+//    (coalesced rows, any order).  The reference's sequential sum and this
+//    one are both within (d_key - 1) * 2^-53 (relative) of the exact sum of
+//    the same nonnegative terms, so the two differ by at most RQ_SUM_REL; the
+//    distance's relative sensitivity to the sum is at most 1/2.  When the f32
+//    rounding of the distance is the same at both ends of that interval it
+//    equals the reference's; otherwise (rare) the wave runs the sequential
+//    sum itself.  |q|^2 (squared_norm, with its clamp below 1) likewise.
+//  - Ranks by (distance bits, slot) counted over the candidates; softmax and
+//    value readout in ascending slot order.
+constexpr int RQ_WAVES = 4;                    // independent waves per workgroup
+constexpr int RQ_V = RK_MAX_DK / 256;          // float4 per lane for one row
+constexpr int RQ_QPW = 4;                      // queries per wave
+constexpr int RQ_G = 2;                        // candidate rows per step
+constexpr double RQ_SUM_REL = 4e-13;           // >= 2 * 1024 * 2^-53, with margin
+constexpr double RQ_DIST_REL = 4e-13;          // distance interval (relative)
+
+// The reference's sequential f64 sum over a row distributed as lane l holding
+// dimensions 256 v + 4 l + e: sum of (x - y)^2 in dimension order.
+__device__ double rq_sequential(const float (&x)[RQ_V * 4], const float (&y)[RQ_V * 4], int dk) {
+  double acc = 0.0;
+#pragma unroll
+  for (int v = 0; v < RQ_V; ++v) {
+    for (int l = 0; l < 64; ++l) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+        const int i = 256 * v + 4 * l + e;
+        if (i < dk) {
+          const float xv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[4 * v + e]), l));
+          const float yv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(y[4 * v + e]), l));
+          const double t = (double)xv - (double)yv;
+          acc = acc + t * t;
+        }
+      }
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ double wave_min_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float rq_qsq(double qs) {
+  float f = (float)qs;
+  if (qs < 1.0 && f == 1.0f) f = __uint_as_float(0x3f7fffffu);
+  return f;
+}
+
+__global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs a, RankedScratch sc, int q0, int nq,
+                                                                    int vec_out) {
+  __shared__ uint16_t s_cand[RQ_WAVES][RK_SLOTS];
+  __shared__ unsigned long long s_key[RQ_WAVES][RK_SLOTS];
+  __shared__ uint32_t s_sel[RQ_WAVES][kMaxTopK];
+  __shared__ float s_selw[RQ_WAVES][kMaxTopK];
+  __shared__ double s_lmin[RQ_WAVES][64];
+  __shared__ double s_sq[RQ_WAVES][RK_SLOTS];
+  __shared__ float s_min[RQ_WAVES];
+  constexpr int SPL = RK_SLOTS / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dk = a.dk, cnt = a.count, K = a.top_k;
+  uint16_t* cand = s_cand[wave];
+  unsigned long long* ckey = s_key[wave];
+  uint32_t* sel = s_sel[wave];
+  float* selw = s_selw[wave];
+  double* csq = s_sq[wave];
+
+  const int row0 = (blockIdx.x * RQ_WAVES + wave) * RQ_QPW;
+  for (int row = row0; row < min(row0 + RQ_QPW, nq); ++row) {
+    const size_t n = (size_t)q0 + row;
+    // ---- candidates ----
+    const double qq = sc.qq[row], qn = sqrt(qq);
+    double L[SPL];
+    double lm = HUGE_VAL;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      const int s = lane + 64 * j;
+      L[j] = HUGE_VAL;
+      if (s < cnt) {
+        const double kk = sc.kk[s];
+        const double sqt = qq + kk - 2.0 * (double)sc.zdot[(size_t)row * RK_SLOTS + s];
+        const double e = 2.0 * RK_DOT_ERR * qn * sc.kn[s] + 1e-12 * (qq + kk);
+        L[j] = (sqt - e) * sc.rk[s];
+        lm = fmin(lm, (sqt + e) * sc.rk[s]);
+      }
+    }
+    s_lmin[wave][lane] = lm;
+    wave_sync();
+    int le = 0;
+    for (int l2 = 0; l2 < 64; ++l2) le += s_lmin[wave][l2] <= lm;
+    const double lim = wave_min_f64(le >= K ? lm : HUGE_VAL) * (1.0 + RK_TIE);
+    int m = 0;
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      const bool c = lane + 64 * j < cnt && L[j] <= lim;
+      const unsigned long long b = __ballot(c);
+      if (c) cand[m + __popcll(b & ((1ull << lane) - 1ull))] = (uint16_t)(lane + 64 * j);
+      m += __popcll(b);
+    }
+    // ---- the query row (f64) and |q|^2 ----
+    const float* qrow = a.q + n * a.ld_q;
+    double qd[RQ_V * 4];
+    double qs = 0.0;
+#pragma unroll
+    for (int v = 0; v < RQ_V; ++v) {
+      const int i = 256 * v + 4 * lane;
+      const float4 x = i < dk ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qd[4 * v] = x.x, qd[4 * v + 1] = x.y, qd[4 * v + 2] = x.z, qd[4 * v + 3] = x.w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qs = fma(qd[4 * v + e], qd[4 * v + e], qs);
+    }
+    qs = wave_sum_f64(qs);
+    float q_sq = rq_qsq(qs);
+    if (rq_qsq(qs * (1.0 - RQ_SUM_REL)) != rq_qsq(qs * (1.0 + RQ_SUM_REL))) {
+      float qf[RQ_V * 4], zero[RQ_V * 4];
+#pragma unroll
+      for (int e = 0; e < RQ_V * 4; ++e) qf[e] = (float)qd[e], zero[e] = 0.0f;
+      q_sq = rq_qsq(rq_sequential(qf, zero, dk));
+    }
+    // ---- candidate sums |q - k|^2 across the wave, RQ_G rows at a time ----
+    for (int c0 = 0; c0 < m; c0 += RQ_G) {
+      float kf[RQ_G][RQ_V * 4];
+#pragma unroll
+      for (int g = 0; g < RQ_G; ++g) {
+        const float* krow = a.keys + (size_t)cand[min(c0 + g, m - 1)] * dk;
+#pragma unroll
+        for (int v = 0; v < RQ_V; ++v) {
+          const int i = 256 * v + 4 * lane;
+          const float4 y = i < dk ? *reinterpret_cast<const float4*>(krow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+          kf[g][4 * v] = y.x, kf[g][4 * v + 1] = y.y, kf[g][4 * v + 2] = y.z, kf[g][4 * v + 3] = y.w;
+        }
+      }
+      double sq[RQ_G];
+#pragma unroll
+      for (int g = 0; g < RQ_G; ++g) {
+        double acc = 0.0;
+#pragma unroll
+        for (int e = 0; e < RQ_V * 4; ++e) {
+          const double t = qd[e] - (double)kf[g][e];
+          acc = fma(t, t, acc);
+        }
+        sq[g] = wave_sum_f64(acc);
+      }
+      if (lane == 0)
+#pragma unroll
+        for (int g = 0; g < RQ_G; ++g)
+          if (c0 + g < m) csq[c0 + g] = sq[g];
+    }
+    wave_sync();
+    // ---- candidate distances, one candidate per lane; the rare ambiguous
+    // rounding is settled by the sequential sum ----
+    for (int cb = 0; cb < m; cb += 64) {
+      const int c = cb + lane;
+      bool ok = true;
+      double den = 1.0;
+      uint32_t slot = 0;
+      if (c < m) {
+        slot = cand[c];
+        den = (1.0 - (double)q_sq) * (1.0 - (double)a.norm_sq[slot]);
+        const double r = 2.0 * rust_asinh(sqrt(csq[c] / den));
+        const double dr = RQ_DIST_REL * r;
+        ok = (float)(r - dr) == (float)(r + dr);
+        ckey[c] = ((unsigned long long)__float_as_uint((float)r) << 32) | slot;
+      }
+      unsigned long long redo = __ballot(!ok);
+      while (redo) {
+        const int l = __ffsll((long long)redo) - 1;
+        redo &= redo - 1;
+        const uint32_t s2 = cand[cb + l];
+        float qf[RQ_V * 4], kf[RQ_V * 4];
+#pragma unroll
+        for (int v = 0; v < RQ_V; ++v) {
+          const int i = 256 * v + 4 * lane;
+          const bool in = i < dk;
+          const float4 x = in ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+          const float4 y = in ? *reinterpret_cast<const float4*>(a.keys + (size_t)s2 * dk + i)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+          qf[4 * v] = x.x, qf[4 * v + 1] = x.y, qf[4 * v + 2] = x.z, qf[4 * v + 3] = x.w;
+          kf[4 * v] = y.x, kf[4 * v + 1] = y.y, kf[4 * v + 2] = y.z, kf[4 * v + 3] = y.w;
+        }
+        const double sq2 = rq_sequential(qf, kf, dk);
+        const double den2 = (1.0 - (double)q_sq) * (1.0 - (double)a.norm_sq[s2]);
+        const float dist = (float)(2.0 * rust_asinh(sqrt(sq2 / den2)));
+        if (lane == 0) ckey[cb + l] = ((unsigned long long)__float_as_uint(dist) << 32) | s2;
+      }
+    }
+    wave_sync();
+    if (lane < K) {
+      sel[lane] = 0xFFFFFFFFu;
+      selw[lane] = 0.0f;
+    }
+    wave_sync();
+    // ---- selection: ranks over the candidates, positions in slot order ----
+    int nsel_before = 0;
+    for (int cb = 0; cb < m; cb += 64) {
+      const int c = cb + lane;
+      const unsigned long long key = c < m ? ckey[c] : ~0ull;
+      int rank = 0;
+      if (c < m)
+        for (int c2 = 0; c2 < m; ++c2) rank += ckey[c2] < key;
+      const bool chosen = c < m && rank < K;
+      if (c < m && rank == 0) s_min[wave] = __uint_as_float((uint32_t)(key >> 32));
+      const unsigned long long b = __ballot(chosen);
+      if (chosen) {
+        const int pos = nsel_before + __popcll(b & ((1ull << lane) - 1ull));
+        sel[pos] = (uint32_t)(key & 0xFFFFFFFFull);
+        selw[pos] = __uint_as_float((uint32_t)(key >> 32));  // the distance, for now
+      }
+      nsel_before += __popcll(b);
+    }
+    wave_sync();
+    const float min_dist = s_min[wave];
+    const float ev = lane < K && sel[lane] != 0xFFFFFFFFu ? expf((min_dist - selw[lane]) / a.tau) : 0.0f;
+    wave_sync();
+    if (lane < K) selw[lane] = ev;
+    wave_sync();
+    float sum = 0.0f;
+    for (int t = 0; t < K; ++t) sum += selw[t];
+    wave_sync();
+    if (lane < K) selw[lane] = ev / sum;
+    wave_sync();
+    if (a.out_min && lane == 0) a.out_min[n] = min_dist;
+    if (a.out_idx && lane < K) a.out_idx[n * K + lane] = sel[lane];
+    if (a.weights || a.weights16) {
+      for (int s = lane; s < a.capacity; s += 64) {
+        float w = 0.0f;
+        for (int t = 0; t < K; ++t)
+          if (sel[t] == (uint32_t)s) w = selw[t];
+        put_weight(a, (int)n, s, w);
+      }
+    }
+    // ---- value readout in ascending slot order, eight rows fetched together ----
+    if (a.out_val) {
+      const int dv = a.dv;
+      if (vec_out) {
+        for (int j4 = lane; j4 < dv / 4; j4 += 64) {
+#pragma clang fp contract(off)
+          float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+          for (int t0 = 0; t0 < K; t0 += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const uint32_t s = t0 + u < K ? sel[t0 + u] : 0u;
+              v[u] = *reinterpret_cast<const float4*>(a.values + (size_t)min(s, (uint32_t)cnt - 1) * dv + 4 * j4);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int t = t0 + u;
+              if (t < K && sel[t] < (uint32_t)cnt) {
+                const float w = selw[t];
+                o.x = o.x + w * v[u].x;
+                o.y = o.y + w * v[u].y;
+                o.z = o.z + w * v[u].z;
+                o.w = o.w + w * v[u].w;
+              }
+            }
+          }
+          *reinterpret_cast<float4*>(a.out_val + n * dv + 4 * j4) = o;
+        }
+      } else {
+        for (int j = lane; j < dv; j += 64) {
+#pragma clang fp contract(off)
+          float o = 0.0f;
+          for (int t = 0; t < K; ++t) {
+            const uint32_t s = sel[t];
+            const float v = a.values[(size_t)min(s, (uint32_t)cnt - 1) * dv + j];
+            if (s < (uint32_t)cnt) o = o + selw[t] * v;
+          }
+          a.out_val[n * dv + j] = o;
+        }
+      }
+    }
+    wave_sync();
+  }
+}
+
+static bool ranked_read_fits(const RetrieveArgs& a) {
+  return a.top_k > 0 && !a.count_dev && a.top_k < a.count && a.count <= RK_SLOTS && !a.project &&
+         !a.q_pnc && !a.q_norm && a.dk % 4 == 0 && a.dk <= RK_MAX_DK && a.ld_q % 4 == 0 &&
+         ((uintptr_t)a.q & 15) == 0 && ((uintptr_t)a.keys & 15) == 0;
+}
+
+size_t retrieve_scratch_bytes(const RetrieveArgs& a) {
+  return ranked_read_fits(a) ? ranked_scratch_bytes(a.dk) : 0;
+}
+
 static bool soft_read_fits(const RetrieveArgs& a) {
   return (a.top_k == 0 || (!a.count_dev && a.top_k >= a.count)) && a.project && !a.q_norm && !a.out_val &&
          !a.out_min && !a.out_idx && a.dk <= SOFT_MAX_DK && a.capacity <= 64 * SOFT_SPL &&
@@ -362,6 +917,8 @@ static Status allow_large_lds() {
   std::lock_guard<std::mutex> g(mu);
   if (dev >= 0 && dev < 64 && done[dev]) return Status::Ok();
   PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&soft_read_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&ranked_dot_kernel),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   if (dev >= 0 && dev < 64) done[dev] = true;
   return Status::Ok();
@@ -389,6 +946,23 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
     if (blocks > 512) blocks = 512;
     soft_read_kernel<<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);
     PSSA_LAUNCH_CHECK("soft_read");
+    return Status::Ok();
+  }
+  if (ranked_read_fits(a) && a.scratch && a.scratch_bytes >= retrieve_scratch_bytes(a)) {
+    PSSA_RETURN_IF(allow_large_lds());
+    const RankedScratch sc = ranked_scratch(a.scratch, a.dk);
+    ranked_prep_kernel<<<RK_SLOTS, 256, 0, stream>>>(a, sc);
+    PSSA_LAUNCH_CHECK("ranked_prep");
+    const int vec_out = a.dv % 4 == 0 && ((uintptr_t)a.values & 15) == 0 && ((uintptr_t)a.out_val & 15) == 0;
+    for (int q0 = 0; q0 < a.n; q0 += RK_CHUNK) {
+      const int nq = std::min(RK_CHUNK, a.n - q0);
+      ranked_dot_kernel<<<dim3((nq + RK_TQ - 1) / RK_TQ, (a.count + RK_TS - 1) / RK_TS), RK_THREADS, RD_LDS,
+                          stream>>>(a, sc, q0, nq);
+      PSSA_LAUNCH_CHECK("ranked_dot");
+      ranked_pick_kernel<<<(nq + RQ_WAVES * RQ_QPW - 1) / (RQ_WAVES * RQ_QPW), 64 * RQ_WAVES, 0, stream>>>(
+          a, sc, q0, nq, vec_out);
+      PSSA_LAUNCH_CHECK("ranked_pick");
+    }
     return Status::Ok();
   }
   const int dk_pad = (a.dk + 3) & ~3;

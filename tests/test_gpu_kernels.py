@@ -167,6 +167,64 @@ def test_retrieve_top_k_indices_bit_exact(hip, n_q, C, dk, dv, k):
     assert rel_err(out, r_out) < 1e-5
 
 
+@pytest.mark.parametrize("n_q,cap,count,dk,dv,k,dup", [(130, 512, 512, 36, 40, 8, "all"),
+                                                      (200, 600, 65, 64, 16, 64, "blocks"),
+                                                      (96, 512, 300, 768, 64, 8, "blocks")])
+def test_ranked_top_k_ties_and_job_batches(hip, n_q, cap, count, dk, dv, k, dup):
+    """The pruned top-k path with exact distance ties.  "all": every slot
+    holds the same key, so every slot is a candidate and a workgroup's
+    exact-distance jobs exceed one batch; ties go to the lower slots.
+    "blocks": runs of duplicated keys and queries that hit keys exactly.
+    Covers k = 64 of 65 slots, a capacity past the occupied 512 slots, a key
+    width that is not a multiple of the slab and a partial last workgroup."""
+    say("ranked top-k ties", n_q, cap, count, dk, dv, k, dup)
+    rng = np.random.default_rng(count + dk)
+    keys = ball(rng, count, dk)
+    if dup == "all":
+        keys[:] = keys[0]
+    else:
+        keys[10:40] = keys[5]
+        keys[50:52] = keys[7]
+    vals = ball(rng, count, dv)
+    q = ball(rng, n_q, dk)
+    q[0], q[1], q[2] = keys[5], keys[7], keys[count - 1]
+    K, N, V, cnt = bank(cap, keys, vals)
+    out, mn, idx, w = hip.retrieve(q, K, N, V, cnt, 0.1, top_k=k, want_weights=True)
+    r_out, r_min, r_idx = O.retrieve_batch(K, N, V, cnt, q, 0.1, k, threads=8)
+    np.testing.assert_array_equal(idx, r_idx)
+    np.testing.assert_array_equal(mn.view(np.uint32), r_min.view(np.uint32))
+    assert rel_err(out, r_out) < 1e-5
+    if dup == "all":
+        assert np.all(idx == np.arange(k, dtype=np.uint32))
+    for i in range(n_q):
+        nz = np.flatnonzero(w[i])
+        assert set(nz.tolist()) <= set(idx[i].tolist())
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-5)
+
+
+def test_retrieve_config4_every_index_bit_exact(hip):
+    """Config 4 at full size on device buffers: 512 x 768 bank, 32768 queries,
+    top-8.  Every index and every minimum distance equals the oracle's bit
+    for bit; the readout within 1e-5."""
+    say("retrieve config4 full")
+    rng = np.random.default_rng(4)
+    C_, dk, nq, k = 512, 768, 32768, 8
+    keys, vals, q = ball(rng, C_, dk), ball(rng, C_, dk), ball(rng, nq, dk)
+    nsq = np.array([O.squared_norm(x) for x in keys], np.float32)
+    bufs = [hip.upload(a) for a in (q, keys, nsq, vals)]
+    out, mn, idx = hip.empty((nq, dk), np.float32), hip.empty((nq,), np.float32), hip.empty((nq, k), np.uint32)
+    hip.retrieve_resident(bufs[0].ptr, nq, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, C_, C_, dk, dk, 0.1, k,
+                          out.ptr, mn.ptr, idx.ptr)
+    hip.synchronize()
+    g_out, g_min, g_idx = out.to_host(), mn.to_host(), idx.to_host()
+    for b in bufs + [out, mn, idx]:
+        b.close()
+    r_out, r_min, r_idx = O.retrieve_batch(keys, nsq, vals, C_, q, 0.1, k, threads=16)
+    np.testing.assert_array_equal(g_idx, r_idx)
+    np.testing.assert_array_equal(g_min.view(np.uint32), r_min.view(np.uint32))
+    assert rel_err(g_out, r_out) < 1e-5
+
+
 def test_retrieve_full_soft_read(hip):
     say("retrieve full soft read")
     rng = np.random.default_rng(11)

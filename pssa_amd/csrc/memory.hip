@@ -397,9 +397,7 @@ __device__ __forceinline__ uint32_t rk_bf16(float f) {
 struct RankedScratch {
   uint16_t* khi;  // [RK_SLOTS][dkp] bf16 hi parts (zero past count and past d_key)
   uint16_t* klo;  // [RK_SLOTS][dkp] bf16 lo parts
-  double* kk;     // [RK_SLOTS] |k|^2 (any order)
-  double* kn;     // [RK_SLOTS] |k|
-  double* rk;     // [RK_SLOTS] 1 / (1 - norm_sq) with the stored f32 norm_sq
+  float4* terms;  // [RK_SLOTS] {|k|^2, 2 RK_DOT_ERR |k|, 1 / (1 - norm_sq), 0} (stored f32 norm_sq)
   float* zdot;    // [RK_CHUNK][RK_SLOTS] approximate q.k
   double* qq;     // [RK_CHUNK] |q|^2 (any order)
 };
@@ -407,7 +405,7 @@ struct RankedScratch {
 __host__ __device__ inline int ranked_dkp(int dk) { return (dk + RK_BK - 1) / RK_BK * RK_BK; }
 
 static size_t ranked_scratch_bytes(int dk) {
-  return (size_t)RK_SLOTS * ranked_dkp(dk) * 2 * sizeof(uint16_t) + 3 * RK_SLOTS * sizeof(double) +
+  return (size_t)RK_SLOTS * ranked_dkp(dk) * 2 * sizeof(uint16_t) + RK_SLOTS * sizeof(float4) +
          (size_t)RK_CHUNK * RK_SLOTS * sizeof(float) + (size_t)RK_CHUNK * sizeof(double);
 }
 
@@ -416,10 +414,8 @@ static RankedScratch ranked_scratch(void* base, int dk) {
   RankedScratch s;
   s.khi = static_cast<uint16_t*>(base);
   s.klo = s.khi + row;
-  s.kk = reinterpret_cast<double*>(s.klo + row);
-  s.kn = s.kk + RK_SLOTS;
-  s.rk = s.kn + RK_SLOTS;
-  s.zdot = reinterpret_cast<float*>(s.rk + RK_SLOTS);
+  s.terms = reinterpret_cast<float4*>(s.klo + row);
+  s.zdot = reinterpret_cast<float*>(s.terms + RK_SLOTS);
   s.qq = reinterpret_cast<double*>(s.zdot + (size_t)RK_CHUNK * RK_SLOTS);
   return s;
 }
@@ -443,11 +439,9 @@ __global__ __launch_bounds__(256) void ranked_prep_kernel(RetrieveArgs a, Ranked
     if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    sc.kk[s] = part[0];
-    sc.kn[s] = sqrt(part[0]);
-    sc.rk[s] = live ? 1.0 / (1.0 - (double)a.norm_sq[s]) : 0.0;
-  }
+  if (threadIdx.x == 0)
+    sc.terms[s] = make_float4((float)part[0], (float)(2.0 * RK_DOT_ERR * sqrt(part[0])),
+                              live ? (float)(1.0 / (1.0 - (double)a.norm_sq[s])) : 0.0f, 0.0f);
 }
 
 // ---- 1. approximate dot products ------------------------------------------
@@ -620,6 +614,7 @@ constexpr int RQ_WAVES = 4;                    // independent waves per workgrou
 constexpr int RQ_V = RK_MAX_DK / 256;          // float4 per lane for one row
 constexpr int RQ_QPW = 4;                      // queries per wave
 constexpr int RQ_G = 2;                        // candidate rows per step
+constexpr int RK_MAX_DV4 = 256;                // vectorised readout: d_val <= 1024
 constexpr double RQ_SUM_REL = 4e-13;           // >= 2 * 1024 * 2^-53, with margin
 constexpr double RQ_DIST_REL = 4e-13;          // distance interval (relative)
 
@@ -664,13 +659,14 @@ __device__ __forceinline__ float rq_qsq(double qs) {
   return f;
 }
 
+template <int V>
 __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs a, RankedScratch sc, int q0, int nq,
                                                                     int vec_out) {
   __shared__ uint16_t s_cand[RQ_WAVES][RK_SLOTS];
   __shared__ unsigned long long s_key[RQ_WAVES][RK_SLOTS];
   __shared__ uint32_t s_sel[RQ_WAVES][kMaxTopK];
   __shared__ float s_selw[RQ_WAVES][kMaxTopK];
-  __shared__ double s_lmin[RQ_WAVES][64];
+  __shared__ __attribute__((aligned(16))) float s_lmin[RQ_WAVES][64];
   __shared__ double s_sq[RQ_WAVES][RK_SLOTS];
   __shared__ float s_min[RQ_WAVES];
   constexpr int SPL = RK_SLOTS / 64;
@@ -685,27 +681,35 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
   const int row0 = (blockIdx.x * RQ_WAVES + wave) * RQ_QPW;
   for (int row = row0; row < min(row0 + RQ_QPW, nq); ++row) {
     const size_t n = (size_t)q0 + row;
-    // ---- candidates ----
-    const double qq = sc.qq[row], qn = sqrt(qq);
-    double L[SPL];
-    double lm = HUGE_VAL;
+    // ---- candidates: bounds in f32 (their rounding, ~1e-7 relative, is far
+    // inside the RK_TIE slack) ----
+    const double qq = sc.qq[row];
+    const float qqf = (float)qq, qnf = (float)sqrt(qq);
+    float L[SPL];
+    float lm = HUGE_VALF;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
       const int s = lane + 64 * j;
-      L[j] = HUGE_VAL;
+      L[j] = HUGE_VALF;
       if (s < cnt) {
-        const double kk = sc.kk[s];
-        const double sqt = qq + kk - 2.0 * (double)sc.zdot[(size_t)row * RK_SLOTS + s];
-        const double e = 2.0 * RK_DOT_ERR * qn * sc.kn[s] + 1e-12 * (qq + kk);
-        L[j] = (sqt - e) * sc.rk[s];
-        lm = fmin(lm, (sqt + e) * sc.rk[s]);
+        const float4 tm = sc.terms[s];
+        const float dot = sc.zdot[(size_t)row * RK_SLOTS + s];
+        const float sqt = qqf + tm.x - 2.0f * dot;
+        const float e = qnf * tm.y + 1e-6f * (qqf + tm.x + 2.0f * fabsf(dot));
+        L[j] = (sqt - e) * tm.z;
+        lm = fminf(lm, (sqt + e) * tm.z);
       }
     }
+    // T = the K-th smallest lane minimum (counted with multiplicity).
     s_lmin[wave][lane] = lm;
     wave_sync();
     int le = 0;
-    for (int l2 = 0; l2 < 64; ++l2) le += s_lmin[wave][l2] <= lm;
-    const double lim = wave_min_f64(le >= K ? lm : HUGE_VAL) * (1.0 + RK_TIE);
+#pragma unroll
+    for (int l4 = 0; l4 < 16; ++l4) {
+      const float4 v = *reinterpret_cast<const float4*>(&s_lmin[wave][4 * l4]);
+      le += (v.x <= lm) + (v.y <= lm) + (v.z <= lm) + (v.w <= lm);
+    }
+    const float lim = wave_min(le >= K ? lm : HUGE_VALF) * (1.0f + (float)RK_TIE);
     int m = 0;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
@@ -716,10 +720,10 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
     }
     // ---- the query row (f64) and |q|^2 ----
     const float* qrow = a.q + n * a.ld_q;
-    double qd[RQ_V * 4];
+    double qd[V * 4];
     double qs = 0.0;
 #pragma unroll
-    for (int v = 0; v < RQ_V; ++v) {
+    for (int v = 0; v < V; ++v) {
       const int i = 256 * v + 4 * lane;
       const float4 x = i < dk ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
       qd[4 * v] = x.x, qd[4 * v + 1] = x.y, qd[4 * v + 2] = x.z, qd[4 * v + 3] = x.w;
@@ -731,17 +735,17 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
     if (rq_qsq(qs * (1.0 - RQ_SUM_REL)) != rq_qsq(qs * (1.0 + RQ_SUM_REL))) {
       float qf[RQ_V * 4], zero[RQ_V * 4];
 #pragma unroll
-      for (int e = 0; e < RQ_V * 4; ++e) qf[e] = (float)qd[e], zero[e] = 0.0f;
+      for (int e = 0; e < RQ_V * 4; ++e) qf[e] = e < V * 4 ? (float)qd[e < V * 4 ? e : 0] : 0.0f, zero[e] = 0.0f;
       q_sq = rq_qsq(rq_sequential(qf, zero, dk));
     }
     // ---- candidate sums |q - k|^2 across the wave, RQ_G rows at a time ----
     for (int c0 = 0; c0 < m; c0 += RQ_G) {
-      float kf[RQ_G][RQ_V * 4];
+      float kf[RQ_G][V * 4];
 #pragma unroll
       for (int g = 0; g < RQ_G; ++g) {
         const float* krow = a.keys + (size_t)cand[min(c0 + g, m - 1)] * dk;
 #pragma unroll
-        for (int v = 0; v < RQ_V; ++v) {
+        for (int v = 0; v < V; ++v) {
           const int i = 256 * v + 4 * lane;
           const float4 y = i < dk ? *reinterpret_cast<const float4*>(krow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
           kf[g][4 * v] = y.x, kf[g][4 * v + 1] = y.y, kf[g][4 * v + 2] = y.z, kf[g][4 * v + 3] = y.w;
@@ -752,7 +756,7 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
       for (int g = 0; g < RQ_G; ++g) {
         double acc = 0.0;
 #pragma unroll
-        for (int e = 0; e < RQ_V * 4; ++e) {
+        for (int e = 0; e < V * 4; ++e) {
           const double t = qd[e] - (double)kf[g][e];
           acc = fma(t, t, acc);
         }
@@ -769,11 +773,9 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
     for (int cb = 0; cb < m; cb += 64) {
       const int c = cb + lane;
       bool ok = true;
-      double den = 1.0;
-      uint32_t slot = 0;
       if (c < m) {
-        slot = cand[c];
-        den = (1.0 - (double)q_sq) * (1.0 - (double)a.norm_sq[slot]);
+        const uint32_t slot = cand[c];
+        const double den = (1.0 - (double)q_sq) * (1.0 - (double)a.norm_sq[slot]);
         const double r = 2.0 * rust_asinh(sqrt(csq[c] / den));
         const double dr = RQ_DIST_REL * r;
         ok = (float)(r - dr) == (float)(r + dr);
@@ -801,7 +803,6 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
         if (lane == 0) ckey[cb + l] = ((unsigned long long)__float_as_uint(dist) << 32) | s2;
       }
     }
-    wave_sync();
     if (lane < K) {
       sel[lane] = 0xFFFFFFFFu;
       selw[lane] = 0.0f;
@@ -846,33 +847,48 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
         put_weight(a, (int)n, s, w);
       }
     }
-    // ---- value readout in ascending slot order, eight rows fetched together ----
+    // ---- value readout in ascending slot order, eight rows at a time ----
     if (a.out_val) {
       const int dv = a.dv;
       if (vec_out) {
-        for (int j4 = lane; j4 < dv / 4; j4 += 64) {
+        float4 o[(RK_MAX_DV4 + 63) / 64];
+#pragma unroll
+        for (int u = 0; u < (RK_MAX_DV4 + 63) / 64; ++u) o[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int t0 = 0; t0 < K; t0 += 8) {
+          const float* vr[8];
+          float w[8];
+          bool use[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const uint32_t s = t0 + u < K ? sel[t0 + u] : 0xFFFFFFFFu;
+            use[u] = s < (uint32_t)cnt;
+            w[u] = use[u] ? selw[t0 + u] : 0.0f;
+            vr[u] = a.values + (size_t)(use[u] ? s : 0u) * dv;
+          }
+#pragma unroll
+          for (int jj = 0; jj < (RK_MAX_DV4 + 63) / 64; ++jj) {
+            const int j4 = lane + 64 * jj;
+            if (j4 < dv / 4) {
+              float4 v[8];
+#pragma unroll
+              for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(vr[u] + 4 * j4);
+#pragma unroll
+              for (int u = 0; u < 8; ++u) {
 #pragma clang fp contract(off)
-          float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-          for (int t0 = 0; t0 < K; t0 += 8) {
-            float4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const uint32_t s = t0 + u < K ? sel[t0 + u] : 0u;
-              v[u] = *reinterpret_cast<const float4*>(a.values + (size_t)min(s, (uint32_t)cnt - 1) * dv + 4 * j4);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int t = t0 + u;
-              if (t < K && sel[t] < (uint32_t)cnt) {
-                const float w = selw[t];
-                o.x = o.x + w * v[u].x;
-                o.y = o.y + w * v[u].y;
-                o.z = o.z + w * v[u].z;
-                o.w = o.w + w * v[u].w;
+                if (use[u]) {
+                  o[jj].x = o[jj].x + w[u] * v[u].x;
+                  o[jj].y = o[jj].y + w[u] * v[u].y;
+                  o[jj].z = o[jj].z + w[u] * v[u].z;
+                  o[jj].w = o[jj].w + w[u] * v[u].w;
+                }
               }
             }
           }
-          *reinterpret_cast<float4*>(a.out_val + n * dv + 4 * j4) = o;
+        }
+#pragma unroll
+        for (int jj = 0; jj < (RK_MAX_DV4 + 63) / 64; ++jj) {
+          const int j4 = lane + 64 * jj;
+          if (j4 < dv / 4) *reinterpret_cast<float4*>(a.out_val + n * dv + 4 * j4) = o[jj];
         }
       } else {
         for (int j = lane; j < dv; j += 64) {
@@ -953,14 +969,28 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
     const RankedScratch sc = ranked_scratch(a.scratch, a.dk);
     ranked_prep_kernel<<<RK_SLOTS, 256, 0, stream>>>(a, sc);
     PSSA_LAUNCH_CHECK("ranked_prep");
-    const int vec_out = a.dv % 4 == 0 && ((uintptr_t)a.values & 15) == 0 && ((uintptr_t)a.out_val & 15) == 0;
+    const int vec_out = a.dv % 4 == 0 && a.dv <= 4 * RK_MAX_DV4 && ((uintptr_t)a.values & 15) == 0 &&
+                        ((uintptr_t)a.out_val & 15) == 0;
     for (int q0 = 0; q0 < a.n; q0 += RK_CHUNK) {
       const int nq = std::min(RK_CHUNK, a.n - q0);
       ranked_dot_kernel<<<dim3((nq + RK_TQ - 1) / RK_TQ, (a.count + RK_TS - 1) / RK_TS), RK_THREADS, RD_LDS,
                           stream>>>(a, sc, q0, nq);
       PSSA_LAUNCH_CHECK("ranked_dot");
-      ranked_pick_kernel<<<(nq + RQ_WAVES * RQ_QPW - 1) / (RQ_WAVES * RQ_QPW), 64 * RQ_WAVES, 0, stream>>>(
-          a, sc, q0, nq, vec_out);
+      const unsigned pg = (nq + RQ_WAVES * RQ_QPW - 1) / (RQ_WAVES * RQ_QPW);
+      switch ((a.dk + 255) / 256) {
+        case 1:
+          ranked_pick_kernel<1><<<pg, 64 * RQ_WAVES, 0, stream>>>(a, sc, q0, nq, vec_out);
+          break;
+        case 2:
+          ranked_pick_kernel<2><<<pg, 64 * RQ_WAVES, 0, stream>>>(a, sc, q0, nq, vec_out);
+          break;
+        case 3:
+          ranked_pick_kernel<3><<<pg, 64 * RQ_WAVES, 0, stream>>>(a, sc, q0, nq, vec_out);
+          break;
+        default:
+          ranked_pick_kernel<4><<<pg, 64 * RQ_WAVES, 0, stream>>>(a, sc, q0, nq, vec_out);
+          break;
+      }
       PSSA_LAUNCH_CHECK("ranked_pick");
     }
     return Status::Ok();

@@ -14,6 +14,7 @@
 namespace pssa {
 Status launch_dense_scan(hipStream_t stream, const float* A, const float* B, const float* H0, float* H,
                          int batch, int L, int s);
+Status init_dense_scan_attributes();
 }
 
 using pssa::DevBuf;
@@ -132,6 +133,7 @@ int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
     PSSA_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
     PSSA_RETURN_IF(pssa::init_retrieve_attributes());
     PSSA_RETURN_IF(pssa::init_decode_attributes());
+    PSSA_RETURN_IF(pssa::init_dense_scan_attributes());
     *out = ctx.release();
     return Status::Ok();
   };

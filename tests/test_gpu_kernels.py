@@ -264,7 +264,8 @@ def test_memory_forward_stage_matches_oracle(hip):
 
 
 # -------------------------------------------------------------- dense scan
-@pytest.mark.parametrize("B,L,s", [(1, 1, 1), (3, 100, 5), (2, 257, 16), (4, 300, 33), (5, 200, 64)])
+@pytest.mark.parametrize("B,L,s", [(1, 1, 1), (3, 100, 5), (2, 257, 16), (4, 300, 33), (5, 200, 64),
+                                   (2, 1, 64), (3, 7, 64), (2, 8, 64), (2, 9, 64), (3, 10, 64), (1, 17, 64)])
 def test_dense_scan_matches_oracle(hip, B, L, s):
     say("dense scan", B, L, s)
     rng = np.random.default_rng(B * L + s)

@@ -470,6 +470,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                                      n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half, l32);
 }
 
+// ---------------------------------------------------------------------------
+// bf16 GEMM for few token rows (decode steps, small batches): one wave per
+// 64 token rows x 32 weight rows, no LDS.  The operand fragments come
+// straight from global memory (L2) through a register ring SK_RING K-steps
+// deep.  Each output element accumulates its 16-wide K-steps in increasing
+// order on the same MFMA as the tiled kernels, so every result is bit-for-bit
+// the one those produce; only the tile shape differs, which gives
+// (N/32) x (M/64) independent waves instead of a handful of 128 x 256 tiles.
+constexpr int SK_RING = 8;
+
+template <int KIND>
+__global__ __launch_bounds__(64) void gemm_skinny_kernel(const uint16_t* __restrict__ A, int lda,
+                                                         const uint16_t* __restrict__ B, int ldb, int M,
+                                                         int N, int K, int vec_epi, EpiParams ep) {
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 64;
+  const uint16_t* pa0 = A + (size_t)min(m0 + l32, M - 1) * lda + 8 * half;
+  const uint16_t* pa1 = A + (size_t)min(m0 + 32 + l32, M - 1) * lda + 8 * half;
+  const uint16_t* pb = B + (size_t)min(n0 + l32, N - 1) * ldb + 8 * half;
+  // K % 16 == 0.  The loop is branch-free (prefetches past the end reload
+  // the last step and go unused), so the compiler's wait counts stay exact
+  // and SK_RING steps of loads remain in flight.
+  const int nk = K / 16;
+  bf16x8_t ra0[SK_RING], ra1[SK_RING], rb[SK_RING];
+  auto fetch = [&](int kt, int slot) {
+    const int ko = min(kt, nk - 1) * 16;
+    uint4 x0 = *reinterpret_cast<const uint4*>(pa0 + ko);
+    uint4 x1 = *reinterpret_cast<const uint4*>(pa1 + ko);
+    uint4 y = *reinterpret_cast<const uint4*>(pb + ko);
+    __builtin_memcpy(&ra0[slot], &x0, 16);
+    __builtin_memcpy(&ra1[slot], &x1, 16);
+    __builtin_memcpy(&rb[slot], &y, 16);
+  };
+  f32x16_t acc0, acc1;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < SK_RING; ++q) fetch(q, q);
+  int k0 = 0;
+  for (; k0 + SK_RING <= nk; k0 += SK_RING) {
+#pragma unroll
+    for (int q = 0; q < SK_RING; ++q) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra0[q], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra1[q], acc1, 0, 0, 0);
+      fetch(k0 + SK_RING + q, q);
+    }
+  }
+  // The remaining nk - k0 < SK_RING steps are in slots 0 ..
+#pragma unroll
+  for (int q = 0; q < SK_RING; ++q) {
+    if (q < nk - k0) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra0[q], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra1[q], acc1, 0, 0, 0);
+    }
+  }
+  epilogue_32x32<uint16_t, KIND>(ep, acc0, m0 + l32, n0, M, N, vec_epi, half, l32);
+  epilogue_32x32<uint16_t, KIND>(ep, acc1, m0 + 32 + l32, n0, M, N, vec_epi, half, l32);
+}
+
+static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const uint16_t* A, int lda,
+                               const uint16_t* B, int ldb, int M, int N, int K, int ve,
+                               const EpiParams& ep) {
+#define PSSA_GEMM_SK_CASE(KD)                                                             \
+  case KD:                                                                                \
+    gemm_skinny_kernel<KD><<<grid, 64, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+    break;
+  switch (kind) {
+    PSSA_GEMM_SK_CASE(EPI_STORE)
+    PSSA_GEMM_SK_CASE(EPI_SEGMENTS)
+    PSSA_GEMM_SK_CASE(EPI_ADD_AUX)
+    PSSA_GEMM_SK_CASE(EPI_ZRAW)
+    PSSA_GEMM_SK_CASE(EPI_SILU)
+    PSSA_GEMM_SK_CASE(EPI_RESIDUAL)
+    PSSA_GEMM_SK_CASE(EPI_SCALE)
+    default:
+      break;
+  }
+#undef PSSA_GEMM_SK_CASE
+}
+
 template <typename T>
 static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int lda, const T* B,
                         int ldb, int M, int N, int K, int vl, int ve, const EpiParams& ep) {
@@ -537,7 +617,17 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   chk32(ep.g, ep.ld_g);
   chk32(ep.tap, ep.ld_tap);
   if (ep.out16) vec_epi = vec_epi && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
-  if (bf16 && K % LDS_BK == 0 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B)) {
+  const bool vec_bf16 = bf16 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B);
+  // Few token rows: the 128 x 256 tiling would leave most CUs idle.
+  if (vec_bf16 && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
+    const dim3 grid((N + 31) / 32, (M + 63) / 64);
+    if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
+    launch_skinny_kind(stream, ep.kind, grid, static_cast<const uint16_t*>(A), lda,
+                       static_cast<const uint16_t*>(B), ldb, M, N, K, vec_epi, ep);
+    PSSA_LAUNCH_CHECK("gemm_skinny");
+    return Status::Ok();
+  }
+  if (vec_bf16 && K % LDS_BK == 0) {
     // Direct-to-LDS pipeline; narrow outputs use 64-column tiles.
     const int nw = N <= 64 ? 1 : 4;
     const long tiles = (long)((M + 127) / 128) * ((N + 64 * nw - 1) / (64 * nw));

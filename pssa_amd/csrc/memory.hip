@@ -262,9 +262,10 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
   double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]
   double* pq = rk + cap;                                               // [waves][SOFT_MAX_DK]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Coalesced reads of the row-major keys, transposed on the way into LDS.
   for (int e = tid; e < cnt * dk; e += 64 * SOFT_WAVES) {
-    const int i = e / cnt, sl = e - i * cnt;
-    keyT[i * cap + sl] = a.keys[(size_t)sl * dk + i];
+    const int sl = e / dk, i = e - sl * dk;
+    keyT[i * cap + sl] = a.keys[e];
   }
   for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
   __syncthreads();

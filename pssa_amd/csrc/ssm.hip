@@ -132,6 +132,64 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// One time step (decode): no staging, just the carry update.  A workgroup
+// owns one lane and 64 channels; its four waves take J states each.  The
+// arithmetic and the readout order are those of the kernels above, so a
+// step here equals the same step inside a prefill bit for bit.  The traffic
+// is the carry read and written once (plus the lane-shared rates from L2).
+template <int J>
+__global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
+  constexpr int GS = J < 16 ? J : 16;
+  constexpr int NG = J / GS;
+  __shared__ float sY[4 * NG][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i0 = blockIdx.x * 64, b = blockIdx.y;
+  const int jw = blockIdx.z * 4 * J + wave * J;
+  const int i = i0 + lane;
+  const bool ivalid = i < a.d;
+  const int d = a.d, s = a.s;
+  const size_t r = b;  // T == 1: lane b's row
+  const float dl = ivalid ? a.delta[r * a.ld_delta + i] : 0.0f;
+  const float u = dl * (ivalid ? a.xn[r * a.ld_x + i] : 0.0f);
+  float* carry = a.carry + (size_t)b * a.carry_stride;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    float h[GS], r2[GS];
+#pragma unroll
+    for (int qq = 0; qq < GS; ++qq) {
+      const int j = jw + g * GS + qq;
+      const bool ok = ivalid && j < s;
+      h[qq] = ok ? carry[(size_t)j * d + i] : 0.0f;
+      r2[qq] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
+    }
+    float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int qq = 0; qq < GS; ++qq) {
+      const int j = jw + g * GS + qq;
+      const float bq = j < s ? a.bproj[r * a.ld_b + j] : 0.0f;
+      const float cq = j < s ? a.cproj[r * a.ld_c + j] : 0.0f;
+      const float ab = __builtin_amdgcn_exp2f(dl * r2[qq]);
+      h[qq] = fmaf(ab, h[qq], u * bq);
+      yp4[qq & 3] = fmaf(h[qq], cq, yp4[qq & 3]);
+      if (ivalid && j < s) carry[(size_t)j * d + i] = h[qq];
+    }
+    sY[wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
+  }
+  __syncthreads();
+  if (wave == 0 && ivalid) {
+    float v = sY[0][lane];
+#pragma unroll
+    for (int g = 1; g < 4 * NG; ++g) v += sY[g][lane];
+    if (a.y_part)
+      a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + i] = v;
+    else if (gridDim.z > 1)
+      atomicAdd(a.y + r * a.ld_y + i, v);
+    else
+      a.y[r * a.ld_y + i] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Production scan.  The next TC time steps' inputs are fetched into registers
 // while the current TC steps run out of LDS, so the global-memory latency of
 // the staging hides behind the recurrence.  Time steps past the end of a lane
@@ -308,6 +366,8 @@ static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   dim3 grid((a.d + 63) / 64, a.lanes, (a.s + 4 * J - 1) / (4 * J));
   if (mat) {
     ssm_materialize_kernel<J, true><<<grid, 256, 0, stream>>>(a);
+  } else if (a.T == 1) {
+    ssm_step_kernel<J><<<grid, 256, 0, stream>>>(a);
   } else if (a.T < SSM_TC) {
     ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);
   } else if constexpr (J == 32) {

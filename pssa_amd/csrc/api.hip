@@ -921,6 +921,7 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
     PSSA_RETURN_IF(L->tap_act.alloc(D * n * c.adapter_rank * 4));
     PSSA_RETURN_IF(L->surprise.alloc(n * 4));
     PSSA_RETURN_IF(L->hebb_rate.alloc(D * n * 4));  // [depth, lanes]
+    PSSA_RETURN_IF(L->bank_writer.alloc(D * c.mem_capacity * 4));
     PSSA_RETURN_IF(L->gen_pos.alloc(4));
     L->dec_lanes = n;
   }
@@ -986,9 +987,13 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
       PSSA_RETURN_IF(need(L->staged_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
     }
     const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
-    if (plastic)
+    if (plastic) {
       PSSA_RETURN_IF(need(pssa::bank_write_lds((int)L->model->cfg.mem_capacity, (int)n_lanes) <= 160 * 1024,
                           "plastic decode: mem_capacity and n_lanes exceed the bank-write LDS budget"));
+      PSSA_RETURN_IF(need(L->model->cfg.adapter_rank <= 256 &&
+                              pssa::hebbian_lds((int)L->model->cfg.adapter_rank, (int)n_lanes) <= 160 * 1024,
+                          "plastic decode: adapter rank and n_lanes exceed the Hebbian-update LDS budget"));
+    }
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;

@@ -27,63 +27,83 @@ __device__ __forceinline__ int32_t total_key(float f) {
   return b ^ (int32_t)((uint32_t)(b >> 31) >> 1);
 }
 
-// One workgroup per lane: greedy id over 1..V-1 (ties to the lower id) and
-// the surprise logsumexp(logits) - logits[chosen].
+__device__ __forceinline__ void argmax_merge(int32_t& bk, int& bi, int32_t k2, int i2) {
+  if (k2 > bk || (k2 == bk && i2 < bi)) {
+    bk = k2;
+    bi = i2;
+  }
+}
+// Running sum of exp(x - m) with its maximum m: merge (m2, s2) into (m, s).
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mm = fmaxf(m, m2);
+  if (mm == -INFINITY) return;
+  s = s * expf(m - mm) + s2 * expf(m2 - mm);
+  m = mm;
+}
+
+constexpr int GR_CHUNK = 16;
+
+// One workgroup per lane, one pass over the logits: greedy id over 1..V-1
+// (ties to the lower id) and the surprise logsumexp(logits) - logits[chosen]
+// from a running maximum and rescaled sum; partials meet through lane
+// shuffles and then across the four waves.
 __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ logits, int V,
                                                      uint32_t* __restrict__ ids,
                                                      uint32_t* __restrict__ gen_ids,
                                                      const int* __restrict__ gen_pos, int n_lanes,
                                                      float* __restrict__ surprise) {
-  __shared__ int32_t sk[256];
-  __shared__ int sid[256];
-  __shared__ float sm[256];
-  const int row = blockIdx.x, tid = threadIdx.x;
+  __shared__ int32_t sk[4];
+  __shared__ int si[4];
+  __shared__ float smx[4], ssm[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* lg = logits + (size_t)row * V;
   int32_t bk = INT32_MIN;
   int bi = V;
-  float mx = -INFINITY;
-  for (int v = tid; v < V; v += 256) {
-    const float x = lg[v];
-    mx = fmaxf(mx, x);
-    if (v >= 1) {
-      const int32_t k = total_key(x);
-      if (k > bk || (k == bk && v < bi)) {
-        bk = k;
-        bi = v;
-      }
+  float m = -INFINITY, sacc = 0.0f;
+  // Chunks of GR_CHUNK logits per thread are loaded together, then scanned
+  // for the maximum and summed as independent exponentials.
+  for (int v0 = 0; v0 < V; v0 += 256 * GR_CHUNK) {
+    float x[GR_CHUNK];
+#pragma unroll
+    for (int k = 0; k < GR_CHUNK; ++k) {
+      const int v = v0 + k * 256 + tid;
+      x[k] = v < V ? lg[v] : -INFINITY;
     }
-  }
-  sk[tid] = bk;
-  sid[tid] = bi;
-  sm[tid] = mx;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (tid < off) {
-      const int32_t k2 = sk[tid + off];
-      const int i2 = sid[tid + off];
-      if (k2 > sk[tid] || (k2 == sk[tid] && i2 < sid[tid])) {
-        sk[tid] = k2;
-        sid[tid] = i2;
-      }
-      sm[tid] = fmaxf(sm[tid], sm[tid + off]);
+    float cm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < GR_CHUNK; ++k) {
+      const int v = v0 + k * 256 + tid;
+      if (v >= 1 && v < V) argmax_merge(bk, bi, total_key(x[k]), v);
+      cm = fmaxf(cm, x[k]);
     }
-    __syncthreads();
+    float cs = 0.0f;
+    if (cm != -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < GR_CHUNK; ++k) cs += expf(x[k] - cm);
+    }
+    lse_merge(m, sacc, cm, cs);
   }
-  const int best = sid[0];
-  const float gmax = sm[0];
-  __syncthreads();
-  float part = 0.0f;
-  for (int v = tid; v < V; v += 256) part += expf(lg[v] - gmax);
-  sm[tid] = part;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (tid < off) sm[tid] += sm[tid + off];
-    __syncthreads();
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    argmax_merge(bk, bi, __shfl_xor(bk, off, 64), __shfl_xor(bi, off, 64));
+    lse_merge(m, sacc, __shfl_xor(m, off, 64), __shfl_xor(sacc, off, 64));
   }
+  if (lane == 0) {
+    sk[wave] = bk;
+    si[wave] = bi;
+    smx[wave] = m;
+    ssm[wave] = sacc;
+  }
+  __syncthreads();
   if (tid == 0) {
+    for (int w = 1; w < 4; ++w) {
+      argmax_merge(bk, bi, sk[w], si[w]);
+      lse_merge(m, sacc, smx[w], ssm[w]);
+    }
+    const int best = bi < V ? bi : 0;  // V == 1 leaves no candidate
     ids[row] = (uint32_t)best;
     if (gen_ids) gen_ids[(size_t)gen_pos[0] * n_lanes + row] = (uint32_t)best;
-    if (surprise) surprise[row] = (gmax + logf(sm[0])) - lg[best];
+    if (surprise) surprise[row] = (m + logf(sacc)) - lg[best];
   }
 }
 
@@ -106,6 +126,7 @@ struct PlasticArgs {
   const float* tap_act;  // [depth, lanes, r]
   const float* surprise; // [lanes]
   float* rate;           // [depth, lanes]
+  int* writer;           // [depth, C]: the lane whose value a slot takes this step, or -1
   const unsigned long long* step;
   int lanes, C, dk, d, r, wt_bf16;
 };
@@ -116,24 +137,44 @@ __device__ __forceinline__ uint16_t to_bf16(float v) {
   return (uint16_t)(b >> 16);
 }
 
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 // up[i,q] += rate_l * clamp(z_l[i] - a_l[i], -4, 4) * act_l[q] for lanes l in
 // order (rounded as the reference: (rate * err) * act, then the add), then
-// the GEMM operand u_eff = up + slow in the weight type.  blockIdx.y = block.
-__global__ void hebbian_kernel(PlasticArgs p) {
-  const int l = blockIdx.y;
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= p.d * p.r) return;
-  const int i = e / p.r, q = e % p.r;
-  const size_t n = p.lanes;
-  const float* z = p.tap_z + (size_t)l * n * p.d;
-  const float* a = p.tap_a + (size_t)l * n * p.d;
-  const float* act = p.tap_act + (size_t)l * n * p.r;
-  const float* rate = p.rate + (size_t)l * n;
-  float u = p.up[l][e];
-  for (int ln = 0; ln < p.lanes; ++ln) {
-    const float err = fminf(fmaxf(z[(size_t)ln * p.d + i] - a[(size_t)ln * p.d + i], -4.0f), 4.0f);
-    u = __fadd_rn(u, __fmul_rn(__fmul_rn(rate[ln], err), act[(size_t)ln * p.r + q]));
+// the GEMM operand u_eff = up + slow in the weight type.  blockIdx.y = block;
+// a workgroup owns hb_i latent rows x r columns and first stages the clamped
+// errors of its rows, every lane's activations and the rates in LDS, so each
+// thread's lane-ordered chain runs out of LDS.
+__global__ __launch_bounds__(256) void hebbian_kernel(PlasticArgs p, int hb_i) {
+  extern __shared__ float hb_smem[];
+  const int l = blockIdx.y, tid = threadIdx.x, nt = blockDim.x;
+  const int i0 = blockIdx.x * hb_i, n = p.lanes, r = p.r, d = p.d;
+  float* serr = hb_smem;          // [lanes][hb_i]
+  float* sact = serr + n * hb_i;  // [lanes][r]
+  float* srate = sact + n * r;    // [lanes]
+  const float* z = p.tap_z + (size_t)l * n * d;
+  const float* a = p.tap_a + (size_t)l * n * d;
+#pragma unroll 8
+  for (int e = tid; e < n * hb_i; e += nt) {
+    const int ln = e / hb_i, i = i0 + e % hb_i;
+    serr[e] = i < d ? fminf(fmaxf(z[(size_t)ln * d + i] - a[(size_t)ln * d + i], -4.0f), 4.0f) : 0.0f;
   }
+  const float* act = p.tap_act + (size_t)l * n * r;
+#pragma unroll 8
+  for (int e = tid; e < n * r; e += nt) sact[e] = act[e];
+  for (int e = tid; e < n; e += nt) srate[e] = p.rate[(size_t)l * n + e];
+  __syncthreads();
+  const int ii = tid / r, q = tid % r, i = i0 + ii;
+  if (ii >= hb_i || i >= d) return;
+  const int e = i * r + q;
+  float u = p.up[l][e];
+#pragma unroll 8
+  for (int ln = 0; ln < n; ++ln)
+    u = __fadd_rn(u, __fmul_rn(__fmul_rn(srate[ln], serr[ln * hb_i + ii]), sact[ln * r + q]));
   p.up[l][e] = u;
   const float eff = u + p.slow[l][e];
   if (p.wt_bf16)
@@ -142,20 +183,33 @@ __global__ void hebbian_kernel(PlasticArgs p) {
     static_cast<float*>(p.u_eff[l])[e] = eff;
 }
 
-// 0.02 / (1 + |z_final|) per (block, lane): the Hebbian rate of
-// dream_replay_value, with the norm as a sequential f64 sum.
-__global__ void hebbian_rate_kernel(PlasticArgs p) {
-  const int l = blockIdx.y;
-  const int ln = blockIdx.x * blockDim.x + threadIdx.x;
+// 0.02 / (1 + |z_final|) per (block, lane), the Hebbian rate of
+// dream_replay_value, one wave per (block, lane).  The norm's square is a
+// sequential f64 sum in the reference; here the wave sums it in any order,
+// which is within RATE_SUM_REL (relative) of that sum, and the sequential sum
+// runs only when the f32 rounding of the norm is not settled by that bound.
+constexpr double RATE_SUM_REL = 4e-13;
+
+__device__ __forceinline__ float rate_norm(double acc) { return (float)fmin(sqrt(acc), (double)FLT_MAX); }
+
+__global__ __launch_bounds__(256) void hebbian_rate_kernel(PlasticArgs p) {
+  const int l = blockIdx.y, lane = threadIdx.x & 63;
+  const int ln = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (ln >= p.lanes) return;
   const float* zr = p.tap_z + ((size_t)l * p.lanes + ln) * p.d;
   double acc = 0.0;
-  {
+  for (int i = lane; i < p.d; i += 64) acc = fma((double)zr[i], (double)zr[i], acc);
+  acc = wave_sum_f64(acc);
+  float tn = rate_norm(acc);
+  if (rate_norm(acc * (1.0 - RATE_SUM_REL)) != rate_norm(acc * (1.0 + RATE_SUM_REL)) && lane == 0) {
+    double seq = 0.0;
+    {
 #pragma clang fp contract(off)
-    for (int i = 0; i < p.d; ++i) acc = acc + (double)zr[i] * (double)zr[i];
+      for (int i = 0; i < p.d; ++i) seq = seq + (double)zr[i] * (double)zr[i];
+    }
+    tn = rate_norm(seq);
   }
-  const double tn = sqrt(acc);
-  p.rate[(size_t)l * p.lanes + ln] = 0.02f / (1.0f + (float)fmin(tn, (double)FLT_MAX));
+  if (lane == 0) p.rate[(size_t)l * p.lanes + ln] = 0.02f / (1.0f + tn);
 }
 
 // Protected writes of every block's bank (blockIdx.x = block) for all lanes,
@@ -179,70 +233,123 @@ __global__ __launch_bounds__(256) void bank_write_kernel(PlasticArgs p) {
   }
   for (int ln = tid; ln < p.lanes; ln += blockDim.x) s_sp[ln] = p.surprise[ln];
   __syncthreads();
-  if (tid == 0) {
+  if (tid < 64) {
+    // Wave 0 runs the decisions in lane order; every lane follows the same
+    // (uniform) path, lane 0 stores.  Surprises come 64 at a time from
+    // registers; the write-head slot's confidence, age and gate gain stay in
+    // registers until the head moves.
+    const int lane = tid;
     const unsigned long long cur = p.step[0] + 1;
     int* meta = p.meta[l];
     int count = meta[0], head = meta[1];
-    for (int ln = 0; ln < p.lanes; ++ln) {
-      const float sp = s_sp[ln];
-      if (!(sp > 3.5f)) continue;
-      int idx;
-      if (count < C) {  // insert() into a free slot
-        idx = count++;
-      } else {
-        idx = head;
-        // RateLimiterGate::apply_refractory_overwrite (src/defense.rs:45-67).
-        const unsigned long long last = s_last[idx];
-        const float dt = (float)(cur > last ? cur - last : 0ull);
-        const float lin = 1.0f - expf(-dt / 60.0f);
-        const float gain = fmaxf(lin * lin, 0.005f);
-        const float damage = 0.08f * sp * gain;
-        if (s_conf[idx] > damage) {
-          s_conf[idx] -= damage;
-          s_last[idx] = cur;
+    float hconf = 0.0f, hgain = 0.0f;
+    unsigned long long hlast = 0ull;
+    // RateLimiterGate::apply_refractory_overwrite (src/defense.rs:45-67):
+    // gain = max((1 - e^(-dt/60))^2, 0.005) with dt = cur - last_seen.
+    auto load_head = [&]() {
+      hconf = s_conf[head];
+      hlast = s_last[head];
+      const float dt = (float)(cur > hlast ? cur - hlast : 0ull);
+      const float lin = 1.0f - expf(-dt / 60.0f);
+      hgain = fmaxf(lin * lin, 0.005f);
+    };
+    if (count >= C) load_head();
+    for (int base = 0; base < p.lanes; base += 64) {
+      const float mysp = base + lane < p.lanes ? s_sp[base + lane] : 0.0f;
+      const int nk = min(64, p.lanes - base);
+      for (int k = 0; k < nk; ++k) {
+        const float sp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mysp), k));
+        if (!(sp > 3.5f)) continue;
+        const int ln = base + k;
+        if (count < C) {  // insert() into a free slot
+          const int idx = count++;
+          if (lane == 0) {
+            s_conf[idx] = 1.0f;
+            s_last[idx] = cur;
+            writer[idx] = ln;
+          }
+          if (count == C) load_head();
           continue;
         }
+        const float damage = 0.08f * sp * hgain;
+        if (hconf > damage) {  // defended: the age resets, so dt = 0 next time
+          hconf -= damage;
+          hlast = cur;
+          hgain = 0.005f;
+          continue;
+        }
+        if (lane == 0) {
+          s_conf[head] = 1.0f;
+          s_last[head] = cur;
+          writer[head] = ln;
+        }
         head = (head + 1) % C;
+        load_head();
       }
-      s_conf[idx] = 1.0f;
-      s_last[idx] = cur;
-      writer[idx] = ln;
     }
-    meta[0] = count;
-    meta[1] = head;
+    if (count >= C && lane == 0) {
+      s_conf[head] = hconf;
+      s_last[head] = hlast;
+    }
+    if (lane == 0) {
+      meta[0] = count;
+      meta[1] = head;
+    }
   }
   __syncthreads();
   for (int c = tid; c < C; c += blockDim.x) {
     conf[c] = s_conf[c];
     last_seen[c] = s_last[c];
+    p.writer[(size_t)l * C + c] = writer[c];
   }
-  const int wave = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+}
+
+// Slot contents of the writes bank_write_kernel decided: a workgroup covers
+// 64 slots x 64 latent columns of one block; values are copied row-wise and
+// the GEMM operand values_t [d, C] is written through an LDS transpose, both
+// coalesced.  The workgroups of the first column tile also copy the keys and
+// their squared norms (squared_norm, src/memory.rs:181-192: sequential f64).
+__global__ __launch_bounds__(256) void bank_copy_kernel(PlasticArgs p) {
+  __shared__ int w[64];
+  __shared__ float tile[64][65];
+  const int l = blockIdx.z, c0 = blockIdx.x * 64, j0 = blockIdx.y * 64, tid = threadIdx.x;
+  const int C = p.C, d = p.d;
   const size_t n = p.lanes;
-  for (int c = wave; c < C; c += nw) {
-    const int ln = writer[c];
-    if (ln < 0) continue;
-    const float* kq = p.tap_q + ((size_t)l * n + ln) * p.dk;
-    const float* vz = p.tap_z + ((size_t)l * n + ln) * p.d;
-    for (int j = lane; j < p.dk; j += 64) p.keys[l][(size_t)c * p.dk + j] = kq[j];
-    for (int j = lane; j < p.d; j += 64) {
-      const float v = vz[j];
-      p.values[l][(size_t)c * p.d + j] = v;
+  if (tid < 64) w[tid] = c0 + tid < C ? p.writer[(size_t)l * C + c0 + tid] : -1;
+  __syncthreads();
+  for (int e = tid; e < 64 * 64; e += 256) {
+    const int cc = e >> 6, jj = e & 63, c = c0 + cc, j = j0 + jj;
+    if (w[cc] >= 0 && j < d) {
+      const float v = p.tap_z[((size_t)l * n + w[cc]) * d + j];
+      p.values[l][(size_t)c * d + j] = v;
+      tile[cc][jj] = v;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < 64 * 64; e += 256) {
+    const int jj = e >> 6, cc = e & 63, c = c0 + cc, j = j0 + jj;
+    if (w[cc] >= 0 && j < d) {
       if (p.wt_bf16)
-        static_cast<uint16_t*>(p.values_t[l])[(size_t)j * C + c] = to_bf16(v);
+        static_cast<uint16_t*>(p.values_t[l])[(size_t)j * C + c] = to_bf16(tile[cc][jj]);
       else
-        static_cast<float*>(p.values_t[l])[(size_t)j * C + c] = v;
+        static_cast<float*>(p.values_t[l])[(size_t)j * C + c] = tile[cc][jj];
     }
-    if (lane == 0) {
-      // squared_norm (src/memory.rs:181-192): sequential f64 sum.
-      double acc = 0.0;
-      {
+  }
+  if (blockIdx.y == 0 && tid < 64 && w[tid] >= 0) {
+    const int c = c0 + tid;
+    const float* kq = p.tap_q + ((size_t)l * n + w[tid]) * p.dk;
+    double acc = 0.0;
+    {
 #pragma clang fp contract(off)
-        for (int j = 0; j < p.dk; ++j) acc = acc + (double)kq[j] * (double)kq[j];
+      for (int j = 0; j < p.dk; ++j) {
+        const float kv = kq[j];
+        p.keys[l][(size_t)c * p.dk + j] = kv;
+        acc = acc + (double)kv * (double)kv;
       }
-      float v = (float)acc;
-      if (acc < 1.0 && v == 1.0f) v = __uint_as_float(0x3f7fffffu);
-      p.norm_sq[l][c] = v;
     }
+    float v = (float)acc;
+    if (acc < 1.0 && v == 1.0f) v = __uint_as_float(0x3f7fffffu);
+    p.norm_sq[l][c] = v;
   }
 }
 
@@ -260,9 +367,15 @@ __global__ void advance_pos_kernel(int* __restrict__ gen_pos) {
 }  // namespace
 
 size_t bank_write_lds(int capacity, int lanes) { return (size_t)capacity * (8 + 4 + 4) + (size_t)lanes * 4; }
+int hebbian_rows(int rank) { return rank >= 256 ? 1 : 256 / rank; }
+size_t hebbian_lds(int rank, int lanes) {
+  return ((size_t)lanes * hebbian_rows(rank) + (size_t)lanes * rank + (size_t)lanes) * sizeof(float);
+}
 
 Status init_decode_attributes() {
   PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&bank_write_kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&hebbian_kernel),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   return Status::Ok();
 }
@@ -309,6 +422,7 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     p.tap_act = L->tap_act.as<float>();
     p.surprise = L->surprise.as<float>();
     p.rate = L->hebb_rate.as<float>();
+    p.writer = L->bank_writer.as<int>();
     p.step = M->step.as<unsigned long long>();
     p.lanes = (int)n;
     p.C = C;
@@ -319,9 +433,13 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     const int depth = (int)c.depth;
     bank_write_kernel<<<depth, 256, bank_write_lds(C, (int)n), st>>>(p);
     PSSA_LAUNCH_CHECK("bank_write");
-    hebbian_rate_kernel<<<dim3((unsigned)((n + 255) / 256), depth), 256, 0, st>>>(p);
+    bank_copy_kernel<<<dim3((unsigned)((C + 63) / 64), (unsigned)((d + 63) / 64), depth), 256, 0, st>>>(p);
+    PSSA_LAUNCH_CHECK("bank_copy");
+    hebbian_rate_kernel<<<dim3((unsigned)((n + 3) / 4), depth), 256, 0, st>>>(p);
     PSSA_LAUNCH_CHECK("hebbian_rate");
-    hebbian_kernel<<<dim3((unsigned)((d * r + 255) / 256), depth), 256, 0, st>>>(p);
+    const int hb_i = hebbian_rows(r);
+    hebbian_kernel<<<dim3((unsigned)((d + hb_i - 1) / hb_i), depth), hb_i * r, hebbian_lds(r, (int)n), st>>>(p,
+                                                                                                         hb_i);
     PSSA_LAUNCH_CHECK("hebbian");
     advance_kernel<<<1, 64, 0, st>>>(M->step.as<unsigned long long>(), L->gen_pos.as<int>());
   } else {

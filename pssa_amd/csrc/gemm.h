@@ -38,7 +38,8 @@ struct EpiParams {
   void* out16 = nullptr;
   int ld16 = 0;
   // Optional fp32 tap: ZRAW writes the adapter output, RESIDUAL writes
-  // z_final (before the residual scaling).
+  // z_final (before the residual scaling), SEGMENTS writes the columns
+  // [seg[2], seg[3]) (the SiLU segment) to tap[row, col - seg[2]].
   float* tap = nullptr;
   int ld_tap = 0;
 };

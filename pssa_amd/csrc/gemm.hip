@@ -156,6 +156,12 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
     if constexpr (KIND == EPI_ZRAW || KIND == EPI_RESIDUAL) {
       if (ep.tap)
         *reinterpret_cast<float4*>(ep.tap + (size_t)row * ep.ld_tap + col) = make_float4(tp[0], tp[1], tp[2], tp[3]);
+    } else if constexpr (KIND == EPI_SEGMENTS) {
+      if (ep.tap)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e >= ep.seg[2] && col + e < ep.seg[3])
+            ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = r[e];
     }
     if (ep.out32)
       *reinterpret_cast<float4*>(ep.out32 + (size_t)row * ep.ld32 + col) = make_float4(r[0], r[1], r[2], r[3]);
@@ -175,6 +181,9 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
         store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
         if constexpr (KIND == EPI_ZRAW) {
           if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ad[e];
+        } else if constexpr (KIND == EPI_SEGMENTS) {
+          if (ep.tap && col + e >= ep.seg[2] && col + e < ep.seg[3])
+            ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = epi_value<KIND>(ep, acc[e], row, col + e, ad[e]);
         } else if constexpr (KIND == EPI_RESIDUAL) {
           if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ep.aux[(size_t)row * ep.ld_aux + col + e] + acc[e];
         }

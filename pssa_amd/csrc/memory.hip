@@ -251,21 +251,49 @@ constexpr int SOFT_MAX_KEYS = 16384;   // dk * capacity floats held in LDS (64 K
 constexpr int SOFT_MAX_DK = 64;
 constexpr int SOFT_WAVES = 8;
 
-__device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
-  return (((size_t)dk * cap + 1) & ~(size_t)1);  // keep the f64 arrays 8-byte aligned
+// keyT rows have an odd pitch (capacity + 1): the transposing stores of a
+// wave (consecutive key dimensions) and the slot reads (consecutive slots)
+// both fall in distinct banks.
+__host__ __device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
+  return (((size_t)dk * (cap + 1) + 1) & ~(size_t)1);  // keep the f64 arrays 8-byte aligned
 }
 
 __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs a) {
   extern __shared__ float smem[];
   const int cap = a.capacity, dk = a.dk, cnt = a.count_dev ? a.count_dev[0] : a.count;
-  float* keyT = smem;                                                  // [dk][cap]
+  float* keyT = smem;                                                  // [dk][cap + 1]
+  const int kp = cap + 1;
   double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]
   double* pq = rk + cap;                                               // [waves][SOFT_MAX_DK]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // Coalesced reads of the row-major keys, transposed on the way into LDS.
-  for (int e = tid; e < cnt * dk; e += 64 * SOFT_WAVES) {
-    const int sl = e / dk, i = e - sl * dk;
-    keyT[i * cap + sl] = a.keys[e];
+  // Coalesced reads of the row-major keys, transposed on the way into LDS;
+  // eight loads per thread are issued before their stores.
+  if (dk % 4 == 0 && ((uintptr_t)a.keys & 15) == 0) {
+    const int nv = cnt * dk / 4;
+    for (int e0 = tid; e0 < nv; e0 += 8 * 64 * SOFT_WAVES) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * 64 * SOFT_WAVES;
+        v[u] = e < nv ? reinterpret_cast<const float4*>(a.keys)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * 64 * SOFT_WAVES;
+        if (e < nv) {
+          const int sl = (4 * e) / dk, i = 4 * e - sl * dk;
+          keyT[i * kp + sl] = v[u].x;
+          keyT[(i + 1) * kp + sl] = v[u].y;
+          keyT[(i + 2) * kp + sl] = v[u].z;
+          keyT[(i + 3) * kp + sl] = v[u].w;
+        }
+      }
+    }
+  } else {
+    for (int e = tid; e < cnt * dk; e += 64 * SOFT_WAVES) {
+      const int sl = e / dk, i = e - sl * dk;
+      keyT[i * kp + sl] = a.keys[e];
+    }
   }
   for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
   __syncthreads();
@@ -307,7 +335,7 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
       for (int j = 0; j < SOFT_SPL; ++j) sq[j] = 0.0;
       for (int i = 0; i < dk; ++i) {
         const double pi = p[i];
-        const float* kr = keyT + i * cap;
+        const float* kr = keyT + i * kp;
 #pragma unroll
         for (int j = 0; j < SOFT_SPL; ++j) {
           const int sl = lane + 64 * j;
@@ -921,7 +949,7 @@ size_t retrieve_scratch_bytes(const RetrieveArgs& a) {
 static bool soft_read_fits(const RetrieveArgs& a) {
   return (a.top_k == 0 || (!a.count_dev && a.top_k >= a.count)) && a.project && !a.q_norm && !a.out_val &&
          !a.out_min && !a.out_idx && a.dk <= SOFT_MAX_DK && a.capacity <= 64 * SOFT_SPL &&
-         (long)a.dk * a.capacity <= SOFT_MAX_KEYS;
+         (long)a.dk * (a.capacity + 1) <= SOFT_MAX_KEYS + SOFT_MAX_DK;
 }
 
 // Raises the kernel's dynamic-LDS limit to the device maximum once per
@@ -956,7 +984,7 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
   if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
   if (soft_read_fits(a)) {
-    const size_t lds = (((size_t)a.dk * a.capacity + 1) & ~(size_t)1) * sizeof(float) +
+    const size_t lds = soft_keys_floats(a.dk, a.capacity) * sizeof(float) +
                        ((size_t)a.capacity + (size_t)SOFT_WAVES * SOFT_MAX_DK) * sizeof(double);
     if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     int blocks = (a.n + SOFT_WAVES - 1) / SOFT_WAVES;

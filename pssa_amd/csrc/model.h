@@ -79,6 +79,7 @@ struct pssa_hip_lanes {
   // [lanes], the Hebbian rates 0.02/(1+|z_final|) [depth, lanes], the
   // generated ids [gen_cap, lanes] and the generation position.
   pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
+  pssa::DevBuf bank_writer;  // [depth, capacity] writing lane of each slot in the current step
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
   hipGraph_t graph = nullptr;
@@ -121,6 +122,8 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic);
 Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes);
 // Dynamic LDS of the bank-write kernel and its per-device attribute set-up.
 size_t bank_write_lds(int capacity, int lanes);
+// LDS of the Hebbian update for adapter rank `rank` and `lanes` lanes.
+size_t hebbian_lds(int rank, int lanes);
 Status init_decode_attributes();
 Status launch_fill_zero(hipStream_t stream, float* p, size_t n);
 Status launch_copy_cols(hipStream_t stream, const float* in, int ld_in, float* out, int ld_out,

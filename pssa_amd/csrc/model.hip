@@ -43,6 +43,8 @@ __device__ __forceinline__ uint16_t bf16_of(float f) {
   return (uint16_t)(u >> 16);
 }
 
+constexpr int RMS_REG = 16;  // rows of up to 1024 columns are held in registers
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta,
@@ -52,6 +54,30 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
   const float* x = X + r * d;
+  if (d <= 64 * RMS_REG) {  // the row stays in registers; all loads issue at once
+    float xv[RMS_REG];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RMS_REG; ++k) {
+      const int i = lane + 64 * k;
+      xv[k] = i < d ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < RMS_REG; ++k) ss = fmaf(xv[k], xv[k], ss);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)d + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < RMS_REG; ++k) {
+      const int i = lane + 64 * k;
+      if (i < d) {
+        const float v = gamma[i] * (xv[k] * inv) + beta[i];
+        XN[r * d + i] = v;
+        if (XNh) XNh[r * d + i] = bf16_of(v);
+      }
+    }
+    return;
+  }
   float ss = 0.0f;
   for (int i = lane; i < d; i += 64) ss = fmaf(x[i], x[i], ss);
 #pragma unroll
@@ -252,13 +278,16 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     e_in.seg[3] = n_in;
     e_in.out32 = P;
     e_in.ld32 = n_in;
+    if (taps) {  // the adapter activations of this step, for the Hebbian update
+      e_in.tap = L->tap_act.as<float>() + l * rows * r;
+      e_in.ld_tap = r;
+    }
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
     if (l == 0 && first_in_done) PSSA_HIP_TRY(hipEventRecord(first_in_done, st));
-    if (taps)
-      PSSA_RETURN_IF(launch_copy_cols(st, P + o_act, n_in, L->tap_act.as<float>() + l * rows * r, r, rows, r));
 
     PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
-    if (ssm_needs_zeroed_y(s)) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
+    const bool step_y = ssm_step_writes_y((int)T, s);
+    if (ssm_needs_zeroed_y(s) && !step_y) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
     PSSA_RETURN_IF(tm.mark(ST_SSM));
     SsmArgs sa;
     sa.delta = P;
@@ -279,9 +308,13 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     sa.s = s;
     sa.lanes = (int)n_lanes;
     sa.y_part = y_part;
+    if (bf16 && step_y) {
+      sa.y16 = static_cast<uint16_t*>(Yh);
+      sa.ld_y16 = d;
+    }
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
     PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
-    if (bf16) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
+    if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
 
     // q_euc = y W_qh^T + q_x.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));

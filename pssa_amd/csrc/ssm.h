@@ -31,6 +31,10 @@ struct SsmArgs {
   // ssm_state_blocks(s) > 2 (the blocks are then summed in a fixed order).
   float* y_part = nullptr;
   size_t rows = 0;  // set by launch_ssm_scan
+  // Optional bf16 copy of y, written by the single-step kernel when
+  // ssm_step_writes_y (other paths leave it untouched).
+  uint16_t* y16 = nullptr;
+  int ld_y16 = 0;
 };
 
 // Rows of lane b are b*T .. b*T+T-1.  The states of a channel are split into
@@ -40,6 +44,9 @@ struct SsmArgs {
 // caller provides y_part and the blocks are summed in a fixed order.
 int ssm_state_blocks(int s);
 bool ssm_needs_zeroed_y(int s);
+// A single time step (T == 1) with at most two state blocks stores y (and
+// y16) directly: no zero-fill of y is needed and y16 is written.
+bool ssm_step_writes_y(int T, int s);
 Status launch_ssm_scan(hipStream_t stream, const SsmArgs& a);
 
 // rates2[i] = rates[i] * log2(e) (stage API receives -softplus(a_raw)).

@@ -133,18 +133,22 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 
 // ---------------------------------------------------------------------------
 // One time step (decode): no staging, just the carry update.  A workgroup
-// owns one lane and 64 channels; its four waves take J states each.  The
-// arithmetic and the readout order are those of the kernels above, so a
-// step here equals the same step inside a prefill bit for bit.  The traffic
-// is the carry read and written once (plus the lane-shared rates from L2).
-template <int J>
-__global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
+// owns one lane and 64 channels, and NB consecutive state blocks of 4*J
+// states (four waves each); with NB covering all of d_state it also finishes
+// the readout, adding the block sums in block order as the multi-block paths
+// do, and writes y (and its bf16 copy) directly.  The arithmetic and the
+// readout order are those of the kernels above, so a step here equals the
+// same step inside a prefill bit for bit.  The traffic is the carry read and
+// written once, streamed past the caches (plus the lane-shared rates from
+// L2).
+template <int J, int NB>
+__global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
   constexpr int GS = J < 16 ? J : 16;
   constexpr int NG = J / GS;
-  __shared__ float sY[4 * NG][64];
+  __shared__ float sY[NB * 4 * NG][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i0 = blockIdx.x * 64, b = blockIdx.y;
-  const int jw = blockIdx.z * 4 * J + wave * J;
+  const int jw = blockIdx.z * NB * 4 * J + wave * J;
   const int i = i0 + lane;
   const bool ivalid = i < a.d;
   const int d = a.d, s = a.s;
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
     for (int qq = 0; qq < GS; ++qq) {
       const int j = jw + g * GS + qq;
       const bool ok = ivalid && j < s;
-      h[qq] = ok ? carry[(size_t)j * d + i] : 0.0f;
+      h[qq] = ok ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
       r2[qq] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
     }
     float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -171,21 +175,32 @@ __global__ __launch_bounds__(256) void ssm_step_kernel(SsmArgs a) {
       const float ab = __builtin_amdgcn_exp2f(dl * r2[qq]);
       h[qq] = fmaf(ab, h[qq], u * bq);
       yp4[qq & 3] = fmaf(h[qq], cq, yp4[qq & 3]);
-      if (ivalid && j < s) carry[(size_t)j * d + i] = h[qq];
+      if (ivalid && j < s) __builtin_nontemporal_store(h[qq], &carry[(size_t)j * d + i]);
     }
     sY[wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
   }
   __syncthreads();
   if (wave == 0 && ivalid) {
-    float v = sY[0][lane];
+    float v = 0.0f;
 #pragma unroll
-    for (int g = 1; g < 4 * NG; ++g) v += sY[g][lane];
-    if (a.y_part)
+    for (int blk = 0; blk < NB; ++blk) {
+      float bv = sY[blk * 4 * NG][lane];
+#pragma unroll
+      for (int g = 1; g < 4 * NG; ++g) bv += sY[blk * 4 * NG + g][lane];
+      v = blk == 0 ? bv : v + bv;
+    }
+    if (a.y_part) {
       a.y_part[((size_t)blockIdx.z * a.rows + r) * a.d + i] = v;
-    else if (gridDim.z > 1)
+    } else if (gridDim.z > 1) {
       atomicAdd(a.y + r * a.ld_y + i, v);
-    else
+    } else {
       a.y[r * a.ld_y + i] = v;
+      if (a.y16) {
+        uint32_t bits = __float_as_uint(v);
+        bits += 0x7FFFu + ((bits >> 16) & 1u);
+        a.y16[r * a.ld_y16 + i] = (uint16_t)(bits >> 16);
+      }
+    }
   }
 }
 
@@ -349,6 +364,8 @@ __global__ void ssm_reduce_kernel(const float* __restrict__ part, int nz, size_t
 
 static int pick_j(int s) { return s >= 128 ? 32 : (s >= 32 ? 8 : 2); }
 
+bool ssm_step_writes_y(int T, int s) { return T == 1 && ssm_state_blocks(s) <= 2; }
+
 int ssm_state_blocks(int s) {
   const int J = pick_j(s);
   return (s + 4 * J - 1) / (4 * J);
@@ -367,7 +384,12 @@ static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   if (mat) {
     ssm_materialize_kernel<J, true><<<grid, 256, 0, stream>>>(a);
   } else if (a.T == 1) {
-    ssm_step_kernel<J><<<grid, 256, 0, stream>>>(a);
+    if (grid.z == 2) {
+      grid.z = 1;
+      ssm_step_kernel<J, 2><<<grid, 512, 0, stream>>>(a);
+    } else {
+      ssm_step_kernel<J, 1><<<grid, 256, 0, stream>>>(a);
+    }
   } else if (a.T < SSM_TC) {
     ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);
   } else if constexpr (J == 32) {

@@ -13,7 +13,8 @@ enum EpiKind : int {
   EPI_SILU = 4,      // r = SiLU(acc)
   EPI_RESIDUAL = 5,  // zf = aux + acc; r = first ? zf : out32 + scale*zf
   EPI_SCALE = 6,     // r = acc * scale
-  EPI_KINDS = 7,
+  EPI_SEGMENTS_TAP = 7,  // SEGMENTS, and the SiLU segment also to `tap`
+  EPI_KINDS = 8,
 };
 
 // Every GEMM writes r to out32 (fp32) and/or out16 (the operand type of the
@@ -38,7 +39,7 @@ struct EpiParams {
   void* out16 = nullptr;
   int ld16 = 0;
   // Optional fp32 tap: ZRAW writes the adapter output, RESIDUAL writes
-  // z_final (before the residual scaling), SEGMENTS writes the columns
+  // z_final (before the residual scaling), SEGMENTS_TAP writes the columns
   // [seg[2], seg[3]) (the SiLU segment) to tap[row, col - seg[2]].
   float* tap = nullptr;
   int ld_tap = 0;

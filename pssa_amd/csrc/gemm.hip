@@ -78,7 +78,7 @@ __device__ __forceinline__ float epi_value(const EpiParams& ep, float acc, int r
     return acc;
   } else if constexpr (KIND == EPI_SCALE) {
     return acc * ep.scale;
-  } else if constexpr (KIND == EPI_SEGMENTS) {
+  } else if constexpr (KIND == EPI_SEGMENTS || KIND == EPI_SEGMENTS_TAP) {
     if (col < ep.seg[0]) return softplus_f(acc);
     if (col < ep.seg[1]) return acc;
     if (col < ep.seg[2]) return sigmoid_f(acc);
@@ -156,7 +156,7 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
     if constexpr (KIND == EPI_ZRAW || KIND == EPI_RESIDUAL) {
       if (ep.tap)
         *reinterpret_cast<float4*>(ep.tap + (size_t)row * ep.ld_tap + col) = make_float4(tp[0], tp[1], tp[2], tp[3]);
-    } else if constexpr (KIND == EPI_SEGMENTS) {
+    } else if constexpr (KIND == EPI_SEGMENTS_TAP) {
       if (ep.tap)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -181,7 +181,7 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
         store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
         if constexpr (KIND == EPI_ZRAW) {
           if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ad[e];
-        } else if constexpr (KIND == EPI_SEGMENTS) {
+        } else if constexpr (KIND == EPI_SEGMENTS_TAP) {
           if (ep.tap && col + e >= ep.seg[2] && col + e < ep.seg[3])
             ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = epi_value<KIND>(ep, acc[e], row, col + e, ad[e]);
         } else if constexpr (KIND == EPI_RESIDUAL) {
@@ -553,6 +553,7 @@ static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const ui
     PSSA_GEMM_SK_CASE(EPI_SILU)
     PSSA_GEMM_SK_CASE(EPI_RESIDUAL)
     PSSA_GEMM_SK_CASE(EPI_SCALE)
+    PSSA_GEMM_SK_CASE(EPI_SEGMENTS_TAP)
     default:
       break;
   }
@@ -574,6 +575,7 @@ static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int
     PSSA_GEMM_CASE(EPI_SILU)
     PSSA_GEMM_CASE(EPI_RESIDUAL)
     PSSA_GEMM_CASE(EPI_SCALE)
+    PSSA_GEMM_CASE(EPI_SEGMENTS_TAP)
     default:
       break;
   }
@@ -596,6 +598,7 @@ static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint1
     PSSA_GEMM_LDS_CASE(EPI_SILU)
     PSSA_GEMM_LDS_CASE(EPI_RESIDUAL)
     PSSA_GEMM_LDS_CASE(EPI_SCALE)
+    PSSA_GEMM_LDS_CASE(EPI_SEGMENTS_TAP)
     default:
       break;
   }

@@ -279,6 +279,7 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     e_in.out32 = P;
     e_in.ld32 = n_in;
     if (taps) {  // the adapter activations of this step, for the Hebbian update
+      e_in.kind = EPI_SEGMENTS_TAP;
       e_in.tap = L->tap_act.as<float>() + l * rows * r;
       e_in.ld_tap = r;
     }

@@ -234,38 +234,75 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Full soft read for the model path (no top-k, small banks): the bank's keys
+// Full soft read for the model path (no top-k, small banks).  The bank's keys
 // stay in LDS for the whole launch, transposed so that lane j of a wave reads
 // slot j + 64q of key dimension i at consecutive addresses, next to
-// 1/(1 - |k|^2) per slot in f64.  One wave per query, up to SOFT_SPL slots
-// per lane, eight waves per workgroup.  The projection and the query norm
-// follow the reference's sequential f64 order exactly; the squared distance
-// sum runs in f64, and x = sum / ((1-|q|^2)(1-|k|^2)) is formed with the two
-// reciprocals.  Only the soft weights depend on the result (no ranking), so
-// 2 asinh(sqrt(x)) is then evaluated in f32 (relative error a few 1e-7, far
-// inside the 1e-4 parity gate), followed by the reference's f32 softmax
-// whose two sums over slots run as wave reductions.  Writes the
-// [n, capacity] weights; the value readout is a GEMM.
+// 1/(1 - |k|^2) and the exact key norm sum_i k_i^2 per slot in f64.
+//
+// Each wave owns a contiguous range of queries.  Their projections follow the
+// reference's sequential f64 order exactly (src/memory.rs:181-211), one query
+// per lane, so the two dependent 32-step chains are paid once per 64 queries
+// rather than once per query.  The squared distance of QG queries at a time
+// is then |q|^2 + |k|^2 - 2 q.k with every term in f64: the products of two
+// f32 values are exact in f64 and each sum has relative error below
+// d_key * 2^-53, so the absolute error of |q - k|^2 stays near 1e-14 (the
+// distance of even coincident points moves by < 1e-6).  One key element read
+// from LDS and converted once serves QG queries' fused multiply-adds.
+//
+// Only the soft weights depend on the distances (no ranking), so the rest is
+// evaluated in f32 with the hardware square root, log2 and exp2:
+//   d = 2 asinh(sqrt(x)) = 2 ln(sqrt(x) + sqrt(1 + x)) = 2 ln2 * l,
+//   l = log2(sqrt(x) + sqrt(1 + x)),  x = |q-k|^2 / ((1-|q|^2)(1-|k|^2)),
+//   exp((d_min - d) / tau) = exp2((l_min - l) * 2 / tau),
+// which moves a weight by a few 1e-6 relative, far inside the 1e-4 parity
+// gate; the softmax sums over slots run as wave reductions and every weight
+// is scaled by one reciprocal of the sum.  Writes the [n, capacity] weights;
+// the value readout is a GEMM.  A query's arithmetic does not depend on its
+// position in the batch or on QG, so one token at a time and a whole prefill
+// give the same bits.
 constexpr int SOFT_SPL = 8;            // slots per lane: capacity <= 512
 constexpr int SOFT_MAX_KEYS = 16384;   // dk * capacity floats held in LDS (64 KiB)
 constexpr int SOFT_MAX_DK = 64;
 constexpr int SOFT_WAVES = 8;
+constexpr int SOFT_QG = 4;             // queries sharing one pass over the keys
 
-// keyT rows have an odd pitch (capacity + 1): the transposing stores of a
-// wave (consecutive key dimensions) and the slot reads (consecutive slots)
-// both fall in distinct banks.
+// Slots per lane for a bank of `cap` slots (a power of two up to SOFT_SPL).
+__host__ __device__ __forceinline__ int soft_spl(int cap) {
+  return cap <= 64 ? 1 : cap <= 128 ? 2 : cap <= 256 ? 4 : 8;
+}
+// keyT rows hold every slot a lane reads (64 * spl, so no read needs a
+// clamp) and have an odd pitch: the transposing stores of a wave
+// (consecutive key dimensions) and the slot reads (consecutive slots) both
+// fall in distinct banks.
+__host__ __device__ __forceinline__ int soft_pitch(int cap) { return 64 * soft_spl(cap) + 1; }
 __host__ __device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
-  return (((size_t)dk * (cap + 1) + 1) & ~(size_t)1);  // keep the f64 arrays 8-byte aligned
+  return (((size_t)dk * soft_pitch(cap) + 1) & ~(size_t)1);  // keep the f64 arrays 8-byte aligned
+}
+// Dynamic LDS: keyT, then 1/(1-|k|^2) and |k|^2 (f64), then each wave's QG
+// projected queries (f32).
+static size_t soft_read_lds(int dk, int cap, int qg) {
+  return soft_keys_floats(dk, cap) * sizeof(float) + 2 * (size_t)cap * sizeof(double) +
+         (size_t)SOFT_WAVES * qg * dk * sizeof(float);
 }
 
-__global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs a) {
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)b, l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+template <int QG, int SPL>
+__global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu(4))) void soft_read_kernel(
+    RetrieveArgs a) {
   extern __shared__ float smem[];
   const int cap = a.capacity, dk = a.dk, cnt = a.count_dev ? a.count_dev[0] : a.count;
-  float* keyT = smem;                                                  // [dk][cap + 1]
-  const int kp = cap + 1;
+  float* keyT = smem;                                                  // [dk][kp]
+  const int kp = soft_pitch(cap);
   double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]
-  double* pq = rk + cap;                                               // [waves][SOFT_MAX_DK]
+  double* kk = rk + cap;                                               // [cap]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* pw = reinterpret_cast<float*>(kk + cap) + wave * QG * dk;     // [QG][dk]
   // Coalesced reads of the row-major keys, transposed on the way into LDS;
   // eight loads per thread are issued before their stores.
   if (dk % 4 == 0 && ((uintptr_t)a.keys & 15) == 0) {
@@ -295,84 +332,118 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) void soft_read_kernel(RetrieveArgs
       keyT[i * kp + sl] = a.keys[e];
     }
   }
-  for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
   __syncthreads();
-  double* p = pq + wave * SOFT_MAX_DK;
-
-  for (int n = blockIdx.x * SOFT_WAVES + wave; n < a.n; n += gridDim.x * SOFT_WAVES) {
-    const float* qrow = a.q + (size_t)n * a.ld_q;
-    // diffeomorphic_project (src/memory.rs:194-211): sequential f64 norm.
-    const float qv = lane < dk ? qrow[lane] : 0.0f;
-    p[lane] = (double)qv;
-    wave_sync();
-    double r2 = 0.0;
-    {
-#pragma clang fp contract(off)
-      for (int i = 0; i < dk; ++i) r2 = r2 + p[i] * p[i];
+  for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) {
+    rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
+    double s2 = 0.0;
+    for (int i = 0; i < dk; ++i) {
+      const double kv = keyT[i * kp + sl];
+      s2 = fma(kv, kv, s2);
     }
-    const double r = sqrt(r2);
-    const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
-    const float pv = (float)((double)qv * scale);
-    if (a.q_pnc && lane < dk) a.q_pnc[(size_t)n * dk + lane] = pv;
-    wave_sync();
-    p[lane] = (double)pv;
-    wave_sync();
-    // squared_norm of the projected query (src/memory.rs:181-192).
-    double qs = 0.0;
-    {
-#pragma clang fp contract(off)
-      for (int i = 0; i < dk; ++i) qs = qs + p[i] * p[i];
-    }
-    float q_sq = (float)qs;
-    if (qs < 1.0 && q_sq == 1.0f) q_sq = __uint_as_float(0x3f7fffffu);
-    const double rq = 1.0 / (1.0 - (double)q_sq);
+    kk[sl] = s2;
+  }
+  __syncthreads();
 
-    float dist[SOFT_SPL];
-    float local_min = FLT_MAX;
-    if (cnt > 0) {
-      double sq[SOFT_SPL];
-#pragma unroll
-      for (int j = 0; j < SOFT_SPL; ++j) sq[j] = 0.0;
+  const float c2 = 2.0f / a.tau;
+
+  const int nw = gridDim.x * SOFT_WAVES;
+  const int per = (a.n + nw - 1) / nw;
+  const int qb = (blockIdx.x * SOFT_WAVES + wave) * per;
+  const int qe = min(a.n, qb + per);
+  for (int c0 = qb; c0 < qe; c0 += 64) {
+    const int na = min(64, qe - c0);
+    // ---- projection, one query per lane (src/memory.rs:181-211) ----
+    double scale = 1.0, qs = 0.0, rq = 1.0;
+    if (lane < na) {
+#pragma clang fp contract(off)
+      const float* qrow = a.q + (size_t)(c0 + lane) * a.ld_q;
+      double r2 = 0.0;
       for (int i = 0; i < dk; ++i) {
-        const double pi = p[i];
-        const float* kr = keyT + i * kp;
+        const double v = qrow[i];
+        r2 = r2 + v * v;
+      }
+      const double r = sqrt(r2);
+      scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+      for (int i = 0; i < dk; ++i) {
+        const double pv = (double)(float)((double)qrow[i] * scale);
+        qs = qs + pv * pv;
+      }
+      float q_sq = (float)qs;
+      if (qs < 1.0 && q_sq == 1.0f) q_sq = __uint_as_float(0x3f7fffffu);
+      rq = 1.0 / (1.0 - (double)q_sq);
+    }
+
+    for (int g0 = 0; g0 < na; g0 += QG) {
+      const int ng = min(QG, na - g0);
+      // Projected queries of this group into LDS (and the q_pnc tap).
 #pragma unroll
-        for (int j = 0; j < SOFT_SPL; ++j) {
+      for (int g = 0; g < QG; ++g) {
+        const int src = g < ng ? g0 + g : g0;
+        const double sc = readlane_f64(scale, src);
+        if (lane < dk) {
+          const float qv = a.q[(size_t)(c0 + src) * a.ld_q + lane];
+          const float pv = (float)((double)qv * sc);
+          pw[g * dk + lane] = pv;
+          if (a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;
+        }
+      }
+      wave_sync();
+      double dot[QG][SPL];
+#pragma unroll
+      for (int g = 0; g < QG; ++g)
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) dot[g][j] = 0.0;
+      // Slots >= count read whatever that part of keyT holds; their results
+      // are discarded below.
+      for (int i = 0; i < dk; ++i) {
+        const float* kr = keyT + i * kp + lane;
+        double kv[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) kv[j] = (double)kr[64 * j];
+#pragma unroll
+        for (int g = 0; g < QG; ++g) {
+          const double pg = (double)pw[g * dk + i];
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) dot[g][j] = fma(pg, kv[j], dot[g][j]);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < QG; ++g) {
+        if (g >= ng) break;
+        const int n = c0 + g0 + g;
+        const double qs_g = readlane_f64(qs, g0 + g), rq_g = readlane_f64(rq, g0 + g);
+        float l[SPL];
+        float lm = FLT_MAX;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
           const int sl = lane + 64 * j;
-          const double t = pi - (double)(sl < cnt ? kr[sl] : 0.0f);
-          sq[j] = fma(t, t, sq[j]);
+          l[j] = 0.0f;
+          if (sl < cnt) {
+            const double sq = fmax(fma(-2.0, dot[g][j], qs_g + kk[sl]), 0.0);
+            const float x = (float)((sq * rq_g) * rk[sl]);
+            const float u = __builtin_amdgcn_sqrtf(x) + __builtin_amdgcn_sqrtf(1.0f + x);
+            l[j] = __builtin_amdgcn_logf(u);
+            lm = fminf(lm, l[j]);
+          }
+        }
+        const float lmin = wave_min(lm);
+        float e[SPL];
+        float part = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+          const int sl = lane + 64 * j;
+          e[j] = sl < cnt ? __builtin_amdgcn_exp2f((lmin - l[j]) * c2) : 0.0f;
+          part += e[j];
+        }
+        const float inv = 1.0f / wave_sum(part);
+#pragma unroll
+        for (int j = 0; j < SPL; ++j) {
+          const int sl = lane + 64 * j;
+          if (sl < cap) put_weight(a, n, sl, sl < cnt ? e[j] * inv : 0.0f);
         }
       }
-#pragma unroll
-      for (int j = 0; j < SOFT_SPL; ++j) {
-        const int sl = lane + 64 * j;
-        if (sl < cnt) {
-          const float x = (float)(sq[j] * rq * rk[sl]);
-          const float y = sqrtf(x);
-          // asinh(y) = log1p(y + y^2 / (1 + sqrt(1 + y^2))), y^2 = x.
-          dist[j] = 2.0f * log1pf(y + x / (1.0f + sqrtf(1.0f + x)));
-          local_min = fminf(local_min, dist[j]);
-        } else {
-          dist[j] = 0.0f;
-        }
-      }
+      wave_sync();
     }
-    const float min_dist = wave_min(local_min);
-    float e[SOFT_SPL];
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < SOFT_SPL; ++j) {
-      const int sl = lane + 64 * j;
-      e[j] = sl < cnt ? expf((min_dist - dist[j]) / a.tau) : 0.0f;
-      part += e[j];
-    }
-    const float sum = wave_sum(part);
-#pragma unroll
-    for (int j = 0; j < SOFT_SPL; ++j) {
-      const int sl = lane + 64 * j;
-      if (sl < cap) put_weight(a, n, sl, sl < cnt ? e[j] / sum : 0.0f);
-    }
-    wave_sync();
   }
 }
 
@@ -949,7 +1020,7 @@ size_t retrieve_scratch_bytes(const RetrieveArgs& a) {
 static bool soft_read_fits(const RetrieveArgs& a) {
   return (a.top_k == 0 || (!a.count_dev && a.top_k >= a.count)) && a.project && !a.q_norm && !a.out_val &&
          !a.out_min && !a.out_idx && a.dk <= SOFT_MAX_DK && a.capacity <= 64 * SOFT_SPL &&
-         (long)a.dk * (a.capacity + 1) <= SOFT_MAX_KEYS + SOFT_MAX_DK;
+         (long)a.dk * soft_pitch(a.capacity) <= SOFT_MAX_KEYS + SOFT_MAX_DK;
 }
 
 // Raises the kernel's dynamic-LDS limit to the device maximum once per
@@ -961,8 +1032,15 @@ static Status allow_large_lds() {
   PSSA_HIP_TRY(hipGetDevice(&dev));
   std::lock_guard<std::mutex> g(mu);
   if (dev >= 0 && dev < 64 && done[dev]) return Status::Ok();
-  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&soft_read_kernel),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  const void* soft[] = {
+      reinterpret_cast<const void*>(&soft_read_kernel<1, 1>), reinterpret_cast<const void*>(&soft_read_kernel<1, 2>),
+      reinterpret_cast<const void*>(&soft_read_kernel<1, 4>), reinterpret_cast<const void*>(&soft_read_kernel<1, 8>),
+      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 1>),
+      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 2>),
+      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 4>),
+      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 8>)};
+  for (const void* f : soft)
+    PSSA_HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&ranked_dot_kernel),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   if (dev >= 0 && dev < 64) done[dev] = true;
@@ -984,14 +1062,23 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
   if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
   if (soft_read_fits(a)) {
-    const size_t lds = soft_keys_floats(a.dk, a.capacity) * sizeof(float) +
-                       ((size_t)a.capacity + (size_t)SOFT_WAVES * SOFT_MAX_DK) * sizeof(double);
-    if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     int blocks = (a.n + SOFT_WAVES - 1) / SOFT_WAVES;
     if (blocks > 512) blocks = 512;
-    soft_read_kernel<<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);
-    PSSA_LAUNCH_CHECK("soft_read");
-    return Status::Ok();
+    const int per = (a.n + blocks * SOFT_WAVES - 1) / (blocks * SOFT_WAVES);
+    const int qg = per >= SOFT_QG ? SOFT_QG : 1;
+    const size_t lds = soft_read_lds(a.dk, a.capacity, qg);
+    if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
+    const int spl = soft_spl(a.capacity);
+#define PSSA_SOFT_CASE(QG, SPL)                                                  \
+  if (qg == QG && spl == SPL) {                                                  \
+    soft_read_kernel<QG, SPL><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);      \
+    PSSA_LAUNCH_CHECK("soft_read");                                              \
+    return Status::Ok();                                                         \
+  }
+    PSSA_SOFT_CASE(1, 1) PSSA_SOFT_CASE(1, 2) PSSA_SOFT_CASE(1, 4) PSSA_SOFT_CASE(1, 8)
+    PSSA_SOFT_CASE(SOFT_QG, 1) PSSA_SOFT_CASE(SOFT_QG, 2) PSSA_SOFT_CASE(SOFT_QG, 4) PSSA_SOFT_CASE(SOFT_QG, 8)
+#undef PSSA_SOFT_CASE
+    return Status::Invalid("retrieve: soft read shape");
   }
   if (ranked_read_fits(a) && a.scratch && a.scratch_bytes >= retrieve_scratch_bytes(a)) {
     PSSA_RETURN_IF(allow_large_lds());

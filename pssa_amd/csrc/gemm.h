@@ -51,6 +51,13 @@ struct EpiParams {
 Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const void* B, int ldb,
                    int M, int N, int K, const EpiParams& ep);
 
+// Same product for bf16 weights B and fp32 activations A, each activation
+// rounded to bf16 (nearest even) inside the kernel: the result equals
+// launch_gemm over a launch_to_bf16 copy of A, bit for bit.  K % 16 == 0,
+// lda % 4 == 0, ldb % 8 == 0, 16-byte aligned operands.
+Status launch_gemm_f32a(hipStream_t stream, const float* A, int lda, const uint16_t* B, int ldb, int M,
+                        int N, int K, const EpiParams& ep);
+
 // fp32 -> bf16 (round to nearest even) copy of a [rows, cols] matrix with
 // leading dimensions ld_in / ld_out.
 Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* out, int ld_out,

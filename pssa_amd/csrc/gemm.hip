@@ -481,69 +481,98 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
 // ---------------------------------------------------------------------------
 // bf16 GEMM for few token rows (decode steps, small batches): one wave per
-// 64 token rows x 32 weight rows, no LDS.  The operand fragments come
-// straight from global memory (L2) through a register ring SK_RING K-steps
+// 32*MT token rows x 32 weight rows, no LDS.  The operand fragments come
+// straight from global memory (L2) through a register ring RING K-steps
 // deep.  Each output element accumulates its 16-wide K-steps in increasing
 // order on the same MFMA as the tiled kernels, so every result is bit-for-bit
 // the one those produce; only the tile shape differs, which gives
-// (N/32) x (M/64) independent waves instead of a handful of 128 x 256 tiles.
+// (N/32) x (M/(32*MT)) independent waves instead of a handful of 128 x 256
+// tiles.  With fp32 activations (TA = float) each fragment is rounded to
+// bf16 (nearest even, as launch_to_bf16) in registers when it is consumed, so
+// the product equals the one over a separately converted copy.
 constexpr int SK_RING = 8;
 
-template <int KIND>
-__global__ __launch_bounds__(64) void gemm_skinny_kernel(const uint16_t* __restrict__ A, int lda,
+template <typename TA>
+struct SkFrag {  // one lane's 8 K-elements of one token row
+  static constexpr int V = sizeof(TA) == 2 ? 1 : 2;  // 16-byte loads
+  uint4 v[V];
+  __device__ __forceinline__ bf16x8_t bf16() const {
+    bf16x8_t f;
+    if constexpr (V == 1) {
+      __builtin_memcpy(&f, &v[0], 16);
+    } else {
+      const uint32_t w[4] = {pack_bf16x2(__uint_as_float(v[0].x), __uint_as_float(v[0].y)),
+                             pack_bf16x2(__uint_as_float(v[0].z), __uint_as_float(v[0].w)),
+                             pack_bf16x2(__uint_as_float(v[1].x), __uint_as_float(v[1].y)),
+                             pack_bf16x2(__uint_as_float(v[1].z), __uint_as_float(v[1].w))};
+      __builtin_memcpy(&f, w, 16);
+    }
+    return f;
+  }
+};
+
+template <int KIND, typename TA, int MT>
+__global__ __launch_bounds__(64) void gemm_skinny_kernel(const TA* __restrict__ A, int lda,
                                                          const uint16_t* __restrict__ B, int ldb, int M,
                                                          int N, int K, int vec_epi, EpiParams ep) {
   const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
-  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 64;
-  const uint16_t* pa0 = A + (size_t)min(m0 + l32, M - 1) * lda + 8 * half;
-  const uint16_t* pa1 = A + (size_t)min(m0 + 32 + l32, M - 1) * lda + 8 * half;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32 * MT;
+  const TA* pa[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) pa[t] = A + (size_t)min(m0 + 32 * t + l32, M - 1) * lda + 8 * half;
   const uint16_t* pb = B + (size_t)min(n0 + l32, N - 1) * ldb + 8 * half;
   // K % 16 == 0.  The loop is branch-free (prefetches past the end reload
   // the last step and go unused), so the compiler's wait counts stay exact
   // and SK_RING steps of loads remain in flight.
   const int nk = K / 16;
-  bf16x8_t ra0[SK_RING], ra1[SK_RING], rb[SK_RING];
+  SkFrag<TA> ra[SK_RING][MT];
+  uint4 rb[SK_RING];
   auto fetch = [&](int kt, int slot) {
     const int ko = min(kt, nk - 1) * 16;
-    uint4 x0 = *reinterpret_cast<const uint4*>(pa0 + ko);
-    uint4 x1 = *reinterpret_cast<const uint4*>(pa1 + ko);
-    uint4 y = *reinterpret_cast<const uint4*>(pb + ko);
-    __builtin_memcpy(&ra0[slot], &x0, 16);
-    __builtin_memcpy(&ra1[slot], &x1, 16);
-    __builtin_memcpy(&rb[slot], &y, 16);
-  };
-  f32x16_t acc0, acc1;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int v = 0; v < SkFrag<TA>::V; ++v)
+        ra[slot][t].v[v] = *reinterpret_cast<const uint4*>(pa[t] + ko + v * (16 / sizeof(TA)));
+    rb[slot] = *reinterpret_cast<const uint4*>(pb + ko);
+  };
+  f32x16_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  auto step = [&](int q) {
+    bf16x8_t fb;
+    __builtin_memcpy(&fb, &rb[q], 16);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb, ra[q][t].bf16(), acc[t], 0, 0, 0);
+  };
 #pragma unroll
   for (int q = 0; q < SK_RING; ++q) fetch(q, q);
   int k0 = 0;
   for (; k0 + SK_RING <= nk; k0 += SK_RING) {
 #pragma unroll
     for (int q = 0; q < SK_RING; ++q) {
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra0[q], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra1[q], acc1, 0, 0, 0);
+      step(q);
       fetch(k0 + SK_RING + q, q);
     }
   }
   // The remaining nk - k0 < SK_RING steps are in slots 0 ..
 #pragma unroll
-  for (int q = 0; q < SK_RING; ++q) {
-    if (q < nk - k0) {
-      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra0[q], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[q], ra1[q], acc1, 0, 0, 0);
-    }
-  }
-  epilogue_32x32<uint16_t, KIND>(ep, acc0, m0 + l32, n0, M, N, vec_epi, half, l32);
-  epilogue_32x32<uint16_t, KIND>(ep, acc1, m0 + 32 + l32, n0, M, N, vec_epi, half, l32);
+  for (int q = 0; q < SK_RING; ++q)
+    if (q < nk - k0) step(q);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    epilogue_32x32<uint16_t, KIND>(ep, acc[t], m0 + 32 * t + l32, n0, M, N, vec_epi, half, l32);
 }
 
-static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const uint16_t* A, int lda,
+template <typename TA, int MT>
+static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const TA* A, int lda,
                                const uint16_t* B, int ldb, int M, int N, int K, int ve,
                                const EpiParams& ep) {
-#define PSSA_GEMM_SK_CASE(KD)                                                             \
-  case KD:                                                                                \
-    gemm_skinny_kernel<KD><<<grid, 64, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+#define PSSA_GEMM_SK_CASE(KD)                                                                      \
+  case KD:                                                                                         \
+    gemm_skinny_kernel<KD, TA, MT><<<grid, 64, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
     break;
   switch (kind) {
     PSSA_GEMM_SK_CASE(EPI_STORE)
@@ -607,35 +636,57 @@ static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint1
 
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const void* B, int ldb,
-                   int M, int N, int K, const EpiParams& ep) {
-  if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
+// Checks the epilogue operands; `vec_epi` tells whether every row operand is
+// 16-byte aligned at multiples of 4 columns (vector epilogue).
+static Status check_epilogue(const EpiParams& ep, bool bf16, int& vec_epi) {
   if (ep.kind < 0 || ep.kind >= EPI_KINDS) return Status::Invalid("gemm: unknown epilogue");
   if (!ep.out32 && !ep.out16) return Status::Invalid("gemm: no output");
   if (ep.kind == EPI_RESIDUAL && !ep.out32) return Status::Invalid("gemm: residual needs the fp32 output");
   if (ep.kind == EPI_ZRAW && (!ep.y || !ep.g || (ep.rank > 0 && (!ep.act || !ep.U))))
     return Status::Invalid("gemm: z_raw epilogue operands missing");
-  const bool bf16 = dtype == PSSA_HIP_BF16;
-  const int ve = bf16 ? 8 : 4;
-  const int vec_load = (K % ve == 0) && (lda % ve == 0) && (ldb % ve == 0) && al16(A) && al16(B);
-  // Epilogue vectors: every row operand 16-byte aligned at multiples of 4 columns.
-  bool vec_epi = true;
+  bool v = true;
   auto chk32 = [&](const float* p, int ld) {
-    if (p) vec_epi = vec_epi && al16(p) && ld % 4 == 0;
+    if (p) v = v && al16(p) && ld % 4 == 0;
   };
   chk32(ep.out32, ep.ld32);
   chk32(ep.aux, ep.ld_aux);
   chk32(ep.y, ep.ld_y);
   chk32(ep.g, ep.ld_g);
   chk32(ep.tap, ep.ld_tap);
-  if (ep.out16) vec_epi = vec_epi && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
+  if (ep.out16) v = v && ((uintptr_t)ep.out16 % (bf16 ? 8 : 16) == 0) && ep.ld16 % 4 == 0;
+  vec_epi = v ? 1 : 0;
+  return Status::Ok();
+}
+
+Status launch_gemm_f32a(hipStream_t stream, const float* A, int lda, const uint16_t* B, int ldb, int M,
+                        int N, int K, const EpiParams& ep) {
+  if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
+  if (K % 16 != 0 || lda % 4 != 0 || ldb % 8 != 0 || !al16(A) || !al16(B))
+    return Status::Invalid("gemm: fp32-activation product needs K % 16 == 0 and 16-byte rows");
+  int vec_epi = 0;
+  PSSA_RETURN_IF(check_epilogue(ep, true, vec_epi));
+  const dim3 grid((N + 31) / 32, (M + 31) / 32);
+  if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
+  launch_skinny_kind<float, 1>(stream, ep.kind, grid, A, lda, B, ldb, M, N, K, vec_epi, ep);
+  PSSA_LAUNCH_CHECK("gemm_skinny_f32a");
+  return Status::Ok();
+}
+
+Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const void* B, int ldb,
+                   int M, int N, int K, const EpiParams& ep) {
+  if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
+  const bool bf16 = dtype == PSSA_HIP_BF16;
+  int vec_epi = 0;
+  PSSA_RETURN_IF(check_epilogue(ep, bf16, vec_epi));
+  const int ve = bf16 ? 8 : 4;
+  const int vec_load = (K % ve == 0) && (lda % ve == 0) && (ldb % ve == 0) && al16(A) && al16(B);
   const bool vec_bf16 = bf16 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B);
   // Few token rows: the 128 x 256 tiling would leave most CUs idle.
   if (vec_bf16 && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
     const dim3 grid((N + 31) / 32, (M + 63) / 64);
     if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
-    launch_skinny_kind(stream, ep.kind, grid, static_cast<const uint16_t*>(A), lda,
-                       static_cast<const uint16_t*>(B), ldb, M, N, K, vec_epi, ep);
+    launch_skinny_kind<uint16_t, 2>(stream, ep.kind, grid, static_cast<const uint16_t*>(A), lda,
+                                    static_cast<const uint16_t*>(B), ldb, M, N, K, vec_epi, ep);
     PSSA_LAUNCH_CHECK("gemm_skinny");
     return Status::Ok();
   }

@@ -45,14 +45,18 @@ __device__ __forceinline__ uint16_t bf16_of(float f) {
 
 constexpr int RMS_REG = 16;  // rows of up to 1024 columns are held in registers
 
+// Also clears row r of Z (may be null), the readout the scan accumulates into.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ X,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta,
                                                       float* __restrict__ XN,
-                                                      uint16_t* __restrict__ XNh, int d, size_t rows) {
+                                                      uint16_t* __restrict__ XNh, float* __restrict__ Z,
+                                                      int d, size_t rows) {
   const size_t r = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (r >= rows) return;
+  if (Z)
+    for (int i = lane; i < d; i += 64) Z[r * d + i] = 0.0f;
   const float* x = X + r * d;
   if (d <= 64 * RMS_REG) {  // the row stays in registers; all loads issue at once
     float xv[RMS_REG];
@@ -262,9 +266,11 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
 
   for (size_t l = 0; l < c.depth; ++l) {
     const DevBlock& B = M->blocks[l];
+    const bool step_y = ssm_step_writes_y((int)T, s);
     PSSA_RETURN_IF(tm.mark(ST_NORM));
     rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
-        X, B.gamma.as<float>(), B.beta.as<float>(), XN, XNh16, d, rows);
+        X, B.gamma.as<float>(), B.beta.as<float>(), XN, XNh16,
+        ssm_needs_zeroed_y(s) && !step_y ? Y : nullptr, d, rows);
     PSSA_LAUNCH_CHECK("rmsnorm");
 
     // [delta | B | C | q_x | gate | adapter act] = x W_in^T with softplus,
@@ -286,9 +292,6 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
     if (l == 0 && first_in_done) PSSA_HIP_TRY(hipEventRecord(first_in_done, st));
 
-    PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
-    const bool step_y = ssm_step_writes_y((int)T, s);
-    if (ssm_needs_zeroed_y(s) && !step_y) PSSA_RETURN_IF(launch_fill_zero(st, Y, rows * d));
     PSSA_RETURN_IF(tm.mark(ST_SSM));
     SsmArgs sa;
     sa.delta = P;
@@ -314,10 +317,9 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
       sa.ld_y16 = d;
     }
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
-    PSSA_RETURN_IF(tm.mark(ST_SSM_AUX));
-    if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
-
-    // q_euc = y W_qh^T + q_x.
+    // q_euc = y W_qh^T + q_x.  In a bf16 model y enters the product rounded
+    // to bf16: the single-step scan writes that copy itself, otherwise the
+    // product rounds the fp32 readout as it loads it.
     PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));
     EpiParams e_q;
     e_q.kind = EPI_ADD_AUX;
@@ -325,7 +327,12 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     e_q.ld_aux = n_in;
     e_q.out32 = Q;
     e_q.ld32 = k;
-    PSSA_RETURN_IF(launch_gemm(st, dt, Yh, d, B.w_qh.p, d, m, k, d, e_q));
+    if (bf16 && !step_y && d % 16 == 0)
+      PSSA_RETURN_IF(launch_gemm_f32a(st, Y, d, static_cast<const uint16_t*>(B.w_qh.p), d, m, k, d, e_q));
+    else {
+      if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
+      PSSA_RETURN_IF(launch_gemm(st, dt, Yh, d, B.w_qh.p, d, m, k, d, e_q));
+    }
 
     PSSA_RETURN_IF(tm.mark(ST_RETRIEVE));
     RetrieveArgs ra;

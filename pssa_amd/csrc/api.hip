@@ -739,10 +739,12 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     const int nz = pssa::ssm_state_blocks((int)s);
     if (nz > 2) PSSA_RETURN_IF(L->Ypart.alloc((size_t)nz * n * d * 4));
     PSSA_RETURN_IF(pssa::launch_fill_zero(ctx->stream, L->carry.as<float>(), lanes * c.depth * d * s));
-    PSSA_HIP_TRY(hipStreamCreateWithFlags(&L->aux_stream, hipStreamNonBlocking));
     PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming));
-    PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_first, hipEventDisableTiming));
-    PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_join, hipEventDisableTiming));
+    for (int g = 0; g < pssa_hip_lanes::kMaxGroups - 1; ++g) {
+      PSSA_HIP_TRY(hipStreamCreateWithFlags(&L->aux_stream[g], hipStreamNonBlocking));
+      PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_first[g], hipEventDisableTiming));
+      PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_join[g], hipEventDisableTiming));
+    }
     PSSA_RETURN_IF(sync(ctx));
     *out = L.release();
     return Status::Ok();

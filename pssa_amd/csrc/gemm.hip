@@ -196,10 +196,40 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
 // n32.  Accumulator layout (weights as the MFMA's first operand): lane l
 // holds token row `row` (= tile row + l%32) and output columns
 // n32 + 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.
+// bf16 pairs of the adapter activations act[row, q0 + 8*half .. +7] (zero
+// past the rank or the rows): the B fragment of the adapter MFMA.  One row's
+// fragment serves every output tile of that row.
+__device__ __forceinline__ void adapter_act_frag(const EpiParams& ep, int row, int M, int q0, int half,
+                                                 uint32_t (&wa)[4]) {
+  const int q = q0 + half * 8;
+  const float* src = ep.act + (size_t)row * ep.ld_act + q;
+  if (row < M && q + 8 <= ep.rank && ((uintptr_t)src & 15) == 0) {
+    const float4 a0 = *reinterpret_cast<const float4*>(src);
+    const float4 a1 = *reinterpret_cast<const float4*>(src + 4);
+    wa[0] = pack_bf16x2(a0.x, a0.y);
+    wa[1] = pack_bf16x2(a0.z, a0.w);
+    wa[2] = pack_bf16x2(a1.x, a1.y);
+    wa[3] = pack_bf16x2(a1.z, a1.w);
+    return;
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float a0 = (row < M && q + 2 * p < ep.rank) ? src[2 * p] : 0.0f;
+    const float a1 = (row < M && q + 2 * p + 1 < ep.rank) ? src[2 * p + 1] : 0.0f;
+    wa[p] = pack_bf16x2(a0, a1);
+  }
+}
+
+// Epilogue of one 32x32 accumulator tile whose weight rows start at column
+// n32.  Accumulator layout (weights as the MFMA's first operand): lane l
+// holds token row `row` (= tile row + l%32) and output columns
+// n32 + 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.  `act0` (bf16 GEMMs with
+// the z_raw epilogue, may be null) is the row's adapter fragment for
+// q0 = 0, loaded once by the caller for all tiles of the row.
 template <typename T, int KIND>
 __device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16_t& acc, int row,
                                                int n32, int M, int N, int vec_epi, int half,
-                                               int l32) {
+                                               int l32, const uint32_t* act0 = nullptr) {
   f32x16_t adv;
 #pragma unroll
   for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
@@ -211,15 +241,24 @@ __device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16
       const uint16_t* U = static_cast<const uint16_t*>(ep.U);
       for (int q0 = 0; q0 < ep.rank; q0 += 16) {
         uint32_t wa[4], wu[4];
+        if (q0 == 0 && act0) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const int q = q0 + half * 8 + 2 * p;
-          const float a0 = (row < M && q < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q] : 0.0f;
-          const float a1 = (row < M && q + 1 < ep.rank) ? ep.act[(size_t)row * ep.ld_act + q + 1] : 0.0f;
-          wa[p] = pack_bf16x2(a0, a1);
-          const uint32_t u0 = (urow < N && q < ep.rank) ? U[(size_t)urow * ep.rank + q] : 0u;
-          const uint32_t u1 = (urow < N && q + 1 < ep.rank) ? U[(size_t)urow * ep.rank + q + 1] : 0u;
-          wu[p] = u0 | (u1 << 16);
+          for (int p = 0; p < 4; ++p) wa[p] = act0[p];
+        } else {
+          adapter_act_frag(ep, row, M, q0, half, wa);
+        }
+        const int q = q0 + half * 8;
+        const uint16_t* us = U + (size_t)urow * ep.rank + q;
+        if (urow < N && q + 8 <= ep.rank && ((uintptr_t)us & 15) == 0) {
+          const uint4 v = *reinterpret_cast<const uint4*>(us);
+          wu[0] = v.x, wu[1] = v.y, wu[2] = v.z, wu[3] = v.w;
+        } else {
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t u0 = (urow < N && q + 2 * p < ep.rank) ? us[2 * p] : 0u;
+            const uint32_t u1 = (urow < N && q + 2 * p + 1 < ep.rank) ? us[2 * p + 1] : 0u;
+            wu[p] = u0 | (u1 << 16);
+          }
         }
         bf16x8_t fa, fu;
         __builtin_memcpy(&fa, wa, 16);
@@ -472,11 +511,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
 
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int t = 0; t < MT; ++t) {
+    const int row = m0 + wm * MT * 32 + t * 32 + l32;
+    uint32_t act0[4] = {0u, 0u, 0u, 0u};
+    if constexpr (KIND == EPI_ZRAW) adapter_act_frag(ep, row, M, 0, half, act0);
 #pragma unroll
     for (int u = 0; u < NW; ++u)
-      epilogue_32x32<uint16_t, KIND>(ep, acc[t][u], m0 + wm * MT * 32 + t * 32 + l32,
-                                     n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half, l32);
+      epilogue_32x32<uint16_t, KIND>(ep, acc[t][u], row, n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half,
+                                     l32, KIND == EPI_ZRAW ? act0 : nullptr);
+  }
 }
 
 // ---------------------------------------------------------------------------

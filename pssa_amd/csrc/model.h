@@ -92,17 +92,22 @@ struct pssa_hip_lanes {
   std::array<int, pssa::ST_COUNT> stage_calls{};
   std::vector<hipEvent_t> events;
   std::vector<int> event_stage;
-  // Second stream (default priority) for the concurrent lane group of a
-  // prefill, and the events that fork and join it.
-  hipStream_t aux_stream = nullptr;
-  hipEvent_t ev_fork = nullptr, ev_first = nullptr, ev_join = nullptr;
+  // Extra streams (default priority) for the concurrent lane groups of a
+  // prefill, and the events that fork, stagger and join them.
+  static constexpr int kMaxGroups = 4;
+  hipStream_t aux_stream[kMaxGroups - 1] = {};
+  hipEvent_t ev_fork = nullptr;
+  hipEvent_t ev_first[kMaxGroups - 1] = {}, ev_join[kMaxGroups - 1] = {};
   ~pssa_hip_lanes() {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
     if (graph) (void)hipGraphDestroy(graph);
-    for (hipEvent_t e : {ev_fork, ev_first, ev_join})
-      if (e) (void)hipEventDestroy(e);
-    if (aux_stream) (void)hipStreamDestroy(aux_stream);
+    if (ev_fork) (void)hipEventDestroy(ev_fork);
+    for (int g = 0; g < kMaxGroups - 1; ++g) {
+      if (ev_first[g]) (void)hipEventDestroy(ev_first[g]);
+      if (ev_join[g]) (void)hipEventDestroy(ev_join[g]);
+      if (aux_stream[g]) (void)hipStreamDestroy(aux_stream[g]);
+    }
   }
 };
 

@@ -15,6 +15,7 @@
 //   head        logits = h_last U^T / sqrt(d)   (last token of each lane only)
 #include "model.h"
 
+#include <algorithm>
 #include <cmath>
 
 #include "gemm.h"
@@ -435,24 +436,38 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
   return tm.finish();
 }
 
+constexpr int kPrefillLaneGroups = 2;
+static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per lane group");
+
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   const hipStream_t st = L->ctx->stream;
   const pssa_hip_config& c = L->model->cfg;
   const int nz = ssm_state_blocks((int)c.d_state);
   float* ypart = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
-  // Two lane groups on two streams: the VALU-bound scan of one group runs
-  // beside the MFMA-bound GEMMs of the other.  Group 1 starts once group 0's
-  // first input projection is issued, which keeps the two a stage apart.
-  if (!taps && !L->timing && L->aux_stream && n_lanes >= 2 && T >= 64) {
-    const size_t g0 = n_lanes / 2, g1 = n_lanes - g0;
+  // Lane groups on their own streams: the VALU-bound scan of one group runs
+  // beside the MFMA-bound GEMMs of the others.  Group g starts once group
+  // g-1's first input projection is issued, which keeps them a stage apart.
+  // Two groups measure best at the 32-lane prefill (three and four run
+  // 2-3% slower: their smaller scans leave the CUs less evenly loaded).
+  const int G = (int)std::min<size_t>(kPrefillLaneGroups, n_lanes);
+  if (!taps && !L->timing && G >= 2 && T >= 64) {
     PSSA_HIP_TRY(hipEventRecord(L->ev_fork, st));
-    PSSA_HIP_TRY(hipStreamWaitEvent(L->aux_stream, L->ev_fork, 0));
-    PSSA_RETURN_IF(prefill_view(L, st, 0, g0, T, false, false, L->ev_first, ypart));
-    PSSA_HIP_TRY(hipStreamWaitEvent(L->aux_stream, L->ev_first, 0));
-    float* ypart1 = ypart ? ypart + (size_t)nz * g0 * T * c.d_latent : nullptr;
-    PSSA_RETURN_IF(prefill_view(L, L->aux_stream, g0, g1, T, false, false, nullptr, ypart1));
-    PSSA_HIP_TRY(hipEventRecord(L->ev_join, L->aux_stream));
-    PSSA_HIP_TRY(hipStreamWaitEvent(st, L->ev_join, 0));
+    size_t lane0 = 0;
+    for (int g = 0; g < G; ++g) {
+      const size_t ng = n_lanes / G + ((size_t)g < n_lanes % G ? 1 : 0);
+      const hipStream_t sg = g == 0 ? st : L->aux_stream[g - 1];
+      if (g > 0) {
+        PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_fork, 0));
+        PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_first[g - 1], 0));
+      }
+      float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
+      PSSA_RETURN_IF(prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp));
+      lane0 += ng;
+    }
+    for (int g = 1; g < G; ++g) {
+      PSSA_HIP_TRY(hipEventRecord(L->ev_join[g - 1], L->aux_stream[g - 1]));
+      PSSA_HIP_TRY(hipStreamWaitEvent(st, L->ev_join[g - 1], 0));
+    }
     return Status::Ok();
   }
   return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart);

@@ -357,16 +357,29 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu
     if (lane < na) {
 #pragma clang fp contract(off)
       const float* qrow = a.q + (size_t)(c0 + lane) * a.ld_q;
+      // Eight loads in flight before the dependent sums (the sums keep the
+      // reference's order).
       double r2 = 0.0;
-      for (int i = 0; i < dk; ++i) {
-        const double v = qrow[i];
-        r2 = r2 + v * v;
+      for (int i0 = 0; i0 < dk; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k < dk ? qrow[i0 + k] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (i0 + k < dk) r2 = r2 + (double)v[k] * (double)v[k];
       }
       const double r = sqrt(r2);
       scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
-      for (int i = 0; i < dk; ++i) {
-        const double pv = (double)(float)((double)qrow[i] * scale);
-        qs = qs + pv * pv;
+      for (int i0 = 0; i0 < dk; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = i0 + k < dk ? qrow[i0 + k] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (i0 + k < dk) {
+            const double pv = (double)(float)((double)v[k] * scale);
+            qs = qs + pv * pv;
+          }
       }
       float q_sq = (float)qs;
       if (qs < 1.0 && q_sq == 1.0f) q_sq = __uint_as_float(0x3f7fffffu);

@@ -81,22 +81,28 @@ __global__ __launch_bounds__(256) void dense_scan_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // d_state = 64 with the operands 16-byte aligned: the transition streams
 // through a ring of DS_RING LDS slots, each holding one step's A_t (16 KiB)
-// and b_t, filled by direct-to-LDS loads (global_load_lds_dwordx4) from
-// waves 1-3 only, so that their s_waitcnt counts cover loads alone; wave 0
-// writes h_(t-1) out.  Every thread owns 16 columns of one row (4 threads a
-// row); the row's partial dot products meet through DPP quad permutes, and
-// one barrier per step publishes h_t and the next ring slot.  Ring depth 9
-// keeps 8 steps (130 KiB) of A in flight per sequence.
+// and b_t, filled by direct-to-LDS loads (global_load_lds_dwordx4).  Waves
+// 0-3 only compute: every thread owns 16 columns of one row (4 threads a
+// row), the row's partial dot products meet through DPP quad permutes, and
+// one barrier per step publishes h_t; wave 0 also writes h_(t-1) out.  Waves
+// 4 and 5 only load (9 and 8 instructions a slot), so their s_waitcnt counts
+// cover loads alone and no load instruction sits on the compute waves'
+// per-step path.  Ring depth 9 keeps 7 slots (116 KiB) in flight per
+// sequence; 7 x 9 = 63 instructions is the most a wave can count.
 constexpr int DS_S = 64;
 constexpr int DS_RING = 9;
 constexpr int DS_SLOT = DS_S * DS_S + DS_S;       // floats per ring slot (A_t then b_t)
 constexpr int DS_CHUNKS = DS_SLOT / 4;            // 16-byte chunks per slot (1040)
-constexpr int DS_PER_INSTR = 3 * 64;              // chunks one round of waves 1-3 moves
+constexpr int DS_LOADERS = 2;                     // waves issuing the ring's loads
+constexpr int DS_NI0 = 9;                         // instructions per slot, first loader
+constexpr int DS_NI1 = (DS_CHUNKS - DS_NI0 * 64 + 63) / 64;  // second loader (8)
+constexpr int DS_THREADS = (4 + DS_LOADERS) * 64;
+static_assert(DS_NI0 >= DS_NI1, "loader 0 carries the larger share");
 
 // s_waitcnt immediate for vmcnt(v) alone (gfx9: vmcnt bits [3:0] and [15:14],
 // expcnt and lgkmcnt left at their no-wait maxima).
 constexpr int vmcnt_only(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
-static_assert((DS_RING - 2) * 6 <= 63, "vmcnt holds at most 63");
+static_assert((DS_RING - 2) * DS_NI0 <= 63, "vmcnt holds at most 63");
 
 __device__ __forceinline__ float quad_sum(float v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // quad_perm 1,0,3,2
@@ -104,29 +110,32 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void dense_scan_ring_kernel(const float* __restrict__ A,
-                                                              const float* __restrict__ Bv,
-                                                              const float* __restrict__ H0,
-                                                              float* __restrict__ H, int L) {
+__global__ __launch_bounds__(DS_THREADS) void dense_scan_ring_kernel(const float* __restrict__ A,
+                                                                     const float* __restrict__ Bv,
+                                                                     const float* __restrict__ H0,
+                                                                     float* __restrict__ H, int L) {
   __shared__ __attribute__((aligned(1024))) float ring_s[DS_RING][DS_SLOT];
   __shared__ __attribute__((aligned(16))) float sh_s[2][DS_S];
   float* ring = &ring_s[0][0];
   float* sh = &sh_s[0][0];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = tid >> 2, part = tid & 3, c0 = part * 16;
+  const bool loader = wave >= 4;
+  const int row = (tid >> 2) & (DS_S - 1), part = tid & 3, c0 = part * 16;
   const int seq = blockIdx.x;
   const float* Aseq = A + (size_t)seq * L * DS_S * DS_S;
   const float* bseq = Bv + (size_t)seq * L * DS_S;
   float* hseq = H + (size_t)seq * L * DS_S;
 
-  // Waves 1-3: chunk c = i * 192 + (wave - 1) * 64 + lane of a slot; the
+  // Loader w (wave 4 + w) moves chunks first_w + 64 i + lane of a slot; the
   // source of chunk c at step t is src[i] + t * (A or b stride).
-  constexpr int NI = (DS_CHUNKS + DS_PER_INSTR - 1) / DS_PER_INSTR;
-  const float* src[NI];
-  size_t stride[NI];
+  const int lw = loader ? wave - 4 : 0;
+  const int ni = lw == 0 ? DS_NI0 : DS_NI1;
+  const int first = lw * DS_NI0 * 64;
+  const float* src[DS_NI0];
+  size_t stride[DS_NI0];
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int c = min(i * DS_PER_INSTR + (max(wave, 1) - 1) * 64 + lane, DS_CHUNKS - 1);
+  for (int i = 0; i < DS_NI0; ++i) {
+    const int c = min(first + i * 64 + lane, DS_CHUNKS - 1);
     const bool in_a = c < DS_S * DS_S / 4;
     src[i] = in_a ? Aseq + 4 * c : bseq + 4 * (c - DS_S * DS_S / 4);
     stride[i] = in_a ? (size_t)DS_S * DS_S : (size_t)DS_S;
@@ -134,34 +143,41 @@ __global__ __launch_bounds__(256) void dense_scan_ring_kernel(const float* __res
   auto issue = [&](int t) {
     float* slot = ring + (t % DS_RING) * DS_SLOT;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int first = i * DS_PER_INSTR + (wave - 1) * 64;
-      if (first < DS_CHUNKS && first + lane < DS_CHUNKS)
+    for (int i = 0; i < DS_NI0; ++i) {
+      const int c = first + i * 64;
+      if (i < ni && c + lane < DS_CHUNKS)
         __builtin_amdgcn_global_load_lds((const void*)(src[i] + (size_t)t * stride[i]),
-                                         (__attribute__((address_space(3))) void*)(slot + 4 * first), 16, 0, 0);
+                                         (__attribute__((address_space(3))) void*)(slot + 4 * c), 16, 0, 0);
     }
   };
   if (tid < DS_S) sh[tid] = H0 ? H0[(size_t)seq * DS_S + tid] : 0.0f;
-  if (wave > 0)
+  if (loader)
     for (int t = 0; t < DS_RING - 1 && t < L; ++t) issue(t);
 
   int cur = 0;
   for (int t = 0; t < L; ++t) {
-    if (wave > 0) {
+    if (loader) {
       // Slot t is complete once only the slots issued after it are in flight.
       if (t + DS_RING - 2 < L) {
-        if (wave == 3)
-          __builtin_amdgcn_s_waitcnt(vmcnt_only((DS_RING - 2) * 5));
+        if (lw == 0)
+          __builtin_amdgcn_s_waitcnt(vmcnt_only((DS_RING - 2) * DS_NI0));
         else
-          __builtin_amdgcn_s_waitcnt(vmcnt_only((DS_RING - 2) * 6));
+          __builtin_amdgcn_s_waitcnt(vmcnt_only((DS_RING - 2) * DS_NI1));
       } else {
         __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // near the end
       }
+    } else {
+      // This wave's LDS writes are done; meet the others (a plain barrier: a
+      // __syncthreads fence would also drain the ring's loads).
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | (0xF) | (0x3 << 14));  // lgkmcnt(0)
     }
-    // This wave's LDS writes are done; meet the others (a plain barrier: a
-    // __syncthreads fence would also drain the ring's loads).
-    __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | (0xF) | (0x3 << 14));  // lgkmcnt(0)
     asm volatile("s_barrier" ::: "memory");
+    if (loader) {
+      // Every compute wave finished step t - 1: refill its slot.
+      if (t + DS_RING - 1 < L) issue(t + DS_RING - 1);
+      continue;
+    }
+
     const float* slot = ring + (t % DS_RING) * DS_SLOT;
     const float* arow = slot + row * DS_S + c0;
     const float* h = sh + cur * DS_S + c0;
@@ -177,14 +193,12 @@ __global__ __launch_bounds__(256) void dense_scan_ring_kernel(const float* __res
     }
     const float acc = quad_sum((p[0] + p[1]) + (p[2] + p[3]));
     if (part == 0) sh[(cur ^ 1) * DS_S + row] = acc + slot[DS_S * DS_S + row];
-    // Off the step's critical path: refill the slot consumed at step t - 1,
-    // write h_(t-1) out.
-    if (wave > 0 && t + DS_RING - 1 < L) issue(t + DS_RING - 1);
+    // Off the step's critical path: write h_(t-1) out.
     if (wave == 0 && t > 0) hseq[(size_t)(t - 1) * DS_S + lane] = sh[cur * DS_S + lane];
     cur ^= 1;
   }
   __syncthreads();
-  if (wave == 0) hseq[(size_t)(L - 1) * DS_S + lane] = sh[cur * DS_S + lane];
+  if (wave == 0) hseq[(size_t)(L - 1) * DS_S + lane] = sh[(L & 1) * DS_S + lane];
 }
 
 static bool ring_fits(const float* A, const float* B, int s) {
@@ -197,7 +211,7 @@ Status launch_dense_scan(hipStream_t stream, const float* A, const float* B, con
                          int batch, int L, int s) {
   if (batch <= 0 || L <= 0 || s <= 0) return Status::Invalid("dense scan: dimensions must be positive");
   if (ring_fits(A, B, s)) {
-    dense_scan_ring_kernel<<<batch, 256, 0, stream>>>(A, B, H0, H, L);
+    dense_scan_ring_kernel<<<batch, DS_THREADS, 0, stream>>>(A, B, H0, H, L);
   } else if (s <= 16)
     dense_scan_kernel<16, 16><<<batch, 256, 0, stream>>>(A, B, H0, H, L, s);
   else if (s <= 32)

@@ -98,6 +98,11 @@ typedef struct {
   uint64_t* mem_last_seen; /* [C]            memory.last_seen_step           */
   uint64_t mem_count;      /*                memory.count                    */
   uint64_t mem_write_head; /*                memory.write_head               */
+  /* Hybrid read (src/memory.rs:19-33, runtime-only, never checkpointed). */
+  float* mem_hybrid_gate;     /* [C] memory.hybrid_gate; NULL reads as 1.0  */
+  uint64_t* mem_hybrid_age;   /* [C] memory.hybrid_age; NULL reads as 0     */
+  uint32_t mem_hybrid_enabled; /*    memory.hybrid_enabled                  */
+  float mem_hybrid_lam;        /*    memory.hybrid_lam, in (0, 1]           */
 } pssa_hip_block;
 
 /* Host view of PSSALayerV2's inference parameters (src/pssa.rs:1920-1960). */
@@ -215,6 +220,20 @@ int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n
                                size_t top_k, float* d_out_val, float* d_out_min,
                                uint32_t* d_out_idx, char* err, size_t err_len);
 
+/* retrieve_hybrid_into (src/memory.rs:568-660) for n_q queries against one
+ * bank state: over the live slots (the top_k nearest by (distance bits, slot),
+ * or all when top_k is 0 or >= count) w_i = exp((min_dist - d_i)/tau) *
+ * gate[i] * (float)exp(age[i] * ln(lam)), renormalised; a read whose live
+ * weights are all zero falls back to the unweighted softmax.  gate and age
+ * [count] are the bank's hybrid_gate / hybrid_age (the caller bumps ages
+ * before the read, as forward_inference does).  Outputs as pssa_hip_retrieve;
+ * out_idx [n_q, top_k] lists the live slots in ascending order. */
+int pssa_hip_retrieve_hybrid(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                             const float* norm_sq, const float* values, size_t capacity, size_t count,
+                             size_t d_key, size_t d_val, float tau, size_t top_k, const float* gate,
+                             const uint64_t* age, float lam, float* out_val, float* out_min,
+                             uint32_t* out_idx, float* out_weights, char* err, size_t err_len);
+
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t (no reference counterpart:
  * the reference's SSM is diagonal; this is the standalone dense kernel).
  * a [batch, L, s, s] row-major (h_t[r] = sum_c A_t[r][c] h_{t-1}[c] + b_t[r]),
@@ -309,6 +328,25 @@ int pssa_hip_model_get_plastic(pssa_hip_model* model, size_t layer, float* adapt
                                float* values, float* norm_sq, float* confidence,
                                uint64_t* last_seen, uint64_t* count, uint64_t* write_head,
                                uint64_t* step, char* err, size_t err_len);
+
+/* set_hybrid_read (src/pssa.rs:2232-2243, src/memory.rs:510-518) on every
+ * block: lam must be finite and in (0, 1].  With the hybrid read on, every
+ * forward step first ages each live slot by one (bump_hybrid_ages,
+ * src/memory.rs:501-507) and then reads with retrieve_hybrid_into
+ * (src/pssa.rs:1153-1162); all lanes of a call advance together, so token t
+ * of a prefill reads with the ages bumped t + 1 times and the ages end T
+ * higher (one lane: exactly the reference's token loop).  The plastic decode
+ * write becomes insert_gated_protected (src/memory.rs:524-556) with the gate
+ * the mean of the block's memory-injection gate at the written token
+ * (src/pssa.rs:3719-3726).  Every bank write resets the slot's gate to 1.0
+ * (gated writes: to that gate) and its age to 0 (src/memory.rs:300-301). */
+int pssa_hip_model_set_hybrid_read(pssa_hip_model* model, int enabled, float lam, char* err,
+                                   size_t err_len);
+
+/* Reads one block's hybrid-read state back from the device: gate [C] and
+ * age [C] (either may be NULL). */
+int pssa_hip_model_get_hybrid(pssa_hip_model* model, size_t layer, float* gate, uint64_t* age,
+                              char* err, size_t err_len);
 
 /* Per-stage kernel time (ms, summed over layers) of the most recent prefill,
  * recorded with HIP events on the stream the kernels run on.  enable = 1 turns

@@ -59,6 +59,13 @@ def lib() -> C.CDLL:
         "oracle_bank_insert_protected": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float,
                                           C.c_uint64], C.c_int64),
         "oracle_refractory_gain": ([C.c_uint64, C.c_float], C.c_float),
+        "oracle_bank_insert_gated": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float], C.c_int64),
+        "oracle_bank_insert_gated_protected": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float,
+                                                C.c_float, C.c_uint64], C.c_int64),
+        "oracle_bank_bump_hybrid_ages": ([vp, C.c_uint64], None),
+        "oracle_retrieve_hybrid_batch": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, fp,
+                                          C.c_size_t, C.c_float, C.c_size_t, fp, C.POINTER(C.c_uint64),
+                                          C.c_float, fp, fp, u32p, fp, C.c_int], None),
         "oracle_gemm_xwt": ([fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp], None),
         "oracle_ssm_forward": ([fp, fp, fp, fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, fp, fp], None),
         "oracle_forward_inference": ([vp, fp, C.c_uint32, fp], None),
@@ -244,6 +251,94 @@ def retrieve_batch(keys, norm_sq, values, count, q_pnc, tau, top_k=0, threads=1)
     lib().oracle_retrieve_batch(ptr(keys), ptr(norm_sq), ptr(values), count, capacity, dk, dv, ptr(q_pnc), n,
                                 tau, top_k, ptr(out), ptr(mn), ptr(idx, C.c_uint32), threads)
     return out, mn, idx
+
+
+def retrieve_hybrid_batch(keys, norm_sq, values, count, q_pnc, tau, gate, age, lam, top_k=0, threads=1):
+    """retrieve_hybrid_into per query against one bank state; returns
+    (out_val [n, dv], min_dist [n], live idx [n, top_k] or None, weights [n, C])."""
+    keys, norm_sq, values, q_pnc, gate = (f32(a) for a in (keys, norm_sq, values, q_pnc, gate))
+    age = np.ascontiguousarray(age, dtype=np.uint64)
+    capacity, dk = keys.shape
+    dv = values.shape[1]
+    n = q_pnc.shape[0]
+    out = np.empty((n, dv), np.float32)
+    mn = np.empty(n, np.float32)
+    idx = np.empty((n, top_k), np.uint32) if top_k else None
+    w = np.empty((n, capacity), np.float32)
+    lib().oracle_retrieve_hybrid_batch(ptr(keys), ptr(norm_sq), ptr(values), count, capacity, dk, dv, ptr(q_pnc), n,
+                                       tau, top_k, ptr(gate), ptr(age, C.c_uint64), lam, ptr(out), ptr(mn),
+                                       ptr(idx, C.c_uint32), ptr(w), threads)
+    return out, mn, idx, w
+
+
+class Bank:
+    """A single HyperbolicEpisodicBankV2 (src/memory.rs) held as numpy arrays,
+    driven through the oracle's bank primitives (for the hybrid-read tests)."""
+
+    def __init__(self, capacity: int, dk: int, dv: int):
+        self.capacity, self.dk, self.dv = capacity, dk, dv
+        self.keys = np.zeros((capacity, dk), np.float32)
+        self.values = np.zeros((capacity, dv), np.float32)
+        self.norm_sq = np.zeros(capacity, np.float32)
+        self.confidence = np.ones(capacity, np.float32)
+        self.last_seen = np.zeros(capacity, np.uint64)
+        self.gate = np.ones(capacity, np.float32)
+        self.age = np.zeros(capacity, np.uint64)
+        self._blk = _OracleBlock()
+        b = self._blk
+        b.mem_keys, b.mem_values, b.mem_norm_sq = ptr(self.keys), ptr(self.values), ptr(self.norm_sq)
+        b.mem_confidence, b.mem_last_seen = ptr(self.confidence), ptr(self.last_seen, C.c_uint64)
+        b.mem_hybrid_gate, b.mem_hybrid_age = ptr(self.gate), ptr(self.age, C.c_uint64)
+        b.mem_count = b.mem_write_head = 0
+
+    @property
+    def count(self) -> int:
+        return int(self._blk.mem_count)
+
+    def _ref(self):
+        return C.cast(C.pointer(self._blk), vp)
+
+    def insert(self, key, val) -> int:
+        k, v = f32(key), f32(val)
+        return int(lib().oracle_bank_insert(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v)))
+
+    def insert_gated(self, key, val, gate) -> int:
+        k, v = f32(key), f32(val)
+        return int(lib().oracle_bank_insert_gated(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v),
+                                                  gate))
+
+    def insert_gated_protected(self, key, val, gate, surprise, step) -> int:
+        k, v = f32(key), f32(val)
+        return int(lib().oracle_bank_insert_gated_protected(self._ref(), self.capacity, self.dk, self.dv, ptr(k),
+                                                            ptr(v), gate, surprise, step))
+
+    def bump_hybrid_ages(self, times: int = 1) -> None:
+        lib().oracle_bank_bump_hybrid_ages(self._ref(), times)
+
+    def retrieve_soft(self, q, tau):
+        out, w, mn = retrieve(self.keys, self.norm_sq, self.values, self.count, q, tau)
+        return out, w, mn
+
+    def retrieve_hybrid(self, q, tau, lam, top_k=0):
+        out, mn, idx, w = retrieve_hybrid_batch(self.keys, self.norm_sq, self.values, self.count,
+                                                f32(q).reshape(1, -1), tau, self.gate, self.age, lam, top_k)
+        return out[0], w[0], mn[0]
+
+
+class _OracleBlock(C.Structure):
+    """oracle_block: only the bank fields are used by the bank primitives."""
+    _fields_ = [(n, fp) for n in (
+        "norm_gamma", "norm_beta", "a_raw", "w_delta", "w_b", "w_c", "w_qx", "w_qh", "w_gate", "w_proj",
+        "adapter_down", "adapter_up", "adapter_slow", "mlp_w1", "mlp_w2", "mem_keys", "mem_values",
+        "mem_norm_sq", "mem_confidence")] + [
+        ("mem_last_seen", C.POINTER(C.c_uint64)),
+        ("mem_count", C.c_uint64),
+        ("mem_write_head", C.c_uint64),
+        ("mem_hybrid_gate", fp),
+        ("mem_hybrid_age", C.POINTER(C.c_uint64)),
+        ("mem_hybrid_enabled", C.c_uint32),
+        ("mem_hybrid_lam", C.c_float),
+    ]
 
 
 def project(q):

@@ -231,6 +231,68 @@ float retrieve(const float* keys, const float* norm_sq, const float* values, siz
   return min_dist;
 }
 
+inline uint64_t sat_add(uint64_t a, uint64_t b) { return a > UINT64_MAX - b ? UINT64_MAX : a + b; }
+
+// --- src/memory.rs:568-660 retrieve_hybrid_into ----------------------------------
+// Slot i's age is age[i] + age_add (the bumps of this pass not yet stored).
+float retrieve_hybrid(const float* keys, const float* norm_sq, const float* values, size_t count,
+                      size_t capacity, size_t dk, size_t dv, const float* q, float tau, size_t top_k,
+                      const float* gate, const uint64_t* age, uint64_t age_add, float lam,
+                      float* out_val, float* w, uint32_t* out_idx) {
+  if (count == 0) {
+    std::fill(out_val, out_val + dv, 0.0f);
+    std::fill(w, w + capacity, 0.0f);
+    return 0.0f;
+  }
+  const double log_lam = std::log((double)lam);
+  float q_sq = squared_norm(q, dk);
+  float min_dist = FLT_MAX;
+  std::vector<float> dists(count);
+  for (size_t idx = 0; idx < count; idx++) {
+    dists[idx] = poincare_distance(q, q_sq, keys + idx * dk, norm_sq[idx], dk);
+    min_dist = std::fmin(min_dist, dists[idx]);
+  }
+  std::vector<char> live(count, 1);
+  if (top_k != 0 && top_k < count) {
+    std::vector<std::pair<uint32_t, uint32_t>> all(count);
+    for (size_t idx = 0; idx < count; idx++) all[idx] = {f2u(dists[idx]), (uint32_t)idx};
+    std::partial_sort(all.begin(), all.begin() + top_k, all.end());
+    std::fill(live.begin(), live.end(), 0);
+    for (size_t i = 0; i < top_k; i++) live[all[i].second] = 1;
+    if (out_idx) {
+      size_t n = 0;
+      for (size_t idx = 0; idx < count; idx++)
+        if (live[idx]) out_idx[n++] = (uint32_t)idx;
+    }
+  }
+  std::fill(w, w + capacity, 0.0f);
+  float sum = 0.0f;
+  for (size_t idx = 0; idx < count; idx++) {
+    if (!live[idx]) continue;
+    const uint64_t a = sat_add(age ? age[idx] : 0, age_add);
+    const float decay = (float)std::exp((double)a * log_lam);
+    const float wi = expf((min_dist - dists[idx]) / tau) * (gate ? gate[idx] : 1.0f) * decay;
+    w[idx] = wi;
+    sum += wi;
+  }
+  if (sum == 0.0f) {  // fully gated out: the unweighted softmax over the live slots
+    for (size_t idx = 0; idx < count; idx++) {
+      if (!live[idx]) continue;
+      w[idx] = expf((min_dist - dists[idx]) / tau);
+      sum += w[idx];
+    }
+  }
+  std::fill(out_val, out_val + dv, 0.0f);
+  for (size_t idx = 0; idx < count; idx++) {
+    if (!live[idx]) continue;
+    const float wi = w[idx] / sum;
+    w[idx] = wi;
+    const float* v = values + idx * dv;
+    for (size_t j = 0; j < dv; j++) out_val[j] += wi * v[j];
+  }
+  return min_dist;
+}
+
 // --- src/defense.rs:18-22, 45-67 --------------------------------------------------
 float refractory_gain(uint64_t delta_tokens, float tau) {
   float dt = (float)delta_tokens;
@@ -241,6 +303,7 @@ float refractory_gain(uint64_t delta_tokens, float tau) {
 // Scratch for one block's token step (src/pssa.rs:506-620 inference buffers).
 struct Scratch {
   std::vector<float> xn, delta, bb, cc, y, qe, qp, mw, mval, g, mp, act, adout, zraw, h1, u, zf;
+  uint64_t age_add = 1;  // hybrid read: bumps of the current pass not yet stored
   std::vector<float> rates;  // -softplus(a_raw), src/pssa.rs:787-796
   void resize(const oracle_config& c) {
     size_t d = c.d_latent, s = c.d_state, k = c.d_mem_key, C = c.mem_capacity, r = c.adapter_rank;
@@ -305,8 +368,13 @@ void block_forward(const oracle_block& b, const oracle_config& c, Scratch& sc, f
   for (size_t q = 0; q < k; q++)
     sc.qe[q] = dot(b.w_qx + q * d, sc.xn.data(), d) + dot(b.w_qh + q * d, sc.y.data(), d);
   project(sc.qe.data(), sc.qp.data(), k);
-  retrieve(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
-           sc.qp.data(), c.tau_mem, 0, sc.mval.data(), sc.mw.data(), nullptr);
+  if (b.mem_hybrid_enabled)  // src/pssa.rs:1153-1162 (the ages are bumped by the caller)
+    retrieve_hybrid(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
+                    sc.qp.data(), c.tau_mem, 0, b.mem_hybrid_gate, b.mem_hybrid_age, sc.age_add,
+                    b.mem_hybrid_lam, sc.mval.data(), sc.mw.data(), nullptr);
+  else
+    retrieve(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
+             sc.qp.data(), c.tau_mem, 0, sc.mval.data(), sc.mw.data(), nullptr);
   matvec(b.w_gate, d, d, sc.xn.data(), sc.g.data());
   for (size_t i = 0; i < d; i++) sc.g[i] = sigmoid(sc.g[i]);
   matvec(b.w_proj, d, d, sc.mval.data(), sc.mp.data());
@@ -348,6 +416,9 @@ struct Runner {
     out.assign(c.d_latent, 0);
   }
   // --- src/pssa.rs:2312-2337 forward_inference_features (single loop) ----------
+  void set_age_add(uint64_t a) {
+    for (auto& x : sc) x.age_add = a;
+  }
   void features(float* state, uint32_t id) {
     const oracle_config& c = m->cfg;
     const size_t d = c.d_latent, ds = c.d_latent * c.d_state;
@@ -367,6 +438,15 @@ struct Runner {
     for (size_t v = 0; v < c.d_vocab; v++) lg[v] *= logit_scale;
   }
 };
+
+// bump_hybrid_ages (src/memory.rs:501-507) `times` times on every hybrid block.
+static void bump_hybrid(const oracle_model* m, uint64_t times) {
+  for (size_t l = 0; l < m->cfg.depth; l++) {
+    const oracle_block& b = m->blocks[l];
+    if (!b.mem_hybrid_enabled || !b.mem_hybrid_age) continue;
+    for (size_t i = 0; i < b.mem_count; i++) b.mem_hybrid_age[i] = sat_add(b.mem_hybrid_age[i], times);
+  }
+}
 
 template <class F>
 void parallel_for(size_t n, int threads, F f) {
@@ -526,6 +606,8 @@ int64_t oracle_bank_insert(oracle_block* b, size_t capacity, size_t dk, size_t d
   std::memcpy(b->mem_values + idx * dv, val, dv * 4);
   b->mem_confidence[idx] = 1.0f;
   b->mem_last_seen[idx] = 0;
+  if (b->mem_hybrid_gate) b->mem_hybrid_gate[idx] = 1.0f;  // src/memory.rs:300-301
+  if (b->mem_hybrid_age) b->mem_hybrid_age[idx] = 0;
   return (int64_t)idx;
 }
 
@@ -554,6 +636,65 @@ int64_t oracle_bank_insert_protected(oracle_block* b, size_t capacity, size_t dk
   int64_t ins = oracle_bank_insert(b, capacity, dk, dv, key, val);
   if (ins >= 0) b->mem_last_seen[ins] = step;
   return ins;
+}
+
+// --- src/memory.rs:488-499 insert_gated ----------------------------------------
+int64_t oracle_bank_insert_gated(oracle_block* b, size_t capacity, size_t dk, size_t dv,
+                                 const float* key, const float* val, float gate) {
+  if (!(std::isfinite(gate) && gate >= 0.0f)) return -1;
+  int64_t idx = oracle_bank_insert(b, capacity, dk, dv, key, val);
+  if (idx >= 0 && b->mem_hybrid_gate) b->mem_hybrid_gate[idx] = gate;
+  return idx;
+}
+
+// --- src/memory.rs:520-556 insert_gated_protected ------------------------------
+int64_t oracle_bank_insert_gated_protected(oracle_block* b, size_t capacity, size_t dk, size_t dv,
+                                           const float* key, const float* val, float gate,
+                                           float surprise, uint64_t step) {
+  if (!(std::isfinite(gate) && gate >= 0.0f)) return -1;
+  if (b->mem_count < capacity) {
+    int64_t idx = oracle_bank_insert_gated(b, capacity, dk, dv, key, val, gate);
+    if (idx >= 0) b->mem_last_seen[idx] = step;
+    return idx;
+  }
+  size_t idx = b->mem_write_head;
+  float* conf = &b->mem_confidence[idx];
+  uint64_t last = b->mem_last_seen[idx];
+  uint64_t delta_t = step > last ? step - last : 0;
+  float gain = refractory_gain(delta_t, 60.0f);
+  float damage = 0.08f * surprise * gain;
+  if (*conf > damage) {
+    *conf -= damage;
+    b->mem_last_seen[idx] = step;
+    return -1;
+  }
+  *conf = 1.0f;
+  b->mem_last_seen[idx] = step;
+  int64_t ins = oracle_bank_insert_gated(b, capacity, dk, dv, key, val, gate);
+  if (ins >= 0) b->mem_last_seen[ins] = step;
+  return ins;
+}
+
+// --- src/memory.rs:501-507 bump_hybrid_ages ------------------------------------
+void oracle_bank_bump_hybrid_ages(oracle_block* b, uint64_t times) {
+  if (!b->mem_hybrid_age) return;
+  for (size_t i = 0; i < b->mem_count; i++) b->mem_hybrid_age[i] = sat_add(b->mem_hybrid_age[i], times);
+}
+
+void oracle_retrieve_hybrid_batch(const float* keys, const float* norm_sq, const float* values,
+                                  size_t count, size_t capacity, size_t d_key, size_t d_val,
+                                  const float* q_pnc, size_t n_q, float tau, size_t top_k,
+                                  const float* gate, const uint64_t* age, float lam,
+                                  float* out_val, float* out_min, uint32_t* out_idx,
+                                  float* out_weights, int threads) {
+  parallel_for(n_q, threads, [&](size_t q) {
+    std::vector<float> w(capacity > 0 ? capacity : 1);
+    float mn = retrieve_hybrid(keys, norm_sq, values, count, capacity, d_key, d_val,
+                               q_pnc + q * d_key, tau, top_k, gate, age, 0, lam, out_val + q * d_val,
+                               w.data(), out_idx ? out_idx + q * top_k : nullptr);
+    if (out_min) out_min[q] = mn;
+    if (out_weights) std::memcpy(out_weights + q * capacity, w.data(), capacity * 4);
+  });
 }
 
 float oracle_refractory_gain(uint64_t delta_tokens, float tau) {
@@ -639,12 +780,14 @@ void oracle_ssm_forward(const float* delta, const float* b_proj, const float* x_
 void oracle_forward_inference(const oracle_model* m, float* state, uint32_t id, float* logits) {
   Runner run(m);
   run.features(state, id);
+  bump_hybrid(m, 1);
   if (logits) run.logits(logits);
 }
 
 void oracle_forward_features(const oracle_model* m, float* state, uint32_t id, float* features) {
   Runner run(m);
   run.features(state, id);
+  bump_hybrid(m, 1);
   std::memcpy(features, run.feat.data(), m->cfg.d_latent * 4);
 }
 
@@ -655,7 +798,25 @@ int oracle_prefill(const oracle_model* m, float* state, const uint32_t* ids, siz
   for (size_t t = 0; t < n; t++)
     if (ids[t] >= m->cfg.d_vocab) return -2;
   Runner run(m);
-  for (size_t t = 0; t < n; t++) run.features(state, ids[t]);
+  for (size_t t = 0; t < n; t++) {
+    run.set_age_add(t + 1);
+    run.features(state, ids[t]);
+  }
+  bump_hybrid(m, n);
+  if (logits) run.logits(logits);
+  return 0;
+}
+
+// Prefill of one lane without storing the hybrid ages (lanes advance together).
+static int prefill_lane(const oracle_model* m, float* state, const uint32_t* ids, size_t n, float* logits) {
+  if (n == 0) return -1;
+  for (size_t t = 0; t < n; t++)
+    if (ids[t] >= m->cfg.d_vocab) return -2;
+  Runner run(m);
+  for (size_t t = 0; t < n; t++) {
+    run.set_age_add(t + 1);
+    run.features(state, ids[t]);
+  }
   if (logits) run.logits(logits);
   return 0;
 }
@@ -666,9 +827,10 @@ int oracle_prefill_lanes(const oracle_model* m, float* states, const uint32_t* i
   size_t per = c.depth * c.d_latent * c.d_state;
   std::atomic<int> rc(0);
   parallel_for(lanes, threads, [&](size_t l) {
-    int r = oracle_prefill(m, states + l * per, ids + l * n, n, logits ? logits + l * c.d_vocab : nullptr);
+    int r = prefill_lane(m, states + l * per, ids + l * n, n, logits ? logits + l * c.d_vocab : nullptr);
     if (r) rc = r;
   });
+  if (rc.load() == 0) bump_hybrid(m, n);
   return rc.load();
 }
 
@@ -681,6 +843,7 @@ float oracle_train_chunk_forward(const oracle_model* m, float* state, const uint
   float total = 0.0f;
   std::vector<float> probs(v);
   for (size_t t = 0; t < n; t++) {
+    run.set_age_add(t + 1);  // src/pssa.rs:1334-1345 bumps per token too
     run.features(state, ids[t]);
     float* lg = logits + t * v;
     run.logits(lg);
@@ -696,6 +859,7 @@ float oracle_train_chunk_forward(const oracle_model* m, float* state, const uint
     float loss = (max_l - lg[targets[t]]) + logf(sum_exp);
     total += loss;
   }
+  bump_hybrid(m, n);
   return total / (float)n;
 }
 
@@ -764,6 +928,7 @@ void oracle_forward_taps(const oracle_model* m, float* state, uint32_t id, float
     if (l > 0)
       for (size_t i = 0; i < d; i++) run.feat[i] += scale * run.out[i];
   }
+  bump_hybrid(m, 1);
   if (logits) run.logits(logits);
 }
 
@@ -788,7 +953,7 @@ int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, s
     if (ids[i] >= V) return -1;
   std::vector<float> lg(lanes * V), surprise(lanes);
   std::vector<float> tq(lanes * depth * k), tz(lanes * depth * d), ta(lanes * depth * d),
-      tact(lanes * depth * r);
+      tact(lanes * depth * r), tgate(lanes * depth);
   // The rate cache does not change during decode (only banks and the fast
   // adapter do), so each stream keeps one runner.
   std::vector<std::unique_ptr<Runner>> runners(lanes);
@@ -806,6 +971,10 @@ int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, s
         std::memcpy(&tz[(ln * depth + l) * d], z, d * 4);
         std::memcpy(&ta[(ln * depth + l) * d], run.sc[l].adout.data(), d * 4);
         std::memcpy(&tact[(ln * depth + l) * r], run.sc[l].act.data(), r * 4);
+        // Hybrid write gate: mean memory-injection gate (src/pssa.rs:3719-3726).
+        float gs = 0.0f;
+        for (size_t i = 0; i < d; i++) gs += run.sc[l].g[i];
+        tgate[ln * depth + l] = gs / (float)d;
         if (l > 0)
           for (size_t i = 0; i < d; i++) run.feat[i] += scale * run.out[i];
       }
@@ -819,14 +988,21 @@ int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, s
       surprise[ln] = (mx + logf(sum)) - lgl[next];
       out_ids[step * lanes + ln] = next;
     });
+    bump_hybrid(m, 1);  // the lanes' reads of this step saw one more bump
     if (plastic) {
       const uint64_t cur = step_base + step + 1;
       for (size_t l = 0; l < depth; l++) {
         oracle_block* b = &m->blocks[l];
         for (size_t ln = 0; ln < lanes; ln++)
-          if (surprise[ln] > 3.5f)
-            oracle_bank_insert_protected(b, c.mem_capacity, k, d, &tq[(ln * depth + l) * k],
-                                         &tz[(ln * depth + l) * d], surprise[ln], cur);
+          if (surprise[ln] > 3.5f) {
+            if (b->mem_hybrid_enabled)
+              oracle_bank_insert_gated_protected(b, c.mem_capacity, k, d, &tq[(ln * depth + l) * k],
+                                                 &tz[(ln * depth + l) * d], tgate[ln * depth + l],
+                                                 surprise[ln], cur);
+            else
+              oracle_bank_insert_protected(b, c.mem_capacity, k, d, &tq[(ln * depth + l) * k],
+                                           &tz[(ln * depth + l) * d], surprise[ln], cur);
+          }
         for (size_t ln = 0; ln < lanes; ln++)
           oracle_hebbian_update(b->adapter_up, &tz[(ln * depth + l) * d], &ta[(ln * depth + l) * d],
                                 &tact[(ln * depth + l) * r], d, r);

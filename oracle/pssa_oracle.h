@@ -28,6 +28,10 @@
  *   refractory gate ................... pinned: closed form (feature_benchmark.rs:446-500)
  *   greedy sample ..................... pinned: total_cmp order and tie rule, closed
  *                                        cases (src/inference.rs:123-127)
+ *   hybrid read ....................... pinned: reference tests (memory.rs:893-1010:
+ *                                        neutral == soft bitwise, recency rebinding,
+ *                                        gate-zero dropout, fully gated fallback,
+ *                                        metadata reset on overwrite)
  *   decode composition (oracle_decode)  parity unpinned as a whole: it composes the
  *                                        pinned forward, greedy, insert_protected and
  *                                        Hebbian rules; the reference has no such step
@@ -80,6 +84,10 @@ typedef struct {
   uint64_t* mem_last_seen; /* [C] */
   uint64_t mem_count;
   uint64_t mem_write_head;
+  float* mem_hybrid_gate;    /* [C] or NULL (reads as 1.0) */
+  uint64_t* mem_hybrid_age;  /* [C] or NULL (reads as 0) */
+  uint32_t mem_hybrid_enabled;
+  float mem_hybrid_lam;
 } oracle_block;
 
 typedef struct {
@@ -134,6 +142,24 @@ int64_t oracle_bank_insert_protected(oracle_block* b, size_t capacity, size_t d_
                                      size_t d_val, const float* key, const float* val,
                                      float surprise, uint64_t step);
 float oracle_refractory_gain(uint64_t delta_tokens, float tau);
+/* Hybrid read state (src/memory.rs:488-556): insert_gated,
+ * insert_gated_protected, bump_hybrid_ages. */
+int64_t oracle_bank_insert_gated(oracle_block* b, size_t capacity, size_t d_key, size_t d_val,
+                                 const float* key, const float* val, float gate);
+int64_t oracle_bank_insert_gated_protected(oracle_block* b, size_t capacity, size_t d_key,
+                                           size_t d_val, const float* key, const float* val,
+                                           float gate, float surprise, uint64_t step);
+void oracle_bank_bump_hybrid_ages(oracle_block* b, uint64_t times);
+/* retrieve_hybrid_into (src/memory.rs:568-660) for n_q queries against one
+ * bank state (gate [count], age [count]); outputs as oracle_retrieve_batch,
+ * plus weights [n_q, capacity] (may be NULL).  out_idx lists the live slots
+ * in ascending order when top_k selects. */
+void oracle_retrieve_hybrid_batch(const float* keys, const float* norm_sq, const float* values,
+                                  size_t count, size_t capacity, size_t d_key, size_t d_val,
+                                  const float* q_pnc, size_t n_q, float tau, size_t top_k,
+                                  const float* gate, const uint64_t* age, float lam,
+                                  float* out_val, float* out_min, uint32_t* out_idx,
+                                  float* out_weights, int threads);
 
 /* Stage twins. */
 void oracle_gemm_xwt(const float* x, const float* w, size_t m, size_t n, size_t k, float* y);

@@ -59,6 +59,10 @@ class Block(C.Structure):
         ("mem_last_seen", u64p),
         ("mem_count", C.c_uint64),
         ("mem_write_head", C.c_uint64),
+        ("mem_hybrid_gate", fp),
+        ("mem_hybrid_age", u64p),
+        ("mem_hybrid_enabled", C.c_uint32),
+        ("mem_hybrid_lam", C.c_float),
     ]
 
 
@@ -114,6 +118,10 @@ def lib() -> C.CDLL:
                                      C.c_float, sz, fp, fp, fp, fp, fp, fp, fp, fp, err_t, sz], C.c_int),
         "pssa_hip_retrieve": ([vp, fp, sz, fp, fp, fp, sz, sz, sz, sz, C.c_float, sz, fp, fp, u32p, fp,
                                err_t, sz], C.c_int),
+        "pssa_hip_retrieve_hybrid": ([vp, fp, sz, fp, fp, fp, sz, sz, sz, sz, C.c_float, sz, fp, u64p, C.c_float,
+                                      fp, fp, u32p, fp, err_t, sz], C.c_int),
+        "pssa_hip_model_set_hybrid_read": ([vp, C.c_int, C.c_float, err_t, sz], C.c_int),
+        "pssa_hip_model_get_hybrid": ([vp, sz, fp, u64p, err_t, sz], C.c_int),
         "pssa_hip_retrieve_resident": ([vp, vp, sz, vp, vp, vp, sz, sz, sz, sz, C.c_float, sz, vp, vp, vp,
                                         err_t, sz], C.c_int),
         "pssa_hip_dense_scan": ([vp, fp, fp, fp, sz, sz, sz, fp, err_t, sz], C.c_int),

@@ -502,10 +502,12 @@ static Status bind_retrieve_scratch(pssa_hip_ctx* ctx, pssa::RetrieveArgs& ra) {
 
 extern "C" {
 
-int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
-                      const float* norm_sq, const float* values, size_t capacity, size_t count,
-                      size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
-                      float* out_min, uint32_t* out_idx, float* out_weights, char* err, size_t err_len) {
+// Host-buffer retrieval; gate/age (both or neither) select the hybrid read.
+static int retrieve_host(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                         const float* norm_sq, const float* values, size_t capacity, size_t count,
+                         size_t d_key, size_t d_val, float tau, size_t top_k, const float* gate,
+                         const uint64_t* age, float lam, float* out_val, float* out_min, uint32_t* out_idx,
+                         float* out_weights, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(check_ctx(ctx));
     PSSA_RETURN_IF(need(n_q && d_key && d_val && capacity, "retrieve: dimensions must be positive"));
@@ -514,17 +516,29 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
     PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
     PSSA_RETURN_IF(need(q_pnc && keys && norm_sq && values && out_val, "retrieve: null buffer"));
     PSSA_RETURN_IF(need(!out_idx || top_k > 0, "retrieve: indices need top_k > 0"));
+    const bool hybrid = gate != nullptr;
+    if (hybrid) {
+      PSSA_RETURN_IF(need(age != nullptr, "retrieve: the hybrid read needs gates and ages"));
+      PSSA_RETURN_IF(need(std::isfinite(lam) && lam > 0.0f && lam <= 1.0f, "hybrid decay lam must be in (0.0, 1.0]"));
+      for (size_t q = 0; q < count; ++q)
+        PSSA_RETURN_IF(need(std::isfinite(gate[q]) && gate[q] >= 0.0f,
+                            "hybrid write gate must be finite and nonnegative"));
+    }
     if (n_q > INT32_MAX / 4 || d_key > 4096 || d_val > 65536 || capacity > 8192)
       return Status::Invalid("retrieve: shape exceeds the supported range");
     // The query must lie in the open ball (retrieve_soft_into's assertion).
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
     const hipStream_t st = ctx->stream;
-    DevBuf dq, dk_, dn, dv, dval, dmin, didx, dw;
+    DevBuf dq, dk_, dn, dv, dval, dmin, didx, dw, dg, da;
     PSSA_RETURN_IF(upload(dq, q_pnc, n_q * d_key * 4, st));
     PSSA_RETURN_IF(upload(dk_, keys, capacity * d_key * 4, st));
     PSSA_RETURN_IF(upload(dn, norm_sq, capacity * 4, st));
     PSSA_RETURN_IF(upload(dv, values, capacity * d_val * 4, st));
+    if (hybrid && count > 0) {
+      PSSA_RETURN_IF(upload(dg, gate, count * 4, st));
+      PSSA_RETURN_IF(upload(da, age, count * 8, st));
+    }
     PSSA_RETURN_IF(dval.alloc(n_q * d_val * 4));
     if (out_min) PSSA_RETURN_IF(dmin.alloc(n_q * 4));
     if (out_idx) PSSA_RETURN_IF(didx.alloc(n_q * top_k * 4));
@@ -547,6 +561,11 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
     ra.out_val = dval.as<float>();
     ra.out_min = out_min ? dmin.as<float>() : nullptr;
     ra.out_idx = out_idx ? didx.as<uint32_t>() : nullptr;
+    if (hybrid && count > 0) {
+      ra.hgate = dg.as<float>();
+      ra.hage = da.as<unsigned long long>();
+      ra.log_lam = std::log((double)lam);
+    }
     PSSA_RETURN_IF(bind_retrieve_scratch(ctx, ra));
     PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
     PSSA_RETURN_IF(download(out_val, dval, n_q * d_val * 4, st));
@@ -556,6 +575,27 @@ int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const f
     return sync(ctx);
   };
   return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_retrieve(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                      const float* norm_sq, const float* values, size_t capacity, size_t count,
+                      size_t d_key, size_t d_val, float tau, size_t top_k, float* out_val,
+                      float* out_min, uint32_t* out_idx, float* out_weights, char* err, size_t err_len) {
+  return retrieve_host(ctx, q_pnc, n_q, keys, norm_sq, values, capacity, count, d_key, d_val, tau, top_k,
+                       nullptr, nullptr, 1.0f, out_val, out_min, out_idx, out_weights, err, err_len);
+}
+
+int pssa_hip_retrieve_hybrid(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, const float* keys,
+                             const float* norm_sq, const float* values, size_t capacity, size_t count,
+                             size_t d_key, size_t d_val, float tau, size_t top_k, const float* gate,
+                             const uint64_t* age, float lam, float* out_val, float* out_min,
+                             uint32_t* out_idx, float* out_weights, char* err, size_t err_len) {
+  if (!gate || !age) {
+    if (err && err_len) std::snprintf(err, err_len, "retrieve: the hybrid read needs gates and ages");
+    return PSSA_HIP_EINVAL;
+  }
+  return retrieve_host(ctx, q_pnc, n_q, keys, norm_sq, values, capacity, count, d_key, d_val, tau, top_k, gate,
+                       age, lam, out_val, out_min, out_idx, out_weights, err, err_len);
 }
 
 int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
@@ -619,6 +659,13 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
                               b.mem_values && b.mem_norm_sq,
                           "weights: null block tensor"));
       PSSA_RETURN_IF(need(b.mem_count <= C, "memory count exceeds capacity"));
+      if (b.mem_hybrid_enabled)
+        PSSA_RETURN_IF(need(std::isfinite(b.mem_hybrid_lam) && b.mem_hybrid_lam > 0.0f && b.mem_hybrid_lam <= 1.0f,
+                            "hybrid decay lam must be in (0.0, 1.0]"));
+      if (b.mem_hybrid_gate)
+        for (size_t q = 0; q < b.mem_count; ++q)
+          PSSA_RETURN_IF(need(std::isfinite(b.mem_hybrid_gate[q]) && b.mem_hybrid_gate[q] >= 0.0f,
+                              "hybrid write gate must be finite and nonnegative"));
       for (size_t q = 0; q < b.mem_count; ++q)
         PSSA_RETURN_IF(need(std::isfinite(b.mem_norm_sq[q]) && b.mem_norm_sq[q] >= 0.0f && b.mem_norm_sq[q] < 1.0f,
                             "memory key norms must lie in [0, 1)"));
@@ -672,6 +719,15 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       if (b.mem_last_seen)
         for (size_t q = 0; q < C; ++q) last[q] = b.mem_last_seen[q];
       const int meta[2] = {(int)b.mem_count, (int)(b.mem_write_head % C)};
+      std::vector<float> hg(C, 1.0f);
+      std::vector<unsigned long long> ha(C, 0ull);
+      if (b.mem_hybrid_gate) std::memcpy(hg.data(), b.mem_hybrid_gate, C * 4);
+      if (b.mem_hybrid_age)
+        for (size_t q = 0; q < C; ++q) ha[q] = b.mem_hybrid_age[q];
+      B.hybrid = b.mem_hybrid_enabled != 0;
+      B.lam = b.mem_hybrid_lam;
+      PSSA_RETURN_IF(upload(B.hgate, hg.data(), C * 4, st));
+      PSSA_RETURN_IF(upload(B.hage, ha.data(), C * 8, st));
       PSSA_RETURN_IF(upload(B.conf, conf.data(), C * 4, st));
       PSSA_RETURN_IF(upload(B.last_seen, last.data(), C * 8, st));
       PSSA_RETURN_IF(upload(B.meta, meta, sizeof(meta), st));
@@ -909,6 +965,42 @@ int pssa_hip_model_get_plastic(pssa_hip_model* M, size_t layer, float* adapter_u
   return pssa::finish(body(), err, err_len);
 }
 
+int pssa_hip_model_set_hybrid_read(pssa_hip_model* M, int enabled, float lam, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(M != nullptr, "null model"));
+    PSSA_RETURN_IF(need(std::isfinite(lam) && lam > 0.0f && lam <= 1.0f, "hybrid decay lam must be in (0.0, 1.0]"));
+    std::lock_guard<std::mutex> g(M->ctx->mu);
+    for (auto& B : M->blocks) {
+      B.hybrid = enabled != 0;
+      B.lam = lam;
+    }
+    ++M->hybrid_epoch;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_model_get_hybrid(pssa_hip_model* M, size_t layer, float* gate, uint64_t* age, char* err,
+                              size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(M != nullptr, "null model"));
+    PSSA_RETURN_IF(need(layer < M->cfg.depth, "layer out of range"));
+    std::lock_guard<std::mutex> g(M->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(M->ctx->device));
+    const hipStream_t st = M->ctx->stream;
+    const pssa::DevBlock& B = M->blocks[layer];
+    const size_t C = M->cfg.mem_capacity;
+    if (gate) PSSA_RETURN_IF(download(gate, B.hgate, C * 4, st));
+    std::vector<unsigned long long> a(C);
+    if (age) PSSA_RETURN_IF(download(a.data(), B.hage, C * 8, st));
+    PSSA_RETURN_IF(sync(M->ctx));
+    if (age)
+      for (size_t q = 0; q < C; ++q) age[q] = a[q];
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 }  // extern "C"
 
 namespace {
@@ -921,6 +1013,7 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
     PSSA_RETURN_IF(L->tap_z.alloc(D * n * c.d_latent * 4));
     PSSA_RETURN_IF(L->tap_a.alloc(D * n * c.d_latent * 4));
     PSSA_RETURN_IF(L->tap_act.alloc(D * n * c.adapter_rank * 4));
+    PSSA_RETURN_IF(L->tap_gmean.alloc(D * n * 4));
     PSSA_RETURN_IF(L->surprise.alloc(n * 4));
     PSSA_RETURN_IF(L->hebb_rate.alloc(D * n * 4));  // [depth, lanes]
     PSSA_RETURN_IF(L->bank_writer.alloc(D * c.mem_capacity * 4));
@@ -943,7 +1036,8 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
 }
 
 Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
-  if (L->graph_exec && L->graph_lanes == n_lanes && L->graph_plastic == (plastic ? 1 : 0))
+  if (L->graph_exec && L->graph_lanes == n_lanes && L->graph_plastic == (plastic ? 1 : 0) &&
+      L->graph_hybrid_epoch == L->model->hybrid_epoch)
     return Status::Ok();
   if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
   if (L->graph) (void)hipGraphDestroy(L->graph);
@@ -963,6 +1057,7 @@ Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   PSSA_HIP_TRY(hipGraphInstantiate(&L->graph_exec, graph, nullptr, nullptr, 0));
   L->graph_lanes = n_lanes;
   L->graph_plastic = plastic ? 1 : 0;
+  L->graph_hybrid_epoch = L->model->hybrid_epoch;
   return Status::Ok();
 }
 

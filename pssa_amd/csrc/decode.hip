@@ -127,6 +127,10 @@ struct PlasticArgs {
   const float* surprise; // [lanes]
   float* rate;           // [depth, lanes]
   int* writer;           // [depth, C]: the lane whose value a slot takes this step, or -1
+  float* hgate[kMaxDepth];               // hybrid write gate per slot
+  unsigned long long* hage[kMaxDepth];   // hybrid age per slot
+  int hybrid[kMaxDepth];                 // block reads (and writes) through the hybrid path
+  const float* gmean;    // [depth, lanes] mean memory-injection gate (hybrid blocks)
   const unsigned long long* step;
   int lanes, C, dk, d, r, wt_bf16;
 };
@@ -337,6 +341,10 @@ __global__ __launch_bounds__(256) void bank_copy_kernel(PlasticArgs p) {
   }
   if (blockIdx.y == 0 && tid < 64 && w[tid] >= 0) {
     const int c = c0 + tid;
+    // insert / insert_gated reset the slot's hybrid metadata (src/memory.rs:
+    // 300-301, 497): gate 1.0, or the write gate on a hybrid block; age 0.
+    p.hgate[l][c] = p.hybrid[l] ? p.gmean[(size_t)l * n + w[tid]] : 1.0f;
+    p.hage[l][c] = 0ull;
     const float* kq = p.tap_q + ((size_t)l * n + w[tid]) * p.dk;
     double acc = 0.0;
     {
@@ -411,6 +419,9 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
       p.values_t[l] = B.values_t.p;
       p.conf[l] = B.conf.as<float>();
       p.last_seen[l] = B.last_seen.as<unsigned long long>();
+      p.hgate[l] = B.hgate.as<float>();
+      p.hage[l] = B.hage.as<unsigned long long>();
+      p.hybrid[l] = B.hybrid ? 1 : 0;
       p.meta[l] = B.meta.as<int>();
       p.up[l] = B.u_fast.as<float>();
       p.slow[l] = B.u_slow.as<float>();
@@ -423,6 +434,7 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     p.surprise = L->surprise.as<float>();
     p.rate = L->hebb_rate.as<float>();
     p.writer = L->bank_writer.as<int>();
+    p.gmean = L->tap_gmean.as<float>();
     p.step = M->step.as<unsigned long long>();
     p.lanes = (int)n;
     p.C = C;

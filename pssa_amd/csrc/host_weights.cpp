@@ -214,6 +214,8 @@ extern "C" int pssa_hip_weights_populate_banks(const pssa_hip_weights* w, uint64
       std::memcpy(b.mem_values + slot * d, val.data(), d * sizeof(float));
       b.mem_confidence[slot] = 1.0f;
       b.mem_last_seen[slot] = 0;
+      if (b.mem_hybrid_gate) b.mem_hybrid_gate[slot] = 1.0f;  // src/memory.rs:300-301
+      if (b.mem_hybrid_age) b.mem_hybrid_age[slot] = 0;
     }
   }
   return PSSA_HIP_OK;

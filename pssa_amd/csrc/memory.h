@@ -26,6 +26,17 @@ struct RetrieveArgs {
   // absent or too small the general kernel runs instead.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // Hybrid read (retrieve_hybrid_into, src/memory.rs:568-660): with hgate
+  // set, live slot s weighs exp((min - d_s)/tau) * hgate[s] * decay_s,
+  // decay_s = (float)exp(age_s * log_lam), age_s = hage[s] + age_base
+  // (+ row % age_T + 1 when age_T > 0, the bumps of a T-token prefill's
+  // earlier tokens), saturating; a read whose live weights sum to zero falls
+  // back to the unweighted softmax.  hage may be null (ages 0).
+  const float* hgate = nullptr;
+  const unsigned long long* hage = nullptr;
+  double log_lam = 0.0;
+  unsigned long long age_base = 0;
+  int age_T = 0;
 };
 
 // Scratch the ranked top-k path needs for these arguments (0: not taken).

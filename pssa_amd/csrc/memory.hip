@@ -104,6 +104,16 @@ __device__ __forceinline__ void put_weight(const RetrieveArgs& a, int n, int s, 
 
 constexpr double kMaxRadius = 1.0 - 8.0 * (double)FLT_EPSILON;  // src/memory.rs:173
 
+// Hybrid read recency factor of slot s for query row n (src/memory.rs:632-633):
+// (float)exp(age * ln(lam)) in f64, the age saturating at 2^64 - 1.
+__device__ __forceinline__ float hybrid_decay(const RetrieveArgs& a, int s, int n) {
+  unsigned long long age = a.hage ? a.hage[s] : 0ull;
+  const unsigned long long add =
+      a.age_base + (a.age_T > 0 ? (unsigned long long)(n % a.age_T) + 1ull : 0ull);
+  age = age > ~0ull - add ? ~0ull : age + add;
+  return (float)exp((double)age * a.log_lam);
+}
+
 __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -179,13 +189,31 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
         }
       }
       wave_sync();
+      // Hybrid read: (e * gate) * decay per live slot, unless every live
+      // weight is zero (then the plain softmax, src/memory.rs:640-650).
+      auto hyb_w = [&](int s, float e) { return (e * a.hgate[s]) * hybrid_decay(a, s, n); };
+      bool hyb = a.hgate != nullptr;
       float sum = 0.0f;
-      for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[wave][r]]) / a.tau);
+      if (hyb) {
+        for (int r = 0; r < k; ++r) {
+          const int s = ssel[wave][r];
+          sum += hyb_w(s, expf((min_dist - sdist[s]) / a.tau));
+        }
+        hyb = sum != 0.0f;
+      }
+      if (!hyb) {
+        sum = 0.0f;
+        for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[wave][r]]) / a.tau);
+      }
+      auto weight_of = [&](int s) {
+        const float e = expf((min_dist - sdist[s]) / a.tau);
+        return (hyb ? hyb_w(s, e) : e) / sum;
+      };
       if (a.weights || a.weights16) {
         for (int s = lane; s < a.capacity; s += 64) {
           bool chosen = false;
           for (int r = 0; r < k; ++r) chosen |= ssel[wave][r] == (uint32_t)s;
-          put_weight(a, n, s, chosen ? expf((min_dist - sdist[s]) / a.tau) / sum : 0.0f);
+          put_weight(a, n, s, chosen ? weight_of(s) : 0.0f);
         }
       }
       if (a.out_idx)
@@ -196,24 +224,29 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
           float acc = 0.0f;
           for (int r = 0; r < k; ++r) {
             const uint32_t s = ssel[wave][r];
-            const float w = expf((min_dist - sdist[s]) / a.tau) / sum;
+            const float w = weight_of((int)s);
             acc = acc + w * a.values[(size_t)s * a.dv + j];
           }
           a.out_val[(size_t)n * a.dv + j] = acc;
         }
       }
     } else {
-      // ---- full soft read (src/memory.rs:409-425) ----
-      float part = 0.0f;
+      // ---- full soft read (src/memory.rs:409-425); hybrid: every slot live ----
+      float part = 0.0f, part_h = 0.0f;
       for (int s = lane; s < cnt; s += 64) {
         const float e = expf((min_dist - sdist[s]) / a.tau);
         sdist[s] = e;
         part += e;
+        if (a.hgate) part_h += (e * a.hgate[s]) * hybrid_decay(a, s, n);
       }
-      const float sum = wave_sum(part);
+      const float sum_p = wave_sum(part);
+      const float sum_h = a.hgate ? wave_sum(part_h) : 0.0f;
+      const bool hyb = a.hgate && sum_h != 0.0f;
+      const float sum = hyb ? sum_h : sum_p;
       wave_sync();
       for (int s = lane; s < a.capacity; s += 64) {
-        const float w = s < cnt ? sdist[s] / sum : 0.0f;
+        float w = 0.0f;
+        if (s < cnt) w = (hyb ? (sdist[s] * a.hgate[s]) * hybrid_decay(a, s, n) : sdist[s]) / sum;
         if (s < cnt) sdist[s] = w;
         put_weight(a, n, s, w);
       }
@@ -292,7 +325,7 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-template <int QG, int SPL>
+template <int QG, int SPL, bool HYB>
 __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu(4))) void soft_read_kernel(
     RetrieveArgs a) {
   extern __shared__ float smem[];
@@ -448,7 +481,24 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu
           e[j] = sl < cnt ? __builtin_amdgcn_exp2f((lmin - l[j]) * c2) : 0.0f;
           part += e[j];
         }
-        const float inv = 1.0f / wave_sum(part);
+        float sum = wave_sum(part);
+        if constexpr (HYB) {  // hybrid read: (e * gate) * decay unless all are zero
+          float eh[SPL];
+          float part_h = 0.0f;
+#pragma unroll
+          for (int j = 0; j < SPL; ++j) {
+            const int sl = lane + 64 * j;
+            eh[j] = sl < cnt ? (e[j] * a.hgate[sl]) * hybrid_decay(a, sl, n) : 0.0f;
+            part_h += eh[j];
+          }
+          const float sum_h = wave_sum(part_h);
+          if (sum_h != 0.0f) {
+#pragma unroll
+            for (int j = 0; j < SPL; ++j) e[j] = eh[j];
+            sum = sum_h;
+          }
+        }
+        const float inv = 1.0f / sum;
 #pragma unroll
         for (int j = 0; j < SPL; ++j) {
           const int sl = lane + 64 * j;
@@ -1021,7 +1071,7 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
 }
 
 static bool ranked_read_fits(const RetrieveArgs& a) {
-  return a.top_k > 0 && !a.count_dev && a.top_k < a.count && a.count <= RK_SLOTS && !a.project &&
+  return a.top_k > 0 && !a.hgate && !a.count_dev && a.top_k < a.count && a.count <= RK_SLOTS && !a.project &&
          !a.q_pnc && !a.q_norm && a.dk % 4 == 0 && a.dk <= RK_MAX_DK && a.ld_q % 4 == 0 &&
          ((uintptr_t)a.q & 15) == 0 && ((uintptr_t)a.keys & 15) == 0;
 }
@@ -1046,12 +1096,13 @@ static Status allow_large_lds() {
   std::lock_guard<std::mutex> g(mu);
   if (dev >= 0 && dev < 64 && done[dev]) return Status::Ok();
   const void* soft[] = {
-      reinterpret_cast<const void*>(&soft_read_kernel<1, 1>), reinterpret_cast<const void*>(&soft_read_kernel<1, 2>),
-      reinterpret_cast<const void*>(&soft_read_kernel<1, 4>), reinterpret_cast<const void*>(&soft_read_kernel<1, 8>),
-      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 1>),
-      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 2>),
-      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 4>),
-      reinterpret_cast<const void*>(&soft_read_kernel<SOFT_QG, 8>)};
+#define PSSA_SOFT_FN(QG, SPL)                                         \
+  reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, false>),  \
+      reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, true>),
+      PSSA_SOFT_FN(1, 1) PSSA_SOFT_FN(1, 2) PSSA_SOFT_FN(1, 4) PSSA_SOFT_FN(1, 8)
+      PSSA_SOFT_FN(SOFT_QG, 1) PSSA_SOFT_FN(SOFT_QG, 2) PSSA_SOFT_FN(SOFT_QG, 4) PSSA_SOFT_FN(SOFT_QG, 8)
+#undef PSSA_SOFT_FN
+  };
   for (const void* f : soft)
     PSSA_HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&ranked_dot_kernel),
@@ -1082,11 +1133,14 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
     const size_t lds = soft_read_lds(a.dk, a.capacity, qg);
     if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     const int spl = soft_spl(a.capacity);
-#define PSSA_SOFT_CASE(QG, SPL)                                                  \
-  if (qg == QG && spl == SPL) {                                                  \
-    soft_read_kernel<QG, SPL><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);      \
-    PSSA_LAUNCH_CHECK("soft_read");                                              \
-    return Status::Ok();                                                         \
+#define PSSA_SOFT_CASE(QG, SPL)                                                    \
+  if (qg == QG && spl == SPL) {                                                    \
+    if (a.hgate)                                                                   \
+      soft_read_kernel<QG, SPL, true><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);  \
+    else                                                                           \
+      soft_read_kernel<QG, SPL, false><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a); \
+    PSSA_LAUNCH_CHECK("soft_read");                                                \
+    return Status::Ok();                                                           \
   }
     PSSA_SOFT_CASE(1, 1) PSSA_SOFT_CASE(1, 2) PSSA_SOFT_CASE(1, 4) PSSA_SOFT_CASE(1, 8)
     PSSA_SOFT_CASE(SOFT_QG, 1) PSSA_SOFT_CASE(SOFT_QG, 2) PSSA_SOFT_CASE(SOFT_QG, 4) PSSA_SOFT_CASE(SOFT_QG, 8)

@@ -27,6 +27,12 @@ struct DevBlock {
   DevBuf conf;     // [C] f32 memory.confidence
   DevBuf last_seen;  // [C] u64 memory.last_seen_step
   DevBuf meta;     // int32 [2]: memory.count, memory.write_head
+  // Hybrid read (src/memory.rs:19-33): per-slot write gate and age on the
+  // device, the toggle and ln(lam) on the host.
+  DevBuf hgate;    // [C] f32 memory.hybrid_gate
+  DevBuf hage;     // [C] u64 memory.hybrid_age
+  bool hybrid = false;
+  float lam = 1.0f;
 };
 
 // Stage ids used for per-kernel timing.
@@ -58,6 +64,9 @@ struct pssa_hip_model {
   pssa::DevBuf unembed;  // [V, d] weight dtype
   std::vector<pssa::DevBlock> blocks;
   pssa::DevBuf step;     // u64: step counter read by the refractory gate in plastic decode
+  // Advances on every set_hybrid_read, so that a captured decode step built
+  // for another hybrid setting is captured again.
+  uint64_t hybrid_epoch = 0;
 };
 
 struct pssa_hip_lanes {
@@ -79,6 +88,7 @@ struct pssa_hip_lanes {
   // [lanes], the Hebbian rates 0.02/(1+|z_final|) [depth, lanes], the
   // generated ids [gen_cap, lanes] and the generation position.
   pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
+  pssa::DevBuf tap_gmean;    // [depth, lanes] mean memory-injection gate (hybrid write gate)
   pssa::DevBuf bank_writer;  // [depth, capacity] writing lane of each slot in the current step
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
@@ -86,6 +96,7 @@ struct pssa_hip_lanes {
   hipGraphExec_t graph_exec = nullptr;
   size_t graph_lanes = 0;
   int graph_plastic = -1;
+  uint64_t graph_hybrid_epoch = 0;
   size_t staged_lanes = 0, staged_len = 0;
   bool timing = false;
   std::array<float, pssa::ST_COUNT> stage_ms{};

@@ -217,6 +217,28 @@ struct Timer {
 
 }  // namespace
 
+// Hybrid write gate of each row: the mean of its memory-injection gate
+// activations g[row, 0..d), summed left to right in f32 as
+// src/pssa.rs:3724 does (one thread per row).
+__global__ void gate_mean_kernel(const float* __restrict__ g, int ld, int d, int rows, float* __restrict__ out) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* x = g + (size_t)r * ld;
+  float s = 0.0f;
+  for (int i = 0; i < d; ++i) s += x[i];
+  out[r] = s / (float)d;
+}
+
+// bump_hybrid_ages (src/memory.rs:501-507) `times` times: every live slot's
+// age grows by `times`, saturating at 2^64 - 1.
+__global__ void hybrid_bump_kernel(unsigned long long* __restrict__ age, const int* __restrict__ meta, int C,
+                                   unsigned long long times) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= C || s >= meta[0]) return;
+  const unsigned long long a = age[s];
+  age[s] = a > ~0ull - times ? ~0ull : a + times;
+}
+
 // Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`.  Every buffer
 // pointer is offset to the view's rows, so disjoint views can run
 // concurrently.  `first_in_done` (may be null) is recorded once layer 0's
@@ -292,6 +314,11 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     }
     PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
     if (l == 0 && first_in_done) PSSA_HIP_TRY(hipEventRecord(first_in_done, st));
+    if (taps && B.hybrid) {  // the write gate of a gated protected insert
+      gate_mean_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(P + o_gate, n_in, d, (int)rows,
+                                                                       L->tap_gmean.as<float>() + l * rows);
+      PSSA_LAUNCH_CHECK("gate_mean");
+    }
 
     PSSA_RETURN_IF(tm.mark(ST_SSM));
     SsmArgs sa;
@@ -350,6 +377,12 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     ra.count_dev = B.meta.as<int>();
     ra.tau = c.tau_mem;
     if (taps) ra.q_pnc = L->tap_q.as<float>() + l * rows * k;
+    if (B.hybrid) {  // token t reads with the ages bumped t + 1 times
+      ra.hgate = B.hgate.as<float>();
+      ra.hage = B.hage.as<unsigned long long>();
+      ra.log_lam = std::log((double)B.lam);
+      ra.age_T = (int)T;
+    }
     if (bf16)
       ra.weights16 = static_cast<uint16_t*>(Wm);
     else
@@ -439,7 +472,23 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
 constexpr int kPrefillLaneGroups = 2;
 static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per lane group");
 
+static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps);
+
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
+  PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, taps));
+  // Every lane read each token with the ages bumped once more; store them.
+  const pssa_hip_model* M = L->model;
+  const int C = (int)M->cfg.mem_capacity;
+  for (const DevBlock& B : M->blocks)
+    if (B.hybrid) {
+      hybrid_bump_kernel<<<(unsigned)((C + 255) / 256), 256, 0, L->ctx->stream>>>(
+          B.hage.as<unsigned long long>(), B.meta.as<int>(), C, (unsigned long long)T);
+      PSSA_LAUNCH_CHECK("hybrid_bump");
+    }
+  return Status::Ok();
+}
+
+static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   const hipStream_t st = L->ctx->stream;
   const pssa_hip_config& c = L->model->cfg;
   const int nz = ssm_state_blocks((int)c.d_state);

@@ -13,6 +13,7 @@ src/pssa.rs:2245-2442) for a batch of independent lanes
 from __future__ import annotations
 
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -32,9 +33,13 @@ class HipDevice:
         h = C.c_void_p()
         _abi.call(self._lib.pssa_hip_init, device, C.byref(h))
         self.handle = h
+        # Objects holding native state tied to this context; closed first.
+        self._children = weakref.WeakSet()
 
     def close(self) -> None:
         if self.handle:
+            for child in list(self._children):
+                child.close()
             self._lib.pssa_hip_destroy(self.handle)
             self.handle = None
 
@@ -142,6 +147,26 @@ class HipDevice:
                   None if out_idx is None else _abi.ptr(out_idx, C.c_uint32), _abi.ptr(out_w))
         return out_val, out_min, out_idx, out_w
 
+    # -- retrieve_hybrid_into (src/memory.rs:568-660) --------------------------
+    def retrieve_hybrid(self, q_pnc, keys, norm_sq, values, count: int, tau: float, gate, age, lam: float,
+                        top_k: int = 0, want_weights: bool = False):
+        """Hybrid read of every query against one bank state; gate/age [count]
+        are the bank's hybrid_gate / hybrid_age.  Returns as `retrieve`."""
+        q_pnc, keys, norm_sq, values = (_f32(a) for a in (q_pnc, keys, norm_sq, values))
+        gate = _f32(np.asarray(gate, np.float32)[:count])
+        age = np.ascontiguousarray(np.asarray(age)[:count], dtype=np.uint64)
+        n_q, d_key = q_pnc.shape
+        capacity, d_val = values.shape
+        out_val = np.empty((n_q, d_val), np.float32)
+        out_min = np.empty(n_q, np.float32)
+        out_idx = np.empty((n_q, top_k), np.uint32) if top_k > 0 else None
+        out_w = np.empty((n_q, capacity), np.float32) if want_weights else None
+        _abi.call(self._lib.pssa_hip_retrieve_hybrid, self.handle, _abi.ptr(q_pnc), n_q, _abi.ptr(keys),
+                  _abi.ptr(norm_sq), _abi.ptr(values), capacity, count, d_key, d_val, tau, top_k,
+                  _abi.ptr(gate), _abi.ptr(age, C.c_uint64), lam, _abi.ptr(out_val), _abi.ptr(out_min),
+                  None if out_idx is None else _abi.ptr(out_idx, C.c_uint32), _abi.ptr(out_w))
+        return out_val, out_min, out_idx, out_w
+
     def retrieve_resident(self, q_ptr: int, n_q: int, keys_ptr: int, norm_sq_ptr: int, values_ptr: int,
                           capacity: int, count: int, d_key: int, d_val: int, tau: float, top_k: int,
                           out_val_ptr: int, out_min_ptr: int | None = None, out_idx_ptr: int | None = None) -> None:
@@ -176,6 +201,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         _abi.call(device._lib.pssa_hip_device_alloc, device.handle, max(nbytes, 1), C.byref(p))
         self.ptr = p.value
+        device._children.add(self)
 
     def to_host(self) -> np.ndarray:
         out = np.empty(self.shape, self.dtype)
@@ -190,9 +216,9 @@ class DeviceBuffer:
                   a.ctypes.data_as(C.c_void_p), a.nbytes, _abi.H2D)
 
     def close(self) -> None:
-        if self.ptr:
+        if self.ptr and self.device.handle:
             self.device._lib.pssa_hip_device_free(self.device.handle, C.c_void_p(self.ptr))
-            self.ptr = None
+        self.ptr = None
 
     def __del__(self):  # pragma: no cover
         try:
@@ -225,6 +251,7 @@ class PSSALayer:
             lib.pssa_hip_model_free(m)
             raise
         self.handle = ln
+        device._children.add(self)
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -317,6 +344,18 @@ class PSSALayer:
                   C.byref(cnt), C.byref(head), C.byref(step))
         out.update(mem_count=int(cnt.value), mem_write_head=int(head.value), step=int(step.value))
         return out
+
+    def set_hybrid_read(self, enabled: bool, lam: float) -> None:
+        """set_hybrid_read on every block (src/pssa.rs:2232-2243)."""
+        _abi.call(self._lib.pssa_hip_model_set_hybrid_read, self.model, 1 if enabled else 0, lam)
+
+    def get_hybrid(self, layer: int):
+        """One block's (hybrid_gate [C], hybrid_age [C]) as held on the device."""
+        C_ = self.cfg.mem_capacity
+        gate = np.empty(C_, np.float32)
+        age = np.empty(C_, np.uint64)
+        _abi.call(self._lib.pssa_hip_model_get_hybrid, self.model, layer, _abi.ptr(gate), _abi.ptr(age, C.c_uint64))
+        return gate, age
 
     # -- device-resident measurement path ------------------------------------
     def stage_ids(self, token_ids) -> None:

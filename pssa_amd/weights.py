@@ -84,6 +84,11 @@ class BlockWeights:
         self.mem_last_seen = np.zeros(cfg.mem_capacity, dtype=np.uint64)
         self.mem_count = 0
         self.mem_write_head = 0
+        # Hybrid read state (src/memory.rs:19-33): runtime-only, never checkpointed.
+        self.mem_hybrid_gate = np.ones(cfg.mem_capacity, dtype=np.float32)
+        self.mem_hybrid_age = np.zeros(cfg.mem_capacity, dtype=np.uint64)
+        self.mem_hybrid_enabled = False
+        self.mem_hybrid_lam = 1.0
 
 
 class ModelWeights:
@@ -108,6 +113,11 @@ class ModelWeights:
             cb.mem_last_seen = _abi.ptr(b.mem_last_seen, C.c_uint64)
             cb.mem_count = int(b.mem_count)
             cb.mem_write_head = int(b.mem_write_head)
+            assert b.mem_hybrid_gate.dtype == np.float32 and b.mem_hybrid_age.dtype == np.uint64
+            cb.mem_hybrid_gate = _abi.ptr(b.mem_hybrid_gate)
+            cb.mem_hybrid_age = _abi.ptr(b.mem_hybrid_age, C.c_uint64)
+            cb.mem_hybrid_enabled = 1 if b.mem_hybrid_enabled else 0
+            cb.mem_hybrid_lam = float(b.mem_hybrid_lam)
         assert self.embed.flags.c_contiguous and self.unembed.flags.c_contiguous
         w = _abi.Weights(self.cfg.to_c(), _abi.ptr(self.embed), _abi.ptr(self.unembed), blocks)
         return w, blocks
@@ -116,6 +126,14 @@ class ModelWeights:
         for b, cb in zip(self.blocks, blocks):
             b.mem_count = int(cb.mem_count)
             b.mem_write_head = int(cb.mem_write_head)
+
+    def set_hybrid_read(self, enabled: bool, lam: float) -> None:
+        """set_hybrid_read on every block (src/pssa.rs:2232-2243)."""
+        if not (np.isfinite(lam) and 0.0 < lam <= 1.0):
+            raise ValueError("hybrid decay lam must be in (0.0, 1.0]")
+        for b in self.blocks:
+            b.mem_hybrid_enabled = bool(enabled)
+            b.mem_hybrid_lam = float(lam)
 
     # -- initialisation (libpssa_hip host code) -----------------------------
     @classmethod
@@ -160,6 +178,9 @@ class ModelWeights:
                 getattr(dst, name)[...] = bf16_round(v) if name in mats else v
             dst.mem_last_seen[:] = src.mem_last_seen
             dst.mem_count, dst.mem_write_head = src.mem_count, src.mem_write_head
+            dst.mem_hybrid_gate[:] = src.mem_hybrid_gate
+            dst.mem_hybrid_age[:] = src.mem_hybrid_age
+            dst.mem_hybrid_enabled, dst.mem_hybrid_lam = src.mem_hybrid_enabled, src.mem_hybrid_lam
         return out
 
 

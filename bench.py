@@ -150,6 +150,49 @@ def bench_decode(dev, args, log):
     }
 
 
+def bench_train_forward(dev, args, log, w=None, ids=None):
+    """Config-3 model and batch through the training forward
+    (SequenceBatch::forward): every lane one sequence of `seq` tokens from a
+    zeroed carry, targets = the next input id, scaled logits and cross
+    entropy for every token.  Each timed call includes its id upload and the
+    per-token loss download."""
+    from pssa_amd import ModelWeights, PSSALayer, Sequence
+
+    cfg = model_config(args)
+    if w is None:
+        w = ModelWeights.init(cfg, 0, "baseline")
+        w.populate_banks(1)
+        ids = np.random.default_rng(0).integers(0, cfg.d_vocab, (args.lanes, args.seq), dtype=np.uint32)
+    lanes, T = ids.shape
+    layer = PSSALayer(dev, w, lanes=lanes, max_tokens=lanes * T, weight_dtype=args.dtype)
+    seqs = [Sequence(i, ids[i], np.roll(ids[i], -1), True) for i in range(lanes)]
+    layer.batch_forward(seqs)  # allocation and warm-up
+    n = max(1, args.steps)
+    t0 = time.perf_counter()
+    for _ in range(n):
+        loss = layer.batch_forward(seqs)
+    step_s = (time.perf_counter() - t0) / n
+    layer.set_stage_timing(True)
+    layer.batch_forward(seqs)
+    stages = layer.stage_times()
+    layer.set_stage_timing(False)
+    layer.close()
+    head_ms = stages.get("head", 0.0)
+    head_flops = 2.0 * lanes * T * cfg.d_vocab * cfg.d_latent
+    log(f"train forward: {step_s * 1e3:.3f} ms, loss {loss:.4f}, head + cross entropy {head_ms:.3f} ms")
+    return {
+        "workload": f"config 3 training forward (SequenceBatch::forward): {lanes} sequences x {T} tokens, "
+                    f"logits and cross entropy for every token, {args.dtype} weights",
+        "tokens_per_s": lanes * T / step_s,
+        "ms_per_step": step_s * 1e3,
+        "loss": loss,
+        "head_ms": head_ms,
+        "head_roofline": {"bound": "mfma", "achieved": head_flops / (head_ms * 1e-3) / 1e12 if head_ms else None,
+                          "peak": BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
+                          "frac": head_flops / (head_ms * 1e-3) / 1e12 / BF16_MFMA_TFLOPS if head_ms else None},
+    }
+
+
 def _ball(rng, n, dim):
     """Vectors uniform in direction with radius U[0, 0.9) (float32)."""
     v = rng.standard_normal((n, dim))
@@ -293,8 +336,9 @@ def main():
                     help="skip the config 2 / 4 / 5 measurements (dense scan, retrieval, decode)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["decode", "retrieval", "dense_scan"],
-                    help="only measure this extra (config 5, 4 or 2) and print its JSON; for profiling")
+    ap.add_argument("--only", choices=["decode", "retrieval", "dense_scan", "train_forward"],
+                    help="only measure this extra (config 5, 4, 2 or the training forward) and print its "
+                         "JSON; for profiling")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe)
@@ -304,7 +348,8 @@ def main():
 
         dev = HipDevice(0)
         log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
-        run = {"decode": bench_decode, "retrieval": bench_retrieval, "dense_scan": bench_dense_scan}[args.only]
+        run = {"decode": bench_decode, "retrieval": bench_retrieval, "dense_scan": bench_dense_scan,
+               "train_forward": bench_train_forward}[args.only]
         print(json.dumps({args.only: run(dev, args, log)}), flush=True)
         dev.close()
         return
@@ -387,7 +432,8 @@ def main():
         layer.close()
         extras = {"decode": bench_decode(dev, args, log),
                   "retrieval": bench_retrieval(dev, args, log),
-                  "dense_scan": bench_dense_scan(dev, args, log)}
+                  "dense_scan": bench_dense_scan(dev, args, log),
+                  "train_forward": bench_train_forward(dev, args, log, w, ids)}
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -281,6 +281,35 @@ int pssa_hip_prefill(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
 int pssa_hip_forward_inference(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
                                float* logits, size_t logits_len, char* err, size_t err_len);
 
+/* ------------------------------------------------- batch training forward */
+
+/* One training sequence of a batch (Sequence, src/sequence_batch.rs:21-28). */
+typedef struct pssa_hip_sequence {
+  uint64_t lane;            /* stable lane index; omitted lanes keep their carry */
+  const uint32_t* inputs;   /* [len] input ids */
+  const uint32_t* targets;  /* [len] target ids */
+  uint64_t len;             /* 1..=max_tokens */
+  uint32_t reset;           /* nonzero: zero this lane's carry first */
+  uint32_t _pad;
+} pssa_hip_sequence;
+
+/* SequenceBatch::forward (src/sequence_batch.rs:233-384; the stages of
+ * forward_train_chunk_batched, src/gpu_batch.rs:1699-1755, per lane of
+ * stacked depth, src/sequence_batch.rs:560-609): each sequence runs from its
+ * lane's carry, every token row gets its scaled logits and cross-entropy
+ * loss, and *out_loss is the token mean over the packed batch (sequences in
+ * the given order, summed left to right in f32).  The logits of every row
+ * stay on the device; token_losses [tokens] and logits [tokens, V] (packed
+ * order, either may be NULL) receive copies.  Errors, before anything runs:
+ * a sequence count outside 1..=lanes, repeated or out-of-range lanes, an
+ * empty or over-long sequence, more than max_tokens tokens in all, an id >=
+ * V, a model with the hybrid read on (the reference's batched stages reject
+ * it).  A non-finite loss is reported after the carries have advanced, as in
+ * the reference. */
+int pssa_hip_batch_forward(pssa_hip_lanes* lanes, const pssa_hip_sequence* seqs, size_t n_seqs,
+                           float* out_loss, float* token_losses, size_t token_losses_len, float* logits,
+                           size_t logits_len, char* err, size_t err_len);
+
 /* Device-resident prefill for measurement: stage ids on the device once,
  * then run prefill with no host traffic (asynchronous on the context stream;
  * pssa_hip_synchronize or a read completes it). */

@@ -8,4 +8,4 @@ for gfx950, C ABI in include/pssa_hip.h).
 """
 from .weights import BlockWeights, ModelWeights, PSSAConfig, bf16_round  # noqa: F401
 from .checkpoint import load as load_checkpoint  # noqa: F401
-from .device import HipDevice, PSSALayer  # noqa: F401
+from .device import HipDevice, PSSALayer, Sequence  # noqa: F401

@@ -75,6 +75,18 @@ class Weights(C.Structure):
     ]
 
 
+class Sequence(C.Structure):
+    """pssa_hip_sequence (Sequence, src/sequence_batch.rs:21-28)."""
+    _fields_ = [
+        ("lane", C.c_uint64),
+        ("inputs", C.POINTER(C.c_uint32)),
+        ("targets", C.POINTER(C.c_uint32)),
+        ("len", C.c_uint64),
+        ("reset", C.c_uint32),
+        ("_pad", C.c_uint32),
+    ]
+
+
 class HipError(RuntimeError):
     """A libpssa_hip call failed; `code` is the PSSA_HIP_* status."""
 
@@ -135,6 +147,7 @@ def lib() -> C.CDLL:
         "pssa_hip_lanes_set_carry": ([vp, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_prefill": ([vp, u32p, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_forward_inference": ([vp, u32p, sz, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_ids": ([vp, u32p, sz, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_prefill_staged": ([vp, err_t, sz], C.c_int),
         "pssa_hip_lanes_read_logits": ([vp, fp, sz, err_t, sz], C.c_int),

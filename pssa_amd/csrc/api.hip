@@ -882,6 +882,139 @@ int pssa_hip_forward_inference(pssa_hip_lanes* L, const uint32_t* ids, size_t n_
   return pssa_hip_prefill(L, ids, n_lanes, 1, logits, logits_len, err, err_len);
 }
 
+int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, size_t n_seqs, float* out_loss,
+                           float* token_losses, size_t token_losses_len, float* logits, size_t logits_len,
+                           char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    // Validation in SequenceBatch::forward's order (src/sequence_batch.rs:243-272),
+    // all before any carry changes.
+    PSSA_RETURN_IF(need(L && out_loss, "null lanes or loss output"));
+    PSSA_RETURN_IF(need(n_seqs >= 1 && n_seqs <= L->lanes && seqs,
+                        "sequence count must be between 1 and the configured batch size"));
+    const pssa_hip_model* M = L->model;
+    const pssa_hip_config& c = M->cfg;
+    const size_t V = c.d_vocab;
+    std::vector<char> used(L->lanes, 0);
+    size_t tokens = 0;
+    for (size_t i = 0; i < n_seqs; ++i) {
+      const pssa_hip_sequence& q = seqs[i];
+      PSSA_RETURN_IF(need(q.lane < L->lanes && !used[q.lane],
+                          "each sequence needs a distinct lane within the configured batch size"));
+      used[q.lane] = 1;
+      PSSA_RETURN_IF(need(q.inputs && q.targets && q.len > 0 && q.len <= L->max_tokens,
+                          "each sequence needs matching nonempty input/target slices no longer than max_tokens"));
+      tokens += q.len;
+    }
+    PSSA_RETURN_IF(need(tokens <= L->max_tokens, "the batch's tokens exceed the lanes' max_tokens"));
+    for (size_t i = 0; i < n_seqs; ++i)
+      for (size_t t = 0; t < seqs[i].len; ++t)
+        if (seqs[i].inputs[t] >= V || seqs[i].targets[t] >= V)
+          return Status::Invalid("batch token ID is outside the model vocabulary");
+    for (const pssa::DevBlock& B : M->blocks)
+      PSSA_RETURN_IF(need(!B.hybrid, "hybrid read currently requires the CPU backend"));
+    if (token_losses)
+      PSSA_RETURN_IF(need(token_losses_len == tokens, "token_losses length must equal the batch's token count"));
+    if (logits) PSSA_RETURN_IF(need(logits_len == tokens * V, "logits length must be tokens*d_vocab"));
+
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    const size_t cw = c.depth * c.d_latent * c.d_state;  // floats of one lane's carry
+    if (!L->tok_logits.p) {
+      PSSA_RETURN_IF(L->tok_logits.alloc(L->max_tokens * V * 4));
+      PSSA_RETURN_IF(L->tok_meta.alloc(2 * L->max_tokens * 4));
+      PSSA_RETURN_IF(L->tok_loss.alloc(L->max_tokens * 4));
+    }
+    L->staged_lanes = L->staged_len = 0;  // lanes->logits no longer follows a prefill
+
+    // Packed token offsets in the given order; the device works in order of
+    // decreasing length so that the lanes still running are always a prefix.
+    std::vector<size_t> offset(n_seqs), order(n_seqs);
+    for (size_t i = 0, o = 0; i < n_seqs; o += seqs[i].len, ++i) offset[i] = o;
+    for (size_t i = 0; i < n_seqs; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](size_t a, size_t b) { return seqs[a].len > seqs[b].len; });
+    bool identity = true;
+    for (size_t i = 0; i < n_seqs; ++i) identity &= seqs[order[i]].lane == i;
+
+    float* carry = L->carry.as<float>();
+    for (size_t i = 0; i < n_seqs; ++i)
+      if (seqs[i].reset) PSSA_RETURN_IF(pssa::launch_fill_zero(st, carry + seqs[i].lane * cw, cw));
+    float* work = carry;
+    if (!identity) {
+      if (!L->carry_work.p) PSSA_RETURN_IF(L->carry_work.alloc(L->lanes * cw * 4));
+      work = L->carry_work.as<float>();
+      for (size_t i = 0; i < n_seqs; ++i)
+        PSSA_HIP_TRY(hipMemcpyAsync(work + i * cw, carry + seqs[order[i]].lane * cw, cw * 4,
+                                    hipMemcpyDeviceToDevice, st));
+    }
+
+    // Segments: times [t0, t1) of the n_active longest sequences.
+    struct Segment {
+      size_t t0, t1, n_active, row;
+    };
+    std::vector<Segment> segs;
+    std::vector<uint32_t> ids_h(tokens), meta_h(2 * tokens);
+    size_t n_active = n_seqs, t0 = 0, row = 0;
+    while (n_active > 0) {
+      const size_t t1 = seqs[order[n_active - 1]].len;
+      const size_t T = t1 - t0;
+      for (size_t i = 0; i < n_active; ++i) {
+        const pssa_hip_sequence& q = seqs[order[i]];
+        for (size_t t = 0; t < T; ++t) {
+          const size_t r = row + i * T + t;
+          ids_h[r] = q.inputs[t0 + t];
+          meta_h[r] = q.targets[t0 + t];
+          meta_h[tokens + r] = (uint32_t)(offset[order[i]] + t0 + t);
+        }
+      }
+      segs.push_back({t0, t1, n_active, row});
+      row += n_active * T;
+      t0 = t1;
+      while (n_active > 0 && seqs[order[n_active - 1]].len == t1) --n_active;
+    }
+    PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids_h.data(), tokens * 4, hipMemcpyHostToDevice, st));
+    PSSA_HIP_TRY(hipMemcpyAsync(L->tok_meta.p, meta_h.data(), 2 * tokens * 4, hipMemcpyHostToDevice, st));
+    const uint32_t* dmeta = L->tok_meta.as<uint32_t>();
+    for (const Segment& sg : segs) {
+      pssa::TrainRows tr;
+      tr.ids = L->ids.as<uint32_t>() + sg.row;
+      tr.targets = dmeta + sg.row;
+      tr.index = dmeta + tokens + sg.row;
+      tr.logits = L->tok_logits.as<float>() + sg.row * V;
+      tr.loss = L->tok_loss.as<float>();
+      tr.carry = work;
+      PSSA_RETURN_IF(pssa::run_train_segment(L, sg.n_active, sg.t1 - sg.t0, tr));
+    }
+    if (!identity)
+      for (size_t i = 0; i < n_seqs; ++i)
+        PSSA_HIP_TRY(hipMemcpyAsync(carry + seqs[order[i]].lane * cw, work + i * cw, cw * 4,
+                                    hipMemcpyDeviceToDevice, st));
+
+    std::vector<float> loss_h(tokens);
+    PSSA_HIP_TRY(hipMemcpyAsync(loss_h.data(), L->tok_loss.p, tokens * 4, hipMemcpyDeviceToHost, st));
+    if (logits)
+      for (const Segment& sg : segs) {
+        const size_t T = sg.t1 - sg.t0;
+        for (size_t i = 0; i < sg.n_active; ++i)
+          PSSA_HIP_TRY(hipMemcpyAsync(logits + (offset[order[i]] + sg.t0) * V,
+                                      L->tok_logits.as<float>() + (sg.row + i * T) * V, T * V * 4,
+                                      hipMemcpyDeviceToHost, st));
+      }
+    PSSA_RETURN_IF(sync(L->ctx));
+    // The token mean in packed order, summed left to right in f32
+    // (stage_logits_loss, src/gpu_batch.rs:1246-1249).
+    float total = 0.0f;
+    for (size_t i = 0; i < tokens; ++i) total += loss_h[i];
+    const float loss = total / (float)tokens;
+    if (token_losses) std::memcpy(token_losses, loss_h.data(), tokens * 4);
+    *out_loss = loss;
+    if (!std::isfinite(loss)) return Status::Invalid("batch forward: non-finite training loss");
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 int pssa_hip_lanes_stage_ids(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
                              char* err, size_t err_len) {
   auto body = [&]() -> Status {

@@ -90,6 +90,12 @@ struct pssa_hip_lanes {
   pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
   pssa::DevBuf tap_gmean;    // [depth, lanes] mean memory-injection gate (hybrid write gate)
   pssa::DevBuf bank_writer;  // [depth, capacity] writing lane of each slot in the current step
+  // Batch training forward (allocated on its first call): the fp32 scaled
+  // logits of every token row [max_tokens, V], each row's target id and
+  // packed token index [2, max_tokens], the per-token losses in packed order
+  // [max_tokens], and a carry workspace [lanes, depth, d*s] for sequences
+  // whose lanes are not 0..n-1 in length order.
+  pssa::DevBuf tok_logits, tok_meta, tok_loss, carry_work;
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
   hipGraph_t graph = nullptr;
@@ -129,6 +135,21 @@ namespace pssa {
 // projected query, adapter output, z_final and adapter activations into the
 // lanes' tap buffers.
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps = false);
+// Rows of one training-forward segment: n_lanes lanes of T tokens.  Every
+// pointer addresses the segment's first row (lane).
+struct TrainRows {
+  const uint32_t* ids;      // [n_lanes * T] input ids
+  const uint32_t* targets;  // [n_lanes * T] target ids
+  const uint32_t* index;    // [n_lanes * T] packed token index of each row
+  float* logits;            // [n_lanes * T, V] scaled logits
+  float* loss;              // per-token losses, indexed by `index`
+  float* carry;             // [n_lanes, depth, d*s] carries, advanced in place
+};
+// The forward of stage_embed_norm .. stage_logits_loss (src/gpu_batch.rs:
+// 445-1250) over one segment: every row gets its scaled logits and its
+// cross-entropy loss.  The hybrid read is not supported here (the
+// reference's batched stages reject it).
+Status run_train_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& tr);
 // One greedy decode step for n_lanes lanes (ids in lanes->ids, replaced by
 // the chosen ids); plastic adds the lane-ordered protected bank writes and
 // the Hebbian adapter update.  Only kernel launches: safe to capture.

@@ -239,12 +239,46 @@ __global__ void hybrid_bump_kernel(unsigned long long* __restrict__ age, const i
   age[s] = a > ~0ull - times ? ~0ull : a + times;
 }
 
+// Cross entropy of one scaled logit row (stage_logits_loss without
+// distillation, src/gpu_batch.rs:1211-1247, 1170): loss = (max - l_target) +
+// ln(sum_i exp(l_i - max)), stored at the row's packed token index.  A NaN
+// logit never becomes the maximum and makes the sum NaN, as in the reference.
+__global__ __launch_bounds__(256) void token_ce_kernel(const float* __restrict__ logits, int V,
+                                                       const uint32_t* __restrict__ targets,
+                                                       const uint32_t* __restrict__ index,
+                                                       float* __restrict__ loss) {
+  __shared__ float red[4];
+  const float* l = logits + (size_t)blockIdx.x * V;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -INFINITY;
+  for (int i = tid; i < V; i += 256) mx = l[i] > mx ? l[i] : mx;
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float other = __shfl_xor(mx, o, 64);
+    mx = other > mx ? other : mx;
+  }
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
+  __syncthreads();
+  float sum = 0.0f;
+  for (int i = tid; i < V; i += 256) sum += expf(l[i] - mx);
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    loss[index[blockIdx.x]] = (mx - l[targets[blockIdx.x]]) + logf(total);
+  }
+}
+
 // Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`.  Every buffer
 // pointer is offset to the view's rows, so disjoint views can run
 // concurrently.  `first_in_done` (may be null) is recorded once layer 0's
 // input projection has been issued.
 static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T,
-                           bool taps, bool timing, hipEvent_t first_in_done, float* y_part) {
+                           bool taps, bool timing, hipEvent_t first_in_done, float* y_part,
+                           const TrainRows* tr) {
   const pssa_hip_model* M = L->model;
   const pssa_hip_config& c = M->cfg;
   const int d = (int)c.d_latent, s = (int)c.d_state, k = (int)c.d_mem_key;
@@ -277,8 +311,8 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
   void* Wm = static_cast<char*>(L->Wm.p) + row0 * C * es;
   void* Mv = static_cast<char*>(L->Mval.p) + row0 * d * es;
   void* H1 = static_cast<char*>(L->H1.p) + row0 * 2 * d * es;
-  const uint32_t* ids = L->ids.as<uint32_t>() + row0;
-  float* carry = L->carry.as<float>() + lane0 * c.depth * (size_t)d * s;
+  const uint32_t* ids = (tr ? tr->ids : L->ids.as<uint32_t>()) + row0;
+  float* carry = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c.depth * (size_t)d * s;
   float* logits = L->logits.as<float>() + lane0 * (size_t)V;
 
   pssa_hip_lanes* TL = timing ? L : nullptr;
@@ -450,8 +484,26 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     PSSA_RETURN_IF(launch_gemm(st, dt, H1, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r));
   }
 
-  // Head on the last token of every lane.
   PSSA_RETURN_IF(tm.mark(ST_HEAD));
+  if (tr) {
+    // Every row: scaled logits, then its cross-entropy loss.
+    const void* hin = X;
+    if (bf16) {
+      PSSA_RETURN_IF(launch_to_bf16(st, X, d, XNh16, d, rows, d));
+      hin = XNh16;
+    }
+    EpiParams e_h;
+    e_h.kind = EPI_SCALE;
+    e_h.scale = logit_scale;
+    e_h.out32 = tr->logits + row0 * (size_t)V;
+    e_h.ld32 = V;
+    PSSA_RETURN_IF(launch_gemm(st, dt, hin, d, M->unembed.p, d, m, V, d, e_h));
+    token_ce_kernel<<<(unsigned)rows, 256, 0, st>>>(tr->logits + row0 * (size_t)V, V, tr->targets + row0,
+                                                   tr->index + row0, tr->loss);
+    PSSA_LAUNCH_CHECK("token_ce");
+    return tm.finish();
+  }
+  // Head on the last token of every lane.
   const float* xlast = X + (T - 1) * (size_t)d;
   const void* hin = xlast;
   int ld_h = (int)(T * d);
@@ -472,10 +524,10 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
 constexpr int kPrefillLaneGroups = 2;
 static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per lane group");
 
-static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps);
+static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, const TrainRows* tr);
 
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
-  PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, taps));
+  PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, taps, nullptr));
   // Every lane read each token with the ages bumped once more; store them.
   const pssa_hip_model* M = L->model;
   const int C = (int)M->cfg.mem_capacity;
@@ -488,7 +540,13 @@ Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   return Status::Ok();
 }
 
-static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
+Status run_train_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& tr) {
+  for (const DevBlock& B : L->model->blocks)
+    if (B.hybrid) return Status::Invalid("hybrid read currently requires the CPU backend");
+  return prefill_groups(L, n_lanes, T, false, &tr);
+}
+
+static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, const TrainRows* tr) {
   const hipStream_t st = L->ctx->stream;
   const pssa_hip_config& c = L->model->cfg;
   const int nz = ssm_state_blocks((int)c.d_state);
@@ -510,7 +568,8 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
         PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_first[g - 1], 0));
       }
       float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
-      PSSA_RETURN_IF(prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp));
+      PSSA_RETURN_IF(
+          prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr));
       lane0 += ng;
     }
     for (int g = 1; g < G; ++g) {
@@ -519,7 +578,7 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
     }
     return Status::Ok();
   }
-  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart);
+  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart, tr);
 }
 
 }  // namespace pssa

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes as C
 import weakref
+from dataclasses import dataclass
 
 import numpy as np
 
@@ -227,6 +228,15 @@ class DeviceBuffer:
             pass
 
 
+@dataclass
+class Sequence:
+    """One training sequence of a batch (Sequence, src/sequence_batch.rs:21-28)."""
+    lane: int
+    inputs: object
+    targets: object
+    reset: bool = False
+
+
 class PSSALayer:
     """Device-resident PSSA model with `lanes` independent recurrent carries."""
 
@@ -301,6 +311,38 @@ class PSSALayer:
         _abi.call(self._lib.pssa_hip_forward_inference, self.handle, _abi.ptr(ids, C.c_uint32), ids.size,
                   _abi.ptr(logits), logits.size)
         return logits
+
+    # -- SequenceBatch::forward (src/sequence_batch.rs:233-384) -----------------
+    def batch_forward(self, sequences, want_token_losses: bool = False, want_logits: bool = False):
+        """Training forward of a batch of sequences, each on its own lane.
+        `sequences` holds `Sequence`s (or (lane, inputs, targets[, reset])
+        tuples).  Returns the token-mean loss, plus the per-token losses
+        [tokens] and logits [tokens, V] in packed order when asked."""
+        seqs = [s if isinstance(s, Sequence) else Sequence(*s) for s in sequences]
+        keep = []
+        arr = (_abi.Sequence * max(len(seqs), 1))()
+        tokens = 0
+        for i, s in enumerate(seqs):
+            ids = np.ascontiguousarray(np.asarray(s.inputs).ravel(), dtype=np.uint32)
+            tg = np.ascontiguousarray(np.asarray(s.targets).ravel(), dtype=np.uint32)
+            if ids.size != tg.size:
+                raise ValueError("each sequence needs matching input/target lengths")
+            keep += [ids, tg]
+            arr[i].lane, arr[i].len, arr[i].reset = s.lane, ids.size, 1 if s.reset else 0
+            arr[i].inputs, arr[i].targets = _abi.ptr(ids, C.c_uint32), _abi.ptr(tg, C.c_uint32)
+            tokens += ids.size
+        loss = C.c_float()
+        tl = np.empty(tokens, np.float32) if want_token_losses else None
+        lg = np.empty((tokens, self.cfg.d_vocab), np.float32) if want_logits else None
+        _abi.call(self._lib.pssa_hip_batch_forward, self.handle, arr, len(seqs), C.byref(loss),
+                  _abi.ptr(tl), 0 if tl is None else tl.size, _abi.ptr(lg), 0 if lg is None else lg.size)
+        del keep
+        out = [float(loss.value)]
+        if want_token_losses:
+            out.append(tl)
+        if want_logits:
+            out.append(lg)
+        return out[0] if len(out) == 1 else tuple(out)
 
     # -- greedy decode (forward_inference + sample, src/pssa.rs:2387-2391,
     #    src/inference.rs:123-127) ------------------------------------------

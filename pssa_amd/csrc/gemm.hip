@@ -742,8 +742,12 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
     return Status::Ok();
   }
   if (vec_bf16 && K % LDS_BK == 0) {
-    // Direct-to-LDS pipeline; narrow outputs use 64-column tiles.
-    const int nw = N <= 64 ? 1 : 4;
+    // Direct-to-LDS pipeline; 128 x 128 tiles, narrow outputs 128 x 64.
+    // The 128-column tile needs about 100 VGPRs (256 columns: 176), so two
+    // of its workgroups fit beside a workgroup of the concurrent lane
+    // group's scan on one CU; the prefill measures 2-4% faster with it,
+    // although each GEMM alone runs about as fast with either width.
+    const int nw = N <= 64 ? 1 : 2;
     const long tiles = (long)((M + 127) / 128) * ((N + 64 * nw - 1) / (64 * nw));
     if (tiles > INT32_MAX) return Status::Invalid("gemm: too many tiles");
     const auto* a16 = static_cast<const uint16_t*>(A);
@@ -751,7 +755,7 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
     if (nw == 1)
       launch_lds_kind<1>(stream, ep.kind, dim3((unsigned)tiles), a16, lda, b16, ldb, M, N, K, vec_epi, ep);
     else
-      launch_lds_kind<4>(stream, ep.kind, dim3((unsigned)tiles), a16, lda, b16, ldb, M, N, K, vec_epi, ep);
+      launch_lds_kind<2>(stream, ep.kind, dim3((unsigned)tiles), a16, lda, b16, ldb, M, N, K, vec_epi, ep);
     PSSA_LAUNCH_CHECK("gemm_lds");
     return Status::Ok();
   }

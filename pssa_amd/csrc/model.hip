@@ -243,31 +243,60 @@ __global__ void hybrid_bump_kernel(unsigned long long* __restrict__ age, const i
 // distillation, src/gpu_batch.rs:1211-1247, 1170): loss = (max - l_target) +
 // ln(sum_i exp(l_i - max)), stored at the row's packed token index.  A NaN
 // logit never becomes the maximum and makes the sum NaN, as in the reference.
+// Rows of up to 256 * 4 * CE_V4 aligned logits stay in registers between the
+// two reductions (one HBM read); exp is the hardware exp2 of (l - max) log2 e.
+constexpr int CE_V4 = 16;
+
+__device__ __forceinline__ float ce_block_max(float v, float* red) {
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float other = __shfl_xor(v, o, 64);
+    v = other > v ? other : v;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = red[0];
+  for (int w = 1; w < 4; ++w) v = red[w] > v ? red[w] : v;
+  return v;
+}
+
 __global__ __launch_bounds__(256) void token_ce_kernel(const float* __restrict__ logits, int V,
                                                        const uint32_t* __restrict__ targets,
                                                        const uint32_t* __restrict__ index,
                                                        float* __restrict__ loss) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   const float* l = logits + (size_t)blockIdx.x * V;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float mx = -INFINITY;
-  for (int i = tid; i < V; i += 256) mx = l[i] > mx ? l[i] : mx;
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float other = __shfl_xor(mx, o, 64);
-    mx = other > mx ? other : mx;
+  const int tid = threadIdx.x;
+  constexpr float kLog2e = 1.44269504088896341f;
+  float sum = 0.0f, mx;
+  if (V % 4 == 0 && V <= 256 * 4 * CE_V4) {
+    float4 v[CE_V4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < CE_V4; ++k) {
+      const int i = 4 * (tid + 256 * k);
+      v[k] = i < V ? *reinterpret_cast<const float4*>(l + i) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      m = v[k].x > m ? v[k].x : m;
+      m = v[k].y > m ? v[k].y : m;
+      m = v[k].z > m ? v[k].z : m;
+      m = v[k].w > m ? v[k].w : m;
+    }
+    mx = ce_block_max(m, red);
+#pragma unroll
+    for (int k = 0; k < CE_V4; ++k)
+      if (4 * (tid + 256 * k) < V)
+        sum += (__builtin_amdgcn_exp2f((v[k].x - mx) * kLog2e) + __builtin_amdgcn_exp2f((v[k].y - mx) * kLog2e)) +
+               (__builtin_amdgcn_exp2f((v[k].z - mx) * kLog2e) + __builtin_amdgcn_exp2f((v[k].w - mx) * kLog2e));
+  } else {
+    float m = -INFINITY;
+    for (int i = tid; i < V; i += 256) m = l[i] > m ? l[i] : m;
+    mx = ce_block_max(m, red);
+    for (int i = tid; i < V; i += 256) sum += __builtin_amdgcn_exp2f((l[i] - mx) * kLog2e);
   }
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = red[0];
-  for (int w = 1; w < 4; ++w) mx = red[w] > mx ? red[w] : mx;
-  __syncthreads();
-  float sum = 0.0f;
-  for (int i = tid; i < V; i += 256) sum += expf(l[i] - mx);
   for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-  if (lane == 0) red[wave] = sum;
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = sum;
   __syncthreads();
   if (tid == 0) {
-    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float total = (red[4] + red[5]) + (red[6] + red[7]);
     loss[index[blockIdx.x]] = (mx - l[targets[blockIdx.x]]) + logf(total);
   }
 }

@@ -159,10 +159,34 @@ int pssa_hip_weights_populate_banks(const pssa_hip_weights* w, uint64_t seed, ui
 
 /* GpuDispatch::try_dispatch_gemm_into (src/backend.rs:1049-1085):
  * y[batch*m, n] = x[batch*m, k] * w[n, k]^T.  w_dtype selects the storage of
- * `w` (F32, or BF16 as uint16 bit patterns); accumulation is fp32. */
+ * `w` (F32, or BF16 as uint16 bit patterns); accumulation is fp32.  `w` goes
+ * through the weight cache below. */
 int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const void* w,
                       size_t w_len, int w_dtype, size_t m, size_t n, size_t k, size_t batch,
                       float* y, size_t y_len, char* err, size_t err_len);
+
+/* GEMM weights stay on the device between calls, keyed by (host address,
+ * element count) like the reference's CUDA weight cache (CudaContext::
+ * weight_buffer, src/cuda.rs:198-227): pssa_hip_gemm_xwt reuses the copy of
+ * a weight it has seen, so a caller that changes a weight's host data in
+ * place must invalidate it.  Stale copies are uploaded again on next use. */
+typedef struct pssa_hip_weight_key {
+  const void* ptr; /* host address of the weight passed to pssa_hip_gemm_xwt */
+  size_t len;      /* its element count (w_len) */
+} pssa_hip_weight_key;
+
+/* GpuDispatch::invalidate_weights (src/backend.rs:1113-1120, src/cuda.rs:229-240):
+ * every cached weight is stale. */
+void pssa_hip_invalidate_weights(pssa_hip_ctx* ctx);
+
+/* GpuDispatch::invalidate_weights_only (src/backend.rs:1122-1134,
+ * src/cuda.rs:242-252): only the weights with these keys are stale. */
+int pssa_hip_invalidate_weights_only(pssa_hip_ctx* ctx, const pssa_hip_weight_key* keys, size_t n_keys,
+                                     char* err, size_t err_len);
+
+/* Cached weights: entries, how many are current, device bytes (no reference
+ * counterpart; for tests and tools). */
+int pssa_hip_weight_cache_stats(pssa_hip_ctx* ctx, size_t* entries, size_t* current, size_t* bytes);
 
 /* GpuDispatch::softplus_in_place (src/backend.rs:1419-1428). */
 int pssa_hip_softplus_in_place(pssa_hip_ctx* ctx, float* values, size_t len, char* err,

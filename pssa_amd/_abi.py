@@ -75,6 +75,11 @@ class Weights(C.Structure):
     ]
 
 
+class WeightKey(C.Structure):
+    """pssa_hip_weight_key: (host address, element count) of a cached weight."""
+    _fields_ = [("ptr", C.c_void_p), ("len", C.c_size_t)]
+
+
 class Sequence(C.Structure):
     """pssa_hip_sequence (Sequence, src/sequence_batch.rs:21-28)."""
     _fields_ = [
@@ -124,6 +129,9 @@ def lib() -> C.CDLL:
         "pssa_hip_weights_populate_banks": ([C.POINTER(Weights), C.c_uint64, C.c_uint64, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_gemm_xwt": ([vp, fp, sz, vp, sz, C.c_int, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_softplus_in_place": ([vp, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_invalidate_weights": ([vp], None),
+        "pssa_hip_invalidate_weights_only": ([vp, C.POINTER(WeightKey), sz, err_t, sz], C.c_int),
+        "pssa_hip_weight_cache_stats": ([vp, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)], C.c_int),
         "pssa_hip_ssm_forward": ([vp, fp, sz, fp, fp, sz, fp, sz, fp, sz, fp, fp, sz, fp, sz, sz, sz, sz,
                                   fp, fp, fp, fp, sz, fp, err_t, sz], C.c_int),
         "pssa_hip_memory_forward": ([vp, fp, fp, fp, fp, fp, fp, fp, fp, fp, sz, sz, sz, sz, sz, sz,

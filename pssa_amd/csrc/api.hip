@@ -88,6 +88,25 @@ Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_devi
   return Status::Ok();
 }
 
+// The device copy of a GEMM weight (CudaContext::weight_buffer,
+// src/cuda.rs:198-227): reused while current, uploaded again when stale,
+// uploaded and kept on first use.  Called with ctx->mu held.
+Status cached_weight(pssa_hip_ctx* ctx, const void* host, size_t n, int dtype, const void** out) {
+  const size_t bytes = n * (dtype == PSSA_HIP_BF16 ? 2 : 4);
+  auto key = std::make_tuple((uintptr_t)host, n, dtype);
+  auto it = ctx->weights.find(key);
+  if (it == ctx->weights.end()) {
+    pssa_hip_ctx::CachedWeight cw;
+    PSSA_RETURN_IF(upload(cw.buf, host, bytes, ctx->stream));
+    it = ctx->weights.emplace(key, std::move(cw)).first;
+  } else if (!it->second.current) {
+    PSSA_HIP_TRY(hipMemcpyAsync(it->second.buf.p, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    it->second.current = true;
+  }
+  *out = it->second.buf.p;
+  return Status::Ok();
+}
+
 Status stage_ids_locked(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T) {
   PSSA_RETURN_IF(need(ids != nullptr, "null ids"));
   PSSA_RETURN_IF(need(T > 0, "prefill requires at least one token"));
@@ -235,9 +254,10 @@ int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const voi
     if (rows > INT32_MAX || n > INT32_MAX || k > INT32_MAX) return Status::Invalid("gemm: too large");
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
-    DevBuf dx, dxh, dw, dy;
+    DevBuf dx, dxh, dy;
     PSSA_RETURN_IF(upload(dx, x, xin * 4, ctx->stream));
-    PSSA_RETURN_IF(upload(dw, w, win * (w_dtype == PSSA_HIP_BF16 ? 2 : 4), ctx->stream));
+    const void* dw = nullptr;
+    PSSA_RETURN_IF(cached_weight(ctx, w, win, w_dtype, &dw));
     PSSA_RETURN_IF(dy.alloc(yout * 4));
     const void* a = dx.p;
     if (w_dtype == PSSA_HIP_BF16) {
@@ -249,11 +269,47 @@ int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const voi
     pssa::EpiParams ep;
     ep.out32 = dy.as<float>();
     ep.ld32 = (int)n;
-    PSSA_RETURN_IF(pssa::launch_gemm(ctx->stream, w_dtype, a, (int)k, dw.p, (int)k, (int)rows, (int)n, (int)k, ep));
+    PSSA_RETURN_IF(pssa::launch_gemm(ctx->stream, w_dtype, a, (int)k, dw, (int)k, (int)rows, (int)n, (int)k, ep));
     PSSA_RETURN_IF(download(y, dy, yout * 4, ctx->stream));
     return sync(ctx);
   };
   return pssa::finish(body(), err, err_len);
+}
+
+void pssa_hip_invalidate_weights(pssa_hip_ctx* ctx) {
+  if (!ctx) return;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  for (auto& kv : ctx->weights) kv.second.current = false;
+}
+
+int pssa_hip_invalidate_weights_only(pssa_hip_ctx* ctx, const pssa_hip_weight_key* keys, size_t n_keys,
+                                     char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(keys || n_keys == 0, "null weight keys"));
+    std::lock_guard<std::mutex> g(ctx->mu);
+    for (auto& kv : ctx->weights)
+      for (size_t i = 0; i < n_keys; ++i)
+        if (std::get<0>(kv.first) == (uintptr_t)keys[i].ptr && std::get<1>(kv.first) == keys[i].len)
+          kv.second.current = false;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_weight_cache_stats(pssa_hip_ctx* ctx, size_t* entries, size_t* current, size_t* bytes) {
+  if (!ctx) return PSSA_HIP_EINVAL;
+  std::lock_guard<std::mutex> g(ctx->mu);
+  size_t e = 0, c = 0, b = 0;
+  for (const auto& kv : ctx->weights) {
+    ++e;
+    c += kv.second.current ? 1 : 0;
+    b += kv.second.buf.bytes;
+  }
+  if (entries) *entries = e;
+  if (current) *current = c;
+  if (bytes) *bytes = b;
+  return PSSA_HIP_OK;
 }
 
 int pssa_hip_softplus_in_place(pssa_hip_ctx* ctx, float* values, size_t len, char* err, size_t err_len) {

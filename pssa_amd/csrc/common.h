@@ -7,8 +7,10 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/pssa_hip.h"
@@ -133,4 +135,12 @@ struct pssa_hip_ctx {
   // context); calls on one context are serialised by `mu` on one stream.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // Device copies of GEMM weights keyed by (host address, element count,
+  // storage dtype), as the reference's CUDA weight cache keys them by
+  // (address, length).  A stale entry is uploaded again on its next use.
+  struct CachedWeight {
+    pssa::DevBuf buf;
+    bool current = true;
+  };
+  std::map<std::tuple<uintptr_t, size_t, int>, CachedWeight> weights;
 };

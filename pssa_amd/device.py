@@ -72,7 +72,13 @@ class HipDevice:
 
     # -- GpuDispatch::try_dispatch_gemm_into (src/backend.rs:1049-1085) -------
     def try_dispatch_gemm(self, x, w, m: int, n: int, k: int, batch: int = 1,
-                          w_dtype: str = "f32") -> np.ndarray:
+                          w_dtype: str = "f32", resident: bool = False) -> np.ndarray:
+        """y = x w^T.  The library keeps a device copy of `w` keyed by its host
+        address and length.  With `resident` the copy stays current for later
+        calls with the same array, as a model parameter would (the caller
+        invalidates it after changing the data in place); otherwise it is
+        marked stale after the call, since a temporary array's address can be
+        reused by other data."""
         x = _f32(x).ravel()
         if w_dtype == "f32":
             wb = _f32(w).ravel()
@@ -82,10 +88,34 @@ class HipDevice:
             code, wlen = _abi.BF16, wb.size
         else:
             raise ValueError("w_dtype must be 'f32' or 'bf16'")
+        if resident and not np.shares_memory(wb, np.asarray(w)):
+            raise ValueError("a resident weight must be a contiguous array of the weight dtype")
         y = np.empty(batch * m * n, dtype=np.float32)
-        _abi.call(self._lib.pssa_hip_gemm_xwt, self.handle, _abi.ptr(x), x.size,
-                  wb.ctypes.data_as(C.c_void_p), wlen, code, m, n, k, batch, _abi.ptr(y), y.size)
+        try:
+            _abi.call(self._lib.pssa_hip_gemm_xwt, self.handle, _abi.ptr(x), x.size,
+                      wb.ctypes.data_as(C.c_void_p), wlen, code, m, n, k, batch, _abi.ptr(y), y.size)
+        finally:
+            if not resident:
+                self.invalidate_weights_only([wb])
         return y
+
+    # -- weight residency (GpuDispatch::invalidate_weights[_only],
+    #    src/backend.rs:1113-1134) ------------------------------------------
+    def invalidate_weights(self) -> None:
+        self._lib.pssa_hip_invalidate_weights(self.handle)
+
+    def invalidate_weights_only(self, arrays) -> None:
+        """Marks the cached copies of these host arrays stale (keyed by data
+        address and element count)."""
+        keys = (_abi.WeightKey * max(len(arrays), 1))()
+        for i, a in enumerate(arrays):
+            keys[i].ptr, keys[i].len = a.ctypes.data, a.size
+        _abi.call(self._lib.pssa_hip_invalidate_weights_only, self.handle, keys, len(arrays))
+
+    def weight_cache_stats(self) -> dict:
+        e, c, b = C.c_size_t(), C.c_size_t(), C.c_size_t()
+        self._lib.pssa_hip_weight_cache_stats(self.handle, C.byref(e), C.byref(c), C.byref(b))
+        return {"entries": e.value, "current": c.value, "bytes": b.value}
 
     def softplus_in_place(self, values: np.ndarray) -> None:
         assert values.dtype == np.float32 and values.flags.c_contiguous

@@ -44,6 +44,37 @@ def test_gemm_bf16_weights(hip, m, n, k, batch):
     assert rel_err(y, O.gemm_xwt(x, w)) < 2e-2
 
 
+def test_gemm_weight_cache_follows_invalidation(hip):
+    """try_dispatch_gemm_into keeps the weight on the device keyed by host
+    address and length (CudaContext::weight_buffer, src/cuda.rs:198-227): a
+    resident weight changed in place keeps its device copy until it is
+    invalidated (src/cuda.rs:229-252); a temporary weight is never reused."""
+    say("gemm weight cache")
+    rng = np.random.default_rng(5)
+    m, n, k = 70, 96, 64
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    w_old = w.copy()
+    s0 = hip.weight_cache_stats()
+    y1 = hip.try_dispatch_gemm(x, w, m, n, k, resident=True)
+    s1 = hip.weight_cache_stats()
+    assert s1["entries"] == s0["entries"] + 1 and s1["current"] == s0["current"] + 1
+    w *= 2.0  # in place: same address and length
+    np.testing.assert_array_equal(hip.try_dispatch_gemm(x, w, m, n, k, resident=True), y1)
+    hip.invalidate_weights_only([np.zeros(5, np.float32)])  # another key: nothing changes
+    np.testing.assert_array_equal(hip.try_dispatch_gemm(x, w, m, n, k, resident=True), y1)
+    hip.invalidate_weights_only([w])
+    np.testing.assert_array_equal(hip.try_dispatch_gemm(x, w, m, n, k, resident=True), 2.0 * y1)
+    w[:] = w_old
+    hip.invalidate_weights()
+    assert hip.weight_cache_stats()["current"] == 0
+    np.testing.assert_array_equal(hip.try_dispatch_gemm(x, w, m, n, k, resident=True), y1)
+    for scale in (4.0, 0.5):  # temporaries (exact scalings), possibly at one recycled address
+        np.testing.assert_array_equal(hip.try_dispatch_gemm(x, w * np.float32(scale), m, n, k),
+                                      np.float32(scale) * y1)
+    assert hip.weight_cache_stats()["current"] == 1
+
+
 def test_gemm_shape_errors_leave_output_untouched(hip):
     from pssa_amd._abi import HipError
 

@@ -165,6 +165,17 @@ int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const voi
                       size_t w_len, int w_dtype, size_t m, size_t n, size_t k, size_t batch,
                       float* y, size_t y_len, char* err, size_t err_len);
 
+/* GpuDispatch::gemm_nn_into (src/backend.rs:1152-1168): row-major
+ * out[m, n] = a[m, k] * b[k, n], fp32. */
+int pssa_hip_gemm_nn(pssa_hip_ctx* ctx, const float* a, size_t a_len, const float* b, size_t b_len, size_t m,
+                     size_t k, size_t n, float* out, size_t out_len, char* err, size_t err_len);
+
+/* GpuDispatch::gemm_tn_accumulate_into (src/backend.rs:1170-1184): row-major
+ * out[k, n] += a[m, k]^T * b[m, n], fp32. */
+int pssa_hip_gemm_tn_accumulate(pssa_hip_ctx* ctx, const float* a, size_t a_len, const float* b, size_t b_len,
+                                size_t m, size_t k, size_t n, float* out, size_t out_len, char* err,
+                                size_t err_len);
+
 /* GEMM weights stay on the device between calls, keyed by (host address,
  * element count) like the reference's CUDA weight cache (CudaContext::
  * weight_buffer, src/cuda.rs:198-227): pssa_hip_gemm_xwt reuses the copy of

@@ -129,6 +129,8 @@ def lib() -> C.CDLL:
         "pssa_hip_weights_populate_banks": ([C.POINTER(Weights), C.c_uint64, C.c_uint64, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_gemm_xwt": ([vp, fp, sz, vp, sz, C.c_int, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_softplus_in_place": ([vp, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_gemm_nn": ([vp, fp, sz, fp, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_gemm_tn_accumulate": ([vp, fp, sz, fp, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_invalidate_weights": ([vp], None),
         "pssa_hip_invalidate_weights_only": ([vp, C.POINTER(WeightKey), sz, err_t, sz], C.c_int),
         "pssa_hip_weight_cache_stats": ([vp, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)], C.c_int),

@@ -276,6 +276,88 @@ int pssa_hip_gemm_xwt(pssa_hip_ctx* ctx, const float* x, size_t x_len, const voi
   return pssa::finish(body(), err, err_len);
 }
 
+// Shared body of gemm_nn and gemm_tn_accumulate: y = x w^T on the device
+// after transposing the operands the layout asks for (`x_t`: x arrives as
+// [kx, rows]; `w_t`: w arrives as [k, n]); `accumulate` adds the product to
+// the caller's y.
+static Status gemm_transposed(pssa_hip_ctx* ctx, const float* x, const float* w, size_t rows, size_t n, size_t k,
+                              bool x_t, bool w_t, bool accumulate, float* y) {
+  std::lock_guard<std::mutex> g(ctx->mu);
+  PSSA_HIP_TRY(hipSetDevice(ctx->device));
+  const hipStream_t st = ctx->stream;
+  DevBuf dx, dw, dxt, dwt, dy, dacc;
+  PSSA_RETURN_IF(upload(dx, x, rows * k * 4, st));
+  PSSA_RETURN_IF(upload(dw, w, n * k * 4, st));
+  const float* xa = dx.as<float>();
+  const float* wa = dw.as<float>();
+  if (x_t) {  // [k, rows] -> [rows, k]
+    PSSA_RETURN_IF(dxt.alloc(rows * k * 4));
+    PSSA_RETURN_IF(pssa::launch_transpose(st, xa, dxt.as<float>(), 1, (int)k, (int)rows, 1.0f));
+    xa = dxt.as<float>();
+  }
+  if (w_t) {  // [k, n] -> [n, k]
+    PSSA_RETURN_IF(dwt.alloc(n * k * 4));
+    PSSA_RETURN_IF(pssa::launch_transpose(st, wa, dwt.as<float>(), 1, (int)k, (int)n, 1.0f));
+    wa = dwt.as<float>();
+  }
+  PSSA_RETURN_IF(dy.alloc(rows * n * 4));
+  pssa::EpiParams ep;
+  ep.out32 = dy.as<float>();
+  ep.ld32 = (int)n;
+  if (accumulate) {
+    PSSA_RETURN_IF(upload(dacc, y, rows * n * 4, st));
+    ep.kind = pssa::EPI_ADD_AUX;
+    ep.aux = dacc.as<float>();
+    ep.ld_aux = (int)n;
+  }
+  PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, xa, (int)k, wa, (int)k, (int)rows, (int)n, (int)k, ep));
+  PSSA_RETURN_IF(download(y, dy, rows * n * 4, st));
+  return sync(ctx);
+}
+
+static Status gemm_dims(size_t m, size_t k, size_t n, size_t a_len, size_t b_len, size_t out_len, size_t a_exp,
+                        size_t b_exp, size_t out_exp) {
+  PSSA_RETURN_IF(need(m && k && n, "GEMM dimensions must be positive"));
+  if (a_exp > INT32_MAX || b_exp > INT32_MAX || out_exp > INT32_MAX) return Status::Invalid("gemm: too large");
+  if (a_len != a_exp || b_len != b_exp || out_len != out_exp)
+    return Status::Invalid("GEMM operand lengths must be " + std::to_string(a_exp) + ", " + std::to_string(b_exp) +
+                           " and " + std::to_string(out_exp));
+  return Status::Ok();
+}
+
+int pssa_hip_gemm_nn(pssa_hip_ctx* ctx, const float* a, size_t a_len, const float* b, size_t b_len, size_t m,
+                     size_t k, size_t n, float* out, size_t out_len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(a && b && out, "gemm: null buffer"));
+    size_t ae = 0, be = 0, oe = 0;
+    PSSA_RETURN_IF(pssa::checked_count({m, k}, &ae, "gemm lhs"));
+    PSSA_RETURN_IF(pssa::checked_count({k, n}, &be, "gemm rhs"));
+    PSSA_RETURN_IF(pssa::checked_count({m, n}, &oe, "gemm output"));
+    PSSA_RETURN_IF(gemm_dims(m, k, n, a_len, b_len, out_len, ae, be, oe));
+    return gemm_transposed(ctx, a, b, m, n, k, false, true, false, out);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_gemm_tn_accumulate(pssa_hip_ctx* ctx, const float* a, size_t a_len, const float* b, size_t b_len,
+                                size_t m, size_t k, size_t n, float* out, size_t out_len, char* err,
+                                size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(a && b && out, "gemm: null buffer"));
+    size_t ae = 0, be = 0, oe = 0;
+    PSSA_RETURN_IF(pssa::checked_count({m, k}, &ae, "gemm lhs"));
+    PSSA_RETURN_IF(pssa::checked_count({m, n}, &be, "gemm rhs"));
+    PSSA_RETURN_IF(pssa::checked_count({k, n}, &oe, "gemm output"));
+    PSSA_RETURN_IF(gemm_dims(m, k, n, a_len, b_len, out_len, ae, be, oe));
+    // C(K,N) += A^T B: rows = K, reduction over M; A [M,K] and B [M,N] both
+    // arrive reduction-major.
+    return gemm_transposed(ctx, a, b, k, n, m, true, true, true, out);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 void pssa_hip_invalidate_weights(pssa_hip_ctx* ctx) {
   if (!ctx) return;
   std::lock_guard<std::mutex> g(ctx->mu);

@@ -99,6 +99,24 @@ class HipDevice:
                 self.invalidate_weights_only([wb])
         return y
 
+    # -- GpuDispatch::gemm_nn_into / gemm_tn_accumulate_into
+    #    (src/backend.rs:1152-1184) ------------------------------------------
+    def gemm_nn(self, a, b, m: int, k: int, n: int) -> np.ndarray:
+        """out[m, n] = a[m, k] b[k, n]."""
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        out = np.empty(m * n, np.float32)
+        _abi.call(self._lib.pssa_hip_gemm_nn, self.handle, _abi.ptr(a), a.size, _abi.ptr(b), b.size, m, k, n,
+                  _abi.ptr(out), out.size)
+        return out
+
+    def gemm_tn_accumulate(self, a, b, m: int, k: int, n: int, out: np.ndarray) -> None:
+        """out[k, n] += a[m, k]^T b[m, n] (out: contiguous float32, updated in place)."""
+        a, b = _f32(a).ravel(), _f32(b).ravel()
+        if out.dtype != np.float32 or not out.flags.c_contiguous:
+            raise ValueError("out must be a contiguous float32 array")
+        _abi.call(self._lib.pssa_hip_gemm_tn_accumulate, self.handle, _abi.ptr(a), a.size, _abi.ptr(b), b.size,
+                  m, k, n, _abi.ptr(out), out.size)
+
     # -- weight residency (GpuDispatch::invalidate_weights[_only],
     #    src/backend.rs:1113-1134) ------------------------------------------
     def invalidate_weights(self) -> None:

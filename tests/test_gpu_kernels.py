@@ -8,6 +8,7 @@ import pytest
 from conftest import rel_err
 from oracle import oracle as O
 from pssa_amd import bf16_round
+from pssa_amd._abi import HipError
 from test_oracle_closed_forms import F32_MIN_SUB, bank, cuda_ssm_fixture
 
 pytestmark = pytest.mark.gpu
@@ -42,6 +43,30 @@ def test_gemm_bf16_weights(hip, m, n, k, batch):
     exact = bf16_round(x).astype(np.float64) @ wb.astype(np.float64).T
     assert rel_err(y, exact) < 1e-5
     assert rel_err(y, O.gemm_xwt(x, w)) < 2e-2
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 5, 3), (130, 64, 257), (300, 768, 96)])
+def test_gemm_nn_and_tn_accumulate(hip, m, k, n):
+    """gemm_nn_into and gemm_tn_accumulate_into (src/backend.rs:1152-1184)
+    against the oracle's GEMM on transposed operands; failed validation
+    leaves the output untouched."""
+    say("gemm nn / tn", m, k, n)
+    rng = np.random.default_rng(m + 7 * k + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal((k, n)) * 0.1).astype(np.float32)
+    got = hip.gemm_nn(a, b, m, k, n).reshape(m, n)
+    ref = O.gemm_xwt(a, np.ascontiguousarray(b.T))
+    assert rel_err(got, ref) < 1e-4
+    bm = (rng.standard_normal((m, n)) * 0.1).astype(np.float32)
+    out = rng.standard_normal((k, n)).astype(np.float32)
+    base = out.copy()
+    hip.gemm_tn_accumulate(a, bm, m, k, n, out)
+    ref = base + O.gemm_xwt(np.ascontiguousarray(a.T), np.ascontiguousarray(bm.T))
+    assert rel_err(out, ref) < 1e-4
+    keep = out.copy()
+    with pytest.raises(HipError, match="operand lengths"):
+        hip.gemm_tn_accumulate(a[:, :-1] if k > 1 else a[:0], bm, m, k, n, out)
+    np.testing.assert_array_equal(out, keep)
 
 
 def test_gemm_weight_cache_follows_invalidation(hip):

@@ -219,6 +219,16 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
                          size_t d_s, float* bar_a, float* bar_b, float* states, float* y_ssm,
                          size_t y_len, float* final_state, char* err, size_t err_len);
 
+/* GpuDispatch::ssm_forward_resident (src/backend.rs:1186-1211): the scan of
+ * pssa_hip_ssm_forward with its tape (bar_a, bar_b, states, y_ssm) kept on
+ * the device for the next pssa_hip_memory_forward_after_ssm on this context,
+ * which consumes it.  A later call replaces an unconsumed tape. */
+int pssa_hip_ssm_forward_resident(pssa_hip_ctx* ctx, const float* delta, size_t delta_len,
+                                  const float* delta_raw, const float* b_proj, size_t b_len,
+                                  const float* x_norm, size_t x_len, const float* rates, size_t rates_len,
+                                  const float* c_proj, size_t c_len, const float* initial, size_t initial_len,
+                                  size_t seq_len, size_t d_m, size_t d_s, char* err, size_t err_len);
+
 /* GpuDispatch::memory_forward (src/backend.rs:1345-1385) for seq_len rows:
  *   q_euc = x_norm W_qx^T + y_ssm W_qh^T; q_pnc = project(q_euc);
  *   soft read over `count` slots (retrieve_soft_into, src/memory.rs:344-426)
@@ -234,6 +244,20 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
                             float* q_euc, float* q_pnc, float* q_norm, float* weights,
                             float* m_val, float* g_mem, float* m_proj, float* m_inj, char* err,
                             size_t err_len);
+
+/* GpuDispatch::memory_forward_after_ssm (src/backend.rs:1246-1289): the
+ * memory stage on the resident y_ssm of the last pssa_hip_ssm_forward_resident
+ * (same seq_len and d_m, else PSSA_HIP_EINVAL), plus copies of that tape:
+ * bar_a, bar_b [L*d*s], states [(L+1)*d*s], y_ssm [L,d] (each may be NULL).
+ * Other arguments and outputs as pssa_hip_memory_forward. */
+int pssa_hip_memory_forward_after_ssm(pssa_hip_ctx* ctx, const float* x_norm, const float* w_qx,
+                                      const float* w_qh, const float* w_gate, const float* w_proj,
+                                      const float* keys, const float* norm_sq, const float* values,
+                                      size_t seq_len, size_t d_m, size_t d_k, size_t d_val, size_t capacity,
+                                      size_t count, float tau, size_t top_k, float* bar_a, float* bar_b,
+                                      float* states, float* y_ssm, float* q_euc, float* q_pnc, float* q_norm,
+                                      float* weights, float* m_val, float* g_mem, float* m_proj, float* m_inj,
+                                      char* err, size_t err_len);
 
 /* Batched retrieve_soft_into (src/memory.rs:344-426; the reference's parallel
  * per-query read, src/gpu_batch.rs:700-740) for n_q projected queries

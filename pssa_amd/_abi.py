@@ -136,6 +136,10 @@ def lib() -> C.CDLL:
         "pssa_hip_weight_cache_stats": ([vp, C.POINTER(sz), C.POINTER(sz), C.POINTER(sz)], C.c_int),
         "pssa_hip_ssm_forward": ([vp, fp, sz, fp, fp, sz, fp, sz, fp, sz, fp, fp, sz, fp, sz, sz, sz, sz,
                                   fp, fp, fp, fp, sz, fp, err_t, sz], C.c_int),
+        "pssa_hip_ssm_forward_resident": ([vp, fp, sz, fp, fp, sz, fp, sz, fp, sz, fp, sz, fp, sz, sz, sz, sz,
+                                           err_t, sz], C.c_int),
+        "pssa_hip_memory_forward_after_ssm": ([vp] + [fp] * 8 + [sz] * 6 + [C.c_float, sz] + [fp] * 12
+                                               + [err_t, sz], C.c_int),
         "pssa_hip_memory_forward": ([vp, fp, fp, fp, fp, fp, fp, fp, fp, fp, sz, sz, sz, sz, sz, sz,
                                      C.c_float, sz, fp, fp, fp, fp, fp, fp, fp, fp, err_t, sz], C.c_int),
         "pssa_hip_retrieve": ([vp, fp, sz, fp, fp, fp, sz, sz, sz, sz, C.c_float, sz, fp, fp, u32p, fp,

@@ -411,6 +411,107 @@ int pssa_hip_softplus_in_place(pssa_hip_ctx* ctx, float* values, size_t len, cha
 }
 
 // -------------------------------------------------------------- SSM stage
+// Device results of one stage-API scan (the reference's SSM tape fields,
+// src/gpu_batch.rs:392-437): y [L,d], the final carry (state-major [s,d]),
+// and when materialised bar_a, bar_b [L*d*s] and states [(L+1)*d*s].
+struct SsmTape {
+  size_t L = 0, d = 0, s = 0;
+  DevBuf y, carry, carry_ds, bar_a, bar_b, states;
+};
+
+static Status check_ssm_shapes(size_t seq_len, size_t d_m, size_t d_s, size_t delta_len, size_t b_len,
+                               size_t x_len, size_t rates_len, size_t c_len, size_t initial_len) {
+  PSSA_RETURN_IF(need(seq_len && d_m && d_s, "ssm: dimensions must be positive"));
+  size_t ld = 0, ls = 0, w = 0, lw1 = 0;
+  PSSA_RETURN_IF(pssa::checked_count({seq_len, d_m}, &ld, "ssm"));
+  PSSA_RETURN_IF(pssa::checked_count({seq_len, d_s}, &ls, "ssm"));
+  PSSA_RETURN_IF(pssa::checked_count({d_m, d_s}, &w, "ssm"));
+  PSSA_RETURN_IF(pssa::checked_count({seq_len + 1, w}, &lw1, "ssm"));
+  if (delta_len != ld || x_len != ld) return Status::Invalid("ssm: delta/x_norm/y_ssm must be seq_len*d_m");
+  if (b_len != ls || c_len != ls) return Status::Invalid("ssm: b_proj/c_proj must be seq_len*d_s");
+  if (rates_len != w || initial_len != w) return Status::Invalid("ssm: rates/initial must be d_m*d_s");
+  if (seq_len > INT32_MAX || d_m > INT32_MAX || d_s > INT32_MAX) return Status::Invalid("ssm: too large");
+  return Status::Ok();
+}
+
+// Runs the scan of the stage API into `t` (called with ctx->mu held).
+static Status run_stage_ssm(pssa_hip_ctx* ctx, const float* delta, const float* b_proj, const float* x_norm,
+                            const float* rates, const float* c_proj, const float* initial, size_t seq_len,
+                            size_t d_m, size_t d_s, bool materialize, SsmTape& t) {
+  const hipStream_t st = ctx->stream;
+  const size_t ld = seq_len * d_m, ls = seq_len * d_s, w = d_m * d_s;
+  t.L = seq_len;
+  t.d = d_m;
+  t.s = d_s;
+  DevBuf dd, db, dx, dr, dc, dr2;
+  PSSA_RETURN_IF(upload(dd, delta, ld * 4, st));
+  PSSA_RETURN_IF(upload(db, b_proj, ls * 4, st));
+  PSSA_RETURN_IF(upload(dx, x_norm, ld * 4, st));
+  PSSA_RETURN_IF(upload(dr, rates, w * 4, st));
+  PSSA_RETURN_IF(upload(dc, c_proj, ls * 4, st));
+  PSSA_RETURN_IF(upload(t.carry_ds, initial, w * 4, st));
+  PSSA_RETURN_IF(t.y.alloc(ld * 4));
+  // The scan keeps states and rates state-major ([s, d]); the stage API
+  // speaks the reference's [d, s].
+  PSSA_RETURN_IF(dr2.alloc(w * 4));
+  PSSA_RETURN_IF(t.carry.alloc(w * 4));
+  PSSA_RETURN_IF(pssa::launch_transpose(st, dr.as<float>(), dr2.as<float>(), 1, (int)d_m, (int)d_s,
+                                        1.4426950408889634f));
+  PSSA_RETURN_IF(pssa::launch_transpose(st, t.carry_ds.as<float>(), t.carry.as<float>(), 1, (int)d_m, (int)d_s, 1.0f));
+  PSSA_RETURN_IF(pssa::launch_fill_zero(st, t.y.as<float>(), ld));
+  pssa::SsmArgs a;
+  a.delta = dd.as<float>();
+  a.ld_delta = (int)d_m;
+  a.bproj = db.as<float>();
+  a.ld_b = (int)d_s;
+  a.cproj = dc.as<float>();
+  a.ld_c = (int)d_s;
+  a.xn = dx.as<float>();
+  a.ld_x = (int)d_m;
+  a.rates2 = dr2.as<float>();
+  a.carry = t.carry.as<float>();
+  a.carry_stride = (long)w;
+  a.y = t.y.as<float>();
+  a.ld_y = (int)d_m;
+  a.T = (int)seq_len;
+  a.d = (int)d_m;
+  a.s = (int)d_s;
+  a.lanes = 1;
+  DevBuf dpart;
+  const int nz = pssa::ssm_state_blocks((int)d_s);
+  if (!materialize && nz > 2) {
+    PSSA_RETURN_IF(dpart.alloc((size_t)nz * ld * 4));
+    a.y_part = dpart.as<float>();
+  }
+  if (materialize) {
+    PSSA_RETURN_IF(t.bar_a.alloc(seq_len * w * 4));
+    PSSA_RETURN_IF(t.bar_b.alloc(seq_len * w * 4));
+    PSSA_RETURN_IF(t.states.alloc((seq_len + 1) * w * 4));
+    a.bar_a = t.bar_a.as<float>();
+    a.bar_b = t.bar_b.as<float>();
+    a.states = t.states.as<float>();
+  }
+  PSSA_RETURN_IF(pssa::launch_ssm_scan(st, a));
+  // Sources of the scan's inputs are freed at return: finish first.
+  return sync(ctx);
+}
+
+// Copies the tape's host outputs (any may be NULL).
+static Status download_ssm(pssa_hip_ctx* ctx, SsmTape& t, float* bar_a, float* bar_b, float* states, float* y_ssm,
+                           float* final_state) {
+  const hipStream_t st = ctx->stream;
+  const size_t ld = t.L * t.d, w = t.d * t.s;
+  if (y_ssm) PSSA_RETURN_IF(download(y_ssm, t.y, ld * 4, st));
+  if (final_state) {
+    PSSA_RETURN_IF(pssa::launch_transpose(st, t.carry.as<float>(), t.carry_ds.as<float>(), 1, (int)t.s, (int)t.d, 1.0f));
+    PSSA_RETURN_IF(download(final_state, t.carry_ds, w * 4, st));
+  }
+  if (bar_a) PSSA_RETURN_IF(download(bar_a, t.bar_a, t.L * w * 4, st));
+  if (bar_b) PSSA_RETURN_IF(download(bar_b, t.bar_b, t.L * w * 4, st));
+  if (states) PSSA_RETURN_IF(download(states, t.states, (t.L + 1) * w * 4, st));
+  return sync(ctx);
+}
+
 int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len,
                          const float* delta_raw, const float* b_proj, size_t b_len,
                          const float* x_norm, size_t x_len, const float* rates, size_t rates_len,
@@ -422,89 +523,149 @@ int pssa_hip_ssm_forward(pssa_hip_ctx* ctx, const float* delta, size_t delta_len
   (void)rate_deriv;
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(check_ctx(ctx));
-    PSSA_RETURN_IF(need(seq_len && d_m && d_s, "ssm: dimensions must be positive"));
     PSSA_RETURN_IF(need(delta && b_proj && x_norm && rates && c_proj && initial && y_ssm, "ssm: null input"));
     PSSA_RETURN_IF(need((bar_a == nullptr) == (bar_b == nullptr) && (bar_a == nullptr) == (states == nullptr),
                         "ssm: bar_a, bar_b and states are materialised together"));
-    size_t ld = 0, ls = 0, w = 0, lw = 0, lw1 = 0;
-    PSSA_RETURN_IF(pssa::checked_count({seq_len, d_m}, &ld, "ssm"));
-    PSSA_RETURN_IF(pssa::checked_count({seq_len, d_s}, &ls, "ssm"));
-    PSSA_RETURN_IF(pssa::checked_count({d_m, d_s}, &w, "ssm"));
-    PSSA_RETURN_IF(pssa::checked_count({seq_len, w}, &lw, "ssm"));
-    PSSA_RETURN_IF(pssa::checked_count({seq_len + 1, w}, &lw1, "ssm"));
-    if (delta_len != ld || x_len != ld || y_len != ld) return Status::Invalid("ssm: delta/x_norm/y_ssm must be seq_len*d_m");
-    if (b_len != ls || c_len != ls) return Status::Invalid("ssm: b_proj/c_proj must be seq_len*d_s");
-    if (rates_len != w || initial_len != w) return Status::Invalid("ssm: rates/initial must be d_m*d_s");
-    if (seq_len > INT32_MAX || d_m > INT32_MAX || d_s > INT32_MAX) return Status::Invalid("ssm: too large");
+    PSSA_RETURN_IF(check_ssm_shapes(seq_len, d_m, d_s, delta_len, b_len, x_len, rates_len, c_len, initial_len));
+    PSSA_RETURN_IF(need(y_len == seq_len * d_m, "ssm: delta/x_norm/y_ssm must be seq_len*d_m"));
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
-    const hipStream_t st = ctx->stream;
-    DevBuf dd, db, dx, dr, dc, dh, dy, da, dbb, dsx;
-    PSSA_RETURN_IF(upload(dd, delta, ld * 4, st));
-    PSSA_RETURN_IF(upload(db, b_proj, ls * 4, st));
-    PSSA_RETURN_IF(upload(dx, x_norm, ld * 4, st));
-    PSSA_RETURN_IF(upload(dr, rates, w * 4, st));
-    PSSA_RETURN_IF(upload(dc, c_proj, ls * 4, st));
-    PSSA_RETURN_IF(upload(dh, initial, w * 4, st));
-    PSSA_RETURN_IF(dy.alloc(ld * 4));
-    // The scan keeps states and rates state-major ([s, d]); the stage API
-    // speaks the reference's [d, s].
-    DevBuf dr2, dh2;
-    PSSA_RETURN_IF(dr2.alloc(w * 4));
-    PSSA_RETURN_IF(dh2.alloc(w * 4));
-    PSSA_RETURN_IF(pssa::launch_transpose(st, dr.as<float>(), dr2.as<float>(), 1, (int)d_m, (int)d_s,
-                                          1.4426950408889634f));
-    PSSA_RETURN_IF(pssa::launch_transpose(st, dh.as<float>(), dh2.as<float>(), 1, (int)d_m, (int)d_s, 1.0f));
-    PSSA_RETURN_IF(pssa::launch_fill_zero(st, dy.as<float>(), ld));
-    pssa::SsmArgs a;
-    a.delta = dd.as<float>();
-    a.ld_delta = (int)d_m;
-    a.bproj = db.as<float>();
-    a.ld_b = (int)d_s;
-    a.cproj = dc.as<float>();
-    a.ld_c = (int)d_s;
-    a.xn = dx.as<float>();
-    a.ld_x = (int)d_m;
-    a.rates2 = dr2.as<float>();
-    a.carry = dh2.as<float>();
-    a.carry_stride = (long)w;
-    a.y = dy.as<float>();
-    a.ld_y = (int)d_m;
-    a.T = (int)seq_len;
-    a.d = (int)d_m;
-    a.s = (int)d_s;
-    a.lanes = 1;
-    DevBuf dpart;
-    const int nz = pssa::ssm_state_blocks((int)d_s);
-    if (!bar_a && nz > 2) {
-      PSSA_RETURN_IF(dpart.alloc((size_t)nz * ld * 4));
-      a.y_part = dpart.as<float>();
-    }
-    if (bar_a) {
-      PSSA_RETURN_IF(da.alloc(lw * 4));
-      PSSA_RETURN_IF(dbb.alloc(lw * 4));
-      PSSA_RETURN_IF(dsx.alloc(lw1 * 4));
-      a.bar_a = da.as<float>();
-      a.bar_b = dbb.as<float>();
-      a.states = dsx.as<float>();
-    }
-    PSSA_RETURN_IF(pssa::launch_ssm_scan(st, a));
-    PSSA_RETURN_IF(download(y_ssm, dy, ld * 4, st));
-    if (final_state) {
-      PSSA_RETURN_IF(pssa::launch_transpose(st, dh2.as<float>(), dh.as<float>(), 1, (int)d_s, (int)d_m, 1.0f));
-      PSSA_RETURN_IF(download(final_state, dh, w * 4, st));
-    }
-    if (bar_a) {
-      PSSA_RETURN_IF(download(bar_a, da, lw * 4, st));
-      PSSA_RETURN_IF(download(bar_b, dbb, lw * 4, st));
-      PSSA_RETURN_IF(download(states, dsx, lw1 * 4, st));
-    }
-    return sync(ctx);
+    SsmTape t;
+    PSSA_RETURN_IF(run_stage_ssm(ctx, delta, b_proj, x_norm, rates, c_proj, initial, seq_len, d_m, d_s,
+                                 bar_a != nullptr, t));
+    return download_ssm(ctx, t, bar_a, bar_b, states, y_ssm, final_state);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_ssm_forward_resident(pssa_hip_ctx* ctx, const float* delta, size_t delta_len, const float* delta_raw,
+                                  const float* b_proj, size_t b_len, const float* x_norm, size_t x_len,
+                                  const float* rates, size_t rates_len, const float* c_proj, size_t c_len,
+                                  const float* initial, size_t initial_len, size_t seq_len, size_t d_m,
+                                  size_t d_s, char* err, size_t err_len) {
+  (void)delta_raw;
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(delta && b_proj && x_norm && rates && c_proj && initial, "ssm: null input"));
+    PSSA_RETURN_IF(check_ssm_shapes(seq_len, d_m, d_s, delta_len, b_len, x_len, rates_len, c_len, initial_len));
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    ctx->ssm_tape.reset();
+    auto t = std::make_shared<SsmTape>();
+    PSSA_RETURN_IF(run_stage_ssm(ctx, delta, b_proj, x_norm, rates, c_proj, initial, seq_len, d_m, d_s, true, *t));
+    ctx->ssm_tape = t;
+    return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);
 }
 
 // ----------------------------------------------------------- memory stage
+static Status check_memory_args(size_t seq_len, size_t d_m, size_t d_k, size_t d_val, size_t capacity,
+                                size_t count, float tau, size_t top_k) {
+  PSSA_RETURN_IF(need(seq_len && d_m && d_k && d_val && capacity, "memory: dimensions must be positive"));
+  PSSA_RETURN_IF(need(d_val == d_m, "memory: the model path reads values of width d_latent"));
+  PSSA_RETURN_IF(need(count <= capacity, "memory: count exceeds capacity"));
+  PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "memory: top_k must be at most 64"));
+  PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
+  if (seq_len > INT32_MAX / 4 || d_m > 16384 || d_k > 4096 || capacity > 8192)
+    return Status::Invalid("memory: shape exceeds the supported range");
+  return Status::Ok();
+}
+
+// The memory stage of the stage API on the device copy `dy` of y_ssm
+// (called with ctx->mu held).
+static Status run_stage_memory(pssa_hip_ctx* ctx, const float* x_norm, const float* dy_ptr, const float* w_qx,
+                               const float* w_qh, const float* w_gate, const float* w_proj, const float* keys,
+                               const float* norm_sq, const float* values, size_t seq_len, size_t d_m,
+                               size_t d_k, size_t capacity, size_t count, float tau, size_t top_k,
+                               float* q_euc, float* q_pnc, float* q_norm, float* weights, float* m_val,
+                               float* g_mem, float* m_proj, float* m_inj) {
+  const hipStream_t st = ctx->stream;
+  const int L = (int)seq_len, d = (int)d_m, k = (int)d_k, C = (int)capacity;
+  DevBuf dx, dwqx, dwqh, dwg, dwp, dk_, dn, dv, dvt, qx, qe, qp, qn, wts, mv, gm, mp, mi;
+  PSSA_RETURN_IF(upload(dx, x_norm, (size_t)L * d * 4, st));
+  PSSA_RETURN_IF(upload(dwqx, w_qx, (size_t)k * d * 4, st));
+  PSSA_RETURN_IF(upload(dwqh, w_qh, (size_t)k * d * 4, st));
+  PSSA_RETURN_IF(upload(dwg, w_gate, (size_t)d * d * 4, st));
+  PSSA_RETURN_IF(upload(dwp, w_proj, (size_t)d * d * 4, st));
+  PSSA_RETURN_IF(upload(dk_, keys, (size_t)C * k * 4, st));
+  PSSA_RETURN_IF(upload(dn, norm_sq, (size_t)C * 4, st));
+  PSSA_RETURN_IF(upload(dv, values, (size_t)C * d * 4, st));
+  std::vector<float> vt((size_t)d * C);
+  for (int s2 = 0; s2 < C; ++s2)
+    for (int j = 0; j < d; ++j) vt[(size_t)j * C + s2] = values[(size_t)s2 * d + j];
+  PSSA_RETURN_IF(upload(dvt, vt.data(), vt.size() * 4, st));
+  for (DevBuf* b : {&qx, &qe, &qp}) PSSA_RETURN_IF(b->alloc((size_t)L * k * 4));
+  PSSA_RETURN_IF(qn.alloc((size_t)L * 4));
+  PSSA_RETURN_IF(wts.alloc((size_t)L * C * 4));
+  for (DevBuf* b : {&mv, &gm, &mp, &mi}) PSSA_RETURN_IF(b->alloc((size_t)L * d * 4));
+  // q_euc = x W_qx^T + y W_qh^T, as dot(row_x, x) + dot(row_h, y) (src/pssa.rs:1147-1152).
+  pssa::EpiParams ex;
+  ex.out32 = qx.as<float>();
+  ex.ld32 = k;
+  PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwqx.p, d, L, k, d, ex));
+  pssa::EpiParams eq;
+  eq.kind = pssa::EPI_ADD_AUX;
+  eq.aux = qx.as<float>();
+  eq.ld_aux = k;
+  eq.out32 = qe.as<float>();
+  eq.ld32 = k;
+  PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dy_ptr, d, dwqh.p, d, L, k, d, eq));
+  pssa::RetrieveArgs ra;
+  ra.q = qe.as<float>();
+  ra.ld_q = k;
+  ra.project = 1;
+  ra.q_pnc = qp.as<float>();
+  ra.q_norm = qn.as<float>();
+  ra.keys = dk_.as<float>();
+  ra.norm_sq = dn.as<float>();
+  ra.values = dv.as<float>();
+  ra.n = L;
+  ra.dk = k;
+  ra.dv = d;
+  ra.capacity = C;
+  ra.count = (int)count;
+  ra.tau = tau;
+  ra.top_k = (int)top_k;
+  ra.weights = wts.as<float>();
+  const bool sparse = top_k > 0 && top_k < count;
+  if (sparse) ra.out_val = mv.as<float>();
+  PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
+  if (!sparse) {
+    if (count > 0) {
+      pssa::EpiParams em;
+      em.out32 = mv.as<float>();
+      em.ld32 = d;
+      PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, wts.p, C, dvt.p, C, L, d, (int)count, em));
+    } else {
+      PSSA_RETURN_IF(pssa::launch_fill_zero(st, mv.as<float>(), (size_t)L * d));
+    }
+  }
+  pssa::EpiParams eg;
+  eg.kind = pssa::EPI_SEGMENTS;
+  eg.seg[0] = 0;
+  eg.seg[1] = 0;
+  eg.seg[2] = d;
+  eg.seg[3] = d;
+  eg.out32 = gm.as<float>();
+  eg.ld32 = d;
+  PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwg.p, d, L, d, d, eg));
+  pssa::EpiParams ep2;
+  ep2.out32 = mp.as<float>();
+  ep2.ld32 = d;
+  PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, mv.p, d, dwp.p, d, L, d, d, ep2));
+  PSSA_RETURN_IF(pssa::launch_mul(st, gm.as<float>(), mp.as<float>(), mi.as<float>(), (size_t)L * d));
+  if (q_euc) PSSA_RETURN_IF(download(q_euc, qe, (size_t)L * k * 4, st));
+  if (q_pnc) PSSA_RETURN_IF(download(q_pnc, qp, (size_t)L * k * 4, st));
+  if (q_norm) PSSA_RETURN_IF(download(q_norm, qn, (size_t)L * 4, st));
+  if (weights) PSSA_RETURN_IF(download(weights, wts, (size_t)L * C * 4, st));
+  if (m_val) PSSA_RETURN_IF(download(m_val, mv, (size_t)L * d * 4, st));
+  if (g_mem) PSSA_RETURN_IF(download(g_mem, gm, (size_t)L * d * 4, st));
+  if (m_proj) PSSA_RETURN_IF(download(m_proj, mp, (size_t)L * d * 4, st));
+  PSSA_RETURN_IF(download(m_inj, mi, (size_t)L * d * 4, st));
+  return sync(ctx);
+}
+
 int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float* y_ssm,
                             const float* w_qx, const float* w_qh, const float* w_gate,
                             const float* w_proj, const float* keys, const float* norm_sq,
@@ -515,104 +676,44 @@ int pssa_hip_memory_forward(pssa_hip_ctx* ctx, const float* x_norm, const float*
                             size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(check_ctx(ctx));
-    PSSA_RETURN_IF(need(seq_len && d_m && d_k && d_val && capacity, "memory: dimensions must be positive"));
-    PSSA_RETURN_IF(need(d_val == d_m, "memory: the model path reads values of width d_latent"));
-    PSSA_RETURN_IF(need(count <= capacity, "memory: count exceeds capacity"));
-    PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "memory: top_k must be at most 64"));
-    PSSA_RETURN_IF(need(std::isfinite(tau) && tau > 0.0f, "tau must be positive and finite"));
+    PSSA_RETURN_IF(check_memory_args(seq_len, d_m, d_k, d_val, capacity, count, tau, top_k));
     PSSA_RETURN_IF(need(x_norm && y_ssm && w_qx && w_qh && w_gate && w_proj && keys && norm_sq &&
                             values && m_inj,
                         "memory: null input"));
-    if (seq_len > INT32_MAX / 4 || d_m > 16384 || d_k > 4096 || capacity > 8192)
-      return Status::Invalid("memory: shape exceeds the supported range");
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
-    const hipStream_t st = ctx->stream;
-    const int L = (int)seq_len, d = (int)d_m, k = (int)d_k, C = (int)capacity;
-    DevBuf dx, dy, dwqx, dwqh, dwg, dwp, dk_, dn, dv, dvt, qx, qe, qp, qn, wts, mv, gm, mp, mi;
-    PSSA_RETURN_IF(upload(dx, x_norm, (size_t)L * d * 4, st));
-    PSSA_RETURN_IF(upload(dy, y_ssm, (size_t)L * d * 4, st));
-    PSSA_RETURN_IF(upload(dwqx, w_qx, (size_t)k * d * 4, st));
-    PSSA_RETURN_IF(upload(dwqh, w_qh, (size_t)k * d * 4, st));
-    PSSA_RETURN_IF(upload(dwg, w_gate, (size_t)d * d * 4, st));
-    PSSA_RETURN_IF(upload(dwp, w_proj, (size_t)d * d * 4, st));
-    PSSA_RETURN_IF(upload(dk_, keys, (size_t)C * k * 4, st));
-    PSSA_RETURN_IF(upload(dn, norm_sq, (size_t)C * 4, st));
-    PSSA_RETURN_IF(upload(dv, values, (size_t)C * d * 4, st));
-    std::vector<float> vt((size_t)d * C);
-    for (int s2 = 0; s2 < C; ++s2)
-      for (int j = 0; j < d; ++j) vt[(size_t)j * C + s2] = values[(size_t)s2 * d + j];
-    PSSA_RETURN_IF(upload(dvt, vt.data(), vt.size() * 4, st));
-    for (DevBuf* b : {&qx, &qe, &qp}) PSSA_RETURN_IF(b->alloc((size_t)L * k * 4));
-    PSSA_RETURN_IF(qn.alloc((size_t)L * 4));
-    PSSA_RETURN_IF(wts.alloc((size_t)L * C * 4));
-    for (DevBuf* b : {&mv, &gm, &mp, &mi}) PSSA_RETURN_IF(b->alloc((size_t)L * d * 4));
-    // q_euc = x W_qx^T + y W_qh^T, as dot(row_x, x) + dot(row_h, y) (src/pssa.rs:1147-1152).
-    pssa::EpiParams ex;
-    ex.out32 = qx.as<float>();
-    ex.ld32 = k;
-    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwqx.p, d, L, k, d, ex));
-    pssa::EpiParams eq;
-    eq.kind = pssa::EPI_ADD_AUX;
-    eq.aux = qx.as<float>();
-    eq.ld_aux = k;
-    eq.out32 = qe.as<float>();
-    eq.ld32 = k;
-    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dy.p, d, dwqh.p, d, L, k, d, eq));
-    pssa::RetrieveArgs ra;
-    ra.q = qe.as<float>();
-    ra.ld_q = k;
-    ra.project = 1;
-    ra.q_pnc = qp.as<float>();
-    ra.q_norm = qn.as<float>();
-    ra.keys = dk_.as<float>();
-    ra.norm_sq = dn.as<float>();
-    ra.values = dv.as<float>();
-    ra.n = L;
-    ra.dk = k;
-    ra.dv = d;
-    ra.capacity = C;
-    ra.count = (int)count;
-    ra.tau = tau;
-    ra.top_k = (int)top_k;
-    ra.weights = wts.as<float>();
-    const bool sparse = top_k > 0 && top_k < count;
-    if (sparse) ra.out_val = mv.as<float>();
-    PSSA_RETURN_IF(pssa::launch_retrieve(st, ra));
-    if (!sparse) {
-      if (count > 0)
-      {
-        pssa::EpiParams em;
-        em.out32 = mv.as<float>();
-        em.ld32 = d;
-        PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, wts.p, C, dvt.p, C, L, d, (int)count, em));
-      }
-      else
-        PSSA_RETURN_IF(pssa::launch_fill_zero(st, mv.as<float>(), (size_t)L * d));
-    }
-    pssa::EpiParams eg;
-    eg.kind = pssa::EPI_SEGMENTS;
-    eg.seg[0] = 0;
-    eg.seg[1] = 0;
-    eg.seg[2] = d;
-    eg.seg[3] = d;
-    eg.out32 = gm.as<float>();
-    eg.ld32 = d;
-    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, dx.p, d, dwg.p, d, L, d, d, eg));
-    pssa::EpiParams ep2;
-    ep2.out32 = mp.as<float>();
-    ep2.ld32 = d;
-    PSSA_RETURN_IF(pssa::launch_gemm(st, PSSA_HIP_F32, mv.p, d, dwp.p, d, L, d, d, ep2));
-    PSSA_RETURN_IF(pssa::launch_mul(st, gm.as<float>(), mp.as<float>(), mi.as<float>(), (size_t)L * d));
-    if (q_euc) PSSA_RETURN_IF(download(q_euc, qe, (size_t)L * k * 4, st));
-    if (q_pnc) PSSA_RETURN_IF(download(q_pnc, qp, (size_t)L * k * 4, st));
-    if (q_norm) PSSA_RETURN_IF(download(q_norm, qn, (size_t)L * 4, st));
-    if (weights) PSSA_RETURN_IF(download(weights, wts, (size_t)L * C * 4, st));
-    if (m_val) PSSA_RETURN_IF(download(m_val, mv, (size_t)L * d * 4, st));
-    if (g_mem) PSSA_RETURN_IF(download(g_mem, gm, (size_t)L * d * 4, st));
-    if (m_proj) PSSA_RETURN_IF(download(m_proj, mp, (size_t)L * d * 4, st));
-    PSSA_RETURN_IF(download(m_inj, mi, (size_t)L * d * 4, st));
-    return sync(ctx);
+    DevBuf dy;
+    PSSA_RETURN_IF(upload(dy, y_ssm, seq_len * d_m * 4, ctx->stream));
+    return run_stage_memory(ctx, x_norm, dy.as<float>(), w_qx, w_qh, w_gate, w_proj, keys, norm_sq, values,
+                            seq_len, d_m, d_k, capacity, count, tau, top_k, q_euc, q_pnc, q_norm, weights, m_val,
+                            g_mem, m_proj, m_inj);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_memory_forward_after_ssm(pssa_hip_ctx* ctx, const float* x_norm, const float* w_qx,
+                                      const float* w_qh, const float* w_gate, const float* w_proj,
+                                      const float* keys, const float* norm_sq, const float* values,
+                                      size_t seq_len, size_t d_m, size_t d_k, size_t d_val, size_t capacity,
+                                      size_t count, float tau, size_t top_k, float* bar_a, float* bar_b,
+                                      float* states, float* y_ssm, float* q_euc, float* q_pnc, float* q_norm,
+                                      float* weights, float* m_val, float* g_mem, float* m_proj, float* m_inj,
+                                      char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(check_memory_args(seq_len, d_m, d_k, d_val, capacity, count, tau, top_k));
+    PSSA_RETURN_IF(need(x_norm && w_qx && w_qh && w_gate && w_proj && keys && norm_sq && values && m_inj,
+                        "memory: null input"));
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_RETURN_IF(need(ctx->ssm_tape && ctx->ssm_tape->L == seq_len && ctx->ssm_tape->d == d_m,
+                        "memory_forward_after_ssm: no resident SSM tape of this shape "
+                        "(pssa_hip_ssm_forward_resident comes first)"));
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    std::shared_ptr<SsmTape> t = std::move(ctx->ssm_tape);  // consumed by this call
+    PSSA_RETURN_IF(run_stage_memory(ctx, x_norm, t->y.as<float>(), w_qx, w_qh, w_gate, w_proj, keys, norm_sq,
+                                    values, seq_len, d_m, d_k, capacity, count, tau, top_k, q_euc, q_pnc, q_norm,
+                                    weights, m_val, g_mem, m_proj, m_inj));
+    return download_ssm(ctx, *t, bar_a, bar_b, states, y_ssm, nullptr);
   };
   return pssa::finish(body(), err, err_len);
 }

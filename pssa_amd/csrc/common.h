@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <tuple>
@@ -143,4 +144,7 @@ struct pssa_hip_ctx {
     bool current = true;
   };
   std::map<std::tuple<uintptr_t, size_t, int>, CachedWeight> weights;
+  // The SSM tape left on the device by pssa_hip_ssm_forward_resident for
+  // the next pssa_hip_memory_forward_after_ssm (opaque here).
+  std::shared_ptr<struct SsmTape> ssm_tape;
 };

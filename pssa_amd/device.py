@@ -180,6 +180,41 @@ class HipDevice:
                                               "g_mem", "m_proj", "m_inj")])
         return out
 
+    # -- GpuDispatch::ssm_forward_resident + memory_forward_after_ssm
+    #    (src/backend.rs:1186-1211, 1246-1289) --------------------------------
+    def ssm_forward_resident(self, delta, b_proj, x_norm, rates, c_proj, initial, seq_len: int, d_m: int,
+                             d_s: int) -> None:
+        args = [_f32(a).ravel() for a in (delta, b_proj, x_norm, rates, c_proj, initial)]
+        delta, b_proj, x_norm, rates, c_proj, initial = args
+        _abi.call(self._lib.pssa_hip_ssm_forward_resident, self.handle, _abi.ptr(delta), delta.size, None,
+                  _abi.ptr(b_proj), b_proj.size, _abi.ptr(x_norm), x_norm.size, _abi.ptr(rates), rates.size,
+                  _abi.ptr(c_proj), c_proj.size, _abi.ptr(initial), initial.size, seq_len, d_m, d_s)
+
+    def memory_forward_after_ssm(self, x_norm, w_qx, w_qh, w_gate, w_proj, keys, norm_sq, values,
+                                 seq_len: int, d_m: int, d_k: int, d_val: int, capacity: int, count: int,
+                                 tau: float, d_s: int, top_k: int = 0) -> dict:
+        """memory_forward on the resident tape; also returns that tape
+        (bar_a, bar_b, states, y_ssm)."""
+        args = [_f32(a).ravel() for a in (x_norm, w_qx, w_qh, w_gate, w_proj, keys, norm_sq, values)]
+        w = d_m * d_s
+        out = {
+            "bar_a": np.empty(seq_len * w, np.float32),
+            "bar_b": np.empty(seq_len * w, np.float32),
+            "states": np.empty((seq_len + 1) * w, np.float32),
+            "y_ssm": np.empty(seq_len * d_m, np.float32),
+            "q_euc": np.empty(seq_len * d_k, np.float32),
+            "q_pnc": np.empty(seq_len * d_k, np.float32),
+            "q_norm": np.empty(seq_len, np.float32),
+            "weights": np.empty(seq_len * capacity, np.float32),
+            "m_val": np.empty(seq_len * d_val, np.float32),
+            "g_mem": np.empty(seq_len * d_val, np.float32),
+            "m_proj": np.empty(seq_len * d_val, np.float32),
+            "m_inj": np.empty(seq_len * d_val, np.float32),
+        }
+        _abi.call(self._lib.pssa_hip_memory_forward_after_ssm, self.handle, *[_abi.ptr(a) for a in args],
+                  seq_len, d_m, d_k, d_val, capacity, count, tau, top_k, *[_abi.ptr(v) for v in out.values()])
+        return out
+
     # -- batched retrieve_soft_into (src/memory.rs:344-426) --------------------
     def retrieve(self, q_pnc, keys, norm_sq, values, count: int, tau: float, top_k: int = 0,
                  want_weights: bool = False):

@@ -319,6 +319,37 @@ def test_memory_forward_stage_matches_oracle(hip):
         assert rel_err(out["m_inj"].reshape(L, d), g * mp) < 1e-4
 
 
+def test_resident_ssm_then_memory_equals_the_two_stages(hip):
+    """ssm_forward_resident + memory_forward_after_ssm (src/backend.rs:
+    1186-1289) give the outputs of ssm_forward + memory_forward bit for bit;
+    the tape is consumed, and a missing or mismatched tape is an error."""
+    say("resident ssm -> memory")
+    rng = np.random.default_rng(21)
+    L, d, s, k, C = 37, 32, 24, 6, 16
+    delta = rng.uniform(0.01, 0.5, (L, d)).astype(np.float32)
+    bp, cp = rng.standard_normal((L, s)).astype(np.float32), rng.standard_normal((L, s)).astype(np.float32)
+    xn = rng.standard_normal((L, d)).astype(np.float32)
+    rates = -rng.uniform(0.1, 2.0, d * s).astype(np.float32)
+    h0 = (rng.standard_normal(d * s) * 0.1).astype(np.float32)
+    wqx, wqh = (rng.standard_normal((k, d)) * 0.1).astype(np.float32), (rng.standard_normal((k, d)) * 0.1).astype(np.float32)
+    wg, wp = (rng.standard_normal((d, d)) * 0.1).astype(np.float32), (rng.standard_normal((d, d)) * 0.1).astype(np.float32)
+    K, N, V, count = bank(C, ball(rng, 12, k), ball(rng, 12, d))
+    mem = (wqx, wqh, wg, wp, K, N, V, L, d, k, d, C, count, 0.1)
+    with pytest.raises(HipError, match="no resident SSM tape"):
+        hip.memory_forward_after_ssm(xn, *mem, d_s=s)
+    bar_a, bar_b, states, y, _ = hip.ssm_forward(delta, bp, xn, rates, cp, h0, L, d, s)
+    ref = hip.memory_forward(xn, y, *mem, top_k=4)
+    hip.ssm_forward_resident(delta[:-1], bp[:-1], xn[:-1], rates, cp[:-1], h0, L - 1, d, s)
+    with pytest.raises(HipError, match="no resident SSM tape"):
+        hip.memory_forward_after_ssm(xn, *mem, d_s=s)  # L rows against an (L-1)-row tape
+    hip.ssm_forward_resident(delta, bp, xn, rates, cp, h0, L, d, s)
+    got = hip.memory_forward_after_ssm(xn, *mem, d_s=s, top_k=4)
+    for name, want in [("bar_a", bar_a), ("bar_b", bar_b), ("states", states), ("y_ssm", y)] + list(ref.items()):
+        np.testing.assert_array_equal(got[name], want, err_msg=name)
+    with pytest.raises(HipError, match="no resident SSM tape"):
+        hip.memory_forward_after_ssm(xn, *mem, d_s=s)
+
+
 # -------------------------------------------------------------- dense scan
 @pytest.mark.parametrize("B,L,s", [(1, 1, 1), (3, 100, 5), (2, 257, 16), (4, 300, 33), (5, 200, 64),
                                    (2, 1, 64), (3, 7, 64), (2, 8, 64), (2, 9, 64), (3, 10, 64), (1, 17, 64)])

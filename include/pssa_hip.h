@@ -336,6 +336,16 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* lanes, const float* in, size_t len,
 int pssa_hip_prefill(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes, size_t seq_len,
                      float* logits_last, size_t logits_len, char* err, size_t err_len);
 
+/* prefill_inference on lanes 0..n_lanes-1 with their own prompt lengths
+ * (the ragged form of the stage API's inference row, lens[B]): lane i
+ * consumes lens[i] >= 1 ids, packed in lane order in `ids`, from its carry;
+ * logits_last [n_lanes, V] (may be NULL) receives each lane's last-token
+ * logits.  Lanes run together as in pssa_hip_prefill: a hybrid read sees
+ * token t of every lane with the ages bumped t + 1 times, and the ages end
+ * max(lens) higher. */
+int pssa_hip_prefill_ragged(pssa_hip_lanes* lanes, const uint32_t* ids, const uint64_t* lens, size_t n_lanes,
+                            float* logits_last, size_t logits_len, char* err, size_t err_len);
+
 /* forward_inference (src/pssa.rs:2387-2391): one token per lane. */
 int pssa_hip_forward_inference(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
                                float* logits, size_t logits_len, char* err, size_t err_len);

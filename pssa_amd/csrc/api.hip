@@ -1121,6 +1121,87 @@ int pssa_hip_forward_inference(pssa_hip_lanes* L, const uint32_t* ids, size_t n_
   return pssa_hip_prefill(L, ids, n_lanes, 1, logits, logits_len, err, err_len);
 }
 
+int pssa_hip_prefill_ragged(pssa_hip_lanes* L, const uint32_t* ids, const uint64_t* lens, size_t n_lanes,
+                            float* logits_last, size_t logits_len, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L && ids && lens, "null argument"));
+    PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
+    const pssa_hip_config& c = L->model->cfg;
+    const size_t V = c.d_vocab;
+    size_t tokens = 0;
+    for (size_t i = 0; i < n_lanes; ++i) {
+      PSSA_RETURN_IF(need(lens[i] > 0, "prefill requires at least one token"));
+      PSSA_RETURN_IF(need(lens[i] <= L->max_tokens, "the lanes' tokens exceed max_tokens"));
+      tokens += lens[i];
+    }
+    PSSA_RETURN_IF(need(tokens <= L->max_tokens, "the lanes' tokens exceed max_tokens"));
+    for (size_t i = 0; i < tokens; ++i)
+      if (ids[i] >= V) return Status::Invalid("prompt ID " + std::to_string(ids[i]) + " outside model vocabulary");
+    if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
+
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    const size_t cw = c.depth * c.d_latent * c.d_state;
+    // Lanes in order of decreasing length, so that the lanes still running
+    // are always a prefix (the segments of pssa_hip_batch_forward).
+    std::vector<size_t> offset(n_lanes), order(n_lanes);
+    for (size_t i = 0, o = 0; i < n_lanes; o += lens[i], ++i) offset[i] = o;
+    for (size_t i = 0; i < n_lanes; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return lens[a] > lens[b]; });
+    bool identity = true;
+    for (size_t i = 0; i < n_lanes; ++i) identity &= order[i] == i;
+    float* carry = L->carry.as<float>();
+    float* work = carry;
+    if (!identity) {
+      if (!L->carry_work.p) PSSA_RETURN_IF(L->carry_work.alloc(L->lanes * cw * 4));
+      work = L->carry_work.as<float>();
+      for (size_t i = 0; i < n_lanes; ++i)
+        PSSA_HIP_TRY(hipMemcpyAsync(work + i * cw, carry + order[i] * cw, cw * 4, hipMemcpyDeviceToDevice, st));
+    }
+    std::vector<uint32_t> ids_h(tokens);
+    struct Segment {
+      size_t T, n_active, row;
+    };
+    std::vector<Segment> segs;
+    size_t n_active = n_lanes, t0 = 0, row = 0;
+    while (n_active > 0) {
+      const size_t t1 = lens[order[n_active - 1]], T = t1 - t0;
+      for (size_t i = 0; i < n_active; ++i)
+        for (size_t t = 0; t < T; ++t) ids_h[row + i * T + t] = ids[offset[order[i]] + t0 + t];
+      segs.push_back({T, n_active, row});
+      row += n_active * T;
+      t0 = t1;
+      while (n_active > 0 && lens[order[n_active - 1]] == t1) --n_active;
+    }
+    PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids_h.data(), tokens * 4, hipMemcpyHostToDevice, st));
+    for (const Segment& sg : segs) {
+      pssa::TrainRows rows;
+      rows.ids = L->ids.as<uint32_t>() + sg.row;
+      rows.carry = work;
+      PSSA_RETURN_IF(pssa::run_prefill_segment(L, sg.n_active, sg.T, rows));
+    }
+    // Each lane's last logits sit in row (its place in length order); put
+    // carries and logits back in lane order.
+    if (!identity) {
+      DevBuf lg;
+      PSSA_RETURN_IF(lg.alloc(n_lanes * V * 4));
+      for (size_t i = 0; i < n_lanes; ++i) {
+        PSSA_HIP_TRY(hipMemcpyAsync(carry + order[i] * cw, work + i * cw, cw * 4, hipMemcpyDeviceToDevice, st));
+        PSSA_HIP_TRY(hipMemcpyAsync(lg.as<float>() + order[i] * V, L->logits.as<float>() + i * V, V * 4,
+                                    hipMemcpyDeviceToDevice, st));
+      }
+      PSSA_HIP_TRY(hipMemcpyAsync(L->logits.p, lg.p, n_lanes * V * 4, hipMemcpyDeviceToDevice, st));
+      PSSA_RETURN_IF(sync(L->ctx));  // lg is freed at return
+    }
+    L->staged_lanes = n_lanes;  // decode may continue from these logits
+    L->staged_len = 0;
+    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, size_t n_seqs, float* out_loss,
                            float* token_losses, size_t token_losses_len, float* logits, size_t logits_len,
                            char* err, size_t err_len) {

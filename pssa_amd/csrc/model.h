@@ -135,21 +135,26 @@ namespace pssa {
 // projected query, adapter output, z_final and adapter activations into the
 // lanes' tap buffers.
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps = false);
-// Rows of one training-forward segment: n_lanes lanes of T tokens.  Every
-// pointer addresses the segment's first row (lane).
+// Rows of one segment of a ragged prefill or training forward: n_lanes
+// lanes of T tokens.  Every pointer addresses the segment's first row
+// (lane).  With `logits` null only each lane's last-token logits are
+// computed, into lanes->logits rows 0..n_lanes-1.
 struct TrainRows {
-  const uint32_t* ids;      // [n_lanes * T] input ids
-  const uint32_t* targets;  // [n_lanes * T] target ids
-  const uint32_t* index;    // [n_lanes * T] packed token index of each row
-  float* logits;            // [n_lanes * T, V] scaled logits
-  float* loss;              // per-token losses, indexed by `index`
-  float* carry;             // [n_lanes, depth, d*s] carries, advanced in place
+  const uint32_t* ids = nullptr;      // [n_lanes * T] input ids
+  const uint32_t* targets = nullptr;  // [n_lanes * T] target ids
+  const uint32_t* index = nullptr;    // [n_lanes * T] packed token index of each row
+  float* logits = nullptr;            // [n_lanes * T, V] scaled logits
+  float* loss = nullptr;              // per-token losses, indexed by `index`
+  float* carry = nullptr;             // [n_lanes, depth, d*s] carries, advanced in place
 };
 // The forward of stage_embed_norm .. stage_logits_loss (src/gpu_batch.rs:
 // 445-1250) over one segment: every row gets its scaled logits and its
 // cross-entropy loss.  The hybrid read is not supported here (the
 // reference's batched stages reject it).
 Status run_train_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& tr);
+// One segment of a ragged prefill (last-token logits only; hybrid ages
+// advance T as in run_prefill).
+Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows);
 // One greedy decode step for n_lanes lanes (ids in lanes->ids, replaced by
 // the chosen ids); plastic adds the lane-ordered protected bank writes and
 // the Hebbian adapter update.  Only kernel launches: safe to capture.

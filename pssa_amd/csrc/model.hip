@@ -514,7 +514,7 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
   }
 
   PSSA_RETURN_IF(tm.mark(ST_HEAD));
-  if (tr) {
+  if (tr && tr->logits) {
     // Every row: scaled logits, then its cross-entropy loss.
     const void* hin = X;
     if (bf16) {
@@ -554,9 +554,20 @@ constexpr int kPrefillLaneGroups = 2;
 static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per lane group");
 
 static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, const TrainRows* tr);
+static Status bump_hybrid_ages(pssa_hip_lanes* L, size_t T);
+
+Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows) {
+  if (rows.logits) return Status::Invalid("prefill segment: the all-token head belongs to the training forward");
+  PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, false, &rows));
+  return bump_hybrid_ages(L, T);
+}
 
 Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
   PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, taps, nullptr));
+  return bump_hybrid_ages(L, T);
+}
+
+static Status bump_hybrid_ages(pssa_hip_lanes* L, size_t T) {
   // Every lane read each token with the ages bumped once more; store them.
   const pssa_hip_model* M = L->model;
   const int C = (int)M->cfg.mem_capacity;

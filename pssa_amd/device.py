@@ -387,6 +387,19 @@ class PSSALayer:
         self._staged = (n_lanes, T)
         return logits
 
+    def prefill_ragged(self, sequences, want_logits: bool = True):
+        """prefill_inference with its own prompt length per lane: sequences[i]
+        (a 1-D id array, at least one id) runs on lane i.  Returns the last
+        logits of every lane [n_lanes, V]."""
+        seqs = [np.ascontiguousarray(np.asarray(q).ravel(), dtype=np.uint32) for q in sequences]
+        ids = np.ascontiguousarray(np.concatenate(seqs) if seqs else np.zeros(0, np.uint32), dtype=np.uint32)
+        lens = np.array([q.size for q in seqs], np.uint64)
+        logits = np.empty((len(seqs), self.cfg.d_vocab), np.float32) if want_logits else None
+        _abi.call(self._lib.pssa_hip_prefill_ragged, self.handle, _abi.ptr(ids, C.c_uint32),
+                  _abi.ptr(lens, C.c_uint64), len(seqs), _abi.ptr(logits), 0 if logits is None else logits.size)
+        self._staged = (len(seqs), 1)
+        return logits
+
     def forward_inference(self, ids):
         """One token per lane; returns logits [n_lanes, V]."""
         ids = np.ascontiguousarray(np.atleast_1d(np.asarray(ids)), dtype=np.uint32)

@@ -195,3 +195,44 @@ def test_config3_full_length_properties(hip):
     np.testing.assert_array_equal(a, c)
     np.testing.assert_array_equal(layer.get_carry(), ca)
     layer.close()
+
+
+def test_ragged_prefill_matches_oracle_and_single_lanes(hip):
+    """Prompts of their own length per lane (the inference row's lens[B]):
+    every lane's last logits and carry against the oracle's prefill of that
+    lane alone, and bit for bit against the device's one-lane prefill; equal
+    lengths reproduce the rectangular prefill bit for bit."""
+    say("ragged prefill")
+    cfg = PSSAConfig(depth=2, d_vocab=151, d_latent=48, d_state=24, d_mem_key=8, mem_capacity=30)
+    w = ModelWeights.init(cfg, 17, "baseline")
+    w.populate_banks(18, count=25)
+    rng = np.random.default_rng(3)
+    lens = [7, 1, 70, 7, 3]
+    seqs = [rng.integers(0, cfg.d_vocab, n, dtype=np.uint32) for n in lens]
+    carry0 = (rng.standard_normal((5, cfg.depth, 48 * 24)) * 0.1).astype(np.float32)
+    layer = PSSALayer(hip, w, lanes=5, max_tokens=128)
+    layer.set_carry(carry0)
+    got = layer.prefill_ragged(seqs)
+    car = layer.get_carry()
+    om = O.OracleModel(w)
+    for i, q in enumerate(seqs):
+        st = carry0[i].copy()
+        ref = om.prefill(st, q)
+        assert rel_err(got[i], ref) < 1e-4, i
+        assert rel_err(car[i], st) < 1e-4, i
+        one = PSSALayer(hip, w, lanes=1, max_tokens=128)
+        one.set_carry(carry0[i:i + 1])
+        np.testing.assert_array_equal(one.prefill_inference(q[None])[0], got[i])
+        np.testing.assert_array_equal(one.get_carry()[0], car[i])
+        one.close()
+    ids = rng.integers(0, cfg.d_vocab, (5, 9), dtype=np.uint32)
+    layer.set_carry(carry0)
+    a = layer.prefill_ragged(list(ids))
+    layer.set_carry(carry0)
+    np.testing.assert_array_equal(layer.prefill_inference(ids), a)
+    for bad, msg in [([seqs[0], np.zeros(0, np.uint32)], "at least one token"),
+                     ([np.zeros(129, np.uint32)], "max_tokens"),
+                     ([np.array([1, 151], np.uint32)], "outside model vocabulary")]:
+        with pytest.raises(HipError, match=msg):
+            layer.prefill_ragged(bad)
+    layer.close()

@@ -401,7 +401,10 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * first step; NULL feeds the greedy choice from the last prefill's logits
  * (which must have covered the same n_lanes lanes).  out_ids [steps, n_lanes]
  * receives the generated ids; logits_last [n_lanes, V] (may be NULL) the last
- * step's logits.
+ * step's logits.  The choice applies the lanes' repetition penalty (see
+ * pssa_hip_lanes_set_repetition_penalty); non-finite logits fail the call
+ * with "model emitted non-finite logits" once its steps have run, as
+ * sample() refuses them (src/inference.rs:110-112).
  *
  * PSSA_HIP_DECODE_PLASTIC adds, after each step and block by block in lane
  * order, the refractory-protected bank write of the lane's projected query and
@@ -414,6 +417,15 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * fast weights change; its step counter advances by one per step.
  * PSSA_HIP_DECODE_GRAPH captures one step into a hipGraph (once per lane
  * count and flag set) and replays it; results equal the eager steps. */
+/* InferenceConfig::repetition_penalty for the lanes' greedy choice
+ * (sample(), src/inference.rs:113-121): before each choice the logits of the
+ * lane's last 64 consumed ids (prompt and generated, since the last
+ * pssa_hip_lanes_reset) are divided by `penalty` when positive and
+ * multiplied otherwise, once per occurrence.  1 (the default) turns it off,
+ * the benchmark's pure argmax; the reference's default is 1.25.  Must be
+ * finite and >= 1 (src/inference.rs:97-99). */
+int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* lanes, float penalty, char* err, size_t err_len);
+
 int pssa_hip_decode(pssa_hip_lanes* lanes, const uint32_t* first_ids, size_t n_lanes,
                     size_t steps, int flags, uint32_t* out_ids, size_t out_len,
                     float* logits_last, size_t logits_len, char* err, size_t err_len);

@@ -74,6 +74,7 @@ def lib() -> C.CDLL:
         "oracle_train_chunk_forward": ([vp, fp, u32p, u32p, C.c_size_t, fp], C.c_float),
         "oracle_forward_features": ([vp, fp, C.c_uint32, fp], None),
         "oracle_greedy": ([fp, C.c_size_t], C.c_uint32),
+        "oracle_sample_greedy": ([fp, C.c_size_t, u32p, C.c_size_t, C.c_float], C.c_int64),
         "oracle_dense_scan": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_int], None),
         "oracle_hebbian_update": ([fp, fp, fp, fp, C.c_size_t, C.c_size_t], None),
         "oracle_forward_taps": ([vp, fp, C.c_uint32, fp, fp, fp, fp, fp], None),
@@ -370,6 +371,15 @@ def dense_scan(a, b, h0=None, threads=1):
 def greedy(logits) -> int:
     logits = f32(logits)
     return int(lib().oracle_greedy(ptr(logits), logits.size))
+
+
+def sample_greedy(logits, history, penalty: float = 1.0) -> int:
+    """sample() at temperature 0 with the repetition penalty over the last 64
+    history ids (the caller's copy of the logits is left alone); -1 for
+    non-finite logits."""
+    lg = np.array(logits, dtype=np.float32, copy=True)
+    hist = np.ascontiguousarray(history, dtype=np.uint32)
+    return int(lib().oracle_sample_greedy(ptr(lg), lg.size, ptr(hist, C.c_uint32), hist.size, penalty))
 
 
 def dot(a, b) -> np.float32:

@@ -879,6 +879,23 @@ uint32_t oracle_greedy(const float* logits, size_t v) {
   return best;
 }
 
+// --- src/inference.rs:104-127 sample() at temperature 0 -------------------------
+int64_t oracle_sample_greedy(float* logits, size_t v, const uint32_t* hist, size_t n_hist, float penalty) {
+  for (size_t i = 0; i < v; i++)
+    if (!std::isfinite(logits[i])) return -1;
+  if (penalty > 1.0f) {
+    // Each of the last 64 ids, once per occurrence, in history order.
+    for (size_t j = n_hist > 64 ? n_hist - 64 : 0; j < n_hist; j++) {
+      float& l = logits[hist[j]];
+      if (l > 0.0f)
+        l /= penalty;
+      else
+        l *= penalty;
+    }
+  }
+  return (int64_t)oracle_greedy(logits, v);
+}
+
 void oracle_dense_scan(const float* a, const float* b, const float* h0, size_t batch, size_t L,
                        size_t s, float* h, int threads) {
   parallel_for(batch, threads, [&](size_t bi) {

@@ -186,6 +186,10 @@ void oracle_forward_features(const oracle_model* m, float* state, uint32_t id, f
 /* Greedy argmax over ids 1..V-1 in f32::total_cmp order, ties to the lower
  * id (src/inference.rs:123-127). */
 uint32_t oracle_greedy(const float* logits, size_t v);
+// sample() at temperature 0 (src/inference.rs:104-127) with the repetition
+// penalty over the last 64 history ids; logits are penalised in place.
+// Returns the id, or -1 for non-finite logits.
+int64_t oracle_sample_greedy(float* logits, size_t v, const uint32_t* hist, size_t n_hist, float penalty);
 
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t, sequential. */
 void oracle_dense_scan(const float* a, const float* b, const float* h0, size_t batch,

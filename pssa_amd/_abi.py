@@ -162,6 +162,7 @@ def lib() -> C.CDLL:
         "pssa_hip_prefill": ([vp, u32p, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_forward_inference": ([vp, u32p, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_prefill_ragged": ([vp, u32p, u64p, sz, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_ids": ([vp, u32p, sz, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_prefill_staged": ([vp, err_t, sz], C.c_int),

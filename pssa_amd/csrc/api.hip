@@ -88,6 +88,13 @@ Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_devi
   return Status::Ok();
 }
 
+// Empties every lane's repetition-penalty window (a new generation,
+// src/inference.rs:345-347).  Fill kernels, so the call may sit in a graph.
+Status clear_history(pssa_hip_lanes* L) {
+  PSSA_RETURN_IF(pssa::launch_fill_zero(L->ctx->stream, static_cast<float*>(L->hist_n.p), L->lanes));
+  return pssa::launch_fill_zero(L->ctx->stream, static_cast<float*>(L->hist_pos.p), L->lanes);
+}
+
 // The device copy of a GEMM weight (CudaContext::weight_buffer,
 // src/cuda.rs:198-227): reused while current, uploaded again when stale,
 // uploaded and kept on first use.  Called with ctx->mu held.
@@ -1034,6 +1041,11 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     const int nz = pssa::ssm_state_blocks((int)s);
     if (nz > 2) PSSA_RETURN_IF(L->Ypart.alloc((size_t)nz * n * d * 4));
     PSSA_RETURN_IF(pssa::launch_fill_zero(ctx->stream, L->carry.as<float>(), lanes * c.depth * d * s));
+    PSSA_RETURN_IF(L->hist.alloc(lanes * pssa_hip_lanes::kHist * 4));
+    PSSA_RETURN_IF(L->hist_n.alloc(lanes * 4));
+    PSSA_RETURN_IF(L->hist_pos.alloc(lanes * 4));
+    PSSA_RETURN_IF(L->nonfinite.alloc(4));
+    PSSA_RETURN_IF(clear_history(L.get()));
     PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming));
     for (int g = 0; g < pssa_hip_lanes::kMaxGroups - 1; ++g) {
       PSSA_HIP_TRY(hipStreamCreateWithFlags(&L->aux_stream[g], hipStreamNonBlocking));
@@ -1062,6 +1074,7 @@ int pssa_hip_lanes_reset(pssa_hip_lanes* L, char* err, size_t err_len) {
     const pssa_hip_config& c = L->model->cfg;
     PSSA_RETURN_IF(pssa::launch_fill_zero(L->ctx->stream, L->carry.as<float>(),
                                           L->lanes * c.depth * c.d_latent * c.d_state));
+    PSSA_RETURN_IF(clear_history(L));
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
@@ -1175,11 +1188,16 @@ int pssa_hip_prefill_ragged(pssa_hip_lanes* L, const uint32_t* ids, const uint64
       while (n_active > 0 && lens[order[n_active - 1]] == t1) --n_active;
     }
     PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids_h.data(), tokens * 4, hipMemcpyHostToDevice, st));
+    // Row i of every segment is lane order[i] (its penalty window).
+    std::vector<int> map_h(n_lanes);
+    for (size_t i = 0; i < n_lanes; ++i) map_h[i] = (int)order[i];
+    DevBuf dmap;
+    PSSA_RETURN_IF(upload(dmap, map_h.data(), n_lanes * 4, st));
     for (const Segment& sg : segs) {
       pssa::TrainRows rows;
       rows.ids = L->ids.as<uint32_t>() + sg.row;
       rows.carry = work;
-      PSSA_RETURN_IF(pssa::run_prefill_segment(L, sg.n_active, sg.T, rows));
+      PSSA_RETURN_IF(pssa::run_prefill_segment(L, sg.n_active, sg.T, rows, dmap.as<int>()));
     }
     // Each lane's last logits sit in row (its place in length order); put
     // carries and logits back in lane order.
@@ -1490,7 +1508,7 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
 
 Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   if (L->graph_exec && L->graph_lanes == n_lanes && L->graph_plastic == (plastic ? 1 : 0) &&
-      L->graph_hybrid_epoch == L->model->hybrid_epoch)
+      L->graph_hybrid_epoch == L->model->hybrid_epoch && L->graph_penalty == L->rep_penalty)
     return Status::Ok();
   if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
   if (L->graph) (void)hipGraphDestroy(L->graph);
@@ -1511,12 +1529,24 @@ Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   L->graph_lanes = n_lanes;
   L->graph_plastic = plastic ? 1 : 0;
   L->graph_hybrid_epoch = L->model->hybrid_epoch;
+  L->graph_penalty = L->rep_penalty;
   return Status::Ok();
 }
 
 }  // namespace
 
 extern "C" {
+
+int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* L, float penalty, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    PSSA_RETURN_IF(need(std::isfinite(penalty) && penalty >= 1.0f, "repetition penalty must be finite and >= 1"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    L->rep_penalty = penalty;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
 
 int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes, size_t steps,
                     int flags, uint32_t* out_ids, size_t out_len, float* logits_last,
@@ -1548,6 +1578,7 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
     PSSA_RETURN_IF(ensure_decode_buffers(L, n_lanes, steps));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(st, static_cast<float*>(L->nonfinite.p), 1));
     if (first_ids)
       PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, first_ids, n_lanes * 4, hipMemcpyHostToDevice, st));
     else
@@ -1562,9 +1593,14 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     }
     PSSA_RETURN_IF(download(out_ids, L->gen_ids, steps * n_lanes * 4, st));
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
+    int nonfinite = 0;
+    PSSA_RETURN_IF(download(&nonfinite, L->nonfinite, 4, st));
     L->staged_lanes = n_lanes;
     L->staged_len = 1;
-    return sync(L->ctx);
+    PSSA_RETURN_IF(sync(L->ctx));
+    // sample() refuses non-finite logits (src/inference.rs:110-112).
+    if (nonfinite) return Status::Invalid("model emitted non-finite logits");
+    return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);
 }

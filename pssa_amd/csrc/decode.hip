@@ -43,23 +43,81 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2
 
 constexpr int GR_CHUNK = 16;
 
+// Repetition-penalty window of the greedy choice (sample(),
+// src/inference.rs:104-127).  `append_row_id` appends the id the lane just
+// consumed (ids[row]) before the window is read.
+struct GreedyWindow {
+  uint32_t* hist = nullptr;  // [lanes, kHist] ring
+  int* hist_n = nullptr;     // [lanes] ids in the ring
+  int* hist_pos = nullptr;   // [lanes] next position
+  float penalty = 1.0f;
+  int append_row_id = 0;
+  int* nonfinite = nullptr;  // raised on any non-finite logit
+};
+
 // One workgroup per lane, one pass over the logits: greedy id over 1..V-1
-// (ties to the lower id) and the surprise logsumexp(logits) - logits[chosen]
-// from a running maximum and rescaled sum; partials meet through lane
-// shuffles and then across the four waves.
+// in f32::total_cmp order (ties to the lower id) after the repetition
+// penalty, and the surprise logsumexp(logits) - logits[chosen] of the raw
+// logits from a running maximum and rescaled sum.  The penalised ids (at
+// most 64) are left out of the pass and enter with their penalised values
+// at the end: each distinct window id is divided (positive) or multiplied
+// (otherwise) by the penalty once per occurrence, as the reference applies
+// it in window order.  Partials meet through lane shuffles and then across
+// the four waves.
 __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ logits, int V,
                                                      uint32_t* __restrict__ ids,
                                                      uint32_t* __restrict__ gen_ids,
                                                      const int* __restrict__ gen_pos, int n_lanes,
-                                                     float* __restrict__ surprise) {
+                                                     float* __restrict__ surprise, GreedyWindow gw) {
+  constexpr int H = pssa_hip_lanes::kHist;
   __shared__ int32_t sk[4];
   __shared__ int si[4];
   __shared__ float smx[4], ssm[4];
+  __shared__ uint32_t s_win[H];
+  __shared__ float s_val[H];
+  __shared__ int s_own[H];
+  __shared__ int s_n;
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* lg = logits + (size_t)row * V;
+  const bool pen = gw.penalty > 1.0f && gw.hist != nullptr;
+  if (gw.hist && tid == 0) {
+    int n = gw.hist_n[row], pos = gw.hist_pos[row];
+    if (gw.append_row_id) {
+      gw.hist[(size_t)row * H + pos] = ids[row];
+      pos = (pos + 1) % H;
+      n = n < H ? n + 1 : H;
+      gw.hist_pos[row] = pos;
+      gw.hist_n[row] = n;
+    }
+    s_n = pen ? n : 0;
+    for (int j = 0; j < n && pen; ++j) s_win[j] = gw.hist[(size_t)row * H + (pos - n + j + H) % H];
+  }
+  __syncthreads();
+  const int wn = s_n;
+  if (wave == 0 && lane < wn) {
+    const uint32_t id = s_win[lane];
+    int own = 1, c = 0;
+    for (int j = 0; j < wn; ++j)
+      if (s_win[j] == id) {
+        own &= j >= lane;
+        ++c;
+      }
+    float l = id < (uint32_t)V ? lg[id] : 0.0f;
+    if (own)
+      for (int q = 0; q < c; ++q) l = l > 0.0f ? l / gw.penalty : l * gw.penalty;
+    s_val[lane] = l;
+    s_own[lane] = own;
+  }
+  __syncthreads();
+  auto in_window = [&](int v) {
+    for (int j = 0; j < wn; ++j)
+      if (s_win[j] == (uint32_t)v) return true;
+    return false;
+  };
   int32_t bk = INT32_MIN;
   int bi = V;
   float m = -INFINITY, sacc = 0.0f;
+  int bad = 0;
   // Chunks of GR_CHUNK logits per thread are loaded together, then scanned
   // for the maximum and summed as independent exponentials.
   for (int v0 = 0; v0 < V; v0 += 256 * GR_CHUNK) {
@@ -73,7 +131,12 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
 #pragma unroll
     for (int k = 0; k < GR_CHUNK; ++k) {
       const int v = v0 + k * 256 + tid;
-      if (v >= 1 && v < V) argmax_merge(bk, bi, total_key(x[k]), v);
+      if (v < V) bad |= !isfinite(x[k]);
+      const int32_t key = total_key(x[k]);
+      if (v >= 1 && v < V && (key > bk || (key == bk && v < bi)) && !(wn && in_window(v))) {
+        bk = key;
+        bi = v;
+      }
       cm = fmaxf(cm, x[k]);
     }
     float cs = 0.0f;
@@ -83,6 +146,7 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
     }
     lse_merge(m, sacc, cm, cs);
   }
+  bad = __syncthreads_or(bad);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     argmax_merge(bk, bi, __shfl_xor(bk, off, 64), __shfl_xor(bi, off, 64));
@@ -100,10 +164,13 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
       argmax_merge(bk, bi, sk[w], si[w]);
       lse_merge(m, sacc, smx[w], ssm[w]);
     }
+    for (int j = 0; j < wn; ++j)
+      if (s_own[j] && s_win[j] >= 1u && s_win[j] < (uint32_t)V) argmax_merge(bk, bi, total_key(s_val[j]), (int)s_win[j]);
     const int best = bi < V ? bi : 0;  // V == 1 leaves no candidate
     ids[row] = (uint32_t)best;
     if (gen_ids) gen_ids[(size_t)gen_pos[0] * n_lanes + row] = (uint32_t)best;
     if (surprise) surprise[row] = (m + logf(sacc)) - lg[best];
+    if (bad && gw.nonfinite) gw.nonfinite[0] = 1;
   }
 }
 
@@ -391,8 +458,14 @@ Status init_decode_attributes() {
 Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes) {
   const hipStream_t st = L->ctx->stream;
   const int V = (int)L->model->cfg.d_vocab;
+  GreedyWindow gw;
+  gw.hist = L->hist.as<uint32_t>();
+  gw.hist_n = L->hist_n.as<int>();
+  gw.hist_pos = L->hist_pos.as<int>();
+  gw.penalty = L->rep_penalty;
+  gw.nonfinite = L->nonfinite.as<int>();
   greedy_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
-                                                   nullptr, nullptr, (int)n_lanes, nullptr);
+                                                   nullptr, nullptr, (int)n_lanes, nullptr, gw);
   PSSA_LAUNCH_CHECK("greedy");
   return Status::Ok();
 }
@@ -404,10 +477,17 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   const int d = (int)c.d_latent, k = (int)c.d_mem_key, r = (int)c.adapter_rank, C = (int)c.mem_capacity;
   const int V = (int)c.d_vocab;
   const size_t n = n_lanes;
-  PSSA_RETURN_IF(run_prefill(L, n_lanes, 1, plastic));
+  PSSA_RETURN_IF(run_prefill(L, n_lanes, 1, plastic, false));
+  GreedyWindow gw;
+  gw.hist = L->hist.as<uint32_t>();
+  gw.hist_n = L->hist_n.as<int>();
+  gw.hist_pos = L->hist_pos.as<int>();
+  gw.penalty = L->rep_penalty;
+  gw.append_row_id = 1;  // the token this step consumed
+  gw.nonfinite = L->nonfinite.as<int>();
   greedy_kernel<<<(unsigned)n, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
                                              L->gen_ids.as<uint32_t>(), L->gen_pos.as<int>(), (int)n,
-                                             L->surprise.as<float>());
+                                             L->surprise.as<float>(), gw);
   PSSA_LAUNCH_CHECK("greedy");
   if (plastic) {
     PlasticArgs p{};

@@ -96,6 +96,14 @@ struct pssa_hip_lanes {
   // [max_tokens], and a carry workspace [lanes, depth, d*s] for sequences
   // whose lanes are not 0..n-1 in length order.
   pssa::DevBuf tok_logits, tok_meta, tok_loss, carry_work;
+  // Repetition-penalty window (sample(), src/inference.rs:113-121): per lane
+  // a ring of the last kHist consumed ids (prompt and generated), its fill
+  // count and next position; the penalty (1 = off) and a flag the greedy
+  // choice raises on non-finite logits.
+  static constexpr int kHist = 64;
+  pssa::DevBuf hist, hist_n, hist_pos, nonfinite;
+  float rep_penalty = 1.0f;
+  float graph_penalty = 1.0f;
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
   hipGraph_t graph = nullptr;
@@ -134,7 +142,10 @@ namespace pssa {
 // With `taps` set (single-token decode) every block also records its
 // projected query, adapter output, z_final and adapter activations into the
 // lanes' tap buffers.
-Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps = false);
+// `append` adds each lane's consumed ids to its repetition-penalty window
+// (a decode step leaves that to the greedy choice, which appends the token
+// it consumed).
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps = false, bool append = true);
 // Rows of one segment of a ragged prefill or training forward: n_lanes
 // lanes of T tokens.  Every pointer addresses the segment's first row
 // (lane).  With `logits` null only each lane's last-token logits are
@@ -154,7 +165,11 @@ struct TrainRows {
 Status run_train_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& tr);
 // One segment of a ragged prefill (last-token logits only; hybrid ages
 // advance T as in run_prefill).
-Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows);
+Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows,
+                           const int* lane_map);
+// Appends each row's last min(T, kHist) ids of ids [n_lanes, T] to the
+// window of lane lane_map[row] (lane_map null: lane = row).
+Status launch_hist_append(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T, const int* lane_map);
 // One greedy decode step for n_lanes lanes (ids in lanes->ids, replaced by
 // the chosen ids); plastic adds the lane-ordered protected bank writes and
 // the Hebbian adapter update.  Only kernel launches: safe to capture.

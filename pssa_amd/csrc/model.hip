@@ -556,15 +556,43 @@ static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per 
 static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, const TrainRows* tr);
 static Status bump_hybrid_ages(pssa_hip_lanes* L, size_t T);
 
-Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows) {
+Status run_prefill_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const TrainRows& rows,
+                           const int* lane_map) {
   if (rows.logits) return Status::Invalid("prefill segment: the all-token head belongs to the training forward");
   PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, false, &rows));
+  PSSA_RETURN_IF(launch_hist_append(L, rows.ids, n_lanes, T, lane_map));
   return bump_hybrid_ages(L, T);
 }
 
-Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps) {
+Status run_prefill(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, bool append) {
   PSSA_RETURN_IF(prefill_groups(L, n_lanes, T, taps, nullptr));
+  if (append) PSSA_RETURN_IF(launch_hist_append(L, L->ids.as<uint32_t>(), n_lanes, T, nullptr));
   return bump_hybrid_ages(L, T);
+}
+
+// One wave per row: the row's last min(T, 64) ids go into its lane's ring.
+__global__ __launch_bounds__(64) void hist_append_kernel(uint32_t* __restrict__ hist, int* __restrict__ hist_n,
+                                                         int* __restrict__ hist_pos, const uint32_t* __restrict__ ids,
+                                                         int T, const int* __restrict__ lane_map) {
+  constexpr int H = pssa_hip_lanes::kHist;
+  const int row = blockIdx.x, j = threadIdx.x;
+  const int lane = lane_map ? lane_map[row] : row;
+  const int take = T < H ? T : H;
+  const int pos = hist_pos[lane];
+  if (j < take) hist[(size_t)lane * H + (pos + j) % H] = ids[(size_t)row * T + (T - take) + j];
+  __syncthreads();
+  if (j == 0) {
+    hist_pos[lane] = (pos + take) % H;
+    const int n = hist_n[lane] + take;
+    hist_n[lane] = n < H ? n : H;
+  }
+}
+
+Status launch_hist_append(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T, const int* lane_map) {
+  hist_append_kernel<<<(unsigned)n_lanes, 64, 0, L->ctx->stream>>>(
+      L->hist.as<uint32_t>(), L->hist_n.as<int>(), L->hist_pos.as<int>(), ids, (int)T, lane_map);
+  PSSA_LAUNCH_CHECK("hist_append");
+  return Status::Ok();
 }
 
 static Status bump_hybrid_ages(pssa_hip_lanes* L, size_t T) {

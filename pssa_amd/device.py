@@ -463,6 +463,10 @@ class PSSALayer:
         self._staged = (n_lanes, 1)
         return (out, logits) if want_logits else out
 
+    def set_repetition_penalty(self, penalty: float) -> None:
+        """InferenceConfig::repetition_penalty for the greedy choice (1 = off)."""
+        _abi.call(self._lib.pssa_hip_lanes_set_repetition_penalty, self.handle, penalty)
+
     def get_plastic(self, layer: int) -> dict:
         """One block's adapter fast weights and bank state as held on the device."""
         c = self.cfg

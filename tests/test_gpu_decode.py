@@ -184,3 +184,63 @@ def test_plastic_decode_many_lanes_and_layers_matches_oracle(hip):
         assert dev["mem_write_head"] == rb.mem_write_head
         assert rel_err(dev["adapter_up"], rb.adapter_up) < 1e-4
     layer.close()
+
+
+def oracle_penalised_decode(w, ids, steps, penalty):
+    """The reference's generate loop at temperature 0 (src/inference.rs:
+    345-391): the first token from the prefill logits, then forward + sample
+    per step, the window being the prompt and every token chosen so far."""
+    om = O.OracleModel(w)
+    out = np.zeros((steps, ids.shape[0]), np.uint32)
+    for i, prompt in enumerate(ids):
+        st = om.zero_state()
+        hist = [int(t) for t in prompt]
+        cur = O.sample_greedy(om.prefill(st, prompt), hist, penalty)
+        for s in range(steps):
+            hist.append(cur)
+            cur = O.sample_greedy(om.forward_inference(st, cur), hist, penalty)
+            out[s, i] = cur
+    return out
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decode_repetition_penalty_matches_oracle_sample(hip, graph):
+    """Greedy decode with the reference's default repetition penalty 1.25
+    against the oracle's sample() over the same windows; the penalty changes
+    the ids here, so the test is not the plain argmax again."""
+    say("decode repetition penalty, graph", graph)
+    w = small_model(seed=23)
+    ids = np.random.default_rng(7).integers(1, w.cfg.d_vocab, (3, 9), dtype=np.uint32)
+    steps = 12
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=64)
+    layer.set_repetition_penalty(1.25)
+    layer.prefill_inference(ids)
+    got = layer.decode(steps, graph=graph)
+    ref = oracle_penalised_decode(w, ids, steps, 1.25)
+    np.testing.assert_array_equal(got, ref)
+    assert not np.array_equal(ref, oracle_penalised_decode(w, ids, steps, 1.0))
+    # A reset empties the window: the same prompt gives the same ids again.
+    layer.reset_recurrent_state()
+    layer.prefill_inference(ids)
+    np.testing.assert_array_equal(layer.decode(steps, graph=graph), ref)
+    layer.set_repetition_penalty(1.0)
+    layer.reset_recurrent_state()
+    layer.prefill_inference(ids)
+    np.testing.assert_array_equal(layer.decode(steps, graph=graph), oracle_penalised_decode(w, ids, steps, 1.0))
+    layer.close()
+
+
+def test_repetition_penalty_validation_and_non_finite_logits(hip):
+    say("decode penalty validation / non-finite logits")
+    w = small_model(seed=2, depth=1)
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    for bad in (0.5, float("nan"), float("inf")):
+        with pytest.raises(HipError, match="finite and >= 1"):
+            layer.set_repetition_penalty(bad)
+    layer.close()
+    w.unembed[5] = np.nan
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    layer.prefill_inference([[1, 2], [3, 4]])
+    with pytest.raises(HipError, match="non-finite logits"):
+        layer.decode(2)
+    layer.close()

@@ -45,6 +45,7 @@ extern "C" {
 #define PSSA_HIP_ENOMEM (-3)      /* device allocation failed, nothing ran */
 #define PSSA_HIP_EDEVICE (-4)     /* HIP runtime or kernel failure: fatal */
 #define PSSA_HIP_EUNSUPPORTED (-5)
+#define PSSA_HIP_CANCELLED 1          /* pssa_hip_prefill_cancellable stopped early (not an error) */
 
 /* Weight storage types. */
 #define PSSA_HIP_F32 0
@@ -332,7 +333,10 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* lanes, const float* in, size_t len,
 /* prefill_inference (src/pssa.rs:2399-2442) on every lane: ids [lanes, seq_len]
  * continue each lane's carry; logits_last [lanes, V] receives the last
  * token's logits (may be NULL for a zero generation budget).  An id >= V
- * fails with PSSA_HIP_EINVAL before anything runs. */
+ * follows the reference (src/pssa.rs:2411-2418): each lane first consumes
+ * the ids before its first invalid one, then the call fails with "prompt ID
+ * <id> outside model vocabulary" (the first lane's) and leaves logits_last
+ * alone.  Shape errors fail before anything runs. */
 int pssa_hip_prefill(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes, size_t seq_len,
                      float* logits_last, size_t logits_len, char* err, size_t err_len);
 
@@ -345,6 +349,18 @@ int pssa_hip_prefill(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
  * max(lens) higher. */
 int pssa_hip_prefill_ragged(pssa_hip_lanes* lanes, const uint32_t* ids, const uint64_t* lens, size_t n_lanes,
                             float* logits_last, size_t logits_len, char* err, size_t err_len);
+
+/* prefill_inference with its cancellation callback (src/pssa.rs:2399-2418):
+ * `cancelled(user)` is asked before every `chunk` tokens (chunk = 1 asks
+ * before every token, as the reference does); a nonzero answer stops the
+ * prefill with PSSA_HIP_CANCELLED, the carries advanced through the
+ * *processed tokens and logits_last untouched.  Invalid ids as in
+ * pssa_hip_prefill, within the chunk they fall in.  n_lanes * min(chunk,
+ * seq_len) must fit max_tokens.  Results equal pssa_hip_prefill bit for bit. */
+typedef int (*pssa_hip_cancel_fn)(void* user);
+int pssa_hip_prefill_cancellable(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes, size_t seq_len,
+                                 size_t chunk, pssa_hip_cancel_fn cancelled, void* user, float* logits_last,
+                                 size_t logits_len, size_t* processed, char* err, size_t err_len);
 
 /* forward_inference (src/pssa.rs:2387-2391): one token per lane. */
 int pssa_hip_forward_inference(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,

@@ -793,32 +793,29 @@ void oracle_forward_features(const oracle_model* m, float* state, uint32_t id, f
 
 // --- src/pssa.rs:2393-2442 prefill_inference (tiles are bit-identical to the
 // token loop, src/pssa.rs:1885-1906; head on the last token only) ------------
-int oracle_prefill(const oracle_model* m, float* state, const uint32_t* ids, size_t n, float* logits) {
+// Prefill of one lane without storing the hybrid ages (lanes advance
+// together).  An invalid id stops it after the tokens before it
+// (src/pssa.rs:2411-2418): *done is the count processed, logits untouched.
+static int prefill_lane(const oracle_model* m, float* state, const uint32_t* ids, size_t n, float* logits,
+                        size_t* done) {
+  *done = 0;
   if (n == 0) return -1;
-  for (size_t t = 0; t < n; t++)
-    if (ids[t] >= m->cfg.d_vocab) return -2;
   Runner run(m);
   for (size_t t = 0; t < n; t++) {
+    if (ids[t] >= m->cfg.d_vocab) return -2;
     run.set_age_add(t + 1);
     run.features(state, ids[t]);
+    *done = t + 1;
   }
-  bump_hybrid(m, n);
   if (logits) run.logits(logits);
   return 0;
 }
 
-// Prefill of one lane without storing the hybrid ages (lanes advance together).
-static int prefill_lane(const oracle_model* m, float* state, const uint32_t* ids, size_t n, float* logits) {
-  if (n == 0) return -1;
-  for (size_t t = 0; t < n; t++)
-    if (ids[t] >= m->cfg.d_vocab) return -2;
-  Runner run(m);
-  for (size_t t = 0; t < n; t++) {
-    run.set_age_add(t + 1);
-    run.features(state, ids[t]);
-  }
-  if (logits) run.logits(logits);
-  return 0;
+int oracle_prefill(const oracle_model* m, float* state, const uint32_t* ids, size_t n, float* logits) {
+  size_t done = 0;
+  const int rc = prefill_lane(m, state, ids, n, logits, &done);
+  bump_hybrid(m, done);
+  return rc;
 }
 
 int oracle_prefill_lanes(const oracle_model* m, float* states, const uint32_t* ids, size_t lanes,
@@ -826,11 +823,15 @@ int oracle_prefill_lanes(const oracle_model* m, float* states, const uint32_t* i
   const oracle_config& c = m->cfg;
   size_t per = c.depth * c.d_latent * c.d_state;
   std::atomic<int> rc(0);
+  std::vector<size_t> done(lanes, 0);
   parallel_for(lanes, threads, [&](size_t l) {
-    int r = prefill_lane(m, states + l * per, ids + l * n, n, logits ? logits + l * c.d_vocab : nullptr);
+    int r = prefill_lane(m, states + l * per, ids + l * n, n, logits ? logits + l * c.d_vocab : nullptr, &done[l]);
     if (r) rc = r;
   });
-  if (rc.load() == 0) bump_hybrid(m, n);
+  // The lanes' tokens t read ages + t + 1; the ages end the longest prefix higher.
+  size_t most = 0;
+  for (size_t d : done) most = d > most ? d : most;
+  bump_hybrid(m, most);
   return rc.load();
 }
 

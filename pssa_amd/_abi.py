@@ -75,6 +75,11 @@ class Weights(C.Structure):
     ]
 
 
+# pssa_hip_cancel_fn: int (*)(void* user)
+CANCEL_FN = C.CFUNCTYPE(C.c_int, C.c_void_p)
+CANCELLED = 1
+
+
 class WeightKey(C.Structure):
     """pssa_hip_weight_key: (host address, element count) of a cached weight."""
     _fields_ = [("ptr", C.c_void_p), ("len", C.c_size_t)]
@@ -162,6 +167,8 @@ def lib() -> C.CDLL:
         "pssa_hip_prefill": ([vp, u32p, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_forward_inference": ([vp, u32p, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_prefill_ragged": ([vp, u32p, u64p, sz, fp, sz, err_t, sz], C.c_int),
+        "pssa_hip_prefill_cancellable": ([vp, u32p, sz, sz, sz, CANCEL_FN, vp, fp, sz, C.POINTER(sz), err_t, sz],
+                                         C.c_int),
         "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_ids": ([vp, u32p, sz, sz, err_t, sz], C.c_int),

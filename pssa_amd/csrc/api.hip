@@ -1113,14 +1113,21 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* L, const float* in, size_t len, cha
   return pssa::finish(body(), err, err_len);
 }
 
+static Status invalid_prefix_locked(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T);
+
 int pssa_hip_prefill(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
                      float* logits_last, size_t logits_len, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
     const size_t V = L->model->cfg.d_vocab;
     if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
+    PSSA_RETURN_IF(need(ids != nullptr, "null ids"));
+    PSSA_RETURN_IF(need(seq_len > 0, "prefill requires at least one token"));
+    PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
+    PSSA_RETURN_IF(need(n_lanes * seq_len <= L->max_tokens, "n_lanes*seq_len exceeds max_tokens"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    PSSA_RETURN_IF(invalid_prefix_locked(L, ids, n_lanes, seq_len));
     PSSA_RETURN_IF(stage_ids_locked(L, ids, n_lanes, seq_len));
     PSSA_RETURN_IF(pssa::run_prefill(L, n_lanes, seq_len));
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
@@ -1134,13 +1141,108 @@ int pssa_hip_forward_inference(pssa_hip_lanes* L, const uint32_t* ids, size_t n_
   return pssa_hip_prefill(L, ids, n_lanes, 1, logits, logits_len, err, err_len);
 }
 
+// Ragged prefill with L->ctx->mu held: lane i consumes lens[i] ids (0 leaves
+// the lane untouched), packed in lane order.  Each lane's last-token logits
+// end in row i of lanes->logits (lanes of length 0: undefined).
+static Status ragged_locked(pssa_hip_lanes* L, const uint32_t* ids, const uint64_t* lens, size_t n_lanes) {
+  const pssa_hip_config& c = L->model->cfg;
+  const size_t V = c.d_vocab;
+  const hipStream_t st = L->ctx->stream;
+  const size_t cw = c.depth * c.d_latent * c.d_state;
+  size_t tokens = 0;
+  for (size_t i = 0; i < n_lanes; ++i) tokens += lens[i];
+  if (tokens == 0) return Status::Ok();
+  // Lanes in order of decreasing length, so that the lanes still running
+  // are always a prefix (the segments of pssa_hip_batch_forward).
+  std::vector<size_t> offset(n_lanes), order(n_lanes);
+  for (size_t i = 0, o = 0; i < n_lanes; o += lens[i], ++i) offset[i] = o;
+  for (size_t i = 0; i < n_lanes; ++i) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return lens[a] > lens[b]; });
+  size_t n_active = 0;
+  while (n_active < n_lanes && lens[order[n_active]] > 0) ++n_active;
+  bool identity = true;
+  for (size_t i = 0; i < n_active; ++i) identity &= order[i] == i;
+  float* carry = L->carry.as<float>();
+  float* work = carry;
+  if (!identity) {
+    if (!L->carry_work.p) PSSA_RETURN_IF(L->carry_work.alloc(L->lanes * cw * 4));
+    work = L->carry_work.as<float>();
+    for (size_t i = 0; i < n_active; ++i)
+      PSSA_HIP_TRY(hipMemcpyAsync(work + i * cw, carry + order[i] * cw, cw * 4, hipMemcpyDeviceToDevice, st));
+  }
+  std::vector<uint32_t> ids_h(tokens);
+  struct Segment {
+    size_t T, n_active, row;
+  };
+  std::vector<Segment> segs;
+  size_t t0 = 0, row = 0;
+  while (n_active > 0) {
+    const size_t t1 = lens[order[n_active - 1]], T = t1 - t0;
+    for (size_t i = 0; i < n_active; ++i)
+      for (size_t t = 0; t < T; ++t) ids_h[row + i * T + t] = ids[offset[order[i]] + t0 + t];
+    segs.push_back({T, n_active, row});
+    row += n_active * T;
+    t0 = t1;
+    while (n_active > 0 && lens[order[n_active - 1]] == t1) --n_active;
+  }
+  PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids_h.data(), tokens * 4, hipMemcpyHostToDevice, st));
+  // Row i of every segment is lane order[i] (its penalty window).
+  std::vector<int> map_h(n_lanes);
+  for (size_t i = 0; i < n_lanes; ++i) map_h[i] = (int)order[i];
+  DevBuf dmap, lg;
+  PSSA_RETURN_IF(upload(dmap, map_h.data(), n_lanes * 4, st));
+  for (const Segment& sg : segs) {
+    pssa::TrainRows rows;
+    rows.ids = L->ids.as<uint32_t>() + sg.row;
+    rows.carry = work;
+    PSSA_RETURN_IF(pssa::run_prefill_segment(L, sg.n_active, sg.T, rows, dmap.as<int>()));
+  }
+  // Each lane's last logits sit in row (its place in length order); put
+  // carries and logits back in lane order.
+  if (!identity) {
+    PSSA_RETURN_IF(lg.alloc(n_lanes * V * 4));
+    for (size_t i = 0; i < n_lanes; ++i) {
+      if (lens[order[i]] == 0) continue;
+      PSSA_HIP_TRY(hipMemcpyAsync(carry + order[i] * cw, work + i * cw, cw * 4, hipMemcpyDeviceToDevice, st));
+      PSSA_HIP_TRY(hipMemcpyAsync(lg.as<float>() + order[i] * V, L->logits.as<float>() + i * V, V * 4,
+                                  hipMemcpyDeviceToDevice, st));
+    }
+    PSSA_HIP_TRY(hipMemcpyAsync(L->logits.p, lg.p, n_lanes * V * 4, hipMemcpyDeviceToDevice, st));
+  }
+  return sync(L->ctx);  // the staging vectors and buffers above are freed at return
+}
+
+// Ids [n_lanes, T] after the reference's rule for invalid ids (src/pssa.rs:
+// 2411-2418: every token before the first invalid one is processed, then the
+// call fails and leaves the logits alone), with L->ctx->mu held.  Returns
+// Ok when every id is valid (nothing run); otherwise advances each lane
+// through its valid prefix and returns the error of the first invalid id.
+static Status invalid_prefix_locked(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t T) {
+  const uint32_t V = (uint32_t)L->model->cfg.d_vocab;
+  std::vector<uint64_t> lens(n_lanes);
+  bool all = true;
+  uint32_t first_bad = 0;
+  for (size_t i = 0; i < n_lanes; ++i) {
+    size_t v = 0;
+    while (v < T && ids[i * T + v] < V) ++v;
+    lens[i] = v;
+    if (v < T && all) first_bad = ids[i * T + v];
+    all &= v == T;
+  }
+  if (all) return Status::Ok();
+  std::vector<uint32_t> packed;
+  for (size_t i = 0; i < n_lanes; ++i) packed.insert(packed.end(), ids + i * T, ids + i * T + lens[i]);
+  PSSA_RETURN_IF(ragged_locked(L, packed.data(), lens.data(), n_lanes));
+  L->staged_lanes = L->staged_len = 0;
+  return Status::Invalid("prompt ID " + std::to_string(first_bad) + " outside model vocabulary");
+}
+
 int pssa_hip_prefill_ragged(pssa_hip_lanes* L, const uint32_t* ids, const uint64_t* lens, size_t n_lanes,
                             float* logits_last, size_t logits_len, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L && ids && lens, "null argument"));
     PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
-    const pssa_hip_config& c = L->model->cfg;
-    const size_t V = c.d_vocab;
+    const size_t V = L->model->cfg.d_vocab;
     size_t tokens = 0;
     for (size_t i = 0; i < n_lanes; ++i) {
       PSSA_RETURN_IF(need(lens[i] > 0, "prefill requires at least one token"));
@@ -1151,73 +1253,58 @@ int pssa_hip_prefill_ragged(pssa_hip_lanes* L, const uint32_t* ids, const uint64
     for (size_t i = 0; i < tokens; ++i)
       if (ids[i] >= V) return Status::Invalid("prompt ID " + std::to_string(ids[i]) + " outside model vocabulary");
     if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
-
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
-    const hipStream_t st = L->ctx->stream;
-    const size_t cw = c.depth * c.d_latent * c.d_state;
-    // Lanes in order of decreasing length, so that the lanes still running
-    // are always a prefix (the segments of pssa_hip_batch_forward).
-    std::vector<size_t> offset(n_lanes), order(n_lanes);
-    for (size_t i = 0, o = 0; i < n_lanes; o += lens[i], ++i) offset[i] = o;
-    for (size_t i = 0; i < n_lanes; ++i) order[i] = i;
-    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return lens[a] > lens[b]; });
-    bool identity = true;
-    for (size_t i = 0; i < n_lanes; ++i) identity &= order[i] == i;
-    float* carry = L->carry.as<float>();
-    float* work = carry;
-    if (!identity) {
-      if (!L->carry_work.p) PSSA_RETURN_IF(L->carry_work.alloc(L->lanes * cw * 4));
-      work = L->carry_work.as<float>();
-      for (size_t i = 0; i < n_lanes; ++i)
-        PSSA_HIP_TRY(hipMemcpyAsync(work + i * cw, carry + order[i] * cw, cw * 4, hipMemcpyDeviceToDevice, st));
-    }
-    std::vector<uint32_t> ids_h(tokens);
-    struct Segment {
-      size_t T, n_active, row;
-    };
-    std::vector<Segment> segs;
-    size_t n_active = n_lanes, t0 = 0, row = 0;
-    while (n_active > 0) {
-      const size_t t1 = lens[order[n_active - 1]], T = t1 - t0;
-      for (size_t i = 0; i < n_active; ++i)
-        for (size_t t = 0; t < T; ++t) ids_h[row + i * T + t] = ids[offset[order[i]] + t0 + t];
-      segs.push_back({T, n_active, row});
-      row += n_active * T;
-      t0 = t1;
-      while (n_active > 0 && lens[order[n_active - 1]] == t1) --n_active;
-    }
-    PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, ids_h.data(), tokens * 4, hipMemcpyHostToDevice, st));
-    // Row i of every segment is lane order[i] (its penalty window).
-    std::vector<int> map_h(n_lanes);
-    for (size_t i = 0; i < n_lanes; ++i) map_h[i] = (int)order[i];
-    DevBuf dmap;
-    PSSA_RETURN_IF(upload(dmap, map_h.data(), n_lanes * 4, st));
-    for (const Segment& sg : segs) {
-      pssa::TrainRows rows;
-      rows.ids = L->ids.as<uint32_t>() + sg.row;
-      rows.carry = work;
-      PSSA_RETURN_IF(pssa::run_prefill_segment(L, sg.n_active, sg.T, rows, dmap.as<int>()));
-    }
-    // Each lane's last logits sit in row (its place in length order); put
-    // carries and logits back in lane order.
-    if (!identity) {
-      DevBuf lg;
-      PSSA_RETURN_IF(lg.alloc(n_lanes * V * 4));
-      for (size_t i = 0; i < n_lanes; ++i) {
-        PSSA_HIP_TRY(hipMemcpyAsync(carry + order[i] * cw, work + i * cw, cw * 4, hipMemcpyDeviceToDevice, st));
-        PSSA_HIP_TRY(hipMemcpyAsync(lg.as<float>() + order[i] * V, L->logits.as<float>() + i * V, V * 4,
-                                    hipMemcpyDeviceToDevice, st));
-      }
-      PSSA_HIP_TRY(hipMemcpyAsync(L->logits.p, lg.p, n_lanes * V * 4, hipMemcpyDeviceToDevice, st));
-      PSSA_RETURN_IF(sync(L->ctx));  // lg is freed at return
-    }
+    PSSA_RETURN_IF(ragged_locked(L, ids, lens, n_lanes));
     L->staged_lanes = n_lanes;  // decode may continue from these logits
     L->staged_len = 0;
-    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
+    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_prefill_cancellable(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, size_t seq_len,
+                                 size_t chunk, pssa_hip_cancel_fn cancelled, void* user, float* logits_last,
+                                 size_t logits_len, size_t* processed, char* err, size_t err_len) {
+  bool was_cancelled = false;
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr && ids != nullptr, "null argument"));
+    PSSA_RETURN_IF(need(seq_len > 0, "prefill requires at least one token"));
+    PSSA_RETURN_IF(need(n_lanes > 0 && n_lanes <= L->lanes, "n_lanes must be in 1..=lanes"));
+    PSSA_RETURN_IF(need(chunk > 0, "chunk must be positive"));
+    const size_t c = std::min(chunk, seq_len);
+    PSSA_RETURN_IF(need(n_lanes * c <= L->max_tokens, "n_lanes*chunk exceeds max_tokens"));
+    const size_t V = L->model->cfg.d_vocab;
+    if (logits_last) PSSA_RETURN_IF(need(logits_len == n_lanes * V, "logits length must be n_lanes*d_vocab"));
+    if (processed) *processed = 0;
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    std::vector<uint32_t> part(n_lanes * c);
+    for (size_t t0 = 0; t0 < seq_len; t0 += c) {
+      // The reference asks before every token (src/pssa.rs:2412-2415); here
+      // before every chunk of `chunk` tokens (1: every token).
+      if (cancelled && cancelled(user)) {
+        was_cancelled = true;
+        L->staged_lanes = L->staged_len = 0;
+        return Status::Ok();
+      }
+      const size_t T = std::min(c, seq_len - t0);
+      for (size_t i = 0; i < n_lanes; ++i)
+        std::memcpy(&part[i * T], ids + i * seq_len + t0, T * 4);
+      PSSA_RETURN_IF(invalid_prefix_locked(L, part.data(), n_lanes, T));
+      PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, part.data(), n_lanes * T * 4, hipMemcpyHostToDevice, L->ctx->stream));
+      PSSA_RETURN_IF(pssa::run_prefill(L, n_lanes, T));
+      PSSA_RETURN_IF(sync(L->ctx));  // `part` is refilled next
+      if (processed) *processed = t0 + T;
+    }
+    L->staged_lanes = n_lanes;
+    L->staged_len = 0;
+    if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
+    return sync(L->ctx);
+  };
+  const int rc = pssa::finish(body(), err, err_len);
+  return rc == PSSA_HIP_OK && was_cancelled ? PSSA_HIP_CANCELLED : rc;
 }
 
 int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, size_t n_seqs, float* out_loss,

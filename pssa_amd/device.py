@@ -387,6 +387,27 @@ class PSSALayer:
         self._staged = (n_lanes, T)
         return logits
 
+    def prefill_cancellable(self, token_ids, cancelled, chunk: int = 1, want_logits: bool = True):
+        """prefill_inference with the reference's cancellation callback
+        (src/pssa.rs:2399-2418): `cancelled()` is asked before every `chunk`
+        tokens.  Returns (finished, processed tokens per lane, logits or None);
+        on cancellation the logits are not produced."""
+        ids = np.ascontiguousarray(np.atleast_2d(np.asarray(token_ids)), dtype=np.uint32)
+        n_lanes, T = ids.shape
+        logits = np.empty((n_lanes, self.cfg.d_vocab), np.float32) if want_logits else None
+        cb = _abi.CANCEL_FN(lambda _user: 1 if cancelled() else 0)
+        done = C.c_size_t(0)
+        buf = C.create_string_buffer(1024)
+        rc = self._lib.pssa_hip_prefill_cancellable(
+            self.handle, _abi.ptr(ids, C.c_uint32), n_lanes, T, chunk, cb, None, _abi.ptr(logits),
+            0 if logits is None else logits.size, C.byref(done), buf, C.sizeof(buf))
+        if rc == _abi.CANCELLED:
+            return False, int(done.value), None
+        if rc != _abi.OK:
+            raise _abi.HipError(rc, buf.value.decode(errors="replace"))
+        self._staged = (n_lanes, T)
+        return True, int(done.value), logits
+
     def prefill_ragged(self, sequences, want_logits: bool = True):
         """prefill_inference with its own prompt length per lane: sequences[i]
         (a 1-D id array, at least one id) runs on lane i.  Returns the last

@@ -134,23 +134,97 @@ def test_scan_variants_keep_token_loop_identity(hip):
     b.close()
 
 
-def test_invalid_ids_fail_before_anything_runs(hip):
-    say("invalid ids")
+def test_shape_errors_fail_before_anything_runs(hip):
+    say("prefill shape errors")
     cfg = PSSAConfig(depth=1, d_vocab=10, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=4)
     w = ModelWeights.init(cfg, 1, "baseline")
     layer = PSSALayer(hip, w, lanes=1, max_tokens=8)
     layer.prefill_inference([[1, 2]])
     before = layer.get_carry()
-    with pytest.raises(HipError, match="outside model vocabulary"):
-        layer.prefill_inference([[3, 10]])
-    np.testing.assert_array_equal(layer.get_carry(), before)
     with pytest.raises(HipError, match="at least one token"):
         layer.prefill_inference(np.zeros((1, 0), np.uint32))
     with pytest.raises(HipError, match="max_tokens"):
         layer.prefill_inference(np.ones((1, 9), np.uint32))
+    np.testing.assert_array_equal(layer.get_carry(), before)
     layer.reset_recurrent_state()
     assert not layer.get_carry().any()
     layer.close()
+
+
+def prefix_fixture():
+    cfg = PSSAConfig(depth=2, d_vocab=37, d_latent=16, d_state=8, d_mem_key=4, mem_capacity=8)
+    w = ModelWeights.init(cfg, 23, "baseline")
+    w.populate_banks(5, 6)
+    return w
+
+
+def test_prefill_cancellation_and_invalid_ids_keep_the_processed_prefix(hip):
+    """src/inference.rs:1114-1160 on the device: a prefill cancelled at the
+    check before token `stop` (asked before every token) or stopped by an
+    invalid id at `stop` leaves the carry where a token loop over ids[:stop]
+    leaves it, and produces no logits."""
+    say("prefill cancellation / invalid-id prefix")
+    w = prefix_fixture()
+    ids = np.array([[t % 37 for t in range(67)]], np.uint32)
+    for stop in (0, 1, 31, 32, 33, 66):
+        ref = PSSALayer(hip, w, lanes=1, max_tokens=128)
+        for t in ids[0, :stop]:
+            ref.forward_inference([t])
+        layer = PSSALayer(hip, w, lanes=1, max_tokens=128)
+        checks = [0]
+
+        def cancelled():
+            checks[0] += 1
+            return checks[0] - 1 == stop
+
+        done, processed, lg = layer.prefill_cancellable(ids, cancelled, chunk=1)
+        assert (done, processed, lg, checks[0]) == (False, stop, None, stop + 1)
+        np.testing.assert_array_equal(layer.get_carry(), ref.get_carry())
+        bad = ids.copy()
+        bad[0, stop] = 37
+        inv = PSSALayer(hip, w, lanes=1, max_tokens=128)
+        with pytest.raises(HipError, match="prompt ID 37 outside model vocabulary"):
+            inv.prefill_inference(bad)
+        np.testing.assert_array_equal(inv.get_carry(), ref.get_carry())
+        for x in (ref, layer, inv):
+            x.close()
+
+
+def test_invalid_ids_advance_each_lane_through_its_own_prefix(hip):
+    """Lanes stop at their own first invalid id; the error names the first
+    lane's; every lane equals its one-lane prefill of the valid prefix, bit
+    for bit, and the oracle's lanes."""
+    say("invalid-id prefixes over lanes")
+    w = prefix_fixture()
+    ids = np.array([[1, 2, 3, 4], [5, 37, 6, 7], [8, 9, 10, 40]], np.uint32)
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=16)
+    with pytest.raises(HipError, match="prompt ID 37 outside model vocabulary"):
+        layer.prefill_inference(ids)
+    car = layer.get_carry()
+    for lane, n in enumerate((4, 1, 3)):
+        one = PSSALayer(hip, w, lanes=1, max_tokens=16)
+        one.prefill_inference(ids[lane:lane + 1, :n])
+        np.testing.assert_array_equal(car[lane], one.get_carry()[0])
+        one.close()
+    states = O.OracleModel(w).zero_state(3)
+    with pytest.raises(ValueError):
+        O.OracleModel(w).prefill_lanes(states, ids)
+    assert rel_err(car, states) < 1e-4
+    layer.close()
+
+
+def test_chunked_cancellable_prefill_equals_prefill(hip):
+    say("chunked prefill == prefill")
+    w = prefix_fixture()
+    ids = np.random.default_rng(4).integers(0, 37, (2, 67), dtype=np.uint32)
+    a = PSSALayer(hip, w, lanes=2, max_tokens=256)
+    b = PSSALayer(hip, w, lanes=2, max_tokens=256)
+    done, processed, lg = a.prefill_cancellable(ids, lambda: False, chunk=8)
+    assert done and processed == 67
+    np.testing.assert_array_equal(lg, b.prefill_inference(ids))
+    np.testing.assert_array_equal(a.get_carry(), b.get_carry())
+    a.close()
+    b.close()
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])

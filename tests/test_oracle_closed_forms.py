@@ -308,6 +308,20 @@ def test_oracle_prefill_equals_token_loop_and_lanes():
         np.testing.assert_array_equal(st, states[lane])
     with pytest.raises(ValueError):
         om.prefill(om.zero_state(), [1, 50])
+    # An invalid id stops the prefill after the tokens before it
+    # (src/inference.rs:1114-1160); the lanes each keep their own prefix.
+    st, ref = om.zero_state(), om.zero_state()
+    om.forward_inference(ref, 1, logits=False)
+    with pytest.raises(ValueError):
+        om.prefill(st, [1, 50, 3])
+    np.testing.assert_array_equal(st, ref)
+    states = om.zero_state(2)
+    with pytest.raises(ValueError):
+        om.prefill_lanes(states, np.array([[4, 9], [50, 2]], np.uint32))
+    ref = om.zero_state()
+    om.prefill(ref, [4, 9])
+    np.testing.assert_array_equal(states[0], ref)
+    assert not states[1].any()
 
 
 def test_product_baseline_init_matches_oracle():

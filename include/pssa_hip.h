@@ -104,6 +104,7 @@ typedef struct {
   uint64_t* mem_hybrid_age;   /* [C] memory.hybrid_age; NULL reads as 0     */
   uint32_t mem_hybrid_enabled; /*    memory.hybrid_enabled                  */
   float mem_hybrid_lam;        /*    memory.hybrid_lam, in (0, 1]           */
+  uint64_t mem_top_k;          /*    memory.top_k (runtime-only), 0 = full read */
 } pssa_hip_block;
 
 /* Host view of PSSALayerV2's inference parameters (src/pssa.rs:1920-1960). */
@@ -468,6 +469,12 @@ int pssa_hip_model_get_plastic(pssa_hip_model* model, size_t layer, float* adapt
  * (gated writes: to that gate) and its age to 0 (src/memory.rs:300-301). */
 int pssa_hip_model_set_hybrid_read(pssa_hip_model* model, int enabled, float lam, char* err,
                                    size_t err_len);
+
+/* set_memory_top_k (src/pssa.rs:2215-2226) on every block: each read keeps
+ * the top_k nearest slots by (distance bits, slot) and renormalises over
+ * them (retrieve_soft_into, src/memory.rs:380-407); 0 = the full read (the
+ * reference's None).  At most 64 here. */
+int pssa_hip_model_set_memory_top_k(pssa_hip_model* model, size_t top_k, char* err, size_t err_len);
 
 /* Reads one block's hybrid-read state back from the device: gate [C] and
  * age [C] (either may be NULL). */

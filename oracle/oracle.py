@@ -339,6 +339,7 @@ class _OracleBlock(C.Structure):
         ("mem_hybrid_age", C.POINTER(C.c_uint64)),
         ("mem_hybrid_enabled", C.c_uint32),
         ("mem_hybrid_lam", C.c_float),
+        ("mem_top_k", C.c_uint64),
     ]
 
 

@@ -370,11 +370,11 @@ void block_forward(const oracle_block& b, const oracle_config& c, Scratch& sc, f
   project(sc.qe.data(), sc.qp.data(), k);
   if (b.mem_hybrid_enabled)  // src/pssa.rs:1153-1162 (the ages are bumped by the caller)
     retrieve_hybrid(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
-                    sc.qp.data(), c.tau_mem, 0, b.mem_hybrid_gate, b.mem_hybrid_age, sc.age_add,
+                    sc.qp.data(), c.tau_mem, b.mem_top_k, b.mem_hybrid_gate, b.mem_hybrid_age, sc.age_add,
                     b.mem_hybrid_lam, sc.mval.data(), sc.mw.data(), nullptr);
   else
     retrieve(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
-             sc.qp.data(), c.tau_mem, 0, sc.mval.data(), sc.mw.data(), nullptr);
+             sc.qp.data(), c.tau_mem, b.mem_top_k, sc.mval.data(), sc.mw.data(), nullptr);
   matvec(b.w_gate, d, d, sc.xn.data(), sc.g.data());
   for (size_t i = 0; i < d; i++) sc.g[i] = sigmoid(sc.g[i]);
   matvec(b.w_proj, d, d, sc.mval.data(), sc.mp.data());

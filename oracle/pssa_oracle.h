@@ -88,6 +88,7 @@ typedef struct {
   uint64_t* mem_hybrid_age;  /* [C] or NULL (reads as 0) */
   uint32_t mem_hybrid_enabled;
   float mem_hybrid_lam;
+  uint64_t mem_top_k; /* memory.top_k, 0 = full read (src/memory.rs:102-108) */
 } oracle_block;
 
 typedef struct {

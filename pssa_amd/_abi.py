@@ -63,6 +63,7 @@ class Block(C.Structure):
         ("mem_hybrid_age", u64p),
         ("mem_hybrid_enabled", C.c_uint32),
         ("mem_hybrid_lam", C.c_float),
+        ("mem_top_k", C.c_uint64),
     ]
 
 
@@ -170,6 +171,7 @@ def lib() -> C.CDLL:
         "pssa_hip_prefill_cancellable": ([vp, u32p, sz, sz, sz, CANCEL_FN, vp, fp, sz, C.POINTER(sz), err_t, sz],
                                          C.c_int),
         "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
+        "pssa_hip_model_set_memory_top_k": ([vp, sz, err_t, sz], C.c_int),
         "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_ids": ([vp, u32p, sz, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_prefill_staged": ([vp, err_t, sz], C.c_int),

@@ -905,6 +905,7 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
                               b.mem_values && b.mem_norm_sq,
                           "weights: null block tensor"));
       PSSA_RETURN_IF(need(b.mem_count <= C, "memory count exceeds capacity"));
+      PSSA_RETURN_IF(need(b.mem_top_k <= (uint64_t)pssa::kMaxTopK, "memory top-k above 64 is not supported"));
       if (b.mem_hybrid_enabled)
         PSSA_RETURN_IF(need(std::isfinite(b.mem_hybrid_lam) && b.mem_hybrid_lam > 0.0f && b.mem_hybrid_lam <= 1.0f,
                             "hybrid decay lam must be in (0.0, 1.0]"));
@@ -972,6 +973,7 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
         for (size_t q = 0; q < C; ++q) ha[q] = b.mem_hybrid_age[q];
       B.hybrid = b.mem_hybrid_enabled != 0;
       B.lam = b.mem_hybrid_lam;
+      B.top_k = (int)b.mem_top_k;
       PSSA_RETURN_IF(upload(B.hgate, hg.data(), C * 4, st));
       PSSA_RETURN_IF(upload(B.hage, ha.data(), C * 8, st));
       PSSA_RETURN_IF(upload(B.conf, conf.data(), C * 4, st));
@@ -1532,6 +1534,18 @@ int pssa_hip_model_set_hybrid_read(pssa_hip_model* M, int enabled, float lam, ch
       B.hybrid = enabled != 0;
       B.lam = lam;
     }
+    ++M->hybrid_epoch;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_model_set_memory_top_k(pssa_hip_model* M, size_t top_k, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(M != nullptr, "null model"));
+    PSSA_RETURN_IF(need(top_k <= (size_t)pssa::kMaxTopK, "memory top-k above 64 is not supported"));
+    std::lock_guard<std::mutex> g(M->ctx->mu);
+    for (pssa::DevBlock& B : M->blocks) B.top_k = (int)top_k;
     ++M->hybrid_epoch;
     return Status::Ok();
   };

@@ -33,6 +33,7 @@ struct DevBlock {
   DevBuf hage;     // [C] u64 memory.hybrid_age
   bool hybrid = false;
   float lam = 1.0f;
+  int top_k = 0;  // memory.top_k (src/memory.rs:102-108), 0 = full read
 };
 
 // Stage ids used for per-kernel timing.
@@ -64,8 +65,8 @@ struct pssa_hip_model {
   pssa::DevBuf unembed;  // [V, d] weight dtype
   std::vector<pssa::DevBlock> blocks;
   pssa::DevBuf step;     // u64: step counter read by the refractory gate in plastic decode
-  // Advances on every set_hybrid_read, so that a captured decode step built
-  // for another hybrid setting is captured again.
+  // Advances on every set_hybrid_read / set_memory_top_k, so that a captured
+  // decode step built for other read settings is captured again.
   uint64_t hybrid_epoch = 0;
 };
 

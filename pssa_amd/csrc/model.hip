@@ -439,6 +439,7 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     ra.count = C;  // upper bound; the live count is read on the device
     ra.count_dev = B.meta.as<int>();
     ra.tau = c.tau_mem;
+    ra.top_k = B.top_k;
     if (taps) ra.q_pnc = L->tap_q.as<float>() + l * rows * k;
     if (B.hybrid) {  // token t reads with the ages bumped t + 1 times
       ra.hgate = B.hgate.as<float>();

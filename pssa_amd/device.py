@@ -512,6 +512,12 @@ class PSSALayer:
         """set_hybrid_read on every block (src/pssa.rs:2232-2243)."""
         _abi.call(self._lib.pssa_hip_model_set_hybrid_read, self.model, 1 if enabled else 0, lam)
 
+    def set_memory_top_k(self, top_k: int | None) -> None:
+        """set_memory_top_k on every block (src/pssa.rs:2215-2226); None = full read."""
+        if top_k is not None and top_k <= 0:
+            raise ValueError("memory top-k must be positive")
+        _abi.call(self._lib.pssa_hip_model_set_memory_top_k, self.model, 0 if top_k is None else top_k)
+
     def get_hybrid(self, layer: int):
         """One block's (hybrid_gate [C], hybrid_age [C]) as held on the device."""
         C_ = self.cfg.mem_capacity

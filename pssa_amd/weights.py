@@ -89,6 +89,8 @@ class BlockWeights:
         self.mem_hybrid_age = np.zeros(cfg.mem_capacity, dtype=np.uint64)
         self.mem_hybrid_enabled = False
         self.mem_hybrid_lam = 1.0
+        # memory.top_k (src/memory.rs:102-108): runtime-only, 0 = full read.
+        self.mem_top_k = 0
 
 
 class ModelWeights:
@@ -118,6 +120,7 @@ class ModelWeights:
             cb.mem_hybrid_age = _abi.ptr(b.mem_hybrid_age, C.c_uint64)
             cb.mem_hybrid_enabled = 1 if b.mem_hybrid_enabled else 0
             cb.mem_hybrid_lam = float(b.mem_hybrid_lam)
+            cb.mem_top_k = int(b.mem_top_k)
         assert self.embed.flags.c_contiguous and self.unembed.flags.c_contiguous
         w = _abi.Weights(self.cfg.to_c(), _abi.ptr(self.embed), _abi.ptr(self.unembed), blocks)
         return w, blocks
@@ -134,6 +137,13 @@ class ModelWeights:
         for b in self.blocks:
             b.mem_hybrid_enabled = bool(enabled)
             b.mem_hybrid_lam = float(lam)
+
+    def set_memory_top_k(self, top_k: int | None) -> None:
+        """set_memory_top_k on every block (src/pssa.rs:2215-2226); None = full read."""
+        if top_k is not None and top_k <= 0:
+            raise ValueError("memory top-k must be positive")
+        for b in self.blocks:
+            b.mem_top_k = 0 if top_k is None else int(top_k)
 
     # -- initialisation (libpssa_hip host code) -----------------------------
     @classmethod
@@ -181,6 +191,7 @@ class ModelWeights:
             dst.mem_hybrid_gate[:] = src.mem_hybrid_gate
             dst.mem_hybrid_age[:] = src.mem_hybrid_age
             dst.mem_hybrid_enabled, dst.mem_hybrid_lam = src.mem_hybrid_enabled, src.mem_hybrid_lam
+            dst.mem_top_k = src.mem_top_k
         return out
 
 

@@ -310,3 +310,51 @@ def test_ragged_prefill_matches_oracle_and_single_lanes(hip):
         with pytest.raises(HipError, match=msg):
             layer.prefill_ragged(bad)
     layer.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_memory_top_k_model_matches_oracle(hip, dtype):
+    """set_memory_top_k on the model (src/pssa.rs:2215-2226): prefill and
+    greedy decode read the top-k slots, against the oracle's model with the
+    same top_k; with the hybrid read on too; toggling re-captures the decode
+    graph."""
+    say("model memory top-k", dtype)
+    cfg = PSSAConfig(depth=2, d_vocab=97, d_latent=48, d_state=32, d_mem_key=8, mem_capacity=24)
+    w = ModelWeights.init(cfg, 31, "baseline")
+    w.populate_banks(32, count=20)
+    ids = np.random.default_rng(2).integers(0, 97, (3, 11), dtype=np.uint32)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    for k, hybrid in ((3, False), (1, False), (4, True)):
+        dev_w = ModelWeights.init(cfg, 31, "baseline")
+        dev_w.populate_banks(32, count=20)
+        dev_w.set_memory_top_k(k)
+        ref_w = ModelWeights.init(cfg, 31, "baseline")
+        ref_w.populate_banks(32, count=20)
+        ref_w.set_memory_top_k(k)
+        if hybrid:
+            for m in (dev_w, ref_w):
+                for b in m.blocks:
+                    b.mem_hybrid_gate[:20] = np.linspace(0.1, 1.0, 20, dtype=np.float32)
+                m.set_hybrid_read(True, 0.9)
+        layer = PSSALayer(hip, dev_w, lanes=3, max_tokens=64, weight_dtype=dtype)
+        got = layer.prefill_inference(ids)
+        om = O.OracleModel(ref_w if dtype == "f32" else ref_w.to_bf16_values())
+        st = om.zero_state(3)
+        ref = om.prefill_lanes(st, ids, threads=3)
+        assert rel_err(got, ref) < tol, (k, hybrid)
+        assert rel_err(layer.get_carry(), st) < tol, (k, hybrid)
+        layer.close()
+    # Graph decode across a top-k toggle equals eager decode.
+    res = []
+    for graph in (False, True):
+        layer = PSSALayer(hip, w, lanes=3, max_tokens=64, weight_dtype=dtype)
+        layer.prefill_inference(ids)
+        a = layer.decode(3, graph=graph)
+        layer.set_memory_top_k(2)
+        b = layer.decode(3, first_ids=a[-1], graph=graph)
+        layer.set_memory_top_k(None)
+        c = layer.decode(3, first_ids=b[-1], graph=graph)
+        res.append((a, b, c, layer.get_carry()))
+        layer.close()
+    for x, y in zip(*res):
+        np.testing.assert_array_equal(x, y)

@@ -199,3 +199,24 @@ def test_set_hybrid_read_validates_lam():
             w.set_hybrid_read(True, bad)
     w.set_hybrid_read(False, 1.0)
     assert not w.blocks[0].mem_hybrid_enabled
+
+
+def test_memory_top_k_at_or_above_count_is_the_full_read():
+    """retrieve_soft_into reads every slot when top_k >= count
+    (self.top_k.filter(|&k| k < self.count), src/memory.rs:380); a smaller
+    top_k changes the forward."""
+    cfg = PSSAConfig(depth=2, d_vocab=40, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=10)
+    full, topk, small = (ModelWeights.init(cfg, 8, "baseline") for _ in range(3))
+    for m in (full, topk, small):
+        m.populate_banks(5, 8)
+    topk.set_memory_top_k(8)
+    small.set_memory_top_k(2)
+    ids = [3, 9, 1, 30, 7]
+    outs = []
+    for m in (full, topk, small):
+        om = O.OracleModel(m)
+        outs.append(om.prefill(om.zero_state(), ids))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert not np.array_equal(outs[0], outs[2])
+    with pytest.raises(ValueError):
+        small.set_memory_top_k(0)

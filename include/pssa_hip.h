@@ -105,6 +105,8 @@ typedef struct {
   uint32_t mem_hybrid_enabled; /*    memory.hybrid_enabled                  */
   float mem_hybrid_lam;        /*    memory.hybrid_lam, in (0, 1]           */
   uint64_t mem_top_k;          /*    memory.top_k (runtime-only), 0 = full read */
+  float mem_value_cap;         /*    memory.value_cap (runtime-only), 0 = none  */
+  uint32_t _pad;
 } pssa_hip_block;
 
 /* Host view of PSSALayerV2's inference parameters (src/pssa.rs:1920-1960). */
@@ -155,6 +157,13 @@ int pssa_hip_weights_init(const pssa_hip_weights* w, uint64_t seed, int mode,
  * U[0, max_radius). */
 int pssa_hip_weights_populate_banks(const pssa_hip_weights* w, uint64_t seed, uint64_t count,
                                     float max_radius, char* err, size_t err_len);
+
+/* set_value_cap (src/memory.rs:121-134) on every block of a host model:
+ * cap > 0 clamps every capacity slot's value to Euclidean norm <= cap with
+ * clamp_value's rule (src/memory.rs:150-170) and records the cap, so later
+ * bank writes on the device are capped too; 0 removes the cap and keeps the
+ * values.  A negative or non-finite cap is an error. */
+int pssa_hip_weights_set_value_cap(const pssa_hip_weights* w, float cap, char* err, size_t err_len);
 
 /* ---------------------------------------------- stage dispatch (GpuDispatch)
  * Host buffers in, host buffers out, synchronous. */
@@ -475,6 +484,12 @@ int pssa_hip_model_set_hybrid_read(pssa_hip_model* model, int enabled, float lam
  * them (retrieve_soft_into, src/memory.rs:380-407); 0 = the full read (the
  * reference's None).  At most 64 here. */
 int pssa_hip_model_set_memory_top_k(pssa_hip_model* model, size_t top_k, char* err, size_t err_len);
+
+/* set_value_cap (src/memory.rs:121-134) on every block of a loaded model:
+ * cap > 0 clamps every slot's value to Euclidean norm <= cap (clamp_value,
+ * src/memory.rs:150-170, bit for bit) and caps the plastic decode's bank
+ * writes; 0 removes the cap and keeps the values. */
+int pssa_hip_model_set_value_cap(pssa_hip_model* model, float cap, char* err, size_t err_len);
 
 /* Reads one block's hybrid-read state back from the device: gate [C] and
  * age [C] (either may be NULL). */

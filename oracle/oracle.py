@@ -63,6 +63,8 @@ def lib() -> C.CDLL:
         "oracle_bank_insert_gated_protected": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float,
                                                 C.c_float, C.c_uint64], C.c_int64),
         "oracle_bank_bump_hybrid_ages": ([vp, C.c_uint64], None),
+        "oracle_bank_set_value_cap": ([vp, C.c_size_t, C.c_size_t, C.c_float], None),
+        "oracle_clamp_value": ([fp, C.c_size_t, C.c_float], None),
         "oracle_retrieve_hybrid_batch": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, fp,
                                           C.c_size_t, C.c_float, C.c_size_t, fp, C.POINTER(C.c_uint64),
                                           C.c_float, fp, fp, u32p, fp, C.c_int], None),
@@ -303,6 +305,20 @@ class Bank:
         k, v = f32(key), f32(val)
         return int(lib().oracle_bank_insert(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v)))
 
+    def insert_protected(self, key, val, surprise, step) -> int:
+        k, v = f32(key), f32(val)
+        return int(lib().oracle_bank_insert_protected(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v),
+                                                      surprise, step))
+
+    def set_value_cap(self, cap) -> None:
+        """set_value_cap (src/memory.rs:121-134); None disables it."""
+        lib().oracle_bank_set_value_cap(self._ref(), self.capacity, self.dv, 0.0 if cap is None else cap)
+
+    @property
+    def value_cap(self):
+        cap = self._blk.mem_value_cap
+        return None if cap == 0.0 else float(cap)
+
     def insert_gated(self, key, val, gate) -> int:
         k, v = f32(key), f32(val)
         return int(lib().oracle_bank_insert_gated(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v),
@@ -340,6 +356,8 @@ class _OracleBlock(C.Structure):
         ("mem_hybrid_enabled", C.c_uint32),
         ("mem_hybrid_lam", C.c_float),
         ("mem_top_k", C.c_uint64),
+        ("mem_value_cap", C.c_float),
+        ("_pad", C.c_uint32),
     ]
 
 
@@ -372,6 +390,13 @@ def dense_scan(a, b, h0=None, threads=1):
 def greedy(logits) -> int:
     logits = f32(logits)
     return int(lib().oracle_greedy(ptr(logits), logits.size))
+
+
+def clamp_value(value, cap) -> np.ndarray:
+    """clamp_value (src/memory.rs:150-170) on a copy."""
+    v = np.array(value, dtype=np.float32, copy=True)
+    lib().oracle_clamp_value(ptr(v), v.size, cap)
+    return v
 
 
 def sample_greedy(logits, history, penalty: float = 1.0) -> int:

@@ -589,6 +589,37 @@ static void ball_vector(Rng& rng, float* out, size_t n, float max_radius) {
 }
 
 // --- src/memory.rs:264-303 insert ------------------------------------------------
+// --- src/memory.rs:150-170 clamp_value ------------------------------------------
+// Iterator::sum over (x as f64)^2, left to right (src/memory.rs:190-192).
+static double value_norm_sq(const float* v, size_t n) {
+  double s = 0.0;
+  for (size_t i = 0; i < n; i++) s += (double)v[i] * (double)v[i];
+  return s;
+}
+
+void oracle_clamp_value(float* value, size_t n, float cap) {
+  const double cap_sq = (double)cap * (double)cap;
+  const double norm_sq = value_norm_sq(value, n);
+  if (norm_sq <= cap_sq) return;
+  const double scale = (double)cap / std::sqrt(norm_sq);
+  for (size_t i = 0; i < n; i++) value[i] = (float)((double)value[i] * scale);
+  // One ulp toward zero per pass until the rounded vector fits.
+  while (value_norm_sq(value, n) > cap_sq)
+    for (size_t i = 0; i < n; i++)
+      if (value[i] != 0.0f) {
+        uint32_t u;
+        std::memcpy(&u, &value[i], 4);
+        u -= 1;
+        std::memcpy(&value[i], &u, 4);
+      }
+}
+
+void oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t dv, float cap) {
+  if (cap > 0.0f)
+    for (size_t s = 0; s < capacity; s++) oracle_clamp_value(b->mem_values + s * dv, dv, cap);
+  b->mem_value_cap = cap;
+}
+
 int64_t oracle_bank_insert(oracle_block* b, size_t capacity, size_t dk, size_t dv,
                            const float* key, const float* val) {
   float key_sq = squared_norm(key, dk);
@@ -604,6 +635,7 @@ int64_t oracle_bank_insert(oracle_block* b, size_t capacity, size_t dk, size_t d
   std::memcpy(b->mem_keys + idx * dk, key, dk * 4);
   b->mem_norm_sq[idx] = key_sq;
   std::memcpy(b->mem_values + idx * dv, val, dv * 4);
+  if (b->mem_value_cap > 0.0f) oracle_clamp_value(b->mem_values + idx * dv, dv, b->mem_value_cap);
   b->mem_confidence[idx] = 1.0f;
   b->mem_last_seen[idx] = 0;
   if (b->mem_hybrid_gate) b->mem_hybrid_gate[idx] = 1.0f;  // src/memory.rs:300-301

@@ -89,6 +89,8 @@ typedef struct {
   uint32_t mem_hybrid_enabled;
   float mem_hybrid_lam;
   uint64_t mem_top_k; /* memory.top_k, 0 = full read (src/memory.rs:102-108) */
+  float mem_value_cap; /* memory.value_cap (src/memory.rs:13-14): > 0 caps written values, 0 = none */
+  uint32_t _pad;
 } oracle_block;
 
 typedef struct {
@@ -151,6 +153,11 @@ int64_t oracle_bank_insert_gated_protected(oracle_block* b, size_t capacity, siz
                                            size_t d_val, const float* key, const float* val,
                                            float gate, float surprise, uint64_t step);
 void oracle_bank_bump_hybrid_ages(oracle_block* b, uint64_t times);
+/* set_value_cap (src/memory.rs:121-134): cap > 0 clamps every capacity slot's
+ * value to Euclidean norm <= cap and caps later writes; 0 disables it and
+ * keeps the values.  clamp_value's rule (src/memory.rs:150-170). */
+void oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t d_val, float cap);
+void oracle_clamp_value(float* value, size_t n, float cap);
 /* retrieve_hybrid_into (src/memory.rs:568-660) for n_q queries against one
  * bank state (gate [count], age [count]); outputs as oracle_retrieve_batch,
  * plus weights [n_q, capacity] (may be NULL).  out_idx lists the live slots

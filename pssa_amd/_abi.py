@@ -64,6 +64,8 @@ class Block(C.Structure):
         ("mem_hybrid_enabled", C.c_uint32),
         ("mem_hybrid_lam", C.c_float),
         ("mem_top_k", C.c_uint64),
+        ("mem_value_cap", C.c_float),
+        ("_pad", C.c_uint32),
     ]
 
 
@@ -133,6 +135,7 @@ def lib() -> C.CDLL:
         "pssa_hip_memcpy": ([vp, vp, vp, sz, C.c_int, err_t, sz], C.c_int),
         "pssa_hip_weights_init": ([C.POINTER(Weights), C.c_uint64, C.c_int, u64p, err_t, sz], C.c_int),
         "pssa_hip_weights_populate_banks": ([C.POINTER(Weights), C.c_uint64, C.c_uint64, C.c_float, err_t, sz], C.c_int),
+        "pssa_hip_weights_set_value_cap": ([C.POINTER(Weights), C.c_float, err_t, sz], C.c_int),
         "pssa_hip_gemm_xwt": ([vp, fp, sz, vp, sz, C.c_int, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_softplus_in_place": ([vp, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_gemm_nn": ([vp, fp, sz, fp, sz, sz, sz, sz, fp, sz, err_t, sz], C.c_int),
@@ -172,6 +175,7 @@ def lib() -> C.CDLL:
                                          C.c_int),
         "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_model_set_memory_top_k": ([vp, sz, err_t, sz], C.c_int),
+        "pssa_hip_model_set_value_cap": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_stage_ids": ([vp, u32p, sz, sz, err_t, sz], C.c_int),
         "pssa_hip_lanes_prefill_staged": ([vp, err_t, sz], C.c_int),

@@ -88,6 +88,23 @@ Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_devi
   return Status::Ok();
 }
 
+// Clamps every slot of a block's bank values to `cap` (set_value_cap,
+// src/memory.rs:121-134) and rebuilds the transposed readout operand.
+Status cap_bank_values(pssa_hip_model* M, pssa::DevBlock& B, float cap) {
+  const hipStream_t st = M->ctx->stream;
+  const int C = (int)M->cfg.mem_capacity, d = (int)M->cfg.d_latent;
+  pssa::ValueCaps caps{};
+  caps.c[0] = cap;
+  PSSA_RETURN_IF(pssa::launch_clamp_rows(st, B.values.as<float>(), B.values.as<float>(), C, d, (size_t)d, caps, C));
+  if (M->dtype == PSSA_HIP_F32)
+    return pssa::launch_transpose(st, B.values.as<float>(), B.values_t.as<float>(), 1, C, d, 1.0f);
+  DevBuf tmp;
+  PSSA_RETURN_IF(tmp.alloc((size_t)C * d * 4));
+  PSSA_RETURN_IF(pssa::launch_transpose(st, B.values.as<float>(), tmp.as<float>(), 1, C, d, 1.0f));
+  PSSA_RETURN_IF(pssa::launch_to_bf16(st, tmp.as<float>(), C, B.values_t.as<uint16_t>(), C, d, C));
+  return sync(M->ctx);  // tmp is freed at return
+}
+
 // Empties every lane's repetition-penalty window (a new generation,
 // src/inference.rs:345-347).  Fill kernels, so the call may sit in a graph.
 Status clear_history(pssa_hip_lanes* L) {
@@ -905,6 +922,8 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
                               b.mem_values && b.mem_norm_sq,
                           "weights: null block tensor"));
       PSSA_RETURN_IF(need(b.mem_count <= C, "memory count exceeds capacity"));
+      PSSA_RETURN_IF(need(std::isfinite(b.mem_value_cap) && b.mem_value_cap >= 0.0f,
+                          "memory value cap must be positive and finite"));
       PSSA_RETURN_IF(need(b.mem_top_k <= (uint64_t)pssa::kMaxTopK, "memory top-k above 64 is not supported"));
       if (b.mem_hybrid_enabled)
         PSSA_RETURN_IF(need(std::isfinite(b.mem_hybrid_lam) && b.mem_hybrid_lam > 0.0f && b.mem_hybrid_lam <= 1.0f,
@@ -974,6 +993,7 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       B.hybrid = b.mem_hybrid_enabled != 0;
       B.lam = b.mem_hybrid_lam;
       B.top_k = (int)b.mem_top_k;
+      B.value_cap = b.mem_value_cap;
       PSSA_RETURN_IF(upload(B.hgate, hg.data(), C * 4, st));
       PSSA_RETURN_IF(upload(B.hage, ha.data(), C * 8, st));
       PSSA_RETURN_IF(upload(B.conf, conf.data(), C * 4, st));
@@ -987,6 +1007,8 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       PSSA_RETURN_IF(upload(B.values, b.mem_values, C * d * 4, st));
       PSSA_RETURN_IF(upload_weight(B.values_t, vt.data(), vt.size(), weight_dtype, st));
       PSSA_RETURN_IF(sync(ctx));  // host staging vectors are reused
+      // Values of a capped bank are capped (a no-op for values that were).
+      if (B.value_cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(m.get(), B, B.value_cap));
     }
     const unsigned long long step0 = 0;
     PSSA_RETURN_IF(upload(m->step, &step0, 8, st));
@@ -1540,6 +1562,22 @@ int pssa_hip_model_set_hybrid_read(pssa_hip_model* M, int enabled, float lam, ch
   return pssa::finish(body(), err, err_len);
 }
 
+int pssa_hip_model_set_value_cap(pssa_hip_model* M, float cap, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(M != nullptr, "null model"));
+    PSSA_RETURN_IF(need(std::isfinite(cap) && cap >= 0.0f, "memory value cap must be positive and finite"));
+    std::lock_guard<std::mutex> g(M->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(M->ctx->device));
+    for (pssa::DevBlock& B : M->blocks) {
+      if (cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(M, B, cap));
+      B.value_cap = cap;
+    }
+    ++M->hybrid_epoch;  // captured bank writes hold the old cap
+    return sync(M->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 int pssa_hip_model_set_memory_top_k(pssa_hip_model* M, size_t top_k, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(M != nullptr, "null model"));
@@ -1586,6 +1624,7 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
     PSSA_RETURN_IF(L->tap_a.alloc(D * n * c.d_latent * 4));
     PSSA_RETURN_IF(L->tap_act.alloc(D * n * c.adapter_rank * 4));
     PSSA_RETURN_IF(L->tap_gmean.alloc(D * n * 4));
+    PSSA_RETURN_IF(L->tap_zcap.alloc(D * n * c.d_latent * 4));
     PSSA_RETURN_IF(L->surprise.alloc(n * 4));
     PSSA_RETURN_IF(L->hebb_rate.alloc(D * n * 4));  // [depth, lanes]
     PSSA_RETURN_IF(L->bank_writer.alloc(D * c.mem_capacity * 4));

@@ -15,6 +15,7 @@
 #include <cfloat>
 #include <cmath>
 
+#include "memory.h"
 #include "model.h"
 
 namespace pssa {
@@ -176,6 +177,8 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
 
 // Per-layer operand pointers of the plastic write kernels (one launch covers
 // every block).
+static_assert(kMaxDepth <= 32, "ValueCaps holds one cap per block");
+
 struct PlasticArgs {
   float* keys[kMaxDepth];
   float* norm_sq[kMaxDepth];
@@ -189,6 +192,7 @@ struct PlasticArgs {
   void* u_eff[kMaxDepth];
   const float* tap_q;    // [depth, lanes, k]
   const float* tap_z;    // [depth, lanes, d]
+  const float* vsrc;     // [depth, lanes, d] the values a bank write stores (tap_z, capped where a cap is set)
   const float* tap_a;    // [depth, lanes, d]
   const float* tap_act;  // [depth, lanes, r]
   const float* surprise; // [lanes]
@@ -391,7 +395,7 @@ __global__ __launch_bounds__(256) void bank_copy_kernel(PlasticArgs p) {
   for (int e = tid; e < 64 * 64; e += 256) {
     const int cc = e >> 6, jj = e & 63, c = c0 + cc, j = j0 + jj;
     if (w[cc] >= 0 && j < d) {
-      const float v = p.tap_z[((size_t)l * n + w[cc]) * d + j];
+      const float v = p.vsrc[((size_t)l * n + w[cc]) * d + j];
       p.values[l][(size_t)c * d + j] = v;
       tile[cc][jj] = v;
     }
@@ -509,6 +513,21 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     }
     p.tap_q = L->tap_q.as<float>();
     p.tap_z = L->tap_z.as<float>();
+    // Bank writes store capped copies of z_final where a block has a value
+    // cap (insert's clamp, src/memory.rs:290-297); the Hebbian update keeps
+    // the raw z_final.
+    ValueCaps caps{};
+    bool any_cap = false;
+    for (size_t l = 0; l < c.depth; ++l) {
+      caps.c[l] = M->blocks[l].value_cap;
+      any_cap |= caps.c[l] > 0.0f;
+    }
+    p.vsrc = p.tap_z;
+    if (any_cap) {
+      PSSA_RETURN_IF(launch_clamp_rows(st, L->tap_z.as<float>(), L->tap_zcap.as<float>(), (int)(c.depth * n), d,
+                                       (size_t)d, caps, (int)n));
+      p.vsrc = L->tap_zcap.as<float>();
+    }
     p.tap_a = L->tap_a.as<float>();
     p.tap_act = L->tap_act.as<float>();
     p.surprise = L->surprise.as<float>();

@@ -220,3 +220,44 @@ extern "C" int pssa_hip_weights_populate_banks(const pssa_hip_weights* w, uint64
   }
   return PSSA_HIP_OK;
 }
+
+// clamp_value (src/memory.rs:150-170): the reference's left-to-right f64
+// squared norm, f64 scale with f32 rounding, then one ulp toward zero per
+// pass until the rounded value fits.
+static double value_norm_sq(const float* v, size_t n) {
+  double s = 0.0;
+  for (size_t i = 0; i < n; i++) s += (double)v[i] * (double)v[i];
+  return s;
+}
+
+static void clamp_value(float* v, size_t n, float cap) {
+  const double cap_sq = (double)cap * (double)cap;
+  const double nsq = value_norm_sq(v, n);
+  if (!(nsq > cap_sq)) return;
+  const double scale = (double)cap / std::sqrt(nsq);
+  for (size_t i = 0; i < n; i++) v[i] = (float)((double)v[i] * scale);
+  for (int pass = 0; pass < 1024 && value_norm_sq(v, n) > cap_sq; ++pass)
+    for (size_t i = 0; i < n; i++)
+      if (v[i] != 0.0f) {
+        uint32_t u;
+        std::memcpy(&u, &v[i], 4);
+        u -= 1;
+        std::memcpy(&v[i], &u, 4);
+      }
+}
+
+extern "C" int pssa_hip_weights_set_value_cap(const pssa_hip_weights* w, float cap, char* err, size_t err_len) {
+  if (!check_weights(w, err, err_len)) return PSSA_HIP_EINVAL;
+  if (!(std::isfinite(cap) && cap >= 0.0f)) {
+    set_err(err, err_len, "memory value cap must be positive and finite");
+    return PSSA_HIP_EINVAL;
+  }
+  const pssa_hip_config& c = w->cfg;
+  for (size_t l = 0; l < c.depth; l++) {
+    pssa_hip_block& b = w->blocks[l];
+    if (cap > 0.0f)
+      for (size_t s = 0; s < c.mem_capacity; s++) clamp_value(b.mem_values + s * c.d_latent, c.d_latent, cap);
+    b.mem_value_cap = cap;
+  }
+  return PSSA_HIP_OK;
+}

@@ -52,4 +52,12 @@ Status init_retrieve_attributes();
 
 constexpr int kMaxTopK = 64;
 
+// Per-row Euclidean norm caps of clamp_rows: c[r / rows_per_cap] (<= 0: none).
+struct ValueCaps {
+  float c[32];
+};
+// clamp_value (src/memory.rs:150-170) on rows [n_rows, d], src -> dst.
+Status launch_clamp_rows(hipStream_t stream, const float* src, float* dst, int n_rows, int d, size_t ld,
+                         const ValueCaps& caps, int rows_per_cap);
+
 }  // namespace pssa

@@ -1070,6 +1070,63 @@ __global__ __launch_bounds__(64 * RQ_WAVES) void ranked_pick_kernel(RetrieveArgs
   }
 }
 
+// clamp_value (src/memory.rs:150-170) on rows [n_rows, d] with leading
+// dimension ld, src -> dst (may alias): a row whose Euclidean norm exceeds
+// its cap is scaled to it (f64 scale, f32 rounding), then its nonzero
+// components move one ulp toward zero per pass while the rounded row still
+// exceeds it.  The squared norm is the reference's left-to-right f64 sum
+// (src/memory.rs:190-192), so every decision and bit equals its own.  One
+// wave per row, staged in LDS.  Row r takes caps.c[r / rows_per_cap]; a cap
+// <= 0 copies the row.
+__global__ __launch_bounds__(64) void clamp_rows_kernel(const float* src, float* dst, int d, size_t ld,
+                                                        ValueCaps caps, int rows_per_cap) {
+  extern __shared__ float srow[];
+  __shared__ double s_norm;
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const float cap = caps.c[row / rows_per_cap];
+  const float* in = src + (size_t)row * ld;
+  float* out = dst + (size_t)row * ld;
+  for (int j = lane; j < d; j += 64) srow[j] = in[j];
+  __syncthreads();
+  auto norm_sq = [&]() {
+    if (lane == 0) {
+      double s = 0.0;
+      for (int j = 0; j < d; ++j) s += (double)srow[j] * (double)srow[j];
+      s_norm = s;
+    }
+    __syncthreads();
+    const double v = s_norm;
+    __syncthreads();
+    return v;
+  };
+  if (cap > 0.0f) {
+    const double cap_sq = (double)cap * (double)cap;
+    const double nsq = norm_sq();
+    if (nsq > cap_sq) {
+      const double scale = (double)cap / sqrt(nsq);
+      for (int j = lane; j < d; j += 64) srow[j] = (float)((double)srow[j] * scale);
+      __syncthreads();
+      // Each pass shrinks every nonzero magnitude; a non-finite row ends the
+      // loop through a NaN norm, and the pass count bounds it regardless.
+      for (int pass = 0; pass < 1024 && norm_sq() > cap_sq; ++pass) {
+        for (int j = lane; j < d; j += 64)
+          if (srow[j] != 0.0f) srow[j] = __uint_as_float(__float_as_uint(srow[j]) - 1u);
+        __syncthreads();
+      }
+    }
+  }
+  for (int j = lane; j < d; j += 64) out[j] = srow[j];
+}
+
+Status launch_clamp_rows(hipStream_t stream, const float* src, float* dst, int n_rows, int d, size_t ld,
+                         const ValueCaps& caps, int rows_per_cap) {
+  if (n_rows <= 0 || d <= 0) return Status::Ok();
+  if ((size_t)d * 4 > 64 * 1024) return Status::Invalid("value cap: rows wider than 16384");
+  clamp_rows_kernel<<<(unsigned)n_rows, 64, (size_t)d * 4, stream>>>(src, dst, d, ld, caps, rows_per_cap);
+  PSSA_LAUNCH_CHECK("clamp_rows");
+  return Status::Ok();
+}
+
 static bool ranked_read_fits(const RetrieveArgs& a) {
   return a.top_k > 0 && !a.hgate && !a.count_dev && a.top_k < a.count && a.count <= RK_SLOTS && !a.project &&
          !a.q_pnc && !a.q_norm && a.dk % 4 == 0 && a.dk <= RK_MAX_DK && a.ld_q % 4 == 0 &&

@@ -34,6 +34,7 @@ struct DevBlock {
   bool hybrid = false;
   float lam = 1.0f;
   int top_k = 0;  // memory.top_k (src/memory.rs:102-108), 0 = full read
+  float value_cap = 0.0f;  // memory.value_cap (src/memory.rs:13-14), 0 = none
 };
 
 // Stage ids used for per-kernel timing.
@@ -90,6 +91,7 @@ struct pssa_hip_lanes {
   // generated ids [gen_cap, lanes] and the generation position.
   pssa::DevBuf tap_q, tap_z, tap_a, tap_act, surprise, hebb_rate, gen_ids, gen_pos;
   pssa::DevBuf tap_gmean;    // [depth, lanes] mean memory-injection gate (hybrid write gate)
+  pssa::DevBuf tap_zcap;     // [depth, lanes, d] z_final rows clamped to the value caps (bank writes)
   pssa::DevBuf bank_writer;  // [depth, capacity] writing lane of each slot in the current step
   // Batch training forward (allocated on its first call): the fp32 scaled
   // logits of every token row [max_tokens, V], each row's target id and

@@ -518,6 +518,10 @@ class PSSALayer:
             raise ValueError("memory top-k must be positive")
         _abi.call(self._lib.pssa_hip_model_set_memory_top_k, self.model, 0 if top_k is None else top_k)
 
+    def set_value_cap(self, cap: float | None) -> None:
+        """set_value_cap on every block of the loaded model (src/memory.rs:121-134)."""
+        _abi.call(self._lib.pssa_hip_model_set_value_cap, self.model, 0.0 if cap is None else cap)
+
     def get_hybrid(self, layer: int):
         """One block's (hybrid_gate [C], hybrid_age [C]) as held on the device."""
         C_ = self.cfg.mem_capacity

@@ -91,6 +91,8 @@ class BlockWeights:
         self.mem_hybrid_lam = 1.0
         # memory.top_k (src/memory.rs:102-108): runtime-only, 0 = full read.
         self.mem_top_k = 0
+        # memory.value_cap (src/memory.rs:13-14): runtime-only, 0 = none.
+        self.mem_value_cap = 0.0
 
 
 class ModelWeights:
@@ -121,6 +123,7 @@ class ModelWeights:
             cb.mem_hybrid_enabled = 1 if b.mem_hybrid_enabled else 0
             cb.mem_hybrid_lam = float(b.mem_hybrid_lam)
             cb.mem_top_k = int(b.mem_top_k)
+            cb.mem_value_cap = float(b.mem_value_cap)
         assert self.embed.flags.c_contiguous and self.unembed.flags.c_contiguous
         w = _abi.Weights(self.cfg.to_c(), _abi.ptr(self.embed), _abi.ptr(self.unembed), blocks)
         return w, blocks
@@ -144,6 +147,14 @@ class ModelWeights:
             raise ValueError("memory top-k must be positive")
         for b in self.blocks:
             b.mem_top_k = 0 if top_k is None else int(top_k)
+
+    def set_value_cap(self, cap: float | None) -> None:
+        """set_value_cap on every block (src/memory.rs:121-134): clamps every slot's
+        value to norm <= cap and caps later writes; None removes the cap."""
+        w, blocks = self.c_view()
+        _abi.call(_abi.lib().pssa_hip_weights_set_value_cap, C.byref(w), 0.0 if cap is None else cap)
+        for b, cb in zip(self.blocks, blocks):
+            b.mem_value_cap = float(cb.mem_value_cap)
 
     # -- initialisation (libpssa_hip host code) -----------------------------
     @classmethod
@@ -192,6 +203,7 @@ class ModelWeights:
             dst.mem_hybrid_age[:] = src.mem_hybrid_age
             dst.mem_hybrid_enabled, dst.mem_hybrid_lam = src.mem_hybrid_enabled, src.mem_hybrid_lam
             dst.mem_top_k = src.mem_top_k
+            dst.mem_value_cap = src.mem_value_cap
         return out
 
 

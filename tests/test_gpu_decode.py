@@ -244,3 +244,54 @@ def test_repetition_penalty_validation_and_non_finite_logits(hip):
     with pytest.raises(HipError, match="non-finite logits"):
         layer.decode(2)
     layer.close()
+
+
+def test_value_cap_on_device_matches_host_clamp_and_oracle_decode(hip):
+    """set_value_cap (src/memory.rs:121-170) on a loaded model equals the host
+    clamp bit for bit, a recorded cap clamps on load, the next prefill reads
+    the capped bank, and plastic bank writes store capped values as the
+    oracle's capped inserts do."""
+    say("value cap")
+    cap = 0.35
+    w = small_model(seed=29)
+    host = small_model(seed=29)
+    host.set_value_cap(cap)
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=64)
+    layer.set_value_cap(cap)
+    for l in range(w.cfg.depth):
+        np.testing.assert_array_equal(layer.get_plastic(l)["mem_values"], host.blocks[l].mem_values)
+    recorded = small_model(seed=29)
+    for b in recorded.blocks:
+        b.mem_value_cap = cap
+    loaded = PSSALayer(hip, recorded, lanes=3, max_tokens=64)
+    for l in range(w.cfg.depth):
+        np.testing.assert_array_equal(loaded.get_plastic(l)["mem_values"], host.blocks[l].mem_values)
+    loaded.close()
+    ids = np.random.default_rng(5).integers(0, w.cfg.d_vocab, (3, 8), dtype=np.uint32)
+    lg = layer.prefill_inference(ids)
+    om = O.OracleModel(host)
+    st = om.zero_state(3)
+    ref_lg = om.prefill_lanes(st, ids, threads=3)
+    assert rel_err(lg, ref_lg) < 1e-4
+    layer.close()
+    # Plastic writes on banks that give way (confidence 0) store capped values.
+    dev_w, ref_w = small_model(seed=29), small_model(seed=29)
+    for m in (dev_w, ref_w):
+        for b in m.blocks:
+            b.mem_confidence[:] = 0.0
+        m.set_value_cap(cap)
+    layer = PSSALayer(hip, dev_w, lanes=3, max_tokens=64)
+    layer.prefill_inference(ids)
+    om = O.OracleModel(ref_w)
+    st = om.zero_state(3)
+    lg = om.prefill_lanes(st, ids, threads=3)
+    first = [O.greedy(lg[i]) for i in range(3)]
+    got = layer.decode(3, first_ids=first, plastic=True)
+    ref_ids, _, _ = om.decode(st, first, steps=3, plastic=True)
+    np.testing.assert_array_equal(got, ref_ids)
+    for l in range(dev_w.cfg.depth):
+        vals = layer.get_plastic(l)["mem_values"]
+        assert rel_err(vals, ref_w.blocks[l].mem_values) < 1e-4
+        assert np.all((vals.astype(np.float64) ** 2).sum(axis=1) <= float(np.float32(cap)) ** 2)
+        assert not np.array_equal(vals, host.blocks[l].mem_values)  # the decode wrote slots
+    layer.close()

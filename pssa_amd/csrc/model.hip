@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void token_ce_kernel(const float* __restrict__
 // input projection has been issued.
 static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T,
                            bool taps, bool timing, hipEvent_t first_in_done, float* y_part,
-                           const TrainRows* tr) {
+                           const TrainRows* tr, bool concurrent) {
   const pssa_hip_model* M = L->model;
   const pssa_hip_config& c = M->cfg;
   const int d = (int)c.d_latent, s = (int)c.d_state, k = (int)c.d_mem_key;
@@ -403,6 +403,7 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     sa.s = s;
     sa.lanes = (int)n_lanes;
     sa.y_part = y_part;
+    sa.concurrent = concurrent ? 1 : 0;
     if (bf16 && step_y) {
       sa.y16 = static_cast<uint16_t*>(Yh);
       sa.ld_y16 = d;
@@ -638,7 +639,7 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
       }
       float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
       PSSA_RETURN_IF(
-          prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr));
+          prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true));
       lane0 += ng;
     }
     for (int g = 1; g < G; ++g) {
@@ -647,7 +648,7 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
     }
     return Status::Ok();
   }
-  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart, tr);
+  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart, tr, false);
 }
 
 }  // namespace pssa

@@ -35,6 +35,10 @@ struct SsmArgs {
   // ssm_step_writes_y (other paths leave it untouched).
   uint16_t* y16 = nullptr;
   int ld_y16 = 0;
+  // Set when another lane group's kernels share the CUs with this scan: the
+  // four-wave variant then runs at any grid size (the eight-wave one is the
+  // faster scan alone on small grids, but leaves those kernels less room).
+  int concurrent = 0;
 };
 
 // Rows of lane b are b*T .. b*T+T-1.  The states of a channel are split into

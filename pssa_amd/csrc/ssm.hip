@@ -393,7 +393,7 @@ static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   } else if (a.T < SSM_TC) {
     ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);
   } else if constexpr (J == 32) {
-    if ((long)grid.x * grid.y * grid.z < kScanFullGrid)
+    if ((long)grid.x * grid.y * grid.z < kScanFullGrid && !a.concurrent)
       ssm_scan_kernel<16, 8, 4><<<grid, 512, 0, stream>>>(a);
     else
       ssm_scan_kernel<32, 4, 3><<<grid, 256, 0, stream>>>(a);

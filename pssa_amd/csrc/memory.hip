@@ -297,6 +297,10 @@ constexpr int SOFT_SPL = 8;            // slots per lane: capacity <= 512
 constexpr int SOFT_MAX_KEYS = 16384;   // dk * capacity floats held in LDS (64 KiB)
 constexpr int SOFT_MAX_DK = 64;
 constexpr int SOFT_WAVES = 8;
+#ifndef SOFT_WAVES_FEW
+#define SOFT_WAVES_FEW 4               // waves per workgroup for few queries (measured: 1, 2, 8 slower)
+#endif
+constexpr int SOFT_FEW_QUERIES = 2048;
 constexpr int SOFT_QG = 4;             // queries sharing one pass over the keys
 
 // Slots per lane for a bank of `cap` slots (a power of two up to SOFT_SPL).
@@ -313,9 +317,9 @@ __host__ __device__ __forceinline__ size_t soft_keys_floats(int dk, int cap) {
 }
 // Dynamic LDS: keyT, then 1/(1-|k|^2) and |k|^2 (f64), then each wave's QG
 // projected queries (f32).
-static size_t soft_read_lds(int dk, int cap, int qg) {
+static size_t soft_read_lds(int dk, int cap, int qg, int nwv) {
   return soft_keys_floats(dk, cap) * sizeof(float) + 2 * (size_t)cap * sizeof(double) +
-         (size_t)SOFT_WAVES * qg * dk * sizeof(float);
+         (size_t)nwv * qg * dk * sizeof(float);
 }
 
 __device__ __forceinline__ double readlane_f64(double v, int l) {
@@ -325,8 +329,8 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-template <int QG, int SPL, bool HYB>
-__global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu(4))) void soft_read_kernel(
+template <int QG, int SPL, bool HYB, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) void soft_read_kernel(
     RetrieveArgs a) {
   extern __shared__ float smem[];
   const int cap = a.capacity, dk = a.dk, cnt = a.count_dev ? a.count_dev[0] : a.count;
@@ -340,16 +344,16 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu
   // eight loads per thread are issued before their stores.
   if (dk % 4 == 0 && ((uintptr_t)a.keys & 15) == 0) {
     const int nv = cnt * dk / 4;
-    for (int e0 = tid; e0 < nv; e0 += 8 * 64 * SOFT_WAVES) {
+    for (int e0 = tid; e0 < nv; e0 += 8 * 64 * NWV) {
       float4 v[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int e = e0 + u * 64 * SOFT_WAVES;
+        const int e = e0 + u * 64 * NWV;
         v[u] = e < nv ? reinterpret_cast<const float4*>(a.keys)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int e = e0 + u * 64 * SOFT_WAVES;
+        const int e = e0 + u * 64 * NWV;
         if (e < nv) {
           const int sl = (4 * e) / dk, i = 4 * e - sl * dk;
           keyT[i * kp + sl] = v[u].x;
@@ -360,13 +364,13 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu
       }
     }
   } else {
-    for (int e = tid; e < cnt * dk; e += 64 * SOFT_WAVES) {
+    for (int e = tid; e < cnt * dk; e += 64 * NWV) {
       const int sl = e / dk, i = e - sl * dk;
       keyT[i * kp + sl] = a.keys[e];
     }
   }
   __syncthreads();
-  for (int sl = tid; sl < cnt; sl += 64 * SOFT_WAVES) {
+  for (int sl = tid; sl < cnt; sl += 64 * NWV) {
     rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
     double s2 = 0.0;
     for (int i = 0; i < dk; ++i) {
@@ -379,9 +383,9 @@ __global__ __launch_bounds__(64 * SOFT_WAVES) __attribute__((amdgpu_waves_per_eu
 
   const float c2 = 2.0f / a.tau;
 
-  const int nw = gridDim.x * SOFT_WAVES;
+  const int nw = gridDim.x * NWV;
   const int per = (a.n + nw - 1) / nw;
-  const int qb = (blockIdx.x * SOFT_WAVES + wave) * per;
+  const int qb = (blockIdx.x * NWV + wave) * per;
   const int qe = min(a.n, qb + per);
   for (int c0 = qb; c0 < qe; c0 += 64) {
     const int na = min(64, qe - c0);
@@ -1156,11 +1160,14 @@ static Status allow_large_lds() {
   std::lock_guard<std::mutex> g(mu);
   if (dev >= 0 && dev < 64 && done[dev]) return Status::Ok();
   const void* soft[] = {
-#define PSSA_SOFT_FN(QG, SPL)                                         \
-  reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, false>),  \
-      reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, true>),
-      PSSA_SOFT_FN(1, 1) PSSA_SOFT_FN(1, 2) PSSA_SOFT_FN(1, 4) PSSA_SOFT_FN(1, 8)
-      PSSA_SOFT_FN(SOFT_QG, 1) PSSA_SOFT_FN(SOFT_QG, 2) PSSA_SOFT_FN(SOFT_QG, 4) PSSA_SOFT_FN(SOFT_QG, 8)
+#define PSSA_SOFT_FN(QG, SPL, NWV)                                         \
+  reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, false, NWV>),  \
+      reinterpret_cast<const void*>(&soft_read_kernel<QG, SPL, true, NWV>),
+      PSSA_SOFT_FN(1, 1, SOFT_WAVES) PSSA_SOFT_FN(1, 2, SOFT_WAVES) PSSA_SOFT_FN(1, 4, SOFT_WAVES)
+      PSSA_SOFT_FN(1, 8, SOFT_WAVES) PSSA_SOFT_FN(SOFT_QG, 1, SOFT_WAVES) PSSA_SOFT_FN(SOFT_QG, 2, SOFT_WAVES)
+      PSSA_SOFT_FN(SOFT_QG, 4, SOFT_WAVES) PSSA_SOFT_FN(SOFT_QG, 8, SOFT_WAVES)
+      PSSA_SOFT_FN(1, 1, SOFT_WAVES_FEW) PSSA_SOFT_FN(1, 2, SOFT_WAVES_FEW) PSSA_SOFT_FN(1, 4, SOFT_WAVES_FEW)
+      PSSA_SOFT_FN(1, 8, SOFT_WAVES_FEW)
 #undef PSSA_SOFT_FN
   };
   for (const void* f : soft)
@@ -1186,24 +1193,30 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
   if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
   if (soft_read_fits(a)) {
-    int blocks = (a.n + SOFT_WAVES - 1) / SOFT_WAVES;
+    // Few queries (a decode step): small workgroups spread them over more
+    // CUs, each staging the bank for fewer waves.
+    const int nwv = a.n <= SOFT_FEW_QUERIES ? SOFT_WAVES_FEW : SOFT_WAVES;
+    int blocks = (a.n + nwv - 1) / nwv;
     if (blocks > 512) blocks = 512;
-    const int per = (a.n + blocks * SOFT_WAVES - 1) / (blocks * SOFT_WAVES);
-    const int qg = per >= SOFT_QG ? SOFT_QG : 1;
-    const size_t lds = soft_read_lds(a.dk, a.capacity, qg);
+    const int per = (a.n + blocks * nwv - 1) / (blocks * nwv);
+    const int qg = per >= SOFT_QG && nwv == SOFT_WAVES ? SOFT_QG : 1;
+    const size_t lds = soft_read_lds(a.dk, a.capacity, qg, nwv);
     if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     const int spl = soft_spl(a.capacity);
-#define PSSA_SOFT_CASE(QG, SPL)                                                    \
-  if (qg == QG && spl == SPL) {                                                    \
-    if (a.hgate)                                                                   \
-      soft_read_kernel<QG, SPL, true><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a);  \
-    else                                                                           \
-      soft_read_kernel<QG, SPL, false><<<blocks, 64 * SOFT_WAVES, lds, stream>>>(a); \
-    PSSA_LAUNCH_CHECK("soft_read");                                                \
-    return Status::Ok();                                                           \
+#define PSSA_SOFT_CASE(QG, SPL, NWV)                                                    \
+  if (qg == QG && spl == SPL && nwv == NWV) {                                           \
+    if (a.hgate)                                                                        \
+      soft_read_kernel<QG, SPL, true, NWV><<<blocks, 64 * NWV, lds, stream>>>(a);       \
+    else                                                                                \
+      soft_read_kernel<QG, SPL, false, NWV><<<blocks, 64 * NWV, lds, stream>>>(a);      \
+    PSSA_LAUNCH_CHECK("soft_read");                                                     \
+    return Status::Ok();                                                                \
   }
-    PSSA_SOFT_CASE(1, 1) PSSA_SOFT_CASE(1, 2) PSSA_SOFT_CASE(1, 4) PSSA_SOFT_CASE(1, 8)
-    PSSA_SOFT_CASE(SOFT_QG, 1) PSSA_SOFT_CASE(SOFT_QG, 2) PSSA_SOFT_CASE(SOFT_QG, 4) PSSA_SOFT_CASE(SOFT_QG, 8)
+    PSSA_SOFT_CASE(1, 1, SOFT_WAVES) PSSA_SOFT_CASE(1, 2, SOFT_WAVES) PSSA_SOFT_CASE(1, 4, SOFT_WAVES)
+    PSSA_SOFT_CASE(1, 8, SOFT_WAVES) PSSA_SOFT_CASE(SOFT_QG, 1, SOFT_WAVES) PSSA_SOFT_CASE(SOFT_QG, 2, SOFT_WAVES)
+    PSSA_SOFT_CASE(SOFT_QG, 4, SOFT_WAVES) PSSA_SOFT_CASE(SOFT_QG, 8, SOFT_WAVES)
+    PSSA_SOFT_CASE(1, 1, SOFT_WAVES_FEW) PSSA_SOFT_CASE(1, 2, SOFT_WAVES_FEW) PSSA_SOFT_CASE(1, 4, SOFT_WAVES_FEW)
+    PSSA_SOFT_CASE(1, 8, SOFT_WAVES_FEW)
 #undef PSSA_SOFT_CASE
     return Status::Invalid("retrieve: soft read shape");
   }

@@ -116,14 +116,38 @@ __device__ __forceinline__ void store_one(const EpiParams& ep, int row, int col,
 
 // Four consecutive columns col..col+3 of one row.  `vec`: all four are in
 // range and every operand row is 16-byte aligned at col.
+// Row operands an epilogue reads at four consecutive columns (z_raw: y and
+// g; add-aux and residual: aux and, for deeper residual layers, the running
+// out32).  A tile loads them for all its quads before its first store: the
+// operand pointers may alias the outputs, so loads written between the
+// stores would each wait out a full memory round trip.
+constexpr bool epi_reads(int kind) { return kind == EPI_ZRAW || kind == EPI_ADD_AUX || kind == EPI_RESIDUAL; }
+
+struct QuadIn {
+  float4 p, q;
+};
+
+template <int KIND>
+__device__ __forceinline__ void load_quad(const EpiParams& ep, int row, int col, QuadIn& in) {
+  if constexpr (KIND == EPI_ZRAW) {
+    in.p = *reinterpret_cast<const float4*>(ep.y + (size_t)row * ep.ld_y + col);
+    in.q = *reinterpret_cast<const float4*>(ep.g + (size_t)row * ep.ld_g + col);
+  } else if constexpr (KIND == EPI_ADD_AUX || KIND == EPI_RESIDUAL) {
+    in.p = *reinterpret_cast<const float4*>(ep.aux + (size_t)row * ep.ld_aux + col);
+    in.q = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (KIND == EPI_RESIDUAL && !ep.first)
+      in.q = *reinterpret_cast<const float4*>(ep.out32 + (size_t)row * ep.ld32 + col);
+  }
+}
+
 template <typename T, int KIND>
 __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, int N, bool vec,
-                                         const float (&acc)[4], const float (&ad)[4]) {
+                                         const float (&acc)[4], const float (&ad)[4], const QuadIn& in) {
   if (vec) {
     float r[4], tp[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (KIND == EPI_ZRAW) {
-      const float4 yv = *reinterpret_cast<const float4*>(ep.y + (size_t)row * ep.ld_y + col);
-      const float4 gv = *reinterpret_cast<const float4*>(ep.g + (size_t)row * ep.ld_g + col);
+      const float4 yv = in.p;
+      const float4 gv = in.q;
       r[0] = (yv.x * ep.scale + gv.x * acc[0]) + ad[0];
       r[1] = (yv.y * ep.scale + gv.y * acc[1]) + ad[1];
       r[2] = (yv.z * ep.scale + gv.z * acc[2]) + ad[2];
@@ -131,17 +155,13 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) tp[e] = ad[e];
     } else if constexpr (KIND == EPI_ADD_AUX || KIND == EPI_RESIDUAL) {
-      const float4 av = *reinterpret_cast<const float4*>(ep.aux + (size_t)row * ep.ld_aux + col);
+      const float4 av = in.p;
       const float a4[4] = {av.x, av.y, av.z, av.w};
       if constexpr (KIND == EPI_ADD_AUX) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = acc[e] + a4[e];
       } else {
-        float o4[4] = {0.f, 0.f, 0.f, 0.f};
-        if (!ep.first) {
-          const float4 ov = *reinterpret_cast<const float4*>(ep.out32 + (size_t)row * ep.ld32 + col);
-          o4[0] = ov.x, o4[1] = ov.y, o4[2] = ov.z, o4[3] = ov.w;
-        }
+        const float o4[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float zf = a4[e] + acc[e];
@@ -226,10 +246,26 @@ __device__ __forceinline__ void adapter_act_frag(const EpiParams& ep, int row, i
 // n32 + 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.  `act0` (bf16 GEMMs with
 // the z_raw epilogue, may be null) is the row's adapter fragment for
 // q0 = 0, loaded once by the caller for all tiles of the row.
+// The row operands of one tile's four quads (see QuadIn).
+template <int KIND>
+__device__ __forceinline__ void epi_tile_load(const EpiParams& ep, int row, int n32, int M, int N,
+                                              int vec_epi, int half, QuadIn (&in)[4]) {
+  const int nb = n32 + half * 4;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    in[g].p = in[g].q = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (epi_reads(KIND)) {
+      const int col = nb + g * 8;
+      if (row < M && vec_epi && col + 3 < N) load_quad<KIND>(ep, row, col, in[g]);
+    }
+  }
+}
+
 template <typename T, int KIND>
-__device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16_t& acc, int row,
+__device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16_t& acc, int row,
                                                int n32, int M, int N, int vec_epi, int half,
-                                               int l32, const uint32_t* act0 = nullptr) {
+                                               int l32, const uint32_t* act0, const QuadIn (&in)[4]) {
+  const int nb = n32 + half * 4;
   f32x16_t adv;
 #pragma unroll
   for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
@@ -276,17 +312,25 @@ __device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16
     }
   }
   if (row < M) {
-    const int nb = n32 + half * 4;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int col = nb + g * 8;
       if (col < N) {
         const float a4[4] = {acc[g * 4 + 0], acc[g * 4 + 1], acc[g * 4 + 2], acc[g * 4 + 3]};
         const float d4[4] = {adv[g * 4 + 0], adv[g * 4 + 1], adv[g * 4 + 2], adv[g * 4 + 3]};
-        epi_quad<T, KIND>(ep, row, col, N, vec_epi && col + 3 < N, a4, d4);
+        epi_quad<T, KIND>(ep, row, col, N, vec_epi && col + 3 < N, a4, d4, in[g]);
       }
     }
   }
+}
+
+template <typename T, int KIND>
+__device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16_t& acc, int row,
+                                               int n32, int M, int N, int vec_epi, int half,
+                                               int l32, const uint32_t* act0 = nullptr) {
+  QuadIn in[4];
+  epi_tile_load<KIND>(ep, row, n32, M, N, vec_epi, half, in);
+  epi_tile_store<T, KIND>(ep, acc, row, n32, M, N, vec_epi, half, l32, act0, in);
 }
 
 template <typename T, int KIND>
@@ -515,6 +559,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     const int row = m0 + wm * MT * 32 + t * 32 + l32;
     uint32_t act0[4] = {0u, 0u, 0u, 0u};
     if constexpr (KIND == EPI_ZRAW) adapter_act_frag(ep, row, M, 0, half, act0);
+    // One column tile's operands in flight at a time: loading both tiles'
+    // before either stores lifts the z_raw kernel to 186 VGPRs, and the
+    // prefill, where a scan workgroup shares the CU, then runs slower.
 #pragma unroll
     for (int u = 0; u < NW; ++u)
       epilogue_32x32<uint16_t, KIND>(ep, acc[t][u], row, n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half,

@@ -354,8 +354,9 @@ def main():
         dev.close()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (sharding is described in "
-              "DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the prefill shards by "
+              "independent lanes, weights and banks replicated, no collective); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
 
     from pssa_amd import HipDevice, ModelWeights, PSSALayer
@@ -403,7 +404,7 @@ def main():
     ssm_tflops = work["ssm_flops"] / cfg.depth / ssm_launch_s / 1e12 if ssm_ms else 0.0
     gemm_ms = sum(v for k_, v in stages.items() if k_.startswith("gemm") or k_ == "head")
     gemm_tflops = work["gemm_flops"] / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
-    # Whole-pass floor (BASELINE.md section 2): GEMMs at the bf16 MFMA peak,
+    # Whole-pass floor: GEMMs at the bf16 MFMA peak,
     # the scan at the VALU issue peak; everything else is left out.
     floor_s = work["gemm_flops"] / (BF16_MFMA_TFLOPS * 1e12) + \
         work["ssm_elems"] * SSM_SLOTS_PER_ELEM / VALU_SLOTS_PER_S

@@ -77,12 +77,30 @@ def pmc_traffic():
     return None
 
 
+def host_threads():
+    """(threads, CPU model) for the CPU baselines: the cores this process may
+    run on (its affinity mask), capped by OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        n = min(n, int(os.environ["OMP_NUM_THREADS"]))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(1, min(n, 64)), model
+
+
 def cpu_baseline(weights, ids, budget_s: float):
     """Times the oracle's scalar prefill (one thread per lane) on a bounded
     prefix sample of the benchmark workload."""
     from oracle import oracle as O
 
-    threads = max(1, min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1, 64))
+    threads, cpu_model = host_threads()
     lanes = min(threads, ids.shape[0])
     om = O.OracleModel(weights)
     # Probe the per-token cost, then size the sample to the budget.
@@ -100,6 +118,7 @@ def cpu_baseline(weights, ids, budget_s: float):
         "value": lanes * T / wall,
         "unit": "tokens/s",
         "cores": lanes,
+        "cpu_model": cpu_model,
         "kind": "port",
         "sample": f"{lanes} lanes x first {T} tokens of the benchmark ids, one thread per lane, "
                   f"oracle prefill_inference restatement (AVX2 dot tree), {wall:.1f} s wall",
@@ -121,15 +140,20 @@ def bench_decode(dev, args, log):
     layer.stage_ids(ids)
     layer.prefill_staged()
     dev.synchronize()
-    layer.decode(4, n_lanes=S, plastic=True, graph=True)  # capture + warm-up
+    # Capture + warm-up: the first token comes from the prefill logits, the
+    # rest from captured steps; the timed runs continue from the last token.
+    warm = layer.decode(4, n_lanes=S, plastic=True, graph=True)
     t0 = time.perf_counter()
-    gen = layer.decode(steps, n_lanes=S, plastic=True, graph=True)
+    gen = layer.decode(steps, first_ids=warm[-1], plastic=True, graph=True)
     t_graph = time.perf_counter() - t0
     eager_steps = max(1, steps // 8)
     t0 = time.perf_counter()
-    layer.decode(eager_steps, n_lanes=S, plastic=True, graph=False)
+    layer.decode(eager_steps, first_ids=gen[-1], plastic=True, graph=False)
     t_eager = (time.perf_counter() - t0) / eager_steps
     layer.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_decode_baseline(w, ids, args.cpu_budget / 2, log)
     step_s = t_graph / steps
     d, s_, L = cfg.d_latent, cfg.d_state, cfg.depth
     state_bytes = 2.0 * S * L * d * s_ * 4          # carry read and written
@@ -147,7 +171,35 @@ def bench_decode(dev, args, log):
         "roofline": {"bound": "hbm", "achieved": bytes_step / step_s / 1e9, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": bytes_step / step_s / 1e9 / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_step": bytes_step},
+        "cpu_baseline": cpu,
     }
+
+
+def cpu_decode_baseline(w, ids, budget_s, log):
+    """The reference's decode loop (forward_inference + greedy choice,
+    src/pssa.rs:2387-2391, with the same plastic writes) in the oracle, one
+    thread per stream, timed over a bounded sample: as many streams as host
+    threads, from an 8-token prompt state (the 512-token prefill is outside
+    the timed region on both sides), as many steps as fit the budget."""
+    from oracle import oracle as O
+
+    threads, cpu_model = host_threads()
+    S = min(threads, ids.shape[0])
+    om = O.OracleModel(w)
+    st = om.zero_state(S)
+    lg = om.prefill_lanes(st, ids[:S, :8], threads=S)
+    cur = np.array([O.greedy(lg[i]) for i in range(S)], np.uint32)
+    t0 = time.perf_counter()
+    out, _, _ = om.decode(st, cur, steps=1, plastic=True, threads=S)
+    per_step = time.perf_counter() - t0
+    steps = int(max(1, min(32, budget_s / max(per_step, 1e-6))))
+    t0 = time.perf_counter()
+    om.decode(st, out[-1], steps=steps, plastic=True, step_base=1, threads=S)
+    wall = time.perf_counter() - t0
+    log(f"decode cpu baseline: {S} streams x {steps} steps, {wall:.1f} s")
+    return {"value": S * steps / wall, "unit": "tokens/s", "cores": S, "cpu_model": cpu_model, "kind": "port",
+            "sample": f"{S} streams x {steps} plastic greedy steps after an 8-token prompt, one thread per stream, "
+                      f"oracle forward_inference restatement, {wall:.1f} s wall"}
 
 
 def bench_train_forward(dev, args, log, w=None, ids=None):
@@ -227,17 +279,37 @@ def bench_retrieval(dev, args, log):
     dt = (time.perf_counter() - t0) / reps
     sample = 64
     _, _, ridx = O.retrieve_batch(keys, nsq, vals, C_, q[:sample], tau, top_k)
-    exact = bool(np.array_equal(idx.to_host()[:sample], ridx))
+    dev_idx = idx.to_host()
+    exact = bool(np.array_equal(dev_idx[:sample], ridx))
     for b in bufs + [out, mn, idx]:
         b.close()
+    cpu = None
+    if not args.no_cpu_baseline:
+        # retrieve_soft_into with top-8 per query, parallel over queries as
+        # the reference's batched read (src/gpu_batch.rs:700-740), on as many
+        # queries as fit the budget; their indices are compared as well.
+        threads, cpu_model = host_threads()
+        t0 = time.perf_counter()
+        O.retrieve_batch(keys, nsq, vals, C_, q[:256], tau, top_k, threads=threads)
+        per_q = (time.perf_counter() - t0) / 256
+        n = int(min(nq, max(256, args.cpu_budget / 2 / per_q)))
+        t0 = time.perf_counter()
+        _, _, cidx = O.retrieve_batch(keys, nsq, vals, C_, q[:n], tau, top_k, threads=threads)
+        wall = time.perf_counter() - t0
+        exact = exact and bool(np.array_equal(dev_idx[:n], cidx))
+        sample = n
+        cpu = {"value": n / wall, "unit": "queries/s", "cores": threads, "cpu_model": cpu_model, "kind": "port",
+               "sample": f"first {n} of the {nq} queries, oracle retrieve_soft_into restatement (f64 distances, "
+                         f"top-{top_k}), {threads} threads, {wall:.1f} s wall"}
     # The distance work is the q.k products of every query-slot pair.  An
     # exact ranking needs them at fp32 precision or better, so they are priced
     # at the fp32 matrix peak (the kernel itself runs split-bf16 MFMAs plus f64
     # sums for the few candidates).
     flops = 2.0 * nq * C_ * dk
-    log(f"retrieval: {dt * 1e3:.3f} ms, sample indices exact: {exact}")
+    log(f"retrieval: {dt * 1e3:.3f} ms, indices of {sample} queries exact: {exact}")
     return {"workload": f"config 4: {C_}x{dk} bank, {nq} queries, top-{top_k}, softmax readout",
-            "ms": dt * 1e3, "queries_per_s": nq / dt, "sample_indices_exact": exact,
+            "ms": dt * 1e3, "queries_per_s": nq / dt, "sample_indices_exact": exact, "queries_checked": sample,
+            "cpu_baseline": cpu,
             "roofline": {"bound": "mfma_fp32", "achieved": flops / dt / 1e12, "peak": FP32_TFLOPS,
                          "unit": "TFLOP/s", "frac": flops / dt / 1e12 / FP32_TFLOPS,
                          "floor_ms": flops / FP32_TFLOPS / 1e9}}
@@ -270,12 +342,12 @@ def bench_dense_scan(dev, args, log):
     a_dev = dev.empty((B, T, s, s), np.float32)
     chunk = 8192
     pool = householder_pair(rng, chunk, s)
-    check = None
+    a_host = np.empty((B * T, s, s), np.float32)
     for c0 in range(0, B * T, chunk):
         a = pool * (0.8 + 0.19 * rng.random((chunk, 1, s), dtype=np.float32))
-        if c0 == 0:
-            check = a[: 2 * T].copy()
+        a_host[c0:c0 + chunk] = a
         a_dev.write(a, c0 * s * s * 4)
+    a_host = a_host.reshape(B, T, s, s)
     b = rng.standard_normal((B, T, s)).astype(np.float32)
     b_dev = dev.upload(b)
     h_dev = dev.empty((B, T, s), np.float32)
@@ -291,15 +363,24 @@ def bench_dense_scan(dev, args, log):
         run()
     dev.synchronize()
     dt = (time.perf_counter() - t0) / reps
-    ref = O.dense_scan(check.reshape(2, T, s, s), b[:2])
-    got = h_dev.to_host()[:2]
-    err = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+    # The sequential recurrence over every sequence, one host thread per
+    # sequence: the CPU baseline and the full-size check at once.
+    threads, cpu_model = host_threads()
+    t0 = time.perf_counter()
+    ref = O.dense_scan(a_host, b, threads=threads)
+    cpu_wall = time.perf_counter() - t0
+    got = h_dev.to_host()
+    err = max(float(np.max(np.abs(got[i] - ref[i])) / np.max(np.abs(ref[i]))) for i in range(B))
     for buf in (a_dev, b_dev, h_dev):
         buf.close()
+    cpu = {"value": cpu_wall * 1e3, "unit": "ms", "cores": threads, "cpu_model": cpu_model, "kind": "port",
+           "sample": f"the whole workload ({B} sequences x {T} steps), oracle sequential recurrence, one thread per "
+                     f"sequence on {threads} threads"}
     nbytes = 4.0 * (B * T * s * s + 2 * B * T * s)
-    log(f"dense scan: {dt * 1e3:.3f} ms, rel err vs sequential {err:.2e}")
+    log(f"dense scan: {dt * 1e3:.3f} ms, rel err vs sequential {err:.2e} (all {B} sequences), "
+        f"cpu {cpu_wall * 1e3:.1f} ms")
     return {"workload": f"config 2: dense scan batch {B} x {T} steps, d_state {s}, fp32",
-            "ms": dt * 1e3, "rel_err_vs_sequential": err,
+            "ms": dt * 1e3, "rel_err_vs_sequential": err, "cpu_baseline": cpu,
             "roofline": {"bound": "hbm", "achieved": nbytes / dt / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": nbytes / dt / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": nbytes}}
 
@@ -451,6 +532,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
+        "precision": ("bf16 weights and GEMM operands, fp32 accumulation; fp32 scan state, "
+                      "norms, softmax and f64 distances" if args.dtype == "bf16" else
+                      "fp32 weights, operands and accumulation; f64 distances"),
         "data": "synthetic (uniform random ids, seeded N(0,0.02) weights, banks filled with 512 slots)",
         "config": {"workload": f"105M PSSA prefill: d768 s256 k32 L{cfg.depth} V16384 C512, "
                                f"{args.lanes} lanes x {args.seq} tokens, {args.dtype} weights",

@@ -407,7 +407,8 @@ int pssa_hip_batch_forward(pssa_hip_lanes* lanes, const pssa_hip_sequence* seqs,
 
 /* Device-resident prefill for measurement: stage ids on the device once,
  * then run prefill with no host traffic (asynchronous on the context stream;
- * pssa_hip_synchronize or a read completes it). */
+ * pssa_hip_synchronize or a read completes it).  read_logits copies the last
+ * prefill's last-token logits [lanes of that prefill, V]. */
 int pssa_hip_lanes_stage_ids(pssa_hip_lanes* lanes, const uint32_t* ids, size_t n_lanes,
                              size_t seq_len, char* err, size_t err_len);
 int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* lanes, char* err, size_t err_len);
@@ -423,11 +424,16 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * carry: every step is forward_inference (src/pssa.rs:2387-2391) on the
  * lane's current token followed by the greedy choice over ids 1..V-1 in
  * f32::total_cmp order, ties to the lower id (sample() at temperature 0,
- * src/inference.rs:123-127).  first_ids [n_lanes] are the tokens fed to the
- * first step; NULL feeds the greedy choice from the last prefill's logits
- * (which must have covered the same n_lanes lanes).  out_ids [steps, n_lanes]
- * receives the generated ids; logits_last [n_lanes, V] (may be NULL) the last
- * step's logits.  The choice applies the lanes' repetition penalty (see
+ * src/inference.rs:123-127).  out_ids [steps, n_lanes] receives the
+ * generated ids.  first_ids NULL continues the last prefill (which must have
+ * covered the same n_lanes lanes, with no reset, carry change or decode since)
+ * as the reference's generate loop does (src/inference.rs:367-379): row 0 is
+ * the greedy choice from the prefill's logits and each later row costs one
+ * step on the row before it (steps - 1 steps).  first_ids [n_lanes] instead
+ * are fed to a first step, and every row costs a step; a decode continues
+ * with its last row as first_ids, since that token is not yet consumed.
+ * logits_last [n_lanes, V] (may be NULL) receives the logits of the last
+ * choice.  The choice applies the lanes' repetition penalty (see
  * pssa_hip_lanes_set_repetition_penalty); non-finite logits fail the call
  * with "model emitted non-finite logits" once its steps have run, as
  * sample() refuses them (src/inference.rs:110-112).

@@ -63,8 +63,8 @@ def lib() -> C.CDLL:
         "oracle_bank_insert_gated_protected": ([vp, C.c_size_t, C.c_size_t, C.c_size_t, fp, fp, C.c_float,
                                                 C.c_float, C.c_uint64], C.c_int64),
         "oracle_bank_bump_hybrid_ages": ([vp, C.c_uint64], None),
-        "oracle_bank_set_value_cap": ([vp, C.c_size_t, C.c_size_t, C.c_float], None),
-        "oracle_clamp_value": ([fp, C.c_size_t, C.c_float], None),
+        "oracle_bank_set_value_cap": ([vp, C.c_size_t, C.c_size_t, C.c_float], C.c_int),
+        "oracle_clamp_value": ([fp, C.c_size_t, C.c_float], C.c_int),
         "oracle_retrieve_hybrid_batch": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, fp,
                                           C.c_size_t, C.c_float, C.c_size_t, fp, C.POINTER(C.c_uint64),
                                           C.c_float, fp, fp, u32p, fp, C.c_int], None),
@@ -301,18 +301,26 @@ class Bank:
     def _ref(self):
         return C.cast(C.pointer(self._blk), vp)
 
+    @staticmethod
+    def _slot(idx) -> int:
+        # -2: a capped bank refused a non-finite value (src/memory.rs:151-152).
+        if idx == -2:
+            raise ValueError("capped memory value must be finite")
+        return int(idx)
+
     def insert(self, key, val) -> int:
         k, v = f32(key), f32(val)
-        return int(lib().oracle_bank_insert(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v)))
+        return self._slot(lib().oracle_bank_insert(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v)))
 
     def insert_protected(self, key, val, surprise, step) -> int:
         k, v = f32(key), f32(val)
-        return int(lib().oracle_bank_insert_protected(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v),
-                                                      surprise, step))
+        return self._slot(lib().oracle_bank_insert_protected(self._ref(), self.capacity, self.dk, self.dv, ptr(k),
+                                                             ptr(v), surprise, step))
 
     def set_value_cap(self, cap) -> None:
         """set_value_cap (src/memory.rs:121-134); None disables it."""
-        lib().oracle_bank_set_value_cap(self._ref(), self.capacity, self.dv, 0.0 if cap is None else cap)
+        if lib().oracle_bank_set_value_cap(self._ref(), self.capacity, self.dv, 0.0 if cap is None else cap) != 0:
+            raise ValueError("capped memory value must be finite")
 
     @property
     def value_cap(self):
@@ -321,13 +329,13 @@ class Bank:
 
     def insert_gated(self, key, val, gate) -> int:
         k, v = f32(key), f32(val)
-        return int(lib().oracle_bank_insert_gated(self._ref(), self.capacity, self.dk, self.dv, ptr(k), ptr(v),
-                                                  gate))
+        return self._slot(lib().oracle_bank_insert_gated(self._ref(), self.capacity, self.dk, self.dv, ptr(k),
+                                                         ptr(v), gate))
 
     def insert_gated_protected(self, key, val, gate, surprise, step) -> int:
         k, v = f32(key), f32(val)
-        return int(lib().oracle_bank_insert_gated_protected(self._ref(), self.capacity, self.dk, self.dv, ptr(k),
-                                                            ptr(v), gate, surprise, step))
+        return self._slot(lib().oracle_bank_insert_gated_protected(self._ref(), self.capacity, self.dk, self.dv,
+                                                                   ptr(k), ptr(v), gate, surprise, step))
 
     def bump_hybrid_ages(self, times: int = 1) -> None:
         lib().oracle_bank_bump_hybrid_ages(self._ref(), times)
@@ -387,6 +395,11 @@ def dense_scan(a, b, h0=None, threads=1):
     return h
 
 
+def softplus(x) -> float:
+    """softplus (src/linalg.rs:548-551) of one f32."""
+    return float(lib().oracle_softplus(float(x)))
+
+
 def greedy(logits) -> int:
     logits = f32(logits)
     return int(lib().oracle_greedy(ptr(logits), logits.size))
@@ -395,7 +408,8 @@ def greedy(logits) -> int:
 def clamp_value(value, cap) -> np.ndarray:
     """clamp_value (src/memory.rs:150-170) on a copy."""
     v = np.array(value, dtype=np.float32, copy=True)
-    lib().oracle_clamp_value(ptr(v), v.size, cap)
+    if lib().oracle_clamp_value(ptr(v), v.size, cap) != 0:
+        raise ValueError("capped memory value must be finite")
     return v
 
 

@@ -597,10 +597,12 @@ static double value_norm_sq(const float* v, size_t n) {
   return s;
 }
 
-void oracle_clamp_value(float* value, size_t n, float cap) {
+int oracle_clamp_value(float* value, size_t n, float cap) {
   const double cap_sq = (double)cap * (double)cap;
   const double norm_sq = value_norm_sq(value, n);
-  if (norm_sq <= cap_sq) return;
+  // assert!(norm_sq.is_finite(), "capped memory value must be finite")
+  if (!std::isfinite(norm_sq)) return -1;
+  if (norm_sq <= cap_sq) return 0;
   const double scale = (double)cap / std::sqrt(norm_sq);
   for (size_t i = 0; i < n; i++) value[i] = (float)((double)value[i] * scale);
   // One ulp toward zero per pass until the rounded vector fits.
@@ -612,18 +614,25 @@ void oracle_clamp_value(float* value, size_t n, float cap) {
         u -= 1;
         std::memcpy(&value[i], &u, 4);
       }
+  return 0;
 }
 
-void oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t dv, float cap) {
-  if (cap > 0.0f)
+int oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t dv, float cap) {
+  if (cap > 0.0f) {
+    // The reference panics at the first non-finite slot; here nothing changes.
+    for (size_t s = 0; s < capacity; s++)
+      if (!std::isfinite(value_norm_sq(b->mem_values + s * dv, dv))) return -1;
     for (size_t s = 0; s < capacity; s++) oracle_clamp_value(b->mem_values + s * dv, dv, cap);
+  }
   b->mem_value_cap = cap;
+  return 0;
 }
 
 int64_t oracle_bank_insert(oracle_block* b, size_t capacity, size_t dk, size_t dv,
                            const float* key, const float* val) {
   float key_sq = squared_norm(key, dk);
   if (!(std::isfinite(key_sq) && key_sq < 1.0f)) return -1;
+  if (b->mem_value_cap > 0.0f && !std::isfinite(value_norm_sq(val, dv))) return -2;  // clamp_value's assertion
   size_t idx;
   if (b->mem_count < capacity) {
     idx = b->mem_count;
@@ -635,7 +644,7 @@ int64_t oracle_bank_insert(oracle_block* b, size_t capacity, size_t dk, size_t d
   std::memcpy(b->mem_keys + idx * dk, key, dk * 4);
   b->mem_norm_sq[idx] = key_sq;
   std::memcpy(b->mem_values + idx * dv, val, dv * 4);
-  if (b->mem_value_cap > 0.0f) oracle_clamp_value(b->mem_values + idx * dv, dv, b->mem_value_cap);
+  if (b->mem_value_cap > 0.0f) (void)oracle_clamp_value(b->mem_values + idx * dv, dv, b->mem_value_cap);
   b->mem_confidence[idx] = 1.0f;
   b->mem_last_seen[idx] = 0;
   if (b->mem_hybrid_gate) b->mem_hybrid_gate[idx] = 1.0f;  // src/memory.rs:300-301

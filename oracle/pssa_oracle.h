@@ -155,9 +155,12 @@ int64_t oracle_bank_insert_gated_protected(oracle_block* b, size_t capacity, siz
 void oracle_bank_bump_hybrid_ages(oracle_block* b, uint64_t times);
 /* set_value_cap (src/memory.rs:121-134): cap > 0 clamps every capacity slot's
  * value to Euclidean norm <= cap and caps later writes; 0 disables it and
- * keeps the values.  clamp_value's rule (src/memory.rs:150-170). */
-void oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t d_val, float cap);
-void oracle_clamp_value(float* value, size_t n, float cap);
+ * keeps the values.  clamp_value's rule (src/memory.rs:150-170).  Where the
+ * reference asserts a finite squared norm (src/memory.rs:151-152) these
+ * return -1 and change nothing; an insert into a capped bank returns -2 for
+ * such a value. */
+int oracle_bank_set_value_cap(oracle_block* b, size_t capacity, size_t d_val, float cap);
+int oracle_clamp_value(float* value, size_t n, float cap);
 /* retrieve_hybrid_into (src/memory.rs:568-660) for n_q queries against one
  * bank state (gate [count], age [count]); outputs as oracle_retrieve_batch,
  * plus weights [n_q, capacity] (may be NULL).  out_idx lists the live slots

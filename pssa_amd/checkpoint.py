@@ -18,6 +18,8 @@ import numpy as np
 from .weights import ADAPTER_RANK, ModelWeights, PSSAConfig
 
 HEADER_LEN = 22
+MAX_MODEL_DEPTH = 32  # src/checkpoint.rs:41
+U64_MAX = (1 << 64) - 1
 
 
 def fnv1a64(data: bytes) -> int:
@@ -90,16 +92,46 @@ class LoadedCheckpoint:
 
 
 def _config(r: _Reader):
+    """config_from_payload + validate_config (src/checkpoint.rs:110-147, 683-700)."""
     dims = [r.u64(n) for n in ("d_vocab", "d_latent", "d_state", "d_mem_key", "mem_capacity", "chunk_len")]
     hyper = {n: r.f32(n) for n in ("lr", "beta1", "beta2", "weight_decay", "eps", "tau_mem", "ema_alpha")}
+    if any(x == 0 for x in dims):
+        raise CheckpointError("all dimensions, memory capacity, and chunk length must be positive")
+    if not (hyper["lr"] > 0 and hyper["eps"] > 0 and hyper["tau_mem"] > 0):
+        raise CheckpointError("lr, eps, and tau_mem must be finite and positive")
+    if not (0.0 <= hyper["beta1"] < 1.0 and 0.0 <= hyper["beta2"] < 1.0):
+        raise CheckpointError("Adam betas must be in [0, 1)")
+    if not (hyper["weight_decay"] >= 0.0 and 0.0 <= hyper["ema_alpha"] <= 1.0):
+        raise CheckpointError("weight decay/ema alpha invalid")
     return dims, hyper
 
 
+def _residual_scales(r: _Reader, depth: int) -> None:
+    """The V8 scale words (src/checkpoint.rs:1053-1061, 817-830): depth - 1
+    of them, each bit-equal to 1/sqrt(depth) in f32 (the device applies that
+    constant)."""
+    scales = r.floats(depth - 1, "residual scales")
+    expected = np.float32(1.0) / np.sqrt(np.float32(depth))
+    if np.any(scales.view(np.uint32) != np.float32(expected).view(np.uint32)):
+        raise CheckpointError("residual scales must equal 1/sqrt(depth)")
+
+
 def _vocab(r: _Reader, d_vocab: int) -> list[str]:
+    """read_vocab + validate_vocab (src/checkpoint.rs:701-757)."""
     n = r.u64("vocabulary count")
     if n not in (0, d_vocab):
         raise CheckpointError("vocabulary count must be zero or d_vocab")
-    return [r.take(r.u64("vocabulary token length"), "vocabulary token").decode("utf-8") for _ in range(n)]
+    if n > (len(r.b) - r.o) // 8:
+        raise CheckpointError("vocabulary count exceeds remaining checkpoint bytes")
+    try:
+        v = [r.take(r.u64("vocabulary token length"), "vocabulary token").decode("utf-8") for _ in range(n)]
+    except UnicodeDecodeError:
+        raise CheckpointError("vocabulary token is not UTF-8") from None
+    if v and v[0] != "<unk>":
+        raise CheckpointError("vocabulary index 0 must be <unk>")
+    if len(set(v)) != len(v):
+        raise CheckpointError("vocabulary tokens must be unique")
+    return v
 
 
 def _block(r: _Reader, w: ModelWeights, l: int, carry: np.ndarray, embed_first: bool) -> None:
@@ -149,13 +181,18 @@ def load_bytes(data: bytes, verify_checksum: bool = True) -> LoadedCheckpoint:
     depth = 1
     if version == 8:
         depth = r.u64("depth")
-        n_scales = r.u64("residual scales length")
-        r.take(4 * n_scales, "residual scales")
+        if not 1 <= depth <= MAX_MODEL_DEPTH:
+            raise CheckpointError(f"depth must be in 1..={MAX_MODEL_DEPTH}")
+        if depth == 1:
+            raise CheckpointError("V8 requires stacked depth; use V7 for depth one")
+        _residual_scales(r, depth)
     cfg = PSSAConfig(depth=depth, d_vocab=V, d_latent=d, d_state=s, d_mem_key=k, mem_capacity=C,
                      tau_mem=hyper["tau_mem"])
     w = ModelWeights(cfg)
     carry = np.zeros((depth, d * s), dtype=np.float32)
     step = r.u64("step_counter")
+    if step == U64_MAX:
+        raise CheckpointError("step_counter is exhausted")
     rng = r.u64("rng state")
     vocab = _vocab(r, V)
     if version == 8:

@@ -90,19 +90,41 @@ Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_devi
 
 // Clamps every slot of a block's bank values to `cap` (set_value_cap,
 // src/memory.rs:121-134) and rebuilds the transposed readout operand.
-Status cap_bank_values(pssa_hip_model* M, pssa::DevBlock& B, float cap) {
+// Every slot's value of each given block clamped to `cap` (clamp_value,
+// src/memory.rs:150-170), committed only when no slot of any of them has a
+// non-finite norm: such a slot fails the call, as the reference's assertion
+// (src/memory.rs:151-152) does, and leaves every bank unchanged.
+Status cap_bank_values(pssa_hip_model* M, const std::vector<pssa::DevBlock*>& blocks, float cap) {
   const hipStream_t st = M->ctx->stream;
   const int C = (int)M->cfg.mem_capacity, d = (int)M->cfg.d_latent;
+  const size_t bytes = (size_t)C * d * 4;
   pssa::ValueCaps caps{};
   caps.c[0] = cap;
-  PSSA_RETURN_IF(pssa::launch_clamp_rows(st, B.values.as<float>(), B.values.as<float>(), C, d, (size_t)d, caps, C));
-  if (M->dtype == PSSA_HIP_F32)
-    return pssa::launch_transpose(st, B.values.as<float>(), B.values_t.as<float>(), 1, C, d, 1.0f);
-  DevBuf tmp;
-  PSSA_RETURN_IF(tmp.alloc((size_t)C * d * 4));
-  PSSA_RETURN_IF(pssa::launch_transpose(st, B.values.as<float>(), tmp.as<float>(), 1, C, d, 1.0f));
-  PSSA_RETURN_IF(pssa::launch_to_bf16(st, tmp.as<float>(), C, B.values_t.as<uint16_t>(), C, d, C));
-  return sync(M->ctx);  // tmp is freed at return
+  std::vector<DevBuf> capped(blocks.size());
+  DevBuf tmp, bad;
+  PSSA_RETURN_IF(bad.alloc(4));
+  PSSA_RETURN_IF(pssa::launch_fill_zero(st, bad.as<float>(), 1));
+  for (size_t i = 0; i < blocks.size(); ++i) {
+    PSSA_RETURN_IF(capped[i].alloc(bytes));
+    PSSA_RETURN_IF(pssa::launch_clamp_rows(st, blocks[i]->values.as<float>(), capped[i].as<float>(), C, d,
+                                           (size_t)d, caps, C, bad.as<int>()));
+  }
+  int flag = 0;
+  PSSA_RETURN_IF(download(&flag, bad, 4, st));
+  PSSA_RETURN_IF(sync(M->ctx));
+  if (flag) return Status::Invalid("capped memory value must be finite");
+  if (M->dtype == PSSA_HIP_BF16) PSSA_RETURN_IF(tmp.alloc(bytes));
+  for (size_t i = 0; i < blocks.size(); ++i) {
+    pssa::DevBlock& B = *blocks[i];
+    PSSA_HIP_TRY(hipMemcpyAsync(B.values.p, capped[i].p, bytes, hipMemcpyDeviceToDevice, st));
+    if (M->dtype == PSSA_HIP_F32) {
+      PSSA_RETURN_IF(pssa::launch_transpose(st, B.values.as<float>(), B.values_t.as<float>(), 1, C, d, 1.0f));
+    } else {
+      PSSA_RETURN_IF(pssa::launch_transpose(st, B.values.as<float>(), tmp.as<float>(), 1, C, d, 1.0f));
+      PSSA_RETURN_IF(pssa::launch_to_bf16(st, tmp.as<float>(), C, B.values_t.as<uint16_t>(), C, d, C));
+    }
+  }
+  return sync(M->ctx);  // the staging buffers are freed at return
 }
 
 // Empties every lane's repetition-penalty window (a new generation,
@@ -1008,7 +1030,7 @@ int pssa_hip_model_load(pssa_hip_ctx* ctx, const pssa_hip_weights* w, int weight
       PSSA_RETURN_IF(upload_weight(B.values_t, vt.data(), vt.size(), weight_dtype, st));
       PSSA_RETURN_IF(sync(ctx));  // host staging vectors are reused
       // Values of a capped bank are capped (a no-op for values that were).
-      if (B.value_cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(m.get(), B, B.value_cap));
+      if (B.value_cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(m.get(), {&B}, B.value_cap));
     }
     const unsigned long long step0 = 0;
     PSSA_RETURN_IF(upload(m->step, &step0, 8, st));
@@ -1068,7 +1090,7 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     PSSA_RETURN_IF(L->hist.alloc(lanes * pssa_hip_lanes::kHist * 4));
     PSSA_RETURN_IF(L->hist_n.alloc(lanes * 4));
     PSSA_RETURN_IF(L->hist_pos.alloc(lanes * 4));
-    PSSA_RETURN_IF(L->nonfinite.alloc(4));
+    PSSA_RETURN_IF(L->nonfinite.alloc(8));  // [0] non-finite logits, [1] non-finite capped bank value
     PSSA_RETURN_IF(clear_history(L.get()));
     PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming));
     for (int g = 0; g < pssa_hip_lanes::kMaxGroups - 1; ++g) {
@@ -1099,6 +1121,9 @@ int pssa_hip_lanes_reset(pssa_hip_lanes* L, char* err, size_t err_len) {
     PSSA_RETURN_IF(pssa::launch_fill_zero(L->ctx->stream, L->carry.as<float>(),
                                           L->lanes * c.depth * c.d_latent * c.d_state));
     PSSA_RETURN_IF(clear_history(L));
+    // No prefill logits to continue from (reset_recurrent_state is followed
+    // by a fresh prefill, src/inference.rs:347-355).
+    L->logit_lanes = 0;
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
@@ -1132,6 +1157,8 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* L, const float* in, size_t len, cha
     DevBuf tmp;
     PSSA_RETURN_IF(upload(tmp, in, n * 4, L->ctx->stream));
     PSSA_RETURN_IF(carry_layout(L, tmp.as<float>(), L->carry.as<float>(), true));
+    // The prefill logits belong to the replaced carries.
+    L->logit_lanes = 0;
     return sync(L->ctx);
   };
   return pssa::finish(body(), err, err_len);
@@ -1154,6 +1181,7 @@ int pssa_hip_prefill(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes, siz
     PSSA_RETURN_IF(invalid_prefix_locked(L, ids, n_lanes, seq_len));
     PSSA_RETURN_IF(stage_ids_locked(L, ids, n_lanes, seq_len));
     PSSA_RETURN_IF(pssa::run_prefill(L, n_lanes, seq_len));
+    L->logit_lanes = n_lanes;
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
     return sync(L->ctx);
   };
@@ -1258,6 +1286,7 @@ static Status invalid_prefix_locked(pssa_hip_lanes* L, const uint32_t* ids, size
   for (size_t i = 0; i < n_lanes; ++i) packed.insert(packed.end(), ids + i * T, ids + i * T + lens[i]);
   PSSA_RETURN_IF(ragged_locked(L, packed.data(), lens.data(), n_lanes));
   L->staged_lanes = L->staged_len = 0;
+  L->logit_lanes = 0;  // no decode continues from a failed prompt
   return Status::Invalid("prompt ID " + std::to_string(first_bad) + " outside model vocabulary");
 }
 
@@ -1280,8 +1309,8 @@ int pssa_hip_prefill_ragged(pssa_hip_lanes* L, const uint32_t* ids, const uint64
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     PSSA_RETURN_IF(ragged_locked(L, ids, lens, n_lanes));
-    L->staged_lanes = n_lanes;  // decode may continue from these logits
-    L->staged_len = 0;
+    L->staged_lanes = L->staged_len = 0;  // `ids` holds the packed prompts
+    L->logit_lanes = n_lanes;             // decode may continue from these logits
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
     return sync(L->ctx);
   };
@@ -1311,6 +1340,7 @@ int pssa_hip_prefill_cancellable(pssa_hip_lanes* L, const uint32_t* ids, size_t 
       if (cancelled && cancelled(user)) {
         was_cancelled = true;
         L->staged_lanes = L->staged_len = 0;
+        L->logit_lanes = 0;
         return Status::Ok();
       }
       const size_t T = std::min(c, seq_len - t0);
@@ -1322,8 +1352,8 @@ int pssa_hip_prefill_cancellable(pssa_hip_lanes* L, const uint32_t* ids, size_t 
       PSSA_RETURN_IF(sync(L->ctx));  // `part` is refilled next
       if (processed) *processed = t0 + T;
     }
-    L->staged_lanes = n_lanes;
-    L->staged_len = 0;
+    L->staged_lanes = L->staged_len = 0;  // `ids` holds the last chunk
+    L->logit_lanes = n_lanes;
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, L->ctx->stream));
     return sync(L->ctx);
   };
@@ -1374,7 +1404,7 @@ int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, siz
       PSSA_RETURN_IF(L->tok_meta.alloc(2 * L->max_tokens * 4));
       PSSA_RETURN_IF(L->tok_loss.alloc(L->max_tokens * 4));
     }
-    L->staged_lanes = L->staged_len = 0;  // lanes->logits no longer follows a prefill
+    L->logit_lanes = 0;  // lanes->logits no longer follows a prefill
 
     // Packed token offsets in the given order; the device works in order of
     // decreasing length so that the lanes still running are always a prefix.
@@ -1482,7 +1512,9 @@ int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* L, char* err, size_t err_len) 
     PSSA_RETURN_IF(need(L->staged_len > 0, "no ids staged"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
-    return pssa::run_prefill(L, L->staged_lanes, L->staged_len);
+    PSSA_RETURN_IF(pssa::run_prefill(L, L->staged_lanes, L->staged_len));
+    L->logit_lanes = L->staged_lanes;
+    return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);
 }
@@ -1490,8 +1522,9 @@ int pssa_hip_lanes_prefill_staged(pssa_hip_lanes* L, char* err, size_t err_len) 
 int pssa_hip_lanes_read_logits(pssa_hip_lanes* L, float* out, size_t len, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L && out, "null argument"));
-    const size_t n = L->staged_lanes * L->model->cfg.d_vocab;
-    PSSA_RETURN_IF(need(n > 0 && len == n, "logits length must be staged_lanes*d_vocab"));
+    const size_t n = L->logit_lanes * L->model->cfg.d_vocab;
+    PSSA_RETURN_IF(need(n > 0, "no prefill logits to read"));
+    PSSA_RETURN_IF(need(len == n, "logits length must be the last prefill's lanes*d_vocab"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     PSSA_RETURN_IF(download(out, L->logits, n * 4, L->ctx->stream));
@@ -1568,10 +1601,10 @@ int pssa_hip_model_set_value_cap(pssa_hip_model* M, float cap, char* err, size_t
     PSSA_RETURN_IF(need(std::isfinite(cap) && cap >= 0.0f, "memory value cap must be positive and finite"));
     std::lock_guard<std::mutex> g(M->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(M->ctx->device));
-    for (pssa::DevBlock& B : M->blocks) {
-      if (cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(M, B, cap));
-      B.value_cap = cap;
-    }
+    std::vector<pssa::DevBlock*> all;
+    for (pssa::DevBlock& B : M->blocks) all.push_back(&B);
+    if (cap > 0.0f) PSSA_RETURN_IF(cap_bank_values(M, all, cap));
+    for (pssa::DevBlock& B : M->blocks) B.value_cap = cap;
     ++M->hybrid_epoch;  // captured bank writes hold the old cap
     return sync(M->ctx);
   };
@@ -1704,7 +1737,7 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
         if (first_ids[i] >= V)
           return Status::Invalid("prompt ID " + std::to_string(first_ids[i]) + " outside model vocabulary");
     } else {
-      PSSA_RETURN_IF(need(L->staged_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
+      PSSA_RETURN_IF(need(L->logit_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
     }
     const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
     if (plastic) {
@@ -1718,28 +1751,38 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
     PSSA_RETURN_IF(ensure_decode_buffers(L, n_lanes, steps));
-    PSSA_RETURN_IF(pssa::launch_fill_zero(st, static_cast<float*>(L->nonfinite.p), 1));
-    if (first_ids)
-      PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, first_ids, n_lanes * 4, hipMemcpyHostToDevice, st));
-    else
-      PSSA_RETURN_IF(pssa::run_greedy_from_logits(L, n_lanes));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(st, static_cast<float*>(L->nonfinite.p), 2));
     const int zero = 0;
     PSSA_HIP_TRY(hipMemcpyAsync(L->gen_pos.p, &zero, 4, hipMemcpyHostToDevice, st));
-    if (flags & PSSA_HIP_DECODE_GRAPH) {
-      PSSA_RETURN_IF(capture_decode_step(L, n_lanes, plastic));
-      for (size_t t = 0; t < steps; ++t) PSSA_HIP_TRY(hipGraphLaunch(L->graph_exec, st));
+    // After a prefill the first generated token is the choice from its logits
+    // (src/inference.rs:367-379), and each later one costs a forward step of
+    // the token before it; given first ids, every token costs a step.
+    size_t fwd_steps = steps;
+    if (first_ids) {
+      PSSA_HIP_TRY(hipMemcpyAsync(L->ids.p, first_ids, n_lanes * 4, hipMemcpyHostToDevice, st));
     } else {
-      for (size_t t = 0; t < steps; ++t) PSSA_RETURN_IF(pssa::run_decode_step(L, n_lanes, plastic));
+      PSSA_RETURN_IF(pssa::run_greedy_from_logits(L, n_lanes, true));
+      fwd_steps = steps - 1;
+    }
+    if (fwd_steps > 0 && (flags & PSSA_HIP_DECODE_GRAPH)) {
+      PSSA_RETURN_IF(capture_decode_step(L, n_lanes, plastic));
+      for (size_t t = 0; t < fwd_steps; ++t) PSSA_HIP_TRY(hipGraphLaunch(L->graph_exec, st));
+    } else {
+      for (size_t t = 0; t < fwd_steps; ++t) PSSA_RETURN_IF(pssa::run_decode_step(L, n_lanes, plastic));
     }
     PSSA_RETURN_IF(download(out_ids, L->gen_ids, steps * n_lanes * 4, st));
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
-    int nonfinite = 0;
-    PSSA_RETURN_IF(download(&nonfinite, L->nonfinite, 4, st));
-    L->staged_lanes = n_lanes;
-    L->staged_len = 1;
+    int nonfinite[2] = {0, 0};
+    PSSA_RETURN_IF(download(nonfinite, L->nonfinite, 8, st));
+    // The last generated token has not been consumed: a continuation passes
+    // it as first_ids.  `ids` now holds the step tokens.
+    L->staged_lanes = L->staged_len = 0;
+    L->logit_lanes = 0;
     PSSA_RETURN_IF(sync(L->ctx));
     // sample() refuses non-finite logits (src/inference.rs:110-112).
-    if (nonfinite) return Status::Invalid("model emitted non-finite logits");
+    if (nonfinite[0]) return Status::Invalid("model emitted non-finite logits");
+    // clamp_value refuses a non-finite value (src/memory.rs:151-152).
+    if (nonfinite[1]) return Status::Invalid("capped memory value must be finite");
     return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);

@@ -459,7 +459,7 @@ Status init_decode_attributes() {
   return Status::Ok();
 }
 
-Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes) {
+Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes, bool record) {
   const hipStream_t st = L->ctx->stream;
   const int V = (int)L->model->cfg.d_vocab;
   GreedyWindow gw;
@@ -469,8 +469,14 @@ Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes) {
   gw.penalty = L->rep_penalty;
   gw.nonfinite = L->nonfinite.as<int>();
   greedy_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
-                                                   nullptr, nullptr, (int)n_lanes, nullptr, gw);
+                                                   record ? L->gen_ids.as<uint32_t>() : nullptr,
+                                                   record ? L->gen_pos.as<int>() : nullptr, (int)n_lanes, nullptr,
+                                                   gw);
   PSSA_LAUNCH_CHECK("greedy");
+  if (record) {
+    advance_pos_kernel<<<1, 64, 0, st>>>(L->gen_pos.as<int>());
+    PSSA_LAUNCH_CHECK("advance");
+  }
   return Status::Ok();
 }
 
@@ -525,7 +531,7 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     p.vsrc = p.tap_z;
     if (any_cap) {
       PSSA_RETURN_IF(launch_clamp_rows(st, L->tap_z.as<float>(), L->tap_zcap.as<float>(), (int)(c.depth * n), d,
-                                       (size_t)d, caps, (int)n));
+                                       (size_t)d, caps, (int)n, L->nonfinite.as<int>() + 1));
       p.vsrc = L->tap_zcap.as<float>();
     }
     p.tap_a = L->tap_a.as<float>();

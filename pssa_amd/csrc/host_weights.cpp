@@ -230,6 +230,8 @@ static double value_norm_sq(const float* v, size_t n) {
   return s;
 }
 
+// The caller has checked that the squared norm is finite (the reference
+// asserts it, src/memory.rs:151-152).
 static void clamp_value(float* v, size_t n, float cap) {
   const double cap_sq = (double)cap * (double)cap;
   const double nsq = value_norm_sq(v, n);
@@ -253,6 +255,15 @@ extern "C" int pssa_hip_weights_set_value_cap(const pssa_hip_weights* w, float c
     return PSSA_HIP_EINVAL;
   }
   const pssa_hip_config& c = w->cfg;
+  // Every capacity slot is clamped, so every one must have a finite norm;
+  // checked for all blocks before any value changes.
+  if (cap > 0.0f)
+    for (size_t l = 0; l < c.depth; l++)
+      for (size_t s = 0; s < c.mem_capacity; s++)
+        if (!std::isfinite(value_norm_sq(w->blocks[l].mem_values + s * c.d_latent, c.d_latent))) {
+          set_err(err, err_len, "capped memory value must be finite");
+          return PSSA_HIP_EINVAL;
+        }
   for (size_t l = 0; l < c.depth; l++) {
     pssa_hip_block& b = w->blocks[l];
     if (cap > 0.0f)

@@ -56,8 +56,9 @@ constexpr int kMaxTopK = 64;
 struct ValueCaps {
   float c[32];
 };
-// clamp_value (src/memory.rs:150-170) on rows [n_rows, d], src -> dst.
+// clamp_value (src/memory.rs:150-170) on rows [n_rows, d], src -> dst.  A
+// capped row with a non-finite norm is copied and sets *bad = 1 (may be null).
 Status launch_clamp_rows(hipStream_t stream, const float* src, float* dst, int n_rows, int d, size_t ld,
-                         const ValueCaps& caps, int rows_per_cap);
+                         const ValueCaps& caps, int rows_per_cap, int* bad);
 
 }  // namespace pssa

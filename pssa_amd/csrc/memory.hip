@@ -1084,9 +1084,11 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
 // exceeds it.  The squared norm is the reference's left-to-right f64 sum
 // (src/memory.rs:190-192), so every decision and bit equals its own.  One
 // wave per row, staged in LDS.  Row r takes caps.c[r / rows_per_cap]; a cap
-// <= 0 copies the row.
+// <= 0 copies the row.  A capped row whose squared norm is not finite is
+// copied unchanged and raises *bad (the reference asserts the norm is
+// finite, src/memory.rs:151-152).
 __global__ __launch_bounds__(64) void clamp_rows_kernel(const float* src, float* dst, int d, size_t ld,
-                                                        ValueCaps caps, int rows_per_cap) {
+                                                        ValueCaps caps, int rows_per_cap, int* bad) {
   extern __shared__ float srow[];
   __shared__ double s_norm;
   const int row = blockIdx.x, lane = threadIdx.x;
@@ -1109,12 +1111,14 @@ __global__ __launch_bounds__(64) void clamp_rows_kernel(const float* src, float*
   if (cap > 0.0f) {
     const double cap_sq = (double)cap * (double)cap;
     const double nsq = norm_sq();
-    if (nsq > cap_sq) {
+    if (!isfinite(nsq)) {
+      if (lane == 0 && bad) bad[0] = 1;
+    } else if (nsq > cap_sq) {
       const double scale = (double)cap / sqrt(nsq);
       for (int j = lane; j < d; j += 64) srow[j] = (float)((double)srow[j] * scale);
       __syncthreads();
-      // Each pass shrinks every nonzero magnitude; a non-finite row ends the
-      // loop through a NaN norm, and the pass count bounds it regardless.
+      // Each pass shrinks every nonzero magnitude; the pass count bounds the
+      // loop regardless.
       for (int pass = 0; pass < 1024 && norm_sq() > cap_sq; ++pass) {
         for (int j = lane; j < d; j += 64)
           if (srow[j] != 0.0f) srow[j] = __uint_as_float(__float_as_uint(srow[j]) - 1u);
@@ -1126,10 +1130,10 @@ __global__ __launch_bounds__(64) void clamp_rows_kernel(const float* src, float*
 }
 
 Status launch_clamp_rows(hipStream_t stream, const float* src, float* dst, int n_rows, int d, size_t ld,
-                         const ValueCaps& caps, int rows_per_cap) {
+                         const ValueCaps& caps, int rows_per_cap, int* bad) {
   if (n_rows <= 0 || d <= 0) return Status::Ok();
   if ((size_t)d * 4 > 64 * 1024) return Status::Invalid("value cap: rows wider than 16384");
-  clamp_rows_kernel<<<(unsigned)n_rows, 64, (size_t)d * 4, stream>>>(src, dst, d, ld, caps, rows_per_cap);
+  clamp_rows_kernel<<<(unsigned)n_rows, 64, (size_t)d * 4, stream>>>(src, dst, d, ld, caps, rows_per_cap, bad);
   PSSA_LAUNCH_CHECK("clamp_rows");
   return Status::Ok();
 }

@@ -114,7 +114,12 @@ struct pssa_hip_lanes {
   size_t graph_lanes = 0;
   int graph_plastic = -1;
   uint64_t graph_hybrid_epoch = 0;
+  // Ids staged on the device by stage_ids (lanes x len; 0 once `ids` holds
+  // anything else) and the lanes whose last-token logits from a prefill are
+  // in `logits` (0 when none are: a decode without first ids continues from
+  // them).
   size_t staged_lanes = 0, staged_len = 0;
+  size_t logit_lanes = 0;
   bool timing = false;
   std::array<float, pssa::ST_COUNT> stage_ms{};
   std::array<int, pssa::ST_COUNT> stage_calls{};
@@ -178,8 +183,9 @@ Status launch_hist_append(pssa_hip_lanes* L, const uint32_t* ids, size_t n_lanes
 // the Hebbian adapter update.  Only kernel launches: safe to capture.
 Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic);
 // Greedy choice from lanes->logits without a forward step (first decode
-// token after a prefill).
-Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes);
+// token after a prefill); with `record` it is also the generated row at
+// gen_pos, which then advances.
+Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes, bool record);
 // Dynamic LDS of the bank-write kernel and its per-device attribute set-up.
 size_t bank_write_lds(int capacity, int lanes);
 // LDS of the Hebbian update for adapter rank `rank` and `lanes` lanes.

@@ -301,134 +301,145 @@ __global__ __launch_bounds__(256) void token_ce_kernel(const float* __restrict__
   }
 }
 
-// Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`.  Every buffer
-// pointer is offset to the view's rows, so disjoint views can run
-// concurrently.  `first_in_done` (may be null) is recorded once layer 0's
-// input projection has been issued.
-static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T,
-                           bool taps, bool timing, hipEvent_t first_in_done, float* y_part,
-                           const TrainRows* tr, bool concurrent) {
-  const pssa_hip_model* M = L->model;
-  const pssa_hip_config& c = M->cfg;
-  const int d = (int)c.d_latent, s = (int)c.d_state, k = (int)c.d_mem_key;
-  const int C = (int)c.mem_capacity, r = (int)c.adapter_rank, V = (int)c.d_vocab;
-  const int n_in = (int)M->n_in;
-  const size_t rows = n_lanes * T;
-  const size_t row0 = lane0 * T;
-  const int m = (int)rows;
-  const int dt = M->dtype;
-  const bool bf16 = dt == PSSA_HIP_BF16;
-  const size_t es = bf16 ? 2 : 4;
-  const float ssm_scale = 1.0f / sqrtf((float)s);
-  const float depth_scale = 1.0f / sqrtf((float)c.depth);
-  const float logit_scale = 1.0f / sqrtf((float)d);
-  // Column offsets inside the fused projection output P.
-  const int o_b = d, o_c = d + s, o_qx = d + 2 * s, o_gate = d + 2 * s + k, o_act = 2 * d + 2 * s + k;
+// Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`, enqueued in
+// pieces (embed, each layer, head) so that concurrent views can be enqueued
+// layer by layer.  Every buffer pointer is offset to the view's rows, so
+// disjoint views can run concurrently.  `first_in_done` (may be null) is
+// recorded once layer 0's input projection has been issued.
+class PrefillView {
+ public:
+  PrefillView(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T, bool taps, bool timing,
+              hipEvent_t first_in_done, float* y_part, const TrainRows* tr, bool concurrent)
+      : L_(L), M_(L->model), c_(L->model->cfg), st_(st), n_lanes_(n_lanes), T_(T), taps_(taps),
+        first_in_done_(first_in_done), y_part_(y_part), tr_(tr), concurrent_(concurrent),
+        tm_{timing ? L : nullptr, st} {
+    d_ = (int)c_.d_latent;
+    s_ = (int)c_.d_state;
+    k_ = (int)c_.d_mem_key;
+    C_ = (int)c_.mem_capacity;
+    r_ = (int)c_.adapter_rank;
+    V_ = (int)c_.d_vocab;
+    n_in_ = (int)M_->n_in;
+    rows_ = n_lanes * T;
+    const size_t row0 = lane0 * T;
+    m_ = (int)rows_;
+    dt_ = M_->dtype;
+    bf16_ = dt_ == PSSA_HIP_BF16;
+    const size_t es = bf16_ ? 2 : 4;
+    const int d = d_, k = k_, C = C_, V = V_;
+    X_ = L->X.as<float>() + row0 * d;
+    XN_ = L->XN.as<float>() + row0 * d;
+    P_ = L->P.as<float>() + row0 * n_in_;
+    Y_ = L->Y.as<float>() + row0 * d;
+    Q_ = L->Q.as<float>() + row0 * k;
+    Zr_ = L->Zraw.as<float>() + row0 * d;
+    // GEMM operands in the model's operand type (aliases of the fp32 buffers
+    // in an fp32 model).
+    XNh16_ = bf16_ ? L->XNh.as<uint16_t>() + row0 * d : nullptr;
+    XNh_ = bf16_ ? (void*)XNh16_ : (void*)XN_;
+    Yh_ = bf16_ ? (void*)(L->Yh.as<uint16_t>() + row0 * d) : (void*)Y_;
+    Zrh_ = bf16_ ? (void*)(L->Zrawh.as<uint16_t>() + row0 * d) : (void*)Zr_;
+    Wm_ = static_cast<char*>(L->Wm.p) + row0 * C * es;
+    Mv_ = static_cast<char*>(L->Mval.p) + row0 * d * es;
+    H1_ = static_cast<char*>(L->H1.p) + row0 * 2 * d * es;
+    ids_ = (tr ? tr->ids : L->ids.as<uint32_t>()) + row0;
+    carry_ = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c_.depth * (size_t)d * s_;
+    logits_ = L->logits.as<float>() + lane0 * (size_t)V;
+    row0_ = row0;
+  }
 
-  float* X = L->X.as<float>() + row0 * d;
-  float* XN = L->XN.as<float>() + row0 * d;
-  float* P = L->P.as<float>() + row0 * n_in;
-  float* Y = L->Y.as<float>() + row0 * d;
-  float* Q = L->Q.as<float>() + row0 * k;
-  float* Zr = L->Zraw.as<float>() + row0 * d;
-  // GEMM operands in the model's operand type (aliases of the fp32 buffers
-  // in an fp32 model).
-  uint16_t* XNh16 = bf16 ? L->XNh.as<uint16_t>() + row0 * d : nullptr;
-  void* XNh = bf16 ? (void*)XNh16 : (void*)XN;
-  void* Yh = bf16 ? (void*)(L->Yh.as<uint16_t>() + row0 * d) : (void*)Y;
-  void* Zrh = bf16 ? (void*)(L->Zrawh.as<uint16_t>() + row0 * d) : (void*)Zr;
-  void* Wm = static_cast<char*>(L->Wm.p) + row0 * C * es;
-  void* Mv = static_cast<char*>(L->Mval.p) + row0 * d * es;
-  void* H1 = static_cast<char*>(L->H1.p) + row0 * 2 * d * es;
-  const uint32_t* ids = (tr ? tr->ids : L->ids.as<uint32_t>()) + row0;
-  float* carry = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c.depth * (size_t)d * s;
-  float* logits = L->logits.as<float>() + lane0 * (size_t)V;
+  Status embed() {
+    PSSA_RETURN_IF(tm_.mark(ST_EMBED));
+    embed_kernel<<<(unsigned)rows_, 256, 0, st_>>>(ids_, M_->embed.as<float>(), X_, d_, rows_);
+    PSSA_LAUNCH_CHECK("embed");
+    return Status::Ok();
+  }
 
-  pssa_hip_lanes* TL = timing ? L : nullptr;
-  Timer tm{TL, st};
-  PSSA_RETURN_IF(tm.mark(ST_EMBED));
-  embed_kernel<<<(unsigned)rows, 256, 0, st>>>(ids, M->embed.as<float>(), X, d, rows);
-  PSSA_LAUNCH_CHECK("embed");
-
-  for (size_t l = 0; l < c.depth; ++l) {
-    const DevBlock& B = M->blocks[l];
+  Status layer(size_t l) {
+    const DevBlock& B = M_->blocks[l];
+    const int d = d_, s = s_, k = k_, C = C_, r = r_, n_in = n_in_, m = m_, dt = dt_;
+    const size_t rows = rows_, T = T_;
+    const bool bf16 = bf16_, taps = taps_;
+    hipStream_t st = st_;
+    // Column offsets inside the fused projection output P.
+    const int o_b = d, o_c = d + s, o_qx = d + 2 * s, o_gate = d + 2 * s + k, o_act = 2 * d + 2 * s + k;
     const bool step_y = ssm_step_writes_y((int)T, s);
-    PSSA_RETURN_IF(tm.mark(ST_NORM));
+    PSSA_RETURN_IF(tm_.mark(ST_NORM));
     rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
-        X, B.gamma.as<float>(), B.beta.as<float>(), XN, XNh16,
-        ssm_needs_zeroed_y(s) && !step_y ? Y : nullptr, d, rows);
+        X_, B.gamma.as<float>(), B.beta.as<float>(), XN_, XNh16_,
+        ssm_needs_zeroed_y(s) && !step_y ? Y_ : nullptr, d, rows);
     PSSA_LAUNCH_CHECK("rmsnorm");
 
     // [delta | B | C | q_x | gate | adapter act] = x W_in^T with softplus,
     // sigmoid and SiLU applied per column segment.
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_IN));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_IN));
     EpiParams e_in;
     e_in.kind = EPI_SEGMENTS;
     e_in.seg[0] = d;
     e_in.seg[1] = o_gate;
     e_in.seg[2] = o_act;
     e_in.seg[3] = n_in;
-    e_in.out32 = P;
+    e_in.out32 = P_;
     e_in.ld32 = n_in;
     if (taps) {  // the adapter activations of this step, for the Hebbian update
       e_in.kind = EPI_SEGMENTS_TAP;
-      e_in.tap = L->tap_act.as<float>() + l * rows * r;
+      e_in.tap = L_->tap_act.as<float>() + l * rows * r;
       e_in.ld_tap = r;
     }
-    PSSA_RETURN_IF(launch_gemm(st, dt, XNh, d, B.w_in.p, d, m, n_in, d, e_in));
-    if (l == 0 && first_in_done) PSSA_HIP_TRY(hipEventRecord(first_in_done, st));
+    PSSA_RETURN_IF(launch_gemm(st, dt, XNh_, d, B.w_in.p, d, m, n_in, d, e_in));
+    if (l == 0 && first_in_done_) PSSA_HIP_TRY(hipEventRecord(first_in_done_, st));
     if (taps && B.hybrid) {  // the write gate of a gated protected insert
-      gate_mean_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(P + o_gate, n_in, d, (int)rows,
-                                                                       L->tap_gmean.as<float>() + l * rows);
+      gate_mean_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(P_ + o_gate, n_in, d, (int)rows,
+                                                                       L_->tap_gmean.as<float>() + l * rows);
       PSSA_LAUNCH_CHECK("gate_mean");
     }
 
-    PSSA_RETURN_IF(tm.mark(ST_SSM));
+    PSSA_RETURN_IF(tm_.mark(ST_SSM));
     SsmArgs sa;
-    sa.delta = P;
+    sa.delta = P_;
     sa.ld_delta = n_in;
-    sa.bproj = P + o_b;
+    sa.bproj = P_ + o_b;
     sa.ld_b = n_in;
-    sa.cproj = P + o_c;
+    sa.cproj = P_ + o_c;
     sa.ld_c = n_in;
-    sa.xn = XN;
+    sa.xn = XN_;
     sa.ld_x = d;
     sa.rates2 = B.rates2.as<float>();
-    sa.carry = carry + l * (size_t)d * s;
-    sa.carry_stride = (long)(c.depth * (size_t)d * s);
-    sa.y = Y;
+    sa.carry = carry_ + l * (size_t)d * s;
+    sa.carry_stride = (long)(c_.depth * (size_t)d * s);
+    sa.y = Y_;
     sa.ld_y = d;
     sa.T = (int)T;
     sa.d = d;
     sa.s = s;
-    sa.lanes = (int)n_lanes;
-    sa.y_part = y_part;
-    sa.concurrent = concurrent ? 1 : 0;
+    sa.lanes = (int)n_lanes_;
+    sa.y_part = y_part_;
+    sa.concurrent = concurrent_ ? 1 : 0;
     if (bf16 && step_y) {
-      sa.y16 = static_cast<uint16_t*>(Yh);
+      sa.y16 = static_cast<uint16_t*>(Yh_);
       sa.ld_y16 = d;
     }
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
     // q_euc = y W_qh^T + q_x.  In a bf16 model y enters the product rounded
     // to bf16: the single-step scan writes that copy itself, otherwise the
     // product rounds the fp32 readout as it loads it.
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_QH));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_QH));
     EpiParams e_q;
     e_q.kind = EPI_ADD_AUX;
-    e_q.aux = P + o_qx;
+    e_q.aux = P_ + o_qx;
     e_q.ld_aux = n_in;
-    e_q.out32 = Q;
+    e_q.out32 = Q_;
     e_q.ld32 = k;
     if (bf16 && !step_y && d % 16 == 0)
-      PSSA_RETURN_IF(launch_gemm_f32a(st, Y, d, static_cast<const uint16_t*>(B.w_qh.p), d, m, k, d, e_q));
+      PSSA_RETURN_IF(launch_gemm_f32a(st, Y_, d, static_cast<const uint16_t*>(B.w_qh.p), d, m, k, d, e_q));
     else {
-      if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y, d, static_cast<uint16_t*>(Yh), d, rows, d));
-      PSSA_RETURN_IF(launch_gemm(st, dt, Yh, d, B.w_qh.p, d, m, k, d, e_q));
+      if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y_, d, static_cast<uint16_t*>(Yh_), d, rows, d));
+      PSSA_RETURN_IF(launch_gemm(st, dt, Yh_, d, B.w_qh.p, d, m, k, d, e_q));
     }
 
-    PSSA_RETURN_IF(tm.mark(ST_RETRIEVE));
+    PSSA_RETURN_IF(tm_.mark(ST_RETRIEVE));
     RetrieveArgs ra;
-    ra.q = Q;
+    ra.q = Q_;
     ra.ld_q = k;
     ra.project = 1;
     ra.keys = B.keys.as<float>();
@@ -439,9 +450,9 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
     ra.capacity = C;
     ra.count = C;  // upper bound; the live count is read on the device
     ra.count_dev = B.meta.as<int>();
-    ra.tau = c.tau_mem;
+    ra.tau = c_.tau_mem;
     ra.top_k = B.top_k;
-    if (taps) ra.q_pnc = L->tap_q.as<float>() + l * rows * k;
+    if (taps) ra.q_pnc = L_->tap_q.as<float>() + l * rows * k;
     if (B.hybrid) {  // token t reads with the ages bumped t + 1 times
       ra.hgate = B.hgate.as<float>();
       ra.hage = B.hage.as<unsigned long long>();
@@ -449,108 +460,136 @@ static Status prefill_view(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size
       ra.age_T = (int)T;
     }
     if (bf16)
-      ra.weights16 = static_cast<uint16_t*>(Wm);
+      ra.weights16 = static_cast<uint16_t*>(Wm_);
     else
-      ra.weights = static_cast<float*>(Wm);
+      ra.weights = static_cast<float*>(Wm_);
     PSSA_RETURN_IF(launch_retrieve(st, ra));
 
     // m_val = weights values (soft read readout).
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_READ));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_READ));
     {
       // Slots past the live count carry zero weight, so the product runs
       // over the whole capacity.
       EpiParams e_m;
-      e_m.out16 = Mv;
+      e_m.out16 = Mv_;
       e_m.ld16 = d;
-      PSSA_RETURN_IF(launch_gemm(st, dt, Wm, C, B.values_t.p, C, m, d, C, e_m));
+      PSSA_RETURN_IF(launch_gemm(st, dt, Wm_, C, B.values_t.p, C, m, d, C, e_m));
     }
 
     // z_raw = y/sqrt(s) + gate * (m_val W_proj^T) + U_eff act.
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_PROJ));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_PROJ));
     EpiParams e_z;
     e_z.kind = EPI_ZRAW;
-    e_z.y = Y;
+    e_z.y = Y_;
     e_z.ld_y = d;
-    e_z.g = P + o_gate;
+    e_z.g = P_ + o_gate;
     e_z.ld_g = n_in;
-    e_z.act = P + o_act;
+    e_z.act = P_ + o_act;
     e_z.ld_act = n_in;
     e_z.U = B.u_eff.p;
     e_z.rank = r;
-    e_z.scale = ssm_scale;
-    e_z.out32 = Zr;
+    e_z.scale = 1.0f / sqrtf((float)s);
+    e_z.out32 = Zr_;
     e_z.ld32 = d;
     if (taps) {
-      e_z.tap = L->tap_a.as<float>() + l * rows * d;
+      e_z.tap = L_->tap_a.as<float>() + l * rows * d;
       e_z.ld_tap = d;
     }
     if (bf16) {
-      e_z.out16 = Zrh;
+      e_z.out16 = Zrh_;
       e_z.ld16 = d;
     }
-    PSSA_RETURN_IF(launch_gemm(st, dt, Mv, d, B.w_proj.p, d, m, d, d, e_z));
+    PSSA_RETURN_IF(launch_gemm(st, dt, Mv_, d, B.w_proj.p, d, m, d, d, e_z));
 
     // a = SiLU(z_raw W1^T).
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP1));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_MLP1));
     EpiParams e_s;
     e_s.kind = EPI_SILU;
-    e_s.out16 = H1;
+    e_s.out16 = H1_;
     e_s.ld16 = 2 * d;
-    PSSA_RETURN_IF(launch_gemm(st, dt, Zrh, d, B.mlp_w1.p, d, m, 2 * d, d, e_s));
+    PSSA_RETURN_IF(launch_gemm(st, dt, Zrh_, d, B.mlp_w1.p, d, m, 2 * d, d, e_s));
 
     // h = z_raw + a W2^T (layer 0), h += (z_raw + a W2^T) / sqrt(depth).
-    PSSA_RETURN_IF(tm.mark(ST_GEMM_MLP2));
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_MLP2));
     EpiParams e_r;
     e_r.kind = EPI_RESIDUAL;
-    e_r.aux = Zr;
+    e_r.aux = Zr_;
     e_r.ld_aux = d;
     e_r.first = l == 0 ? 1 : 0;
-    e_r.scale = depth_scale;
-    e_r.out32 = X;
+    e_r.scale = 1.0f / sqrtf((float)c_.depth);
+    e_r.out32 = X_;
     e_r.ld32 = d;
     if (taps) {
-      e_r.tap = L->tap_z.as<float>() + l * rows * d;
+      e_r.tap = L_->tap_z.as<float>() + l * rows * d;
       e_r.ld_tap = d;
     }
-    PSSA_RETURN_IF(launch_gemm(st, dt, H1, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r));
+    return launch_gemm(st, dt, H1_, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r);
   }
 
-  PSSA_RETURN_IF(tm.mark(ST_HEAD));
-  if (tr && tr->logits) {
-    // Every row: scaled logits, then its cross-entropy loss.
-    const void* hin = X;
-    if (bf16) {
-      PSSA_RETURN_IF(launch_to_bf16(st, X, d, XNh16, d, rows, d));
-      hin = XNh16;
+  Status head() {
+    const int d = d_, V = V_, m = m_, dt = dt_;
+    const size_t rows = rows_, T = T_;
+    hipStream_t st = st_;
+    const float logit_scale = 1.0f / sqrtf((float)d);
+    PSSA_RETURN_IF(tm_.mark(ST_HEAD));
+    if (tr_ && tr_->logits) {
+      // Every row: scaled logits, then its cross-entropy loss.
+      const void* hin = X_;
+      if (bf16_) {
+        PSSA_RETURN_IF(launch_to_bf16(st, X_, d, XNh16_, d, rows, d));
+        hin = XNh16_;
+      }
+      EpiParams e_h;
+      e_h.kind = EPI_SCALE;
+      e_h.scale = logit_scale;
+      e_h.out32 = tr_->logits + row0_ * (size_t)V;
+      e_h.ld32 = V;
+      PSSA_RETURN_IF(launch_gemm(st, dt, hin, d, M_->unembed.p, d, m, V, d, e_h));
+      token_ce_kernel<<<(unsigned)rows, 256, 0, st>>>(tr_->logits + row0_ * (size_t)V, V, tr_->targets + row0_,
+                                                     tr_->index + row0_, tr_->loss);
+      PSSA_LAUNCH_CHECK("token_ce");
+      return tm_.finish();
+    }
+    // Head on the last token of every lane.
+    const float* xlast = X_ + (T - 1) * (size_t)d;
+    const void* hin = xlast;
+    int ld_h = (int)(T * d);
+    if (bf16_) {
+      PSSA_RETURN_IF(launch_to_bf16(st, xlast, (int)(T * d), XNh16_, d, n_lanes_, d));
+      hin = XNh16_;
+      ld_h = d;
     }
     EpiParams e_h;
     e_h.kind = EPI_SCALE;
     e_h.scale = logit_scale;
-    e_h.out32 = tr->logits + row0 * (size_t)V;
+    e_h.out32 = logits_;
     e_h.ld32 = V;
-    PSSA_RETURN_IF(launch_gemm(st, dt, hin, d, M->unembed.p, d, m, V, d, e_h));
-    token_ce_kernel<<<(unsigned)rows, 256, 0, st>>>(tr->logits + row0 * (size_t)V, V, tr->targets + row0,
-                                                   tr->index + row0, tr->loss);
-    PSSA_LAUNCH_CHECK("token_ce");
-    return tm.finish();
+    PSSA_RETURN_IF(launch_gemm(st, dt, hin, ld_h, M_->unembed.p, d, (int)n_lanes_, V, d, e_h));
+    return tm_.finish();
   }
-  // Head on the last token of every lane.
-  const float* xlast = X + (T - 1) * (size_t)d;
-  const void* hin = xlast;
-  int ld_h = (int)(T * d);
-  if (bf16) {
-    PSSA_RETURN_IF(launch_to_bf16(st, xlast, (int)(T * d), XNh16, d, n_lanes, d));
-    hin = XNh16;
-    ld_h = d;
-  }
-  EpiParams e_h;
-  e_h.kind = EPI_SCALE;
-  e_h.scale = logit_scale;
-  e_h.out32 = logits;
-  e_h.ld32 = V;
-  PSSA_RETURN_IF(launch_gemm(st, dt, hin, ld_h, M->unembed.p, d, (int)n_lanes, V, d, e_h));
-  return tm.finish();
-}
+
+ private:
+  pssa_hip_lanes* L_;
+  const pssa_hip_model* M_;
+  const pssa_hip_config& c_;
+  hipStream_t st_;
+  size_t n_lanes_, T_;
+  bool taps_;
+  hipEvent_t first_in_done_;
+  float* y_part_;
+  const TrainRows* tr_;
+  bool concurrent_;
+  Timer tm_;
+  int d_ = 0, s_ = 0, k_ = 0, C_ = 0, r_ = 0, V_ = 0, n_in_ = 0, m_ = 0, dt_ = 0;
+  bool bf16_ = false;
+  size_t rows_ = 0, row0_ = 0;
+  float *X_ = nullptr, *XN_ = nullptr, *P_ = nullptr, *Y_ = nullptr, *Q_ = nullptr, *Zr_ = nullptr;
+  uint16_t* XNh16_ = nullptr;
+  void *XNh_ = nullptr, *Yh_ = nullptr, *Zrh_ = nullptr, *Wm_ = nullptr, *Mv_ = nullptr, *H1_ = nullptr;
+  const uint32_t* ids_ = nullptr;
+  float* carry_ = nullptr;
+  float* logits_ = nullptr;
+};
 
 constexpr int kPrefillLaneGroups = 2;
 static_assert(kPrefillLaneGroups <= pssa_hip_lanes::kMaxGroups, "one stream per lane group");
@@ -623,32 +662,46 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
   float* ypart = L->Ypart.p ? L->Ypart.as<float>() : nullptr;
   // Lane groups on their own streams: the VALU-bound scan of one group runs
   // beside the MFMA-bound GEMMs of the others.  Group g starts once group
-  // g-1's first input projection is issued, which keeps them a stage apart.
-  // Two groups measure best at the 32-lane prefill (three and four run
-  // 2-3% slower: their smaller scans leave the CUs less evenly loaded).
+  // g-1's first input projection is issued, which keeps them a stage apart,
+  // and the groups are enqueued layer by layer, interleaved, so that the
+  // later groups' work is queued as early as the first group's.  Two groups
+  // measure best at the 32-lane prefill (three and four run 2-3% slower:
+  // their smaller scans leave the CUs less evenly loaded).
   const int G = (int)std::min<size_t>(kPrefillLaneGroups, n_lanes);
   if (!taps && !L->timing && G >= 2 && T >= 64) {
     PSSA_HIP_TRY(hipEventRecord(L->ev_fork, st));
+    std::vector<PrefillView> views;
+    views.reserve(G);
     size_t lane0 = 0;
     for (int g = 0; g < G; ++g) {
       const size_t ng = n_lanes / G + ((size_t)g < n_lanes % G ? 1 : 0);
       const hipStream_t sg = g == 0 ? st : L->aux_stream[g - 1];
+      float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
+      views.emplace_back(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true);
+      lane0 += ng;
+    }
+    for (int g = 0; g < G; ++g) {
       if (g > 0) {
+        const hipStream_t sg = L->aux_stream[g - 1];
         PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_fork, 0));
         PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_first[g - 1], 0));
       }
-      float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
-      PSSA_RETURN_IF(
-          prefill_view(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true));
-      lane0 += ng;
+      PSSA_RETURN_IF(views[g].embed());
+      PSSA_RETURN_IF(views[g].layer(0));
     }
+    for (size_t l = 1; l < c.depth; ++l)
+      for (int g = 0; g < G; ++g) PSSA_RETURN_IF(views[g].layer(l));
+    for (int g = 0; g < G; ++g) PSSA_RETURN_IF(views[g].head());
     for (int g = 1; g < G; ++g) {
       PSSA_HIP_TRY(hipEventRecord(L->ev_join[g - 1], L->aux_stream[g - 1]));
       PSSA_HIP_TRY(hipStreamWaitEvent(st, L->ev_join[g - 1], 0));
     }
     return Status::Ok();
   }
-  return prefill_view(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart, tr, false);
+  PrefillView v(L, st, 0, n_lanes, T, taps, L->timing, nullptr, ypart, tr, false);
+  PSSA_RETURN_IF(v.embed());
+  for (size_t l = 0; l < c.depth; ++l) PSSA_RETURN_IF(v.layer(l));
+  return v.head();
 }
 
 }  // namespace pssa

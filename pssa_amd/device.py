@@ -418,7 +418,7 @@ class PSSALayer:
         logits = np.empty((len(seqs), self.cfg.d_vocab), np.float32) if want_logits else None
         _abi.call(self._lib.pssa_hip_prefill_ragged, self.handle, _abi.ptr(ids, C.c_uint32),
                   _abi.ptr(lens, C.c_uint64), len(seqs), _abi.ptr(logits), 0 if logits is None else logits.size)
-        self._staged = (len(seqs), 1)
+        self._staged = (len(seqs), 0)
         return logits
 
     def forward_inference(self, ids):
@@ -466,8 +466,13 @@ class PSSALayer:
     def decode(self, steps: int, first_ids=None, n_lanes: int | None = None, plastic: bool = False,
                graph: bool = False, want_logits: bool = False):
         """Generates `steps` greedy tokens on lanes 0..n_lanes-1.  first_ids=None
-        continues from the last prefill's logits.  Returns ids [steps, n_lanes]
-        (and the last step's logits [n_lanes, V] when want_logits)."""
+        continues the last prefill as the reference's generate loop does
+        (src/inference.rs:367-379): row 0 is the greedy choice from the
+        prefill's logits and each later row costs a forward step of the row
+        before it.  Given first_ids, every row is the choice after a forward
+        step of the previous token (first_ids for row 0); a continuation of a
+        decode passes its last row.  Returns ids [steps, n_lanes] (and the
+        logits of the last choice [n_lanes, V] when want_logits)."""
         if first_ids is not None:
             first = np.ascontiguousarray(np.atleast_1d(np.asarray(first_ids)), dtype=np.uint32)
             n_lanes = first.size
@@ -481,7 +486,7 @@ class PSSALayer:
         flags = (_abi.DECODE_PLASTIC if plastic else 0) | (_abi.DECODE_GRAPH if graph else 0)
         _abi.call(self._lib.pssa_hip_decode, self.handle, fp_, n_lanes, steps, flags,
                   _abi.ptr(out, C.c_uint32), out.size, _abi.ptr(logits), 0 if logits is None else logits.size)
-        self._staged = (n_lanes, 1)
+        self._staged = None
         return (out, logits) if want_logits else out
 
     def set_repetition_penalty(self, penalty: float) -> None:

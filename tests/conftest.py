@@ -26,6 +26,32 @@ def rel_err(actual, expected) -> float:
     return float(np.max(np.abs(a - e))) / scale if e.size else 0.0
 
 
+def elem_rel_err(actual, expected, floor=None) -> float:
+    """max over elements of |actual - expected| / max(|expected|, floor): the
+    element-wise relative error, with an absolute floor for elements near
+    zero.  The floor defaults to the root mean square of `expected` (a
+    typical element's magnitude), so elements above it are held to a true
+    relative bound and the smaller ones to tol * rms absolute."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    assert a.shape == e.shape, (a.shape, e.shape)
+    assert np.all(np.isfinite(a)), "non-finite output"
+    if not e.size:
+        return 0.0
+    if floor is None:
+        floor = float(np.sqrt(np.mean(e * e)))
+    return float(np.max(np.abs(a - e) / np.maximum(np.abs(e), max(floor, 1e-30))))
+
+
+def assert_parity(actual, expected, tol, what="", floor=None):
+    """The parity gate: normwise (max |d| / max |expected|) and element-wise
+    (elem_rel_err, floor as there) relative errors both below `tol`."""
+    nw = rel_err(actual, expected)
+    ew = elem_rel_err(actual, expected, floor)
+    assert nw < tol and ew < tol, f"{what}: normwise {nw:.3e}, element-wise {ew:.3e}, tolerance {tol:g}"
+    return nw, ew
+
+
 @pytest.fixture(scope="session")
 def hip():
     """The GPU context, shared by every GPU test of the session."""

@@ -10,7 +10,7 @@ fast weights within 1e-4.  Graph replay must equal eager stepping bit for bit.
 import numpy as np
 import pytest
 
-from conftest import rel_err
+from conftest import assert_parity, rel_err
 from oracle import oracle as O
 from pssa_amd import ModelWeights, PSSAConfig, PSSALayer
 from pssa_amd._abi import HipError
@@ -44,13 +44,16 @@ def test_decode_matches_oracle_forward_loop(hip):
     layer = PSSALayer(hip, w, lanes=3, max_tokens=64)
     layer.prefill_inference(ids)
     first = [O.greedy(lg[i]) for i in range(3)]
-    got, glog = layer.decode(6, want_logits=True)  # continues from the prefill logits
+    # Continuing the prefill: row 0 is the choice from its logits, then one
+    # forward step per further row (src/inference.rs:367-379).
+    got, glog = layer.decode(7, want_logits=True)
     ref_w = ModelWeights.init(w.cfg, 5, "baseline")
     ref_w.populate_banks(6, count=w.cfg.mem_capacity)
     ref_ids, ref_lg, _ = O.OracleModel(ref_w).decode(st, first, steps=6)
-    np.testing.assert_array_equal(got, ref_ids)
-    assert rel_err(glog, ref_lg) < 1e-4
-    assert rel_err(layer.get_carry(), st) < 1e-4
+    np.testing.assert_array_equal(got[0], first)
+    np.testing.assert_array_equal(got[1:], ref_ids)
+    assert_parity(glog, ref_lg, 1e-4, 'glog')
+    assert_parity(layer.get_carry(), st, 1e-4, 'layer.get_carry()')
     layer.close()
 
 
@@ -91,7 +94,7 @@ def test_plastic_decode_matches_oracle(hip, graph):
         b.adapter_up[:] = b0.adapter_up
     ref_ids, ref_lg, ref_sp = O.OracleModel(ref).decode(st, first, steps=steps, plastic=True)
     np.testing.assert_array_equal(got, ref_ids)
-    assert rel_err(glog, ref_lg) < 1e-4
+    assert_parity(glog, ref_lg, 1e-4, 'glog')
     assert np.all(ref_sp > 3.5)  # every lane writes (small random model: flat logits)
     for l in range(w.cfg.depth):
         dev = layer.get_plastic(l)
@@ -100,10 +103,10 @@ def test_plastic_decode_matches_oracle(hip, graph):
         np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
         assert dev["step"] == steps
         np.testing.assert_allclose(dev["mem_confidence"], rb.mem_confidence, rtol=1e-5, atol=1e-6)
-        assert rel_err(dev["mem_keys"], rb.mem_keys) < 1e-4
-        assert rel_err(dev["mem_values"], rb.mem_values) < 1e-4
-        assert rel_err(dev["mem_norm_sq"], rb.mem_norm_sq) < 1e-4
-        assert rel_err(dev["adapter_up"], rb.adapter_up) < 1e-4
+        assert_parity(dev["mem_keys"], rb.mem_keys, 1e-4, 'dev["mem_keys"]')
+        assert_parity(dev["mem_values"], rb.mem_values, 1e-4, 'dev["mem_values"]')
+        assert_parity(dev["mem_norm_sq"], rb.mem_norm_sq, 1e-4, 'dev["mem_norm_sq"]')
+        assert_parity(dev["adapter_up"], rb.adapter_up, 1e-4, 'dev["adapter_up"]')
         assert not np.array_equal(dev["adapter_up"], w.blocks[l].adapter_up)
     layer.close()
 
@@ -115,7 +118,7 @@ def test_plastic_decode_fills_free_slots_first(hip):
     w = small_model(seed=13, full_banks=False, depth=1)
     layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
     layer.prefill_inference([[1, 2, 3], [4, 5, 6]])
-    layer.decode(3, plastic=True)
+    layer.decode(4, plastic=True)  # the choice from the prefill logits, then three steps
     dev = layer.get_plastic(0)
     assert dev["mem_count"] == 10 + 6 and dev["mem_write_head"] == 0
     assert set(dev["mem_last_seen"][10:16].tolist()) == {1, 2, 3}
@@ -134,6 +137,22 @@ def test_decode_rejects_bad_arguments(hip):
         layer.decode(2, first_ids=[1, 2, 3])
     with pytest.raises(HipError, match="last prefill"):
         layer.decode(2, n_lanes=1)
+    # Only a prefill's logits can be continued without first ids: not those of
+    # a decode (its last token is unconsumed), nor any after a reset or a
+    # carry change.
+    layer.prefill_inference([[1, 2], [3, 4]])
+    out = layer.decode(2)
+    with pytest.raises(HipError, match="last prefill"):
+        layer.decode(2, n_lanes=2)
+    layer.decode(2, first_ids=out[-1])
+    layer.prefill_inference([[1, 2], [3, 4]])
+    layer.reset_recurrent_state()
+    with pytest.raises(HipError, match="last prefill"):
+        layer.decode(2, n_lanes=2)
+    layer.prefill_inference([[1, 2], [3, 4]])
+    layer.set_carry(layer.get_carry())
+    with pytest.raises(HipError, match="last prefill"):
+        layer.decode(2, n_lanes=2)
     layer.close()
 
 
@@ -174,29 +193,32 @@ def test_plastic_decode_many_lanes_and_layers_matches_oracle(hip):
     first = [O.greedy(lg[i]) for i in range(lanes)]
     layer = PSSALayer(hip, w, lanes=lanes, max_tokens=lanes * 3)
     layer.prefill_inference(ids)
-    got = layer.decode(2, plastic=True, graph=True)
+    got = layer.decode(3, plastic=True, graph=True)
     ref_ids, _, _ = om.decode(st, first, steps=2, plastic=True, threads=8)
-    np.testing.assert_array_equal(got, ref_ids)
+    np.testing.assert_array_equal(got[0], first)
+    np.testing.assert_array_equal(got[1:], ref_ids)
     for l in (0, 5, 11):
         dev = layer.get_plastic(l)
         rb = ref.blocks[l]
         np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
         assert dev["mem_write_head"] == rb.mem_write_head
-        assert rel_err(dev["adapter_up"], rb.adapter_up) < 1e-4
+        assert_parity(dev["adapter_up"], rb.adapter_up, 1e-4, 'dev["adapter_up"]')
     layer.close()
 
 
 def oracle_penalised_decode(w, ids, steps, penalty):
-    """The reference's generate loop at temperature 0 (src/inference.rs:
-    345-391): the first token from the prefill logits, then forward + sample
-    per step, the window being the prompt and every token chosen so far."""
+    """The reference's generate loop at temperature 0 with max_new_tokens =
+    steps (src/inference.rs:345-391): the first token from the prefill
+    logits, then forward + sample per further token, the window being the
+    prompt and every token chosen so far.  Returns every generated token."""
     om = O.OracleModel(w)
     out = np.zeros((steps, ids.shape[0]), np.uint32)
     for i, prompt in enumerate(ids):
         st = om.zero_state()
         hist = [int(t) for t in prompt]
         cur = O.sample_greedy(om.prefill(st, prompt), hist, penalty)
-        for s in range(steps):
+        out[0, i] = cur
+        for s in range(1, steps):
             hist.append(cur)
             cur = O.sample_greedy(om.forward_inference(st, cur), hist, penalty)
             out[s, i] = cur
@@ -272,7 +294,7 @@ def test_value_cap_on_device_matches_host_clamp_and_oracle_decode(hip):
     om = O.OracleModel(host)
     st = om.zero_state(3)
     ref_lg = om.prefill_lanes(st, ids, threads=3)
-    assert rel_err(lg, ref_lg) < 1e-4
+    assert_parity(lg, ref_lg, 1e-4, 'lg')
     layer.close()
     # Plastic writes on banks that give way (confidence 0) store capped values.
     dev_w, ref_w = small_model(seed=29), small_model(seed=29)
@@ -291,7 +313,58 @@ def test_value_cap_on_device_matches_host_clamp_and_oracle_decode(hip):
     np.testing.assert_array_equal(got, ref_ids)
     for l in range(dev_w.cfg.depth):
         vals = layer.get_plastic(l)["mem_values"]
-        assert rel_err(vals, ref_w.blocks[l].mem_values) < 1e-4
+        assert_parity(vals, ref_w.blocks[l].mem_values, 1e-4, 'vals')
         assert np.all((vals.astype(np.float64) ** 2).sum(axis=1) <= float(np.float32(cap)) ** 2)
         assert not np.array_equal(vals, host.blocks[l].mem_values)  # the decode wrote slots
+    layer.close()
+
+
+def test_config5_width_and_depth_plastic_decode_matches_oracle(hip):
+    """Config 5's model and stream count: 256 streams x 12 blocks at d=768,
+    s=256, k=32, C=512, V=16384 (fp32 weights, so that the lane-ordered
+    write decisions can be compared exactly), an 8-token prompt, then three
+    plastic graph-replayed steps.  Each step is teacher-forced (both sides
+    consume the oracle's previous choice) so one near-tie cannot cascade; a
+    chosen id may differ only where the oracle's two logits are within the
+    fp32 gate.  The 256-way protected writes into each block's shared bank
+    (insert_protected, src/memory.rs:305-342) must land identically:
+    count, write head, last-seen steps, confidences, keys, values, fast
+    weights."""
+    say("config 5 width/depth plastic decode")
+    cfg = PSSAConfig(depth=12, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    ref = ModelWeights.init(cfg, 0, "baseline")
+    ref.populate_banks(1)
+    S, P, steps = 256, 8, 3
+    ids = np.random.default_rng(31).integers(0, cfg.d_vocab, (S, P), dtype=np.uint32)
+    layer = PSSALayer(hip, w, lanes=S, max_tokens=S * P, weight_dtype="f32")
+    dev_lg = layer.prefill_inference(ids)
+    om = O.OracleModel(ref)
+    st = om.zero_state(S)
+    lg = om.prefill_lanes(st, ids, threads=16)
+    assert_parity(dev_lg, lg, 1e-4, "prefill logits")
+    cur = np.array([O.greedy(lg[i]) for i in range(S)], np.uint32)
+    ties = 0
+    for t in range(steps):
+        got, glog = layer.decode(1, first_ids=cur, plastic=True, graph=True, want_logits=True)
+        want, r_lg, _ = om.decode(st, cur, steps=1, plastic=True, step_base=t, threads=16)
+        for i in np.nonzero(got[0] != want[0])[0]:
+            gap = abs(float(r_lg[i, got[0, i]]) - float(r_lg[i, want[0, i]]))
+            assert gap <= 1e-4 * float(np.max(np.abs(r_lg[i]))), (t, i, got[0, i], want[0, i], gap)
+            ties += 1
+        assert_parity(glog, r_lg, 1e-4, f"step {t} logits")
+        cur = want[0].copy()
+    say("near-tie choices", ties)
+    assert_parity(layer.get_carry(), st, 1e-4, "carries")
+    for l in range(cfg.depth):
+        dev = layer.get_plastic(l)
+        rb = ref.blocks[l]
+        assert dev["step"] == steps
+        assert dev["mem_count"] == rb.mem_count and dev["mem_write_head"] == rb.mem_write_head, l
+        np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
+        np.testing.assert_allclose(dev["mem_confidence"], rb.mem_confidence, rtol=1e-4, atol=1e-6)
+        assert_parity(dev["mem_keys"], rb.mem_keys, 1e-4, f"keys {l}")
+        assert_parity(dev["mem_values"], rb.mem_values, 1e-4, f"values {l}")
+        assert_parity(dev["adapter_up"], rb.adapter_up, 1e-4, f"adapter_up {l}")
     layer.close()

@@ -5,7 +5,7 @@ slot indices bit-exact.  Small shapes run first."""
 import numpy as np
 import pytest
 
-from conftest import rel_err
+from conftest import assert_parity, elem_rel_err, rel_err
 from oracle import oracle as O
 from pssa_amd import bf16_round
 from pssa_amd._abi import HipError
@@ -363,3 +363,52 @@ def test_dense_scan_matches_oracle(hip, B, L, s):
     h = hip.dense_scan(a, b, h0)
     ref = O.dense_scan(a, b, h0, threads=4)
     assert rel_err(h, ref) < 1e-4
+
+
+def householder_pool(rng, n, s):
+    """n random orthogonal matrices, each a product of two Householder
+    reflections (the pool config 2's transitions are drawn from)."""
+    v1 = rng.standard_normal((n, s)).astype(np.float32)
+    v2 = rng.standard_normal((n, s)).astype(np.float32)
+    v1 /= np.linalg.norm(v1, axis=1, keepdims=True)
+    v2 /= np.linalg.norm(v2, axis=1, keepdims=True)
+    dot = np.einsum("ns,ns->n", v1, v2)[:, None, None]
+    q = -2.0 * v1[:, :, None] * v1[:, None, :] - 2.0 * v2[:, :, None] * v2[:, None, :] \
+        + 4.0 * dot * v1[:, :, None] * v2[:, None, :]
+    q[:, np.arange(s), np.arange(s)] += 1.0
+    return q.astype(np.float32)
+
+
+def test_dense_scan_config2_full_workload(hip):
+    """Config 2 at its full size: 64 sequences x 2048 steps, d_state 64,
+    A_t = Q_t diag(u_t) (Q_t orthogonal, u_t ~ U[0.8, 0.99]^64), b_t ~ N(0, 1),
+    h_0 = 0.  Every sequence against the sequential recurrence."""
+    say("dense scan config 2 full")
+    B, T, s = 64, 2048, 64
+    rng = np.random.default_rng(12)
+    pool = householder_pool(rng, 8192, s)
+    a = np.empty((B * T, s, s), np.float32)
+    for c0 in range(0, B * T, 8192):
+        a[c0:c0 + 8192] = pool * (0.8 + 0.19 * rng.random((8192, 1, s), dtype=np.float32))
+    a = a.reshape(B, T, s, s)
+    b = rng.standard_normal((B, T, s)).astype(np.float32)
+    h = hip.dense_scan(a, b, None)
+    ref = O.dense_scan(a, b, None, threads=16)
+    for i in range(B):
+        assert_parity(h[i], ref[i], 1e-4, f"sequence {i}")
+
+
+def test_softplus_in_place_matches_oracle(hip):
+    """GpuDispatch::softplus_in_place (src/backend.rs:1419-1428) against the
+    reference's softplus (src/linalg.rs:548-551) over both branches, the
+    x > 20 cut and the far tails."""
+    say("softplus_in_place")
+    rng = np.random.default_rng(3)
+    # Down to -87, where e^x is still a normal float.
+    x = np.concatenate([rng.standard_normal(5000) * 6, np.linspace(-87, 60, 3001), [0.0, 20.0, 20.000002, 19.999998,
+                        -1e-30, 1e-30, -87.0]]).astype(np.float32)
+    got = x.copy()
+    hip.softplus_in_place(got)
+    ref = np.array([O.softplus(v) for v in x], np.float32)
+    np.testing.assert_array_equal(got[x > 20], x[x > 20])
+    assert elem_rel_err(got, ref, floor=1e-37) < 2e-6

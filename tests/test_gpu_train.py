@@ -11,7 +11,7 @@ import os
 import numpy as np
 import pytest
 
-from conftest import GOLDEN, rel_err
+from conftest import GOLDEN, assert_parity, rel_err
 from oracle import oracle as O
 from pssa_amd import ModelWeights, PSSAConfig, PSSALayer, Sequence, checkpoint
 from pssa_amd._abi import HipError
@@ -56,7 +56,7 @@ def test_fixture_chunks_match_reference_golden_words(hip):
     layer.set_carry(ck.carry[None])
     loss, lg = layer.batch_forward([Sequence(0, [1, 2, 1], [2, 1, 3])], want_logits=True)
     assert abs(loss - words[0]) <= 1e-5 * abs(words[0])
-    assert rel_err(lg.ravel(), words[1:22]) < 1e-5
+    assert_parity(lg.ravel(), words[1:22], 1e-5, 'lg.ravel()')
     loss2 = layer.batch_forward([(0, [4], [5])])
     assert abs(loss2 - words[22]) <= 1e-5 * abs(words[22])
     layer.close()
@@ -94,12 +94,12 @@ def test_ragged_batch_matches_oracle(hip, dtype):
         seqs = random_seqs(rng, V, spec)
         loss, tl, lg = layer.batch_forward(seqs, want_token_losses=True, want_logits=True)
         r_loss, r_tl, r_lg, carries = oracle_batch(ref_w, carries, seqs)
-        assert rel_err(lg, r_lg) < tol
-        assert rel_err(tl, r_tl) < tol
+        assert_parity(lg, r_lg, tol, 'lg')
+        assert_parity(tl, r_tl, tol, 'tl')
         assert abs(loss - r_loss) <= tol * abs(r_loss)
         np.testing.assert_allclose(loss, np.float32(sum(np.float32(x) for x in tl) / np.float32(tl.size)), rtol=1e-6)
         got = layer.get_carry()
-        assert rel_err(got, carries) < tol
+        assert_parity(got, carries, tol, 'got')
     layer.close()
 
 
@@ -116,8 +116,8 @@ def test_lane_groups_and_permuted_lanes_match_oracle(hip):
     layer = PSSALayer(hip, w, lanes=4, max_tokens=4 * T)
     loss, tl, lg = layer.batch_forward(seqs, want_token_losses=True, want_logits=True)
     r_loss, r_tl, r_lg, r_car = oracle_batch(w, np.zeros((4, 2, 48 * 24), np.float32), seqs)
-    assert rel_err(lg, r_lg) < 1e-4 and rel_err(tl, r_tl) < 1e-4
-    assert rel_err(layer.get_carry(), r_car) < 1e-4
+    assert_parity(lg, r_lg) < 1e-4 and rel_err(tl, r_tl, 1e-4, 'lg')
+    assert_parity(layer.get_carry(), r_car, 1e-4, 'layer.get_carry()')
     trained = layer.get_carry()
     pre = PSSALayer(hip, w, lanes=4, max_tokens=4 * T)
     ids = np.zeros((4, T), np.uint32)

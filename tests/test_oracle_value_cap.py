@@ -127,3 +127,39 @@ def test_product_host_cap_equals_the_oracle_clamp_bit_for_bit():
         assert b.mem_value_cap == np.float32(0.75)
     w.set_value_cap(None)
     assert all(b.mem_value_cap == 0.0 for b in w.blocks)
+
+
+def test_non_finite_capped_values_are_refused_and_nothing_changes():
+    """clamp_value asserts a finite squared norm (src/memory.rs:151-152):
+    the oracle, the library's host cap and a capped insert refuse a value
+    with an infinite or NaN component and leave every bank as it was."""
+    from pssa_amd import ModelWeights, PSSAConfig
+    from pssa_amd._abi import HipError
+    import pytest
+
+    for bad in (np.inf, np.nan):
+        with pytest.raises(ValueError, match="must be finite"):
+            O.clamp_value([1.0, bad, 0.5], 0.5)
+        bank = O.Bank(3, 1, 2)
+        bank.insert([0.1], [3.0, 4.0])
+        bank.insert([0.2], [bad, 1.0])
+        before = bits(bank.values).tolist()
+        with pytest.raises(ValueError, match="must be finite"):
+            bank.set_value_cap(1.0)
+        assert bits(bank.values).tolist() == before and bank.value_cap is None
+        capped = O.Bank(2, 1, 2)
+        capped.set_value_cap(1.0)
+        with pytest.raises(ValueError, match="must be finite"):
+            capped.insert([0.1], [bad, 0.0])
+        assert capped.count == 0
+
+    cfg = PSSAConfig(depth=2, d_vocab=20, d_latent=8, d_state=4, d_mem_key=4, mem_capacity=6)
+    w = ModelWeights.init(cfg, 3, "baseline")
+    w.populate_banks(4, 6)
+    w.blocks[1].mem_values[4, 2] = np.inf
+    before = [bits(b.mem_values).copy() for b in w.blocks]
+    with pytest.raises(HipError, match="must be finite"):
+        w.set_value_cap(0.01)
+    for b, v in zip(w.blocks, before):
+        np.testing.assert_array_equal(bits(b.mem_values), v)
+        assert b.mem_value_cap == 0.0

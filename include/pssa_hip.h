@@ -53,7 +53,8 @@ extern "C" {
 
 /* Weight initialisation modes (pssa_hip_weights_init). */
 #define PSSA_HIP_INIT_REFERENCE 0 /* PSSALayerV2::new draw order, src/pssa.rs:2019-2072 */
-#define PSSA_HIP_INIT_BASELINE 1  /* seeded N(0, 0.02) for every matrix, HiPPO rates */
+#define PSSA_HIP_INIT_BASELINE 1  /* seeded N(0, 0.02) for every matrix; log-spaced rates with
+                                     timescales 1.5..13, so exp(ln 2 * A) < 0.95 */
 
 typedef struct pssa_hip_ctx pssa_hip_ctx;       /* device context (CudaContext peer) */
 typedef struct pssa_hip_model pssa_hip_model;   /* device-resident weights + banks   */

@@ -493,9 +493,12 @@ static void xavier(Rng& rng, float* w, size_t rows, size_t cols) {
 }
 
 // HiPPO log-spaced timescales, src/pssa.rs:649-665.
-static void hippo_rates(float* a_raw, size_t d, size_t s) {
+// tau_max = 200 is the reference's range (src/pssa.rs:649-665); the baseline
+// initialisation uses 13, so that the slowest mode's transition at the
+// initial step size softplus(0) = ln 2 is exp(-ln 2 / 13) = 0.948 < 0.95.
+static void hippo_rates(float* a_raw, size_t d, size_t s, float tau_max) {
   const float ln_min = logf(1.5f);
-  const float ln_max = logf(200.0f);
+  const float ln_max = logf(tau_max);
   for (size_t i = 0; i < d; i++)
     for (size_t j = 0; j < s; j++) {
       float ratio = s > 1 ? (float)j / (float)(s - 1) : 0.0f;
@@ -505,13 +508,13 @@ static void hippo_rates(float* a_raw, size_t d, size_t s) {
     }
 }
 
-static void reset_block_common(const oracle_block& b, const oracle_config& c) {
+static void reset_block_common(const oracle_block& b, const oracle_config& c, float tau_max) {
   const size_t d = c.d_latent, C = c.mem_capacity, k = c.d_mem_key;
   for (size_t i = 0; i < d; i++) {
     b.norm_gamma[i] = 1.0f;
     b.norm_beta[i] = 0.0f;
   }
-  hippo_rates(b.a_raw, d, c.d_state);
+  hippo_rates(b.a_raw, d, c.d_state, tau_max);
   std::fill(b.mem_keys, b.mem_keys + C * k, 0.0f);
   std::fill(b.mem_values, b.mem_values + C * d, 0.0f);
   std::fill(b.mem_norm_sq, b.mem_norm_sq + C, 0.0f);
@@ -524,7 +527,7 @@ uint64_t oracle_init_reference(const oracle_model* m, uint64_t seed) {
   const size_t v = c.d_vocab, d = c.d_latent, s = c.d_state, k = c.d_mem_key, r = c.adapter_rank;
   Rng rng(seed);
   auto block = [&](oracle_block& b) {
-    reset_block_common(b, c);
+    reset_block_common(b, c, 200.0f);
     xavier(rng, b.w_delta, d, d);
     xavier(rng, b.w_b, s, d);
     xavier(rng, b.w_c, s, d);
@@ -557,7 +560,7 @@ uint64_t oracle_init_baseline(const oracle_model* m, uint64_t seed) {
   Rng rng(seed);
   const double sd = 0.02;
   auto block = [&](oracle_block& b) {
-    reset_block_common(b, c);
+    reset_block_common(b, c, 13.0f);
     normal_fill(rng, b.w_delta, d * d, sd);
     normal_fill(rng, b.w_b, s * d, sd);
     normal_fill(rng, b.w_c, s * d, sd);

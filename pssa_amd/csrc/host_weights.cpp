@@ -54,10 +54,14 @@ void fill_gauss(XorShift64Star& g, float* w, size_t n, double sd) {
   for (size_t i = 0; i < n; ++i) w[i] = (float)(sd * g.gauss());
 }
 
-// Log-spaced decay timescales tau in [1.5, 200] stored as raw rates
-// ln(expm1(1/tau)) so that -softplus(raw) = -1/tau (src/pssa.rs:649-665).
-void fill_hippo(float* a_raw, size_t d, size_t s) {
-  const float lo = logf(1.5f), hi = logf(200.0f);
+// Log-spaced decay timescales tau in [1.5, tau_max] stored as raw rates
+// ln(expm1(1/tau)) so that -softplus(raw) = -1/tau (src/pssa.rs:649-665,
+// where tau_max = 200).  The baseline initialisation takes tau_max = 13: its
+// slowest mode's transition at the initial step size softplus(0) = ln 2 is
+// exp(-ln 2 / 13) = 0.948, a spectral radius below 0.95.
+constexpr float kTauMaxReference = 200.0f, kTauMaxBaseline = 13.0f;
+void fill_hippo(float* a_raw, size_t d, size_t s, float tau_max) {
+  const float lo = logf(1.5f), hi = logf(tau_max);
   for (size_t j = 0; j < s; ++j) {
     const float frac = s > 1 ? (float)j / (float)(s - 1) : 0.0f;
     const float raw = logf(expm1f(1.0f / expf(lo + frac * (hi - lo))));
@@ -109,11 +113,11 @@ bool check_weights(const pssa_hip_weights* w, char* err, size_t n) {
   return true;
 }
 
-void clear_block(const pssa_hip_config& c, pssa_hip_block& b) {
+void clear_block(const pssa_hip_config& c, pssa_hip_block& b, float tau_max) {
   const size_t d = c.d_latent, s = c.d_state, k = c.d_mem_key, C = c.mem_capacity;
   std::fill(b.norm_gamma, b.norm_gamma + d, 1.0f);
   std::fill(b.norm_beta, b.norm_beta + d, 0.0f);
-  fill_hippo(b.a_raw, d, s);
+  fill_hippo(b.a_raw, d, s, tau_max);
   std::fill(b.mem_keys, b.mem_keys + C * k, 0.0f);
   std::fill(b.mem_values, b.mem_values + C * d, 0.0f);
   std::fill(b.mem_norm_sq, b.mem_norm_sq + C, 0.0f);
@@ -145,7 +149,7 @@ extern "C" int pssa_hip_weights_init(const pssa_hip_weights* w, uint64_t seed, i
   // Draw order of PSSAContinuousBlockV2::new_with_rng_and_loops
   // (src/pssa.rs:630-700) and PlasticAdapterV2::new (src/adapter.rs:16-24).
   auto block = [&](pssa_hip_block& b) {
-    clear_block(c, b);
+    clear_block(c, b, ref ? kTauMaxReference : kTauMaxBaseline);
     mat(b.w_delta, d, d);
     mat(b.w_b, s, d);
     mat(b.w_c, s, d);

@@ -321,29 +321,31 @@ def test_value_cap_on_device_matches_host_clamp_and_oracle_decode(hip):
 
 def test_config5_width_and_depth_plastic_decode_matches_oracle(hip):
     """Config 5's model and stream count: 256 streams x 12 blocks at d=768,
-    s=256, k=32, C=512, V=16384 (fp32 weights, so that the lane-ordered
-    write decisions can be compared exactly), an 8-token prompt, then three
-    plastic graph-replayed steps.  Each step is teacher-forced (both sides
-    consume the oracle's previous choice) so one near-tie cannot cascade; a
-    chosen id may differ only where the oracle's two logits are within the
-    fp32 gate.  The 256-way protected writes into each block's shared bank
-    (insert_protected, src/memory.rs:305-342) must land identically:
-    count, write head, last-seen steps, confidences, keys, values, fast
-    weights."""
+    s=256, k=32, C=512, V=16384 with bf16 weights, an 8-token prompt, then
+    three plastic graph-replayed steps against the oracle on the same
+    bf16-rounded weights (2e-2 gate).  Each step is teacher-forced (both
+    sides consume the oracle's previous choice) so that one near-tie cannot
+    cascade; a chosen id may differ only where the oracle's two logits lie
+    within the gate.  The 256-way lane-ordered protected writes into each
+    block's shared bank (insert_protected, src/memory.rs:305-342) must make
+    the same decisions: count, write head and last-seen steps equal,
+    confidences, keys, values and fast weights within the gate."""
     say("config 5 width/depth plastic decode")
     cfg = PSSAConfig(depth=12, d_vocab=16384, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
     w = ModelWeights.init(cfg, 0, "baseline")
     w.populate_banks(1)
     ref = ModelWeights.init(cfg, 0, "baseline")
     ref.populate_banks(1)
+    ref = ref.to_bf16_values()
+    tol = 2e-2
     S, P, steps = 256, 8, 3
     ids = np.random.default_rng(31).integers(0, cfg.d_vocab, (S, P), dtype=np.uint32)
-    layer = PSSALayer(hip, w, lanes=S, max_tokens=S * P, weight_dtype="f32")
+    layer = PSSALayer(hip, w, lanes=S, max_tokens=S * P, weight_dtype="bf16")
     dev_lg = layer.prefill_inference(ids)
     om = O.OracleModel(ref)
     st = om.zero_state(S)
     lg = om.prefill_lanes(st, ids, threads=16)
-    assert_parity(dev_lg, lg, 1e-4, "prefill logits")
+    assert_parity(dev_lg, lg, tol, "prefill logits")
     cur = np.array([O.greedy(lg[i]) for i in range(S)], np.uint32)
     ties = 0
     for t in range(steps):
@@ -351,20 +353,21 @@ def test_config5_width_and_depth_plastic_decode_matches_oracle(hip):
         want, r_lg, _ = om.decode(st, cur, steps=1, plastic=True, step_base=t, threads=16)
         for i in np.nonzero(got[0] != want[0])[0]:
             gap = abs(float(r_lg[i, got[0, i]]) - float(r_lg[i, want[0, i]]))
-            assert gap <= 1e-4 * float(np.max(np.abs(r_lg[i]))), (t, i, got[0, i], want[0, i], gap)
+            assert gap <= tol * float(np.max(np.abs(r_lg[i]))), (t, i, got[0, i], want[0, i], gap)
             ties += 1
-        assert_parity(glog, r_lg, 1e-4, f"step {t} logits")
+        assert_parity(glog, r_lg, tol, f"step {t} logits")
         cur = want[0].copy()
-    say("near-tie choices", ties)
-    assert_parity(layer.get_carry(), st, 1e-4, "carries")
+    say("near-tie choices", ties, "of", S * steps)
+    assert ties <= S * steps // 10
+    assert_parity(layer.get_carry(), st, tol, "carries")
     for l in range(cfg.depth):
         dev = layer.get_plastic(l)
         rb = ref.blocks[l]
         assert dev["step"] == steps
         assert dev["mem_count"] == rb.mem_count and dev["mem_write_head"] == rb.mem_write_head, l
         np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
-        np.testing.assert_allclose(dev["mem_confidence"], rb.mem_confidence, rtol=1e-4, atol=1e-6)
-        assert_parity(dev["mem_keys"], rb.mem_keys, 1e-4, f"keys {l}")
-        assert_parity(dev["mem_values"], rb.mem_values, 1e-4, f"values {l}")
-        assert_parity(dev["adapter_up"], rb.adapter_up, 1e-4, f"adapter_up {l}")
+        assert_parity(dev["mem_confidence"], rb.mem_confidence, tol, f"confidence {l}")
+        assert_parity(dev["mem_keys"], rb.mem_keys, tol, f"keys {l}")
+        assert_parity(dev["mem_values"], rb.mem_values, tol, f"values {l}")
+        assert_parity(dev["adapter_up"], rb.adapter_up, tol, f"adapter_up {l}")
     layer.close()

@@ -425,3 +425,28 @@ def test_oracle_decode_plastic_steps_equal_the_composed_primitives():
         assert b.mem_write_head == b2.mem_write_head and b.mem_count == b2.mem_count
     np.testing.assert_array_equal(states, st2)
     assert w.blocks[0].mem_last_seen.max() >= 101  # the gate saw the protected writes
+
+
+def test_baseline_rates_give_spectral_radius_below_095():
+    """The baseline initialisation's transitions (stable,
+    spectral radius < 0.95): with the diagonal A = -softplus(a_raw), the
+    per-token transition at the initial step size softplus(0) = ln 2 is
+    exp(ln 2 * A), below 0.95 for every mode; the timescales are log-spaced
+    1/tau from 1.5 to 13.  The reference initialisation keeps its [1.5, 200]."""
+    from pssa_amd import ModelWeights, PSSAConfig
+    cfg = PSSAConfig(depth=2, d_vocab=50, d_latent=16, d_state=64, d_mem_key=4, mem_capacity=8)
+    for mode, tau_max in (("baseline", 13.0), ("reference", 200.0)):
+        for w in (ModelWeights.init(cfg, 0, mode),):
+            om = O.OracleModel(ModelWeights(cfg))
+            (om.init_baseline if mode == "baseline" else om.init_reference)(0)
+            for b, ob in zip(w.blocks, om.w.blocks):
+                np.testing.assert_array_equal(b.a_raw, ob.a_raw)  # product and oracle agree
+                A = -np.logaddexp(0.0, b.a_raw.astype(np.float64))
+                tau = 1.0 / -A
+                np.testing.assert_allclose(tau.min(), 1.5, rtol=1e-5)
+                np.testing.assert_allclose(tau.max(), tau_max, rtol=1e-5)
+                rho = np.exp(np.log(2.0) * A).max()
+                if mode == "baseline":
+                    assert rho < 0.95, rho
+                else:
+                    assert rho > 0.95  # the reference's slow modes

@@ -38,6 +38,9 @@ def lib() -> C.CDLL:
     L = C.CDLL(LIB_PATH)
     sig = {
         "oracle_set_dot_avx2": ([C.c_int], None),
+        "oracle_set_bf16_operands": ([C.c_int], None),
+        "oracle_get_bf16_operands": ([], C.c_int),
+        "oracle_bf16_round": ([C.c_float], C.c_float),
         "oracle_get_dot_avx2": ([], C.c_int),
         "oracle_rng_new": ([C.c_uint64], C.c_uint64),
         "oracle_rng_next_u32": ([C.POINTER(C.c_uint64)], C.c_uint32),
@@ -115,12 +118,34 @@ class Dot:
         lib().oracle_set_dot_avx2(self.prev)
 
 
-class OracleModel:
-    """Runs the oracle on a product ModelWeights (aliasing its numpy arrays)."""
+def _operands(method):
+    """Runs an OracleModel method in its operand mode (the process-wide
+    oracle_set_bf16_operands switch), restoring the previous mode after."""
+    import functools
 
-    def __init__(self, weights):
+    @functools.wraps(method)
+    def run(self, *args, **kwargs):
+        prev = lib().oracle_get_bf16_operands()
+        lib().oracle_set_bf16_operands(1 if self.bf16_operands else 0)
+        try:
+            return method(self, *args, **kwargs)
+        finally:
+            lib().oracle_set_bf16_operands(prev)
+
+    return run
+
+
+class OracleModel:
+    """Runs the oracle on a product ModelWeights (aliasing its numpy arrays).
+    bf16_operands restates the device's bf16 mode (every product's activation
+    operand rounded to bf16, fp32 accumulation and state); pass weights
+    already rounded (ModelWeights.to_bf16_values).  Off: the reference's
+    arithmetic."""
+
+    def __init__(self, weights, bf16_operands: bool = False):
         self.w = weights
         self.cfg = weights.cfg
+        self.bf16_operands = bf16_operands
         self.view, self.keep = weights.c_view()
         self.ref = C.cast(C.pointer(self.view), vp)
 
@@ -145,11 +170,13 @@ class OracleModel:
         lib().oracle_populate_banks(self.ref, seed, count, max_radius)
         self.sync()
 
+    @_operands
     def forward_inference(self, state: np.ndarray, token: int, logits: bool = True):
         out = np.empty(self.cfg.d_vocab, np.float32) if logits else None
         lib().oracle_forward_inference(self.ref, ptr(state), token, ptr(out))
         return out
 
+    @_operands
     def prefill(self, state: np.ndarray, ids, logits: bool = True):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         out = np.empty(self.cfg.d_vocab, np.float32) if logits else None
@@ -158,6 +185,7 @@ class OracleModel:
             raise ValueError(f"oracle prefill rejected the ids ({rc})")
         return out
 
+    @_operands
     def prefill_lanes(self, states: np.ndarray, ids: np.ndarray, threads: int = 1, logits: bool = True):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         lanes, n = ids.shape
@@ -167,6 +195,7 @@ class OracleModel:
             raise ValueError(f"oracle prefill rejected the ids ({rc})")
         return out
 
+    @_operands
     def train_chunk_forward(self, state: np.ndarray, ids, targets):
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         tg = np.ascontiguousarray(targets, dtype=np.uint32)
@@ -175,6 +204,7 @@ class OracleModel:
                                                 ptr(tg, C.c_uint32), ids.size, ptr(logits))
         return np.float32(loss), logits
 
+    @_operands
     def forward_taps(self, state: np.ndarray, token: int):
         """forward_inference with per-block (q_pnc, z_final, adapter out, adapter act) and logits."""
         c = self.cfg
@@ -186,6 +216,7 @@ class OracleModel:
         lib().oracle_forward_taps(self.ref, ptr(state), token, ptr(q), ptr(z), ptr(a), ptr(act), ptr(lg))
         return q, z, a, act, lg
 
+    @_operands
     def decode(self, states: np.ndarray, first_ids, steps: int, plastic: bool = False, step_base: int = 0,
                threads: int = 1):
         """Greedy decode of every lane for `steps` steps (oracle_decode).  Returns
@@ -203,6 +234,7 @@ class OracleModel:
         self.sync()
         return out, lg, sp
 
+    @_operands
     def features(self, state: np.ndarray, token: int) -> np.ndarray:
         out = np.empty(self.cfg.d_latent, np.float32)
         lib().oracle_forward_features(self.ref, ptr(state), token, ptr(out))

@@ -27,6 +27,23 @@ namespace {
 
 int g_dot_avx2 = 1;
 
+// The bf16 mode of this build (weights and every GEMM's activation operand in
+// bf16, fp32 accumulation, fp32 state path; the reference has no such mode,
+// all its parameters are f32, src/pssa.rs:11-205).  When set, block_forward
+// rounds each product's activation operand to bf16 where the device does;
+// the weights are rounded by the caller.  Off: the reference's arithmetic.
+int g_bf16_ops = 0;
+
+// Round to the nearest bf16 (ties to even), widened back to f32.
+inline float bf16r(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  u &= 0xFFFF0000u;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
 // --- src/linalg.rs:1-28 SimpleRng (xorshift64*) --------------------------------
 struct Rng {
   uint64_t state;
@@ -209,9 +226,14 @@ float retrieve(const float* keys, const float* norm_sq, const float* values, siz
       float weight = expf((min_dist - u2f(s.first)) / tau) / sum;
       w[s.second] = weight;
       const float* v = values + (size_t)s.second * dv;
-      for (size_t j = 0; j < dv; j++) out_val[j] += weight * v[j];
+      if (g_bf16_ops)
+        for (size_t j = 0; j < dv; j++) out_val[j] += bf16r(weight) * bf16r(v[j]);
+      else
+        for (size_t j = 0; j < dv; j++) out_val[j] += weight * v[j];
       if (out_idx) out_idx[n++] = s.second;
     }
+    if (g_bf16_ops)
+      for (size_t j = 0; j < dv; j++) out_val[j] = bf16r(out_val[j]);
     return min_dist;
   }
   float sum = 0.0f;
@@ -224,8 +246,13 @@ float retrieve(const float* keys, const float* norm_sq, const float* values, siz
     float wi = w[idx] / sum;
     w[idx] = wi;
     const float* v = values + idx * dv;
-    for (size_t j = 0; j < dv; j++) out_val[j] += wi * v[j];
+    if (g_bf16_ops)
+      for (size_t j = 0; j < dv; j++) out_val[j] += bf16r(wi) * bf16r(v[j]);
+    else
+      for (size_t j = 0; j < dv; j++) out_val[j] += wi * v[j];
   }
+  if (g_bf16_ops)
+    for (size_t j = 0; j < dv; j++) out_val[j] = bf16r(out_val[j]);
   if (out_idx)
     for (size_t i = 0; i < top_k; i++) out_idx[i] = i < count ? (uint32_t)i : 0xFFFFFFFFu;
   return min_dist;
@@ -288,8 +315,13 @@ float retrieve_hybrid(const float* keys, const float* norm_sq, const float* valu
     const float wi = w[idx] / sum;
     w[idx] = wi;
     const float* v = values + idx * dv;
-    for (size_t j = 0; j < dv; j++) out_val[j] += wi * v[j];
+    if (g_bf16_ops)
+      for (size_t j = 0; j < dv; j++) out_val[j] += bf16r(wi) * bf16r(v[j]);
+    else
+      for (size_t j = 0; j < dv; j++) out_val[j] += wi * v[j];
   }
+  if (g_bf16_ops)
+    for (size_t j = 0; j < dv; j++) out_val[j] = bf16r(out_val[j]);
   return min_dist;
 }
 
@@ -303,11 +335,15 @@ float refractory_gain(uint64_t delta_tokens, float tau) {
 // Scratch for one block's token step (src/pssa.rs:506-620 inference buffers).
 struct Scratch {
   std::vector<float> xn, delta, bb, cc, y, qe, qp, mw, mval, g, mp, act, adout, zraw, h1, u, zf;
+  std::vector<float> xb, yb, zb;  // bf16-rounded GEMM operands (bf16 mode)
   uint64_t age_add = 1;  // hybrid read: bumps of the current pass not yet stored
   std::vector<float> rates;  // -softplus(a_raw), src/pssa.rs:787-796
   void resize(const oracle_config& c) {
     size_t d = c.d_latent, s = c.d_state, k = c.d_mem_key, C = c.mem_capacity, r = c.adapter_rank;
     xn.assign(d, 0);
+    xb.assign(d, 0);
+    yb.assign(d, 0);
+    zb.assign(d, 0);
     delta.assign(d, 0);
     bb.assign(s, 0);
     cc.assign(s, 0);
@@ -344,11 +380,18 @@ void block_forward(const oracle_block& b, const oracle_config& c, Scratch& sc, f
   for (size_t i = 0; i < d; i++) sum_sq += e[i] * e[i];
   float inv_rms = 1.0f / sqrtf(sum_sq / (float)d + 1e-5f);
   for (size_t i = 0; i < d; i++) sc.xn[i] = b.norm_gamma[i] * (e[i] * inv_rms) + b.norm_beta[i];
+  // The products' activation operand: x-hat itself, or its bf16 rounding in
+  // the bf16 mode (the SSM below always reads the f32 x-hat).
+  const float* xg = sc.xn.data();
+  if (g_bf16_ops) {
+    for (size_t i = 0; i < d; i++) sc.xb[i] = bf16r(sc.xn[i]);
+    xg = sc.xb.data();
+  }
   // 2. data-dependent projections
-  matvec(b.w_delta, d, d, sc.xn.data(), sc.delta.data());
+  matvec(b.w_delta, d, d, xg, sc.delta.data());
   for (size_t i = 0; i < d; i++) sc.delta[i] = softplus(sc.delta[i]);
-  matvec(b.w_b, s, d, sc.xn.data(), sc.bb.data());
-  matvec(b.w_c, s, d, sc.xn.data(), sc.cc.data());
+  matvec(b.w_b, s, d, xg, sc.bb.data());
+  matvec(b.w_c, s, d, xg, sc.cc.data());
   // 3. SSM state update, i outer / j inner
   const float ssm_scale = 1.0f / sqrtf((float)s);
   for (size_t i = 0; i < d; i++) {
@@ -365,8 +408,12 @@ void block_forward(const oracle_block& b, const oracle_config& c, Scratch& sc, f
     sc.y[i] = yi;
   }
   // 4. retrieval query, projection, soft read
-  for (size_t q = 0; q < k; q++)
-    sc.qe[q] = dot(b.w_qx + q * d, sc.xn.data(), d) + dot(b.w_qh + q * d, sc.y.data(), d);
+  const float* yg = sc.y.data();
+  if (g_bf16_ops) {
+    for (size_t i = 0; i < d; i++) sc.yb[i] = bf16r(sc.y[i]);
+    yg = sc.yb.data();
+  }
+  for (size_t q = 0; q < k; q++) sc.qe[q] = dot(b.w_qx + q * d, xg, d) + dot(b.w_qh + q * d, yg, d);
   project(sc.qe.data(), sc.qp.data(), k);
   if (b.mem_hybrid_enabled)  // src/pssa.rs:1153-1162 (the ages are bumped by the caller)
     retrieve_hybrid(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
@@ -375,27 +422,35 @@ void block_forward(const oracle_block& b, const oracle_config& c, Scratch& sc, f
   else
     retrieve(b.mem_keys, b.mem_norm_sq, b.mem_values, b.mem_count, c.mem_capacity, k, d,
              sc.qp.data(), c.tau_mem, b.mem_top_k, sc.mval.data(), sc.mw.data(), nullptr);
-  matvec(b.w_gate, d, d, sc.xn.data(), sc.g.data());
+  matvec(b.w_gate, d, d, xg, sc.g.data());
   for (size_t i = 0; i < d; i++) sc.g[i] = sigmoid(sc.g[i]);
-  matvec(b.w_proj, d, d, sc.mval.data(), sc.mp.data());
+  matvec(b.w_proj, d, d, sc.mval.data(), sc.mp.data());  // bf16 mode: the readout is already rounded
   // 5. plastic adapter (src/adapter.rs:37-48)
-  matvec(b.adapter_down, r, d, sc.xn.data(), sc.act.data());
+  matvec(b.adapter_down, r, d, xg, sc.act.data());
   for (size_t q = 0; q < r; q++) {
     float hv = sc.act[q];
     sc.act[q] = hv * sigmoid(hv);
   }
   for (size_t i = 0; i < d; i++) {
     float total = 0.0f;
-    for (size_t q = 0; q < r; q++)
-      total += (b.adapter_up[i * r + q] + b.adapter_slow[i * r + q]) * sc.act[q];
+    if (g_bf16_ops)  // the device's operand: bf16(fast + slow) times bf16(act)
+      for (size_t q = 0; q < r; q++)
+        total += bf16r(b.adapter_up[i * r + q] + b.adapter_slow[i * r + q]) * bf16r(sc.act[q]);
+    else
+      for (size_t q = 0; q < r; q++) total += (b.adapter_up[i * r + q] + b.adapter_slow[i * r + q]) * sc.act[q];
     sc.adout[i] = total;
   }
   // 6. aggregation and SiLU MLP
   for (size_t i = 0; i < d; i++) sc.zraw[i] = (sc.y[i] * ssm_scale) + (sc.g[i] * sc.mp[i]) + sc.adout[i];
-  matvec(b.mlp_w1, dmlp, d, sc.zraw.data(), sc.h1.data());
+  const float* zg = sc.zraw.data();
+  if (g_bf16_ops) {
+    for (size_t i = 0; i < d; i++) sc.zb[i] = bf16r(sc.zraw[i]);
+    zg = sc.zb.data();
+  }
+  matvec(b.mlp_w1, dmlp, d, zg, sc.h1.data());
   for (size_t i = 0; i < dmlp; i++) {
     float hv = sc.h1[i];
-    sc.h1[i] = hv * sigmoid(hv);
+    sc.h1[i] = g_bf16_ops ? bf16r(hv * sigmoid(hv)) : hv * sigmoid(hv);
   }
   matvec(b.mlp_w2, d, dmlp, sc.h1.data(), sc.u.data());
   for (size_t i = 0; i < d; i++) z_out[i] = sc.zraw[i] + sc.u[i];
@@ -433,7 +488,13 @@ struct Runner {
   void logits(float* lg) {
     const oracle_config& c = m->cfg;
     const size_t d = c.d_latent;
-    matvec(m->unembed, c.d_vocab, d, feat.data(), lg);
+    if (g_bf16_ops) {
+      std::vector<float> fb(d);
+      for (size_t i = 0; i < d; i++) fb[i] = bf16r(feat[i]);
+      matvec(m->unembed, c.d_vocab, d, fb.data(), lg);
+    } else {
+      matvec(m->unembed, c.d_vocab, d, feat.data(), lg);
+    }
     const float logit_scale = 1.0f / sqrtf((float)d);
     for (size_t v = 0; v < c.d_vocab; v++) lg[v] *= logit_scale;
   }
@@ -472,6 +533,9 @@ void parallel_for(size_t n, int threads, F f) {
 extern "C" {
 
 void oracle_set_dot_avx2(int enabled) { g_dot_avx2 = enabled ? 1 : 0; }
+void oracle_set_bf16_operands(int enabled) { g_bf16_ops = enabled ? 1 : 0; }
+float oracle_bf16_round(float x) { return bf16r(x); }
+int oracle_get_bf16_operands(void) { return g_bf16_ops; }
 int oracle_get_dot_avx2(void) { return g_dot_avx2; }
 
 uint64_t oracle_rng_new(uint64_t seed) { return Rng(seed).state; }

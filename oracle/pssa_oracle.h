@@ -102,6 +102,14 @@ typedef struct {
 
 /* Reduction tree used by dot_slice: 1 = AVX2/FMA tree, 0 = portable tree. */
 void oracle_set_dot_avx2(int enabled);
+/* The bf16 mode of the device path (not a reference mode): every product's
+ * activation operand rounded to bf16 (nearest even) where the device rounds
+ * it, fp32 accumulation, the fp32 state path unchanged.  The caller rounds
+ * the weights.  Process-wide; 0 (the default) is the reference arithmetic. */
+void oracle_set_bf16_operands(int enabled);
+int oracle_get_bf16_operands(void);
+/* The rounding of that mode: nearest bf16, ties to even, as f32. */
+float oracle_bf16_round(float x);
 int oracle_get_dot_avx2(void);
 
 /* linalg primitives */

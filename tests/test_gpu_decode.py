@@ -322,8 +322,9 @@ def test_value_cap_on_device_matches_host_clamp_and_oracle_decode(hip):
 def test_config5_width_and_depth_plastic_decode_matches_oracle(hip):
     """Config 5's model and stream count: 256 streams x 12 blocks at d=768,
     s=256, k=32, C=512, V=16384 with bf16 weights, an 8-token prompt, then
-    three plastic graph-replayed steps against the oracle on the same
-    bf16-rounded weights (2e-2 gate).  Each step is teacher-forced (both
+    three plastic graph-replayed steps against the oracle's restatement of
+    the bf16 mode (the same bf16-rounded weights, every product's activation
+    operand rounded to bf16; 2e-2 gate).  Each step is teacher-forced (both
     sides consume the oracle's previous choice) so that one near-tie cannot
     cascade; a chosen id may differ only where the oracle's two logits lie
     within the gate.  The 256-way lane-ordered protected writes into each
@@ -342,7 +343,7 @@ def test_config5_width_and_depth_plastic_decode_matches_oracle(hip):
     ids = np.random.default_rng(31).integers(0, cfg.d_vocab, (S, P), dtype=np.uint32)
     layer = PSSALayer(hip, w, lanes=S, max_tokens=S * P, weight_dtype="bf16")
     dev_lg = layer.prefill_inference(ids)
-    om = O.OracleModel(ref)
+    om = O.OracleModel(ref, bf16_operands=True)
     st = om.zero_state(S)
     lg = om.prefill_lanes(st, ids, threads=16)
     assert_parity(dev_lg, lg, tol, "prefill logits")

@@ -20,8 +20,10 @@ def say(*a):
     print("[case]", *a, flush=True)
 
 
-def oracle_prefill(w, ids, carry=None, threads=8):
-    om = O.OracleModel(w)
+def oracle_prefill(w, ids, carry=None, threads=8, bf16=False):
+    """The oracle's prefill; bf16 restates the device's bf16 mode (weights
+    rounded by the caller, every product's activation operand rounded)."""
+    om = O.OracleModel(w, bf16_operands=bf16)
     lanes = ids.shape[0]
     states = om.zero_state(lanes) if carry is None else carry.copy()
     logits = om.prefill_lanes(states, ids, threads=threads)
@@ -58,7 +60,7 @@ def test_prefill_matches_oracle_small(hip, dtype):
     layer = PSSALayer(hip, w, lanes=3, max_tokens=3 * 37, weight_dtype=dtype)
     got = layer.prefill_inference(ids)
     ref_w = w if dtype == "f32" else w.to_bf16_values()
-    ref, st = oracle_prefill(ref_w, ids)
+    ref, st = oracle_prefill(ref_w, ids, bf16=dtype == "bf16")
     tol = 1e-4 if dtype == "f32" else 2e-2
     assert_parity(got, ref, tol, 'got')
     assert_parity(layer.get_carry(), st, tol, 'layer.get_carry()')
@@ -75,7 +77,7 @@ def test_config1_shape_fp32_and_bf16(hip, init):
     w.populate_banks(1)
     ids = np.random.default_rng(0).integers(0, cfg.d_vocab, (1, 512), dtype=np.uint32)
     ref, st = oracle_prefill(w, ids)
-    ref_bf, st_bf = oracle_prefill(w.to_bf16_values(), ids)
+    ref_bf, st_bf = oracle_prefill(w.to_bf16_values(), ids, bf16=True)
     for dtype, r, s, tol in (("f32", ref, st, 1e-4), ("bf16", ref_bf, st_bf, 2e-2)):
         say("config1", init, dtype)
         layer = PSSALayer(hip, w, lanes=1, max_tokens=512, weight_dtype=dtype)
@@ -248,7 +250,7 @@ def test_config3_full_model_prefix_against_oracle(hip, dtype):
     carry = layer.get_carry()
     ref_w = w if dtype == "f32" else w.to_bf16_values()
     pick = [0, 15, 16, 31]
-    ref, st = oracle_prefill(ref_w, ids[pick], threads=4)
+    ref, st = oracle_prefill(ref_w, ids[pick], threads=4, bf16=dtype == "bf16")
     tol = 1e-4 if dtype == "f32" else 2e-2
     for j, lane in enumerate(pick):
         assert_parity(got[lane], ref[j], tol, f"logits lane {lane}")
@@ -346,7 +348,7 @@ def test_memory_top_k_model_matches_oracle(hip, dtype):
                 m.set_hybrid_read(True, 0.9)
         layer = PSSALayer(hip, dev_w, lanes=3, max_tokens=64, weight_dtype=dtype)
         got = layer.prefill_inference(ids)
-        om = O.OracleModel(ref_w if dtype == "f32" else ref_w.to_bf16_values())
+        om = O.OracleModel(ref_w if dtype == "f32" else ref_w.to_bf16_values(), bf16_operands=dtype == "bf16")
         st = om.zero_state(3)
         ref = om.prefill_lanes(st, ids, threads=3)
         assert_parity(got, ref, tol, (k, hybrid))

@@ -25,11 +25,12 @@ def say(*a):
     print("[case]", *a, flush=True)
 
 
-def oracle_batch(w, carries, seqs):
+def oracle_batch(w, carries, seqs, bf16=False):
     """Per-sequence forward_train_chunk on each lane's carry (forward_stacked,
     src/sequence_batch.rs:560-609): token losses and logits in packed order,
-    the token-mean loss, and the carries after the batch."""
-    om = O.OracleModel(w)
+    the token-mean loss, and the carries after the batch (bf16: the device's
+    bf16 operand rounding restated, weights rounded by the caller)."""
+    om = O.OracleModel(w, bf16_operands=bf16)
     carries = carries.copy()
     losses, logits = [], []
     for s in seqs:
@@ -93,7 +94,7 @@ def test_ragged_batch_matches_oracle(hip, dtype):
                  [(0, 5, False), (2, 9, False)]):
         seqs = random_seqs(rng, V, spec)
         loss, tl, lg = layer.batch_forward(seqs, want_token_losses=True, want_logits=True)
-        r_loss, r_tl, r_lg, carries = oracle_batch(ref_w, carries, seqs)
+        r_loss, r_tl, r_lg, carries = oracle_batch(ref_w, carries, seqs, bf16=dtype == "bf16")
         assert_parity(lg, r_lg, tol, 'lg')
         assert_parity(tl, r_tl, tol, 'tl')
         assert abs(loss - r_loss) <= tol * abs(r_loss)

@@ -450,3 +450,30 @@ def test_baseline_rates_give_spectral_radius_below_095():
                     assert rho < 0.95, rho
                 else:
                     assert rho > 0.95  # the reference's slow modes
+
+
+def test_bf16_operand_rounding_and_mode_switch():
+    """The oracle's bf16 mode rounds to the nearest bf16 with ties to even:
+    exact cases (halfway points, a carry into the exponent, signed zero,
+    infinities) and a bulk comparison with an integer restatement; the mode
+    switch is restored after each model call."""
+    r = lambda x: np.float32(O.lib().oracle_bf16_round(float(x)))  # noqa: E731
+    one = np.float32(1.0)
+    assert r(one + np.float32(2.0 ** -8)) == one                       # tie, even below
+    assert r(one + np.float32(3 * 2.0 ** -8)) == np.float32(1.015625)  # tie, even above
+    assert r(one + np.float32(2.0 ** -8 + 2.0 ** -20)) == np.float32(1.0078125)
+    assert r(np.float32(1.9999999)) == np.float32(2.0)                 # carry into the exponent
+    assert r(np.float32(-0.0)) == 0.0 and np.signbit(r(np.float32(-0.0)))
+    assert r(np.float32(np.inf)) == np.inf and r(np.float32(-np.inf)) == -np.inf
+    x = np.random.default_rng(0).standard_normal(20000).astype(np.float32) * 37
+    u = x.view(np.uint32).astype(np.uint64)
+    want = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+    got = np.array([r(v) for v in x], np.float32)
+    np.testing.assert_array_equal(got, want)
+    # The switch is per call: a bf16-mode model call leaves the mode off.
+    from pssa_amd import ModelWeights, PSSAConfig
+    cfg = PSSAConfig(depth=1, d_vocab=20, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=6)
+    w = ModelWeights.init(cfg, 1, "baseline").to_bf16_values()
+    om = O.OracleModel(w, bf16_operands=True)
+    om.forward_inference(om.zero_state(), 3)
+    assert O.lib().oracle_get_bf16_operands() == 0

@@ -46,15 +46,18 @@ def elem_rel_err(actual, expected, floor=None) -> float:
 def assert_parity(actual, expected, tol, what="", floor=None):
     """The parity gate: normwise (max |d| / max |expected|) and element-wise
     relative errors both below `tol`.  The element-wise floor (elem_rel_err)
-    is the RMS of `expected` at the fp32 gates (tol < 1e-2) and twice it at
-    the bf16 gates: rounding GEMM operands to bf16 moves every element by a
-    fraction of the typical element's size, not of its own."""
+    is the RMS of `expected` at the fp32 gates (tol < 1e-2) and four times
+    it at the bf16 gates: rounding a product's operands to bf16 moves each
+    element by a fraction of the terms that formed it, which is the typical
+    element's size rather than its own, and the bf16 gate (2e-2) leaves about
+    ten units of bf16 roundoff where the fp32 gate leaves some 1700 of fp32's."""
     if floor is None:
         e = np.asarray(expected, dtype=np.float64)
-        floor = (2.0 if tol >= 1e-2 else 1.0) * float(np.sqrt(np.mean(e * e))) if e.size else 0.0
+        floor = (4.0 if tol >= 1e-2 else 1.0) * float(np.sqrt(np.mean(e * e))) if e.size else 0.0
     nw = rel_err(actual, expected)
     ew = elem_rel_err(actual, expected, floor)
     assert nw < tol and ew < tol, f"{what}: normwise {nw:.3e}, element-wise {ew:.3e}, tolerance {tol:g}"
+    print(f"[parity] {what}: normwise {nw:.3e}, element-wise {ew:.3e}, tolerance {tol:g}", flush=True)
     return nw, ew
 
 

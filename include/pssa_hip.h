@@ -291,6 +291,21 @@ int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n
                                size_t top_k, float* d_out_val, float* d_out_min,
                                uint32_t* d_out_idx, char* err, size_t err_len);
 
+/* pssa_hip_retrieve_resident without any device allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Results equal pssa_hip_retrieve_resident's bit for bit.  The
+ * exact top-k path runs 8192 queries per pass in a static scratch array of
+ * 19 MiB that each GPU the library runs on holds until the process ends;
+ * a shape needing more scratch fails with PSSA_HIP_EINVAL.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (from two
+ * contexts, or two streams) race and must be serialised by the caller. */
+int pssa_hip_retrieve_resident_noalloc(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q,
+                                       const float* d_keys, const float* d_norm_sq, const float* d_values,
+                                       size_t capacity, size_t count, size_t d_key, size_t d_val, float tau,
+                                       size_t top_k, float* d_out_val, float* d_out_min,
+                                       uint32_t* d_out_idx, char* err, size_t err_len);
+
 /* retrieve_hybrid_into (src/memory.rs:568-660) for n_q queries against one
  * bank state: over the live slots (the top_k nearest by (distance bits, slot),
  * or all when top_k is 0 or >= count) w_i = exp((min_dist - d_i)/tau) *

@@ -159,6 +159,8 @@ def lib() -> C.CDLL:
         "pssa_hip_model_get_hybrid": ([vp, sz, fp, u64p, err_t, sz], C.c_int),
         "pssa_hip_retrieve_resident": ([vp, vp, sz, vp, vp, vp, sz, sz, sz, sz, C.c_float, sz, vp, vp, vp,
                                         err_t, sz], C.c_int),
+        "pssa_hip_retrieve_resident_noalloc": ([vp, vp, sz, vp, vp, vp, sz, sz, sz, sz, C.c_float, sz, vp, vp, vp,
+                                                err_t, sz], C.c_int),
         "pssa_hip_dense_scan": ([vp, fp, fp, fp, sz, sz, sz, fp, err_t, sz], C.c_int),
         "pssa_hip_dense_scan_resident": ([vp, vp, vp, vp, sz, sz, sz, vp, err_t, sz], C.c_int),
         "pssa_hip_model_load": ([vp, C.POINTER(Weights), C.c_int, pp, err_t, sz], C.c_int),

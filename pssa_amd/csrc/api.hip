@@ -199,6 +199,7 @@ int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
     PSSA_RETURN_IF(pssa::init_retrieve_attributes());
     PSSA_RETURN_IF(pssa::init_decode_attributes());
     PSSA_RETURN_IF(pssa::init_dense_scan_attributes());
+    PSSA_RETURN_IF(pssa::noalloc_scratch_address(&ctx->noalloc_scratch));
     *out = ctx.release();
     return Status::Ok();
   };
@@ -883,11 +884,13 @@ int pssa_hip_retrieve_hybrid(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, 
                        age, lam, out_val, out_min, out_idx, out_weights, err, err_len);
 }
 
-int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
-                               const float* d_norm_sq, const float* d_values, size_t capacity,
-                               size_t count, size_t d_key, size_t d_val, float tau, size_t top_k,
-                               float* d_out_val, float* d_out_min, uint32_t* d_out_idx,
-                               char* err, size_t err_len) {
+// Device-buffer retrieval.  no_alloc: the ranked path's scratch is the
+// device's static array (kNoallocChunk queries per pass) instead of the
+// context's grown buffer, so nothing is allocated.
+static int retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
+                             const float* d_norm_sq, const float* d_values, size_t capacity, size_t count,
+                             size_t d_key, size_t d_val, float tau, size_t top_k, float* d_out_val,
+                             float* d_out_min, uint32_t* d_out_idx, bool no_alloc, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(check_ctx(ctx));
     PSSA_RETURN_IF(need(n_q && d_key && d_val && capacity, "retrieve: dimensions must be positive"));
@@ -917,10 +920,40 @@ int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n
     ra.out_val = d_out_val;
     ra.out_min = d_out_min;
     ra.out_idx = d_out_idx;
-    PSSA_RETURN_IF(bind_retrieve_scratch(ctx, ra));
+    if (no_alloc) {
+      ra.chunk = pssa::kNoallocChunk;
+      const size_t need_bytes = pssa::retrieve_scratch_bytes(ra);
+      if (need_bytes > pssa::kNoallocScratchBytes)
+        return Status::Invalid("retrieve (allocation-free): needs " + std::to_string(need_bytes) +
+                               " bytes of scratch, the static scratch holds " +
+                               std::to_string(pssa::kNoallocScratchBytes));
+      if (!ctx->noalloc_scratch) return Status::Device("retrieve (allocation-free): scratch address unresolved");
+      ra.scratch = ctx->noalloc_scratch;
+      ra.scratch_bytes = pssa::kNoallocScratchBytes;
+    } else {
+      PSSA_RETURN_IF(bind_retrieve_scratch(ctx, ra));
+    }
     return pssa::launch_retrieve(ctx->stream, ra);
   };
   return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_retrieve_resident(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
+                               const float* d_norm_sq, const float* d_values, size_t capacity,
+                               size_t count, size_t d_key, size_t d_val, float tau, size_t top_k,
+                               float* d_out_val, float* d_out_min, uint32_t* d_out_idx,
+                               char* err, size_t err_len) {
+  return retrieve_resident(ctx, d_q_pnc, n_q, d_keys, d_norm_sq, d_values, capacity, count, d_key, d_val, tau,
+                           top_k, d_out_val, d_out_min, d_out_idx, false, err, err_len);
+}
+
+int pssa_hip_retrieve_resident_noalloc(pssa_hip_ctx* ctx, const float* d_q_pnc, size_t n_q, const float* d_keys,
+                                       const float* d_norm_sq, const float* d_values, size_t capacity,
+                                       size_t count, size_t d_key, size_t d_val, float tau, size_t top_k,
+                                       float* d_out_val, float* d_out_min, uint32_t* d_out_idx, char* err,
+                                       size_t err_len) {
+  return retrieve_resident(ctx, d_q_pnc, n_q, d_keys, d_norm_sq, d_values, capacity, count, d_key, d_val, tau,
+                           top_k, d_out_val, d_out_min, d_out_idx, true, err, err_len);
 }
 
 // ------------------------------------------------------------------ model

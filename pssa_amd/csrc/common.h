@@ -136,6 +136,9 @@ struct pssa_hip_ctx {
   // context); calls on one context are serialised by `mu` on one stream.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  // Device address of this device's static scratch array (the
+  // allocation-free retrieval), resolved when the context is created.
+  void* noalloc_scratch = nullptr;
   // Device copies of GEMM weights keyed by (host address, element count,
   // storage dtype), as the reference's CUDA weight cache keys them by
   // (address, length).  A stale entry is uploaded again on its next use.

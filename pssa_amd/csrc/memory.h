@@ -26,6 +26,7 @@ struct RetrieveArgs {
   // absent or too small the general kernel runs instead.
   void* scratch = nullptr;
   size_t scratch_bytes = 0;
+  int chunk = 0;  // queries per ranked dot/pick pass (0: the default, 32768)
   // Hybrid read (retrieve_hybrid_into, src/memory.rs:568-660): with hgate
   // set, live slot s weighs exp((min - d_s)/tau) * hgate[s] * decay_s,
   // decay_s = (float)exp(age_s * log_lam), age_s = hage[s] + age_base
@@ -41,6 +42,15 @@ struct RetrieveArgs {
 
 // Scratch the ranked top-k path needs for these arguments (0: not taken).
 size_t retrieve_scratch_bytes(const RetrieveArgs& a);
+
+// The allocation-free retrieval (pssa_hip_retrieve_resident_noalloc) runs
+// the ranked path kNoallocChunk queries per pass in a static per-device
+// scratch array of kNoallocScratchBytes.
+constexpr int kNoallocChunk = 8192;
+constexpr size_t kNoallocScratchBytes = (size_t)19 << 20;  // 19 MiB
+// The device address of the current device's scratch array (resolved once
+// per device with hipGetSymbolAddress; call with the device current).
+Status noalloc_scratch_address(void** out);
 
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a);
 // One-time per-device set-up a later launch_retrieve with these arguments

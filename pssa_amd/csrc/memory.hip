@@ -571,21 +571,32 @@ struct RankedScratch {
 
 __host__ __device__ inline int ranked_dkp(int dk) { return (dk + RK_BK - 1) / RK_BK * RK_BK; }
 
-static size_t ranked_scratch_bytes(int dk) {
-  return (size_t)RK_SLOTS * ranked_dkp(dk) * 2 * sizeof(uint16_t) + RK_SLOTS * sizeof(float4) +
-         (size_t)RK_CHUNK * RK_SLOTS * sizeof(float) + (size_t)RK_CHUNK * sizeof(double);
+// Queries per dot/pick pass: RK_CHUNK unless the arguments name a smaller chunk.
+static int ranked_chunk(const RetrieveArgs& a) { return a.chunk > 0 && a.chunk < RK_CHUNK ? a.chunk : RK_CHUNK; }
+
+static constexpr size_t ranked_scratch_bytes(int dk, int chunk) {
+  return (size_t)RK_SLOTS * ((dk + RK_BK - 1) / RK_BK * RK_BK) * 2 * sizeof(uint16_t) + RK_SLOTS * sizeof(float4) +
+         (size_t)chunk * RK_SLOTS * sizeof(float) + (size_t)chunk * sizeof(double);
 }
 
-static RankedScratch ranked_scratch(void* base, int dk) {
+static RankedScratch ranked_scratch(void* base, int dk, int chunk) {
   const size_t row = (size_t)RK_SLOTS * ranked_dkp(dk);
   RankedScratch s;
   s.khi = static_cast<uint16_t*>(base);
   s.klo = s.khi + row;
   s.terms = reinterpret_cast<float4*>(s.klo + row);
   s.zdot = reinterpret_cast<float*>(s.terms + RK_SLOTS);
-  s.qq = reinterpret_cast<double*>(s.zdot + (size_t)RK_CHUNK * RK_SLOTS);
+  s.qq = reinterpret_cast<double*>(s.zdot + (size_t)chunk * RK_SLOTS);
   return s;
 }
+
+// The allocation-free retrieval's scratch: one array per device, sized for
+// the ranked path at the largest key width and kNoallocChunk queries per
+// pass.  Host code reaches it only through the address hipGetSymbolAddress
+// returns (noalloc_scratch_address); the symbol itself is not a device
+// address on the host.
+static_assert(ranked_scratch_bytes(RK_MAX_DK, kNoallocChunk) <= kNoallocScratchBytes, "scratch size");
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 __global__ __launch_bounds__(256) void ranked_prep_kernel(RetrieveArgs a, RankedScratch sc) {
   __shared__ double part[256];
@@ -1145,7 +1156,24 @@ static bool ranked_read_fits(const RetrieveArgs& a) {
 }
 
 size_t retrieve_scratch_bytes(const RetrieveArgs& a) {
-  return ranked_read_fits(a) ? ranked_scratch_bytes(a.dk) : 0;
+  return ranked_read_fits(a) ? ranked_scratch_bytes(a.dk, ranked_chunk(a)) : 0;
+}
+
+Status noalloc_scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  PSSA_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return Status::Invalid("allocation-free scratch: device index above 63");
+  std::lock_guard<std::mutex> g(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    PSSA_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return Status::Device("hipGetSymbolAddress returned a null scratch address");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return Status::Ok();
 }
 
 static bool soft_read_fits(const RetrieveArgs& a) {
@@ -1226,13 +1254,14 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   }
   if (ranked_read_fits(a) && a.scratch && a.scratch_bytes >= retrieve_scratch_bytes(a)) {
     PSSA_RETURN_IF(allow_large_lds());
-    const RankedScratch sc = ranked_scratch(a.scratch, a.dk);
+    const int chunk = ranked_chunk(a);
+    const RankedScratch sc = ranked_scratch(a.scratch, a.dk, chunk);
     ranked_prep_kernel<<<RK_SLOTS, 256, 0, stream>>>(a, sc);
     PSSA_LAUNCH_CHECK("ranked_prep");
     const int vec_out = a.dv % 4 == 0 && a.dv <= 4 * RK_MAX_DV4 && ((uintptr_t)a.values & 15) == 0 &&
                         ((uintptr_t)a.out_val & 15) == 0;
-    for (int q0 = 0; q0 < a.n; q0 += RK_CHUNK) {
-      const int nq = std::min(RK_CHUNK, a.n - q0);
+    for (int q0 = 0; q0 < a.n; q0 += chunk) {
+      const int nq = std::min(chunk, a.n - q0);
       ranked_dot_kernel<<<dim3((nq + RK_TQ - 1) / RK_TQ, (a.count + RK_TS - 1) / RK_TS), RK_THREADS, RD_LDS,
                           stream>>>(a, sc, q0, nq);
       PSSA_LAUNCH_CHECK("ranked_dot");

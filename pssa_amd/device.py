@@ -260,6 +260,18 @@ class HipDevice:
                   vp(values_ptr), capacity, count, d_key, d_val, tau, top_k, vp(out_val_ptr),
                   vp(out_min_ptr) if out_min_ptr else None, vp(out_idx_ptr) if out_idx_ptr else None)
 
+    def retrieve_resident_noalloc(self, q_ptr: int, n_q: int, keys_ptr: int, norm_sq_ptr: int, values_ptr: int,
+                                  capacity: int, count: int, d_key: int, d_val: int, tau: float, top_k: int,
+                                  out_val_ptr: int, out_min_ptr: int | None = None,
+                                  out_idx_ptr: int | None = None) -> None:
+        """retrieve_resident with no device allocation: the exact top-k path's
+        scratch is the device's static array (shared by every call on the GPU;
+        overlapping calls race)."""
+        vp = C.c_void_p
+        _abi.call(self._lib.pssa_hip_retrieve_resident_noalloc, self.handle, vp(q_ptr), n_q, vp(keys_ptr),
+                  vp(norm_sq_ptr), vp(values_ptr), capacity, count, d_key, d_val, tau, top_k, vp(out_val_ptr),
+                  vp(out_min_ptr) if out_min_ptr else None, vp(out_idx_ptr) if out_idx_ptr else None)
+
     def dense_scan(self, a, b, h0=None):
         a, b = _f32(a), _f32(b)
         batch, L, s = b.shape

@@ -13,7 +13,9 @@
 
 namespace pssa {
 Status launch_dense_scan(hipStream_t stream, const float* A, const float* B, const float* H0, float* H,
-                         int batch, int L, int s);
+                         int batch, int L, int s, void* scratch, size_t scratch_bytes);
+// Scratch the two-level schedule needs (0: the sequential kernels run).
+size_t dense_scan_scratch_bytes(int batch, int L, int s);
 Status init_dense_scan_attributes();
 }
 
@@ -783,6 +785,20 @@ static Status bind_retrieve_scratch(pssa_hip_ctx* ctx, pssa::RetrieveArgs& ra) {
   }
   ra.scratch = ctx->scratch;
   ra.scratch_bytes = ctx->scratch_bytes;
+  return Status::Ok();
+}
+
+// Grows the context's scratch to what the two-level dense scan needs.
+// Called with ctx->mu held.
+static Status bind_dense_scan_scratch(pssa_hip_ctx* ctx, int batch, int L, int s) {
+  const size_t need_bytes = pssa::dense_scan_scratch_bytes(batch, L, s);
+  if (!need_bytes || ctx->scratch_bytes >= need_bytes) return Status::Ok();
+  PSSA_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  if (ctx->scratch) PSSA_HIP_TRY(hipFree(ctx->scratch));
+  ctx->scratch = nullptr;
+  ctx->scratch_bytes = 0;
+  PSSA_HIP_TRY(hipMalloc(&ctx->scratch, need_bytes));
+  ctx->scratch_bytes = need_bytes;
   return Status::Ok();
 }
 
@@ -1840,8 +1856,10 @@ int pssa_hip_dense_scan(pssa_hip_ctx* ctx, const float* a, const float* b, const
     PSSA_RETURN_IF(upload(db, b, nb * 4, st));
     if (h0) PSSA_RETURN_IF(upload(dh0, h0, batch * d_state * 4, st));
     PSSA_RETURN_IF(dh.alloc(nb * 4));
+    PSSA_RETURN_IF(bind_dense_scan_scratch(ctx, (int)batch, (int)seq_len, (int)d_state));
     PSSA_RETURN_IF(pssa::launch_dense_scan(st, da.as<float>(), db.as<float>(), h0 ? dh0.as<float>() : nullptr,
-                                           dh.as<float>(), (int)batch, (int)seq_len, (int)d_state));
+                                           dh.as<float>(), (int)batch, (int)seq_len, (int)d_state, ctx->scratch,
+                                           ctx->scratch_bytes));
     PSSA_RETURN_IF(download(h, dh, nb * 4, st));
     return sync(ctx);
   };
@@ -1859,7 +1877,9 @@ int pssa_hip_dense_scan_resident(pssa_hip_ctx* ctx, const float* d_a, const floa
     if (batch > INT32_MAX || seq_len > INT32_MAX) return Status::Invalid("dense scan: too large");
     std::lock_guard<std::mutex> g(ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(ctx->device));
-    return pssa::launch_dense_scan(ctx->stream, d_a, d_b, d_h0, d_h, (int)batch, (int)seq_len, (int)d_state);
+    PSSA_RETURN_IF(bind_dense_scan_scratch(ctx, (int)batch, (int)seq_len, (int)d_state));
+    return pssa::launch_dense_scan(ctx->stream, d_a, d_b, d_h0, d_h, (int)batch, (int)seq_len, (int)d_state,
+                                   ctx->scratch, ctx->scratch_bytes);
   };
   return pssa::finish(body(), err, err_len);
 }

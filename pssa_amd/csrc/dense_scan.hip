@@ -1,17 +1,23 @@
 // Dense-transition linear recurrence h_t = A_t h_(t-1) + b_t for gfx950.
 //
 // There is no counterpart in the reference (its SSM is diagonal); this is the
-// standalone dense kernel.  The work is dominated by streaming the transition
-// matrices (s*s floats per step) from HBM exactly once, so the kernel is
-// built around bandwidth, not flops: one 256-thread workgroup walks one
-// sequence in time order, every thread owns S/TPR columns of one row of A_t
-// and keeps a ring of DEPTH future steps of its slice in registers, so the
-// loads for step t+DEPTH are in flight while step t is reduced.  h_(t-1) is
-// double-buffered in LDS (one barrier per step); the TPR partial dot products
-// of a row meet through lane shuffles.  A two-level chunked scan would need
-// s^3 flops per step for the A_2 A_1 combines (64x the sequential work at
-// s=64) and still read A once, so time-sequential is the roofline choice
-// whenever batch * (bytes per step) saturates HBM.
+// standalone dense kernel.  Two schedules:
+//
+//  - Time-sequential (dense_scan_ring_kernel, dense_scan_kernel): one
+//    workgroup walks one sequence in time order and reads every A_t once.
+//    With one workgroup per sequence only `batch` CUs stream, and a CU
+//    streams about 22 B/clk from HBM (3.3 TB/s with 64 CUs, measured), so
+//    this bounds long sequences of few lanes.
+//
+//  - Chunked two-level (dense_twolevel_kernel, d_state 64): time is cut into
+//    windows of TL_SUB sub-chunks of TL_LC steps.  Level 1 composes each
+//    sub-chunk's affine map (P, q) = (A_last ... A_first, local response from
+//    zero) with matrix-core products P <- A_t P; level 2 carries the window's
+//    entry state through the composed maps (h <- P h + q) so every sub-chunk
+//    of the window knows its entry state, and re-runs its steps exactly in
+//    fp32.  Launch l composes window l and re-runs window l - 1, so a
+//    window's transitions are read the second time shortly after the first,
+//    while they are still in the device's last-level cache.
 #include "common.h"
 
 namespace pssa {
@@ -201,6 +207,353 @@ __global__ __launch_bounds__(DS_THREADS) void dense_scan_ring_kernel(const float
   if (wave == 0) hseq[(size_t)(L - 1) * DS_S + lane] = sh[(L & 1) * DS_S + lane];
 }
 
+// ---------------------------------------------------------------------------
+// Chunked two-level scan, d_state 64.  One launch runs two roles side by side
+// (workgroup-uniform): the re-run role for window w_rerun (TL_SUB workgroups
+// per sequence) and the compose role for window w_agg (TL_SUB - 1 per
+// sequence: the last sub-chunk's map is never needed, the next window starts
+// from the exact re-run state).  Both stream one step's A_t and b_t per LDS
+// ring slot with direct-to-LDS loads from two loader waves, as the ring
+// kernel does; the slot's A_t rows keep their sixteen 16-byte chunks
+// XOR-swizzled by the row index, so 16 lanes reading one chunk column of 16
+// rows hit 16 distinct bank groups.
+//
+// Compose role, per step (four compute waves):
+//  - q <- A_t q + b_t in fp32 (four threads a row, DPP quad sums);
+//  - P <- A_t P on the matrix cores: wave c computes rows 16c .. 16c+15 of
+//    the new P (one 16-row tile, four 16-column tiles, 16x16 accumulator
+//    layout: lane l holds column l%16 and rows 4(l/16)+r).  Both operands are
+//    split into bf16 hi + lo parts (x = hi + lo to about 2^-17 relative) and
+//    three v_mfma_f32_16x16x32_bf16 products (lo.hi, hi.lo, hi.hi) accumulate
+//    each 16x16x32 block in fp32.  The waves exchange P through LDS as
+//    ready-split B fragments: the k slots of a 32-row block are rows
+//    4(l/16)+r of its first and second 16-row tiles, which lane l of waves
+//    2kb and 2kb+1 hold, so every lane reads the 16 bytes its own lane index
+//    wrote and A_t's fragments use the same k order.  Over a sub-chunk of
+//    contracting transitions the composed map shrinks (about 0.9^32 at
+//    config 2), so its relative error of a few 1e-5 moves the carried state
+//    by a few 1e-6 of its size; the re-run of every step is exact fp32.
+// A map that is not finite is marked unusable, and a re-run that would need
+// it replays the earlier sub-chunks of its window in fp32 instead.
+constexpr int TL_SUB = 4;                          // sub-chunks per window
+constexpr int TL_LC = 32;                          // steps per sub-chunk
+constexpr int TL_W = TL_SUB * TL_LC;               // steps per window
+constexpr int TL_RING = 7;                         // LDS ring slots (one step each)
+constexpr int TL_AGG = DS_S * DS_S + DS_S + 4;     // P [64][64], q [64], unusable flag, pad
+
+// s_waitcnt vmcnt(after * NI): the loads of a slot have landed once at most
+// the `after` slots issued later are in flight.
+template <int NI>
+__device__ __forceinline__ void tl_wait_loads(int after) {
+  switch (after) {
+    case 7: __builtin_amdgcn_s_waitcnt(vmcnt_only(7 * NI)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_only(6 * NI)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_only(5 * NI)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_only(4 * NI)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_only(3 * NI)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * NI)); break;
+    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_only(NI)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_only(0)); break;
+  }
+}
+static_assert(TL_RING - 2 <= 7, "tl_wait_loads covers up to seven slots in flight");
+
+typedef __bf16 tl_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float tl_f32x4_t __attribute__((ext_vector_type(4)));
+
+struct TwoLevelArgs {
+  const float* A;
+  const float* B;
+  const float* H0;
+  float* H;
+  float* agg;   // [2][batch][TL_SUB - 1][TL_AGG] composed maps, by window parity
+  float* hend;  // [2][batch][DS_S] state after a window, by window parity
+  int L, batch;
+  int w_rerun, w_agg;  // windows re-run / composed by this launch (-1: none)
+};
+
+// Float offset of 16-byte chunk `c` of row `r` of an A_t slot.
+__device__ __forceinline__ int tl_off(int r, int c) { return 4 * (r * 16 + (c ^ (r & 15))); }
+
+// x = hi + lo in bf16 (round to nearest even both times).
+__device__ __forceinline__ void tl_split(const float (&x)[8], tl_bf16x8_t& hi, tl_bf16x8_t& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)x[e];
+    hi[e] = h;
+    lo[e] = (__bf16)(x[e] - (float)h);
+  }
+}
+
+// One exact fp32 step: out[row] = A_t[row, :] . h + b_t[row] (four threads a
+// row, 16 columns each, DPP quad sum).
+__device__ __forceinline__ void tl_exact_step(const float* slot, const float* h, float* out, int row, int part) {
+  float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = 4 * part + q;
+    const float4 av = *reinterpret_cast<const float4*>(slot + tl_off(row, c));
+    const float4 hv = *reinterpret_cast<const float4*>(h + 4 * c);
+    p[q] = fmaf(av.x, hv.x, p[q]);
+    p[q] = fmaf(av.y, hv.y, p[q]);
+    p[q] = fmaf(av.z, hv.z, p[q]);
+    p[q] = fmaf(av.w, hv.w, p[q]);
+  }
+  const float acc = quad_sum((p[0] + p[1]) + (p[2] + p[3]));
+  if (part == 0) out[row] = acc + slot[DS_S * DS_S + row];
+}
+
+constexpr int TL_CW = 8;                      // compute waves (two per SIMD)
+constexpr int TL_LOADERS = 4;                 // loader waves: 16 rows of A_t each, the first also b_t
+constexpr int TL_NI = DS_S * DS_S / 4 / 64 / TL_LOADERS;  // A instructions per loader per slot (4)
+constexpr int TL_THREADS = (TL_CW + TL_LOADERS) * 64;
+static_assert((TL_RING - 2) * (TL_NI + 1) <= 63, "vmcnt holds at most 63");
+
+__global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs a) {
+  __shared__ __attribute__((aligned(1024))) float ring_s[TL_RING][DS_SLOT];
+  __shared__ __attribute__((aligned(16))) float vec_s[2][DS_S];
+  // P as B fragments, [buffer][hi/lo][k block][16-column tile][lane]
+  __shared__ __attribute__((aligned(16))) tl_bf16x8_t pf_s[2][2][2][4][64];
+  __shared__ int bad_s;
+  float* ring = &ring_s[0][0];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool loader = wave >= TL_CW;
+  const bool rowwave = wave < 4;  // the exact steps: four threads a row
+  const int seq = blockIdx.x / TL_SUB, j = blockIdx.x % TL_SUB;
+  const int L = a.L;
+  const float* Aseq = a.A + (size_t)seq * L * DS_S * DS_S;
+  const float* bseq = a.B + (size_t)seq * L * DS_S;
+  const int row = (tid >> 2) & (DS_S - 1), part = tid & 3;
+  const size_t hb = (size_t)a.batch * DS_S;
+
+  // Loader w (wave TL_CW + w) moves A_t rows 16w .. 16w+15 of a slot (TL_NI
+  // instructions of four rows), loader 0 also b_t (one instruction, 16 lanes).
+  const int lw = loader ? wave - TL_CW : 0;
+  const float* asrc[TL_NI];
+#pragma unroll
+  for (int i = 0; i < TL_NI; ++i) {
+    const int c = (lw * TL_NI + i) * 64 + lane;  // LDS chunk of the slot
+    const int r = c >> 4, p = c & 15;
+    asrc[i] = Aseq + r * DS_S + 4 * (p ^ (r & 15));
+  }
+  const float* bsrc = bseq + 4 * min(lane, DS_S / 4 - 1);
+  // Streams steps ts .. ts+nst-1 through the ring; compute(k, slot) runs on
+  // the compute waves once step ts+k has landed, one barrier per step.
+  auto stream = [&](int ts, int nst, auto&& compute) {
+    auto issue = [&](int k) {
+      float* slot = ring + (k % TL_RING) * DS_SLOT;
+      const size_t t = (size_t)(ts + k);
+#pragma unroll
+      for (int i = 0; i < TL_NI; ++i)
+        __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + t * (DS_S * DS_S)),
+                                         (__attribute__((address_space(3))) void*)(slot + 4 * (lw * TL_NI + i) * 64),
+                                         16, 0, 0);
+      if (lw == 0 && lane < DS_S / 4)
+        __builtin_amdgcn_global_load_lds((const void*)(bsrc + t * DS_S),
+                                         (__attribute__((address_space(3))) void*)(slot + DS_S * DS_S), 16, 0, 0);
+    };
+    if (loader)
+      for (int k = 0; k < TL_RING - 1 && k < nst; ++k) issue(k);
+    for (int k = 0; k < nst; ++k) {
+      if (loader) {
+        // Slot k has landed once at most the slots issued after it are in flight.
+        if (lw == 0)
+          tl_wait_loads<TL_NI + 1>(min(TL_RING - 2, nst - 1 - k));
+        else
+          tl_wait_loads<TL_NI>(min(TL_RING - 2, nst - 1 - k));
+      } else {
+        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | (0xF) | (0x3 << 14));  // lgkmcnt(0)
+      }
+      asm volatile("s_barrier" ::: "memory");
+      if (loader) {
+        if (k + TL_RING - 1 < nst) issue(k + TL_RING - 1);
+        continue;
+      }
+      compute(k, ring + (k % TL_RING) * DS_SLOT);
+    }
+    __syncthreads();
+  };
+
+  // ---- re-run role: entry state of sub-chunk j of window w_rerun, then its
+  // steps exactly in fp32 ----
+  auto rerun_role = [&]() {
+  if (a.w_rerun >= 0) {
+    const int w = a.w_rerun;
+    const int wstart = w * TL_W, wend = min(L, wstart + TL_W);
+    const int t0 = wstart + j * TL_LC;
+    const int n = min(wend, t0 + TL_LC) - t0;
+    if (n > 0) {  // uniform over the workgroup
+      int cur = 0;
+      if (tid < DS_S)
+        vec_s[0][tid] = w == 0 ? (a.H0 ? a.H0[(size_t)seq * DS_S + tid] : 0.0f)
+                               : a.hend[(size_t)((w - 1) & 1) * hb + (size_t)seq * DS_S + tid];
+      const float* maps = a.agg + ((size_t)(w & 1) * a.batch + seq) * (TL_SUB - 1) * TL_AGG;
+      bool usable = true;
+      for (int i = 0; i < j; ++i) usable = usable && maps[(size_t)i * TL_AGG + DS_S * DS_S + DS_S] == 0.0f;
+      __syncthreads();
+      if (usable) {
+        for (int i = 0; i < j; ++i) {
+          if (rowwave) {
+            const float* P = maps + (size_t)i * TL_AGG;
+            const float* h = &vec_s[cur][0];
+            float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float4 pv = *reinterpret_cast<const float4*>(P + row * DS_S + 16 * part + 4 * q);
+              const float4 hv = *reinterpret_cast<const float4*>(h + 16 * part + 4 * q);
+              p[q] = fmaf(pv.x, hv.x, p[q]);
+              p[q] = fmaf(pv.y, hv.y, p[q]);
+              p[q] = fmaf(pv.z, hv.z, p[q]);
+              p[q] = fmaf(pv.w, hv.w, p[q]);
+            }
+            const float acc = quad_sum((p[0] + p[1]) + (p[2] + p[3]));
+            if (part == 0) vec_s[cur ^ 1][row] = acc + P[DS_S * DS_S + row];
+          }
+          __syncthreads();
+          cur ^= 1;
+        }
+      } else {
+        // A map is unusable: replay the window's earlier sub-chunks exactly.
+        stream(wstart, t0 - wstart, [&](int, const float* slot) {
+          if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
+          cur ^= 1;
+        });
+      }
+      float* Hseq = a.H + (size_t)seq * L * DS_S;
+      stream(t0, n, [&](int k, const float* slot) {
+        if (wave == 0 && k > 0) Hseq[(size_t)(t0 + k - 1) * DS_S + lane] = vec_s[cur][lane];
+        if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
+        cur ^= 1;
+      });
+      if (wave == 0) {
+        Hseq[(size_t)(t0 + n - 1) * DS_S + lane] = vec_s[cur][lane];
+        if (t0 + n == wend) a.hend[(size_t)(w & 1) * hb + (size_t)seq * DS_S + lane] = vec_s[cur][lane];
+      }
+      __syncthreads();
+    }
+  }
+
+  };
+
+  // ---- compose role: (P, q) of sub-chunk j < TL_SUB - 1 of window w_agg ----
+  auto compose_role = [&]() {
+  if (a.w_agg >= 0 && j < TL_SUB - 1) {
+    const int w = a.w_agg;
+    const int wstart = w * TL_W, wend = min(L, wstart + TL_W);
+    const int t0 = wstart + j * TL_LC;
+    const int n = min(wend, t0 + TL_LC) - t0;
+    if (n <= 0) return;  // uniform over the workgroup
+    int cur = 0;
+    if (tid < DS_S) vec_s[0][tid] = 0.0f;
+    if (tid == 0) bad_s = 0;
+    __syncthreads();
+    const int g = lane >> 4, cl = lane & 15;
+    // Compute wave cw owns the 16-row tile rt = cw % 4 of the new P and the
+    // 16-column tiles 2 (cw / 4) and 2 (cw / 4) + 1.
+    const int rt = wave & 3, nt0 = 2 * (wave >> 2);
+    // This wave's values of P as bf16 halves of B fragments: values r = 0..3
+    // of tile nt go to k block rt/2, slots 4 (rt%2) + r.
+    auto put_rows = [&](int buf, const tl_f32x4_t (&v)[2]) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        __bf16 h[4], l[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          h[r] = (__bf16)v[u][r];
+          l[r] = (__bf16)(v[u][r] - (float)h[r]);
+        }
+        __bf16* ph = reinterpret_cast<__bf16*>(&pf_s[buf][0][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
+        __bf16* pl = reinterpret_cast<__bf16*>(&pf_s[buf][1][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ph[r] = h[r], pl[r] = l[r];
+      }
+    };
+    tl_f32x4_t pm[2];  // this wave's tile rows of P, column tiles nt0, nt0 + 1
+    if (!loader) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pm[u][r] = (16 * rt + 4 * g + r == 16 * (nt0 + u) + cl) ? 1.0f : 0.0f;
+      put_rows(0, pm);
+    }
+    __syncthreads();
+    int pb = 0;
+    stream(t0, n, [&](int k, const float* slot) {
+      // B fragments of the previous P for this wave's column tiles.
+      tl_bf16x8_t bh[2][2], bl[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          bh[u][kb] = pf_s[pb][0][kb][nt0 + u][lane];
+          bl[u][kb] = pf_s[pb][1][kb][nt0 + u][lane];
+        }
+      // A_t fragments of this wave's rows: row 16 rt + l%16, columns
+      // 32 kb + 4 g .. +3 and 32 kb + 16 + 4 g .. +3.
+      tl_bf16x8_t ah[2], al[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const float4 u = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + g));
+        const float4 v = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + 4 + g));
+        const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+        tl_split(x, ah[kb], al[kb]);
+      }
+      if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        tl_f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kb], bh[u][kb], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bl[u][kb], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bh[u][kb], acc, 0, 0, 0);
+        }
+        pm[u] = acc;
+      }
+      put_rows(pb ^ 1, pm);
+      pb ^= 1;
+      cur ^= 1;
+    });
+    bool bad = false;
+    if (!loader)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad = bad || !(fabsf(pm[u][r]) <= 3.0e38f);
+    if (!loader && (bad || (tid < DS_S && !(fabsf(vec_s[cur][tid]) <= 3.0e38f)))) atomicOr(&bad_s, 1);
+    __syncthreads();
+    float* out = a.agg + (((size_t)(w & 1) * a.batch + seq) * (TL_SUB - 1) + j) * TL_AGG;
+    if (!loader) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          out[(16 * rt + 4 * g + r) * DS_S + 16 * (nt0 + u) + cl] = pm[u][r];
+      if (tid < DS_S) out[DS_S * DS_S + tid] = vec_s[cur][tid];
+      if (tid == 0) out[DS_S * DS_S + DS_S] = bad_s ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+  }
+  };
+
+  // The roles of one workgroup are independent (the re-run reads the maps
+  // and end states of earlier launches).  Half the workgroups compose first,
+  // so that at any time some stream transitions while others run the
+  // matrix products.
+  if (seq & 1) {
+    compose_role();
+    rerun_role();
+  } else {
+    rerun_role();
+    compose_role();
+  }
+}
+
+size_t dense_scan_scratch_bytes(int batch, int L, int s) {
+  if (s != DS_S || L < 2 * TL_W) return 0;
+  return ((size_t)2 * batch * (TL_SUB - 1) * TL_AGG + (size_t)2 * batch * DS_S) * sizeof(float);
+}
+
 static bool ring_fits(const float* A, const float* B, int s) {
   return s == DS_S && ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0;
 }
@@ -208,8 +561,31 @@ static bool ring_fits(const float* A, const float* B, int s) {
 Status init_dense_scan_attributes() { return Status::Ok(); }
 
 Status launch_dense_scan(hipStream_t stream, const float* A, const float* B, const float* H0, float* H,
-                         int batch, int L, int s) {
+                         int batch, int L, int s, void* scratch, size_t scratch_bytes) {
   if (batch <= 0 || L <= 0 || s <= 0) return Status::Invalid("dense scan: dimensions must be positive");
+  const size_t need = dense_scan_scratch_bytes(batch, L, s);
+  if (need && ring_fits(A, B, s) && scratch && scratch_bytes >= need) {
+    // Two-level: launch l composes window l and re-runs window l - 1.
+    TwoLevelArgs ta;
+    ta.A = A;
+    ta.B = B;
+    ta.H0 = H0;
+    ta.H = H;
+    ta.agg = static_cast<float*>(scratch);
+    ta.hend = ta.agg + (size_t)2 * batch * (TL_SUB - 1) * TL_AGG;
+    ta.L = L;
+    ta.batch = batch;
+    const int nw = (L + TL_W - 1) / TL_W;
+    const long blocks = (long)batch * TL_SUB;
+    if (blocks > INT32_MAX) return Status::Invalid("dense scan: too many workgroups");
+    for (int l = 0; l <= nw; ++l) {
+      ta.w_agg = l < nw ? l : -1;
+      ta.w_rerun = l - 1;
+      dense_twolevel_kernel<<<(unsigned)blocks, TL_THREADS, 0, stream>>>(ta);
+      PSSA_LAUNCH_CHECK("dense_twolevel");
+    }
+    return Status::Ok();
+  }
   if (ring_fits(A, B, s)) {
     dense_scan_ring_kernel<<<batch, DS_THREADS, 0, stream>>>(A, B, H0, H, L);
   } else if (s <= 16)

@@ -365,6 +365,48 @@ def test_dense_scan_matches_oracle(hip, B, L, s):
     assert rel_err(h, ref) < 1e-4
 
 
+@pytest.mark.parametrize("B,L", [(1, 256), (3, 300), (2, 513), (5, 1000)])
+def test_dense_scan_two_level_matches_oracle(hip, B, L):
+    """d_state 64 and at least two windows of 128 steps take the chunked
+    two-level schedule (composed sub-chunk maps on the matrix cores, exact
+    fp32 re-runs); ragged last windows leave sub-chunks partial or empty."""
+    say("dense scan two-level", B, L)
+    s = 64
+    rng = np.random.default_rng(B * L)
+    q, _ = np.linalg.qr(rng.standard_normal((B, L, s, s)))
+    a = (q * rng.uniform(0.8, 0.99, (B, L, 1, s))).astype(np.float32)
+    b = rng.standard_normal((B, L, s)).astype(np.float32)
+    h0 = rng.standard_normal((B, s)).astype(np.float32)
+    h = hip.dense_scan(a, b, h0)
+    ref = O.dense_scan(a, b, h0, threads=4)
+    assert_parity(h, ref, 1e-4, f"two-level {B}x{L}")
+
+
+def test_dense_scan_two_level_replays_when_a_map_is_not_finite(hip):
+    """An infinite transition entry (sequence 1, step 170 = window 1,
+    sub-chunk 1) makes that sub-chunk's composed map non-finite: it is marked
+    unusable and the later sub-chunks of the window replay it in fp32.  The
+    states before the entry match the sequential recurrence, every state
+    from it on is non-finite as in the recurrence, and the other sequences
+    are unaffected."""
+    say("dense scan two-level fallback")
+    B, L, s = 3, 400, 64
+    rng = np.random.default_rng(77)
+    q, _ = np.linalg.qr(rng.standard_normal((B, L, s, s)))
+    a = (q * rng.uniform(0.8, 0.99, (B, L, 1, s))).astype(np.float32)
+    a[1, 170, 5, 9] = np.inf
+    b = rng.standard_normal((B, L, s)).astype(np.float32)
+    h = hip.dense_scan(a, b, None)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = O.dense_scan(a, b, None, threads=4)
+    for i in (0, 2):
+        assert_parity(h[i], ref[i], 1e-4, f"sequence {i}")
+    assert_parity(h[1, :170], ref[1, :170], 1e-4, "sequence 1 before the entry")
+    assert not np.isfinite(ref[1, 171:]).any()
+    assert not np.isfinite(h[1, 171:]).any()
+    np.testing.assert_array_equal(np.isfinite(h[1, 170]), np.isfinite(ref[1, 170]))
+
+
 def householder_pool(rng, n, s):
     """n random orthogonal matrices, each a product of two Householder
     reflections (the pool config 2's transitions are drawn from)."""

@@ -145,37 +145,47 @@ template <int J, int NB>
 __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
   constexpr int GS = J < 16 ? J : 16;
   constexpr int NG = J / GS;
+  static_assert(J <= 32, "one B/C load per wave covers at most 32 states");
   __shared__ float sY[NB * 4 * NG][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i0 = blockIdx.x * 64, b = blockIdx.y;
   const int jw = blockIdx.z * NB * 4 * J + wave * J;
   const int i = i0 + lane;
   const bool ivalid = i < a.d;
   const int d = a.d, s = a.s;
   const size_t r = b;  // T == 1: lane b's row
+  float* carry = a.carry + (size_t)b * a.carry_stride;
+  // Every load is issued before the first carry store: the wave's B values
+  // (lanes 0..J-1) and C values (lanes 32..32+J-1) in one load, broadcast
+  // with readlane, then the carry and rate of each of its J states.
+  const int jb = jw + (lane & 31);
+  float bc = 0.0f;
+  if ((lane & 31) < J && jb < s) bc = lane < 32 ? a.bproj[r * a.ld_b + jb] : a.cproj[r * a.ld_c + jb];
   const float dl = ivalid ? a.delta[r * a.ld_delta + i] : 0.0f;
   const float u = dl * (ivalid ? a.xn[r * a.ld_x + i] : 0.0f);
-  float* carry = a.carry + (size_t)b * a.carry_stride;
+  float h[J], r2[J];
+#pragma unroll
+  for (int q = 0; q < J; ++q) {
+    const int j = jw + q;
+    const bool ok = ivalid && j < s;
+    h[q] = ok ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
+    r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
+  }
+  const int bc_bits = __float_as_int(bc);
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
-    float h[GS], r2[GS];
-#pragma unroll
-    for (int qq = 0; qq < GS; ++qq) {
-      const int j = jw + g * GS + qq;
-      const bool ok = ivalid && j < s;
-      h[qq] = ok ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
-      r2[qq] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
-    }
     float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int qq = 0; qq < GS; ++qq) {
-      const int j = jw + g * GS + qq;
-      const float bq = j < s ? a.bproj[r * a.ld_b + j] : 0.0f;
-      const float cq = j < s ? a.cproj[r * a.ld_c + j] : 0.0f;
-      const float ab = __builtin_amdgcn_exp2f(dl * r2[qq]);
-      h[qq] = fmaf(ab, h[qq], u * bq);
-      yp4[qq & 3] = fmaf(h[qq], cq, yp4[qq & 3]);
-      if (ivalid && j < s) __builtin_nontemporal_store(h[qq], &carry[(size_t)j * d + i]);
+      const int q = g * GS + qq;
+      const int j = jw + q;
+      const float bq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, q));
+      const float cq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, 32 + q));
+      const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
+      h[q] = fmaf(ab, h[q], u * bq);
+      yp4[qq & 3] = fmaf(h[q], cq, yp4[qq & 3]);
+      if (ivalid && j < s) __builtin_nontemporal_store(h[q], &carry[(size_t)j * d + i]);
     }
     sY[wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
   }

@@ -819,16 +819,46 @@ __device__ double rq_sequential(const float (&x)[RQ_V * 4], const float (&y)[RQ_
   return acc;
 }
 
-__device__ __forceinline__ double wave_min_f64(double v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
-  return v;
+// Lane exchanges inside each row of 16 lanes (DPP; gfx9 dpp_ctrl codes:
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror).  They
+// run in the VALU pipe, with none of the LDS round trip of a shuffle.
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140;
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// Sum over the 64 lanes of a fully active wave, the same in every lane:
+// pairs, quads, halves and whole rows of 16 lanes by DPP (each exchange adds
+// the same two operands in both lanes), then the four row sums as
+// (r0 + r1) + (r2 + r3).  Deterministic; the order differs from a
+// sequential sum (callers bound the difference).
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_f64<DPP_QUAD_XOR1>(v);
+  v += dpp_f64<DPP_QUAD_XOR2>(v);
+  v += dpp_f64<DPP_ROW_HALF_MIRROR>(v);
+  v += dpp_f64<DPP_ROW_MIRROR>(v);
+  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+// Minimum over the 64 lanes of a fully active wave (order-free), by DPP.
+__device__ __forceinline__ float wave_min_dpp(float v) {
+  v = fminf(v, dpp_f32<DPP_QUAD_XOR1>(v));
+  v = fminf(v, dpp_f32<DPP_QUAD_XOR2>(v));
+  v = fminf(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+  v = fminf(v, dpp_f32<DPP_ROW_MIRROR>(v));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fminf(fminf(r0, r1), fminf(r2, r3));
 }
 
 __device__ __forceinline__ float rq_qsq(double qs) {
@@ -890,7 +920,7 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
       const float4 v = *reinterpret_cast<const float4*>(&s_lmin[wave][4 * l4]);
       le += (v.x <= lm) + (v.y <= lm) + (v.z <= lm) + (v.w <= lm);
     }
-    const float lim = wave_min(le >= K ? lm : HUGE_VALF) * (1.0f + (float)RK_TIE);
+    const float lim = wave_min_dpp(le >= K ? lm : HUGE_VALF) * (1.0f + (float)RK_TIE);
     int m = 0;
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
@@ -899,27 +929,30 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
       if (c) cand[m + __popcll(b & ((1ull << lane) - 1ull))] = (uint16_t)(lane + 64 * j);
       m += __popcll(b);
     }
-    // ---- the query row (f64) and |q|^2 ----
+    // ---- the query row and |q|^2 ----
     const float* qrow = a.q + n * a.ld_q;
-    double qd[V * 4];
+    float qv[V * 4];
     double qs = 0.0;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int i = 256 * v + 4 * lane;
       const float4 x = i < dk ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-      qd[4 * v] = x.x, qd[4 * v + 1] = x.y, qd[4 * v + 2] = x.z, qd[4 * v + 3] = x.w;
+      qv[4 * v] = x.x, qv[4 * v + 1] = x.y, qv[4 * v + 2] = x.z, qv[4 * v + 3] = x.w;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qs = fma(qd[4 * v + e], qd[4 * v + e], qs);
+      for (int e = 0; e < 4; ++e) qs = fma((double)qv[4 * v + e], (double)qv[4 * v + e], qs);
     }
     qs = wave_sum_f64(qs);
     float q_sq = rq_qsq(qs);
     if (rq_qsq(qs * (1.0 - RQ_SUM_REL)) != rq_qsq(qs * (1.0 + RQ_SUM_REL))) {
       float qf[RQ_V * 4], zero[RQ_V * 4];
 #pragma unroll
-      for (int e = 0; e < RQ_V * 4; ++e) qf[e] = e < V * 4 ? (float)qd[e < V * 4 ? e : 0] : 0.0f, zero[e] = 0.0f;
+      for (int e = 0; e < RQ_V * 4; ++e) qf[e] = e < V * 4 ? qv[e < V * 4 ? e : 0] : 0.0f, zero[e] = 0.0f;
       q_sq = rq_qsq(rq_sequential(qf, zero, dk));
     }
-    // ---- candidate sums |q - k|^2 across the wave, RQ_G rows at a time ----
+    // ---- candidate sums |q - k|^2 across the wave, RQ_G rows at a time
+    // (prefetching the next group's rows measured no faster: the sums are
+    // bound by the L2 -> CU bandwidth of the key rows, and the extra
+    // registers cost waves) ----
     for (int c0 = 0; c0 < m; c0 += RQ_G) {
       float kf[RQ_G][V * 4];
 #pragma unroll
@@ -938,7 +971,7 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
         double acc = 0.0;
 #pragma unroll
         for (int e = 0; e < V * 4; ++e) {
-          const double t = qd[e] - (double)kf[g][e];
+          const double t = (double)qv[e] - (double)kf[g][e];
           acc = fma(t, t, acc);
         }
         sq[g] = wave_sum_f64(acc);

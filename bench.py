@@ -125,6 +125,62 @@ def cpu_baseline(weights, ids, budget_s: float):
     }
 
 
+def bench_small_prefill(dev, args, log):
+    """Config 1: the ~1.5M-parameter model the reference runs on its CPU path
+    (d128 s64, 2 layers, V8192, 512-slot bank of dim 128), fp32 weights in the
+    config's N(0, 0.02) initialisation from seed 0 with filled banks, one lane
+    x 512 uniform random tokens.  The last-token logits are checked against
+    the oracle (1e-4)."""
+    from oracle import oracle as O
+    from pssa_amd import ModelWeights, PSSAConfig, PSSALayer
+
+    cfg = PSSAConfig(depth=2, d_vocab=8192, d_latent=128, d_state=64, d_mem_key=128, mem_capacity=512)
+    w = ModelWeights.init(cfg, 0, "baseline")
+    w.populate_banks(1)
+    T = 512
+    ids = np.random.default_rng(0).integers(0, cfg.d_vocab, (1, T), dtype=np.uint32)
+    layer = PSSALayer(dev, w, lanes=1, max_tokens=T, weight_dtype="f32")
+    layer.stage_ids(ids)
+
+    def step():
+        layer.reset_recurrent_state()
+        layer.prefill_staged()
+
+    for _ in range(3):
+        step()
+    dev.synchronize()
+    reps = 20
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    dev.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    got = layer.read_logits()
+    layer.close()
+    om = O.OracleModel(w)
+    st = om.zero_state(1)
+    t0 = time.perf_counter()
+    ref = om.prefill_lanes(st, ids, threads=1, logits=True)
+    cpu_wall = time.perf_counter() - t0
+    err = float(np.max(np.abs(got - ref)) / max(1e-30, float(np.max(np.abs(ref)))))
+    _, cpu_model = host_threads()
+    log(f"config 1 prefill: {dt * 1e3:.3f} ms, {T / dt:.0f} tok/s, rel err {err:.2e}")
+    # Forward work: 2 flops per multiply-accumulate of every per-token product
+    # and scan element (stage_work), against the fp32 vector peak.
+    work = stage_work(cfg, 1, T)
+    flops = work["gemm_flops"] + work["ssm_flops"]
+    return {"workload": "config 1: d128 s64 k128 L2 V8192 C512, fp32, N(0,0.02) init, 1 lane x 512 tokens",
+            "ms": dt * 1e3, "tokens_per_s": T / dt, "last_logits_rel_err": err,
+            "roofline": {"bound": "latency", "achieved": flops / dt / 1e12, "peak": FP32_TFLOPS,
+                         "unit": "TFLOP/s", "frac": flops / dt / 1e12 / FP32_TFLOPS,
+                         "note": "one lane: each layer's scan is a 512-step dependent chain over 8192 "
+                                 "state elements, so the pass is bound by step latency, not by any unit's rate"},
+            "cpu_baseline": {"value": T / cpu_wall, "unit": "tokens/s", "cores": 1, "cpu_model": cpu_model,
+                             "kind": "port",
+                             "sample": f"the whole workload (1 lane x {T} tokens), oracle prefill_inference "
+                                       f"restatement on one thread, {cpu_wall:.2f} s wall"}}
+
+
 def bench_decode(dev, args, log):
     """Config 5: 256 streams of the prefill model, each with a 512-token
     prefilled state (untimed), then 128 greedy steps, each one hipGraph-captured
@@ -414,11 +470,11 @@ def main():
     ap.add_argument("--decode-prompt", type=int, default=512)
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the config 2 / 4 / 5 measurements (dense scan, retrieval, decode)")
+                    help="skip the config 1 / 2 / 4 / 5 measurements (small prefill, dense scan, retrieval, decode)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["decode", "retrieval", "dense_scan", "train_forward"],
-                    help="only measure this extra (config 5, 4, 2 or the training forward) and print its "
+    ap.add_argument("--only", choices=["small_prefill", "decode", "retrieval", "dense_scan", "train_forward"],
+                    help="only measure this extra (config 1, 5, 4, 2 or the training forward) and print its "
                          "JSON; for profiling")
     args = ap.parse_args()
     if args.copy_probe:
@@ -429,7 +485,8 @@ def main():
 
         dev = HipDevice(0)
         log = lambda *a: print("[bench]", *a, file=sys.stderr, flush=True)  # noqa: E731
-        run = {"decode": bench_decode, "retrieval": bench_retrieval, "dense_scan": bench_dense_scan,
+        run = {"small_prefill": bench_small_prefill, "decode": bench_decode, "retrieval": bench_retrieval,
+               "dense_scan": bench_dense_scan,
                "train_forward": bench_train_forward}[args.only]
         print(json.dumps({args.only: run(dev, args, log)}), flush=True)
         dev.close()
@@ -512,7 +569,8 @@ def main():
     extras = None
     if not args.no_extras:
         layer.close()
-        extras = {"decode": bench_decode(dev, args, log),
+        extras = {"small_prefill": bench_small_prefill(dev, args, log),
+                  "decode": bench_decode(dev, args, log),
                   "retrieval": bench_retrieval(dev, args, log),
                   "dense_scan": bench_dense_scan(dev, args, log),
                   "train_forward": bench_train_forward(dev, args, log, w, ids)}

@@ -288,6 +288,32 @@ def bench_train_forward(dev, args, log, w=None, ids=None):
     head_ms = stages.get("head", 0.0)
     head_flops = 2.0 * lanes * T * cfg.d_vocab * cfg.d_latent
     log(f"train forward: {step_s * 1e3:.3f} ms, loss {loss:.4f}, head + cross entropy {head_ms:.3f} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        # forward_train_chunk (src/pssa.rs:2597-2752) restated by the oracle,
+        # one thread, on a prefix of the first sequence sized to the budget.
+        from oracle import oracle as O
+
+        _, cpu_model = host_threads()
+        om = O.OracleModel(w)
+        tg = np.roll(ids[0], -1)
+        probe = 4
+        t0 = time.perf_counter()
+        om.train_chunk_forward(om.zero_state(), ids[0, :probe], tg[:probe])
+        per_tok = (time.perf_counter() - t0) / probe
+        n_cpu = int(max(8, min(T, args.cpu_budget / 2 / per_tok)))
+        t0 = time.perf_counter()
+        om.train_chunk_forward(om.zero_state(), ids[0, :n_cpu], tg[:n_cpu])
+        wall = time.perf_counter() - t0
+        cpu = {"value": n_cpu / wall, "unit": "tokens/s", "cores": 1, "cpu_model": cpu_model, "kind": "port",
+               "sample": f"first {n_cpu} tokens of sequence 0, oracle forward_train_chunk restatement "
+                         f"(logits and cross entropy per token), one thread, {wall:.1f} s wall"}
+    # The part this pass adds to the prefill: the all-token head GEMM and the
+    # cross entropy (the layers are the prefill's kernels, measured there).
+    head_roof = {"kernel": "head GEMM + cross entropy", "bound": "mfma",
+                 "achieved": head_flops / (head_ms * 1e-3) / 1e12 if head_ms else None,
+                 "peak": BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
+                 "frac": head_flops / (head_ms * 1e-3) / 1e12 / BF16_MFMA_TFLOPS if head_ms else None}
     return {
         "workload": f"config 3 training forward (SequenceBatch::forward): {lanes} sequences x {T} tokens, "
                     f"logits and cross entropy for every token, {args.dtype} weights",
@@ -295,9 +321,8 @@ def bench_train_forward(dev, args, log, w=None, ids=None):
         "ms_per_step": step_s * 1e3,
         "loss": loss,
         "head_ms": head_ms,
-        "head_roofline": {"bound": "mfma", "achieved": head_flops / (head_ms * 1e-3) / 1e12 if head_ms else None,
-                          "peak": BF16_MFMA_TFLOPS, "unit": "TFLOP/s",
-                          "frac": head_flops / (head_ms * 1e-3) / 1e12 / BF16_MFMA_TFLOPS if head_ms else None},
+        "roofline": head_roof,
+        "cpu_baseline": cpu,
     }
 
 

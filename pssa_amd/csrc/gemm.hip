@@ -678,6 +678,87 @@ static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const TA
 #undef PSSA_GEMM_SK_CASE
 }
 
+// fp32 GEMM for few token rows: one wave per 32*MT token rows x 32 weight
+// rows, operand fragments straight from global memory through a register
+// ring of RING 8-deep K steps.  A lane holds the four K values
+// k0 + 4*half .. +3 of its row of each operand, and MFMA q of a step sums the
+// pair (k0 + q, k0 + 4 + q): the v_mfma_f32_32x32x2f32 sequence of
+// gemm_kernel<float> for every output element, so both give the same bits
+// (K % 16 == 0: the tiled kernel's zero-padded last slab adds nothing).
+template <int KIND, int MT, int RING>
+__global__ __launch_bounds__(64) void gemm_skinny_f32_kernel(const float* __restrict__ A, int lda,
+                                                             const float* __restrict__ B, int ldb, int M, int N,
+                                                             int K, int vec_epi, EpiParams ep) {
+  const int lane = threadIdx.x, half = lane >> 5, l32 = lane & 31;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * 32 * MT;
+  const float* pa[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) pa[t] = A + (size_t)min(m0 + 32 * t + l32, M - 1) * lda + 4 * half;
+  const float* pb = B + (size_t)min(n0 + l32, N - 1) * ldb + 4 * half;
+  // Branch-free loop: prefetches past the end reload the last step and go
+  // unused, so the compiler's wait counts stay partial.
+  const int nk = K / 8;
+  float4 ra[RING][MT], rb[RING];
+  auto fetch = [&](int kt, int slot) {
+    const int ko = min(kt, nk - 1) * 8;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) ra[slot][t] = *reinterpret_cast<const float4*>(pa[t] + ko);
+    rb[slot] = *reinterpret_cast<const float4*>(pb + ko);
+  };
+  f32x16_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[t][i] = 0.0f;
+  auto step = [&](int q) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(rb[q].x, ra[q][t].x, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(rb[q].y, ra[q][t].y, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(rb[q].z, ra[q][t].z, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(rb[q].w, ra[q][t].w, acc[t], 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int q = 0; q < RING; ++q) fetch(q, q);
+  int k0 = 0;
+  for (; k0 + RING <= nk; k0 += RING) {
+#pragma unroll
+    for (int q = 0; q < RING; ++q) {
+      step(q);
+      fetch(k0 + RING + q, q);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < RING; ++q)
+    if (q < nk - k0) step(q);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    epilogue_32x32<float, KIND>(ep, acc[t], m0 + 32 * t + l32, n0, M, N, vec_epi, half, l32);
+}
+
+template <int MT, int RING>
+static void launch_skinny_f32_kind(hipStream_t stream, int kind, dim3 grid, const float* A, int lda,
+                                   const float* B, int ldb, int M, int N, int K, int ve, const EpiParams& ep) {
+#define PSSA_GEMM_SKF_CASE(KD)                                                                    \
+  case KD:                                                                                        \
+    gemm_skinny_f32_kernel<KD, MT, RING><<<grid, 64, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+    break;
+  switch (kind) {
+    PSSA_GEMM_SKF_CASE(EPI_STORE)
+    PSSA_GEMM_SKF_CASE(EPI_SEGMENTS)
+    PSSA_GEMM_SKF_CASE(EPI_ADD_AUX)
+    PSSA_GEMM_SKF_CASE(EPI_ZRAW)
+    PSSA_GEMM_SKF_CASE(EPI_SILU)
+    PSSA_GEMM_SKF_CASE(EPI_RESIDUAL)
+    PSSA_GEMM_SKF_CASE(EPI_SCALE)
+    PSSA_GEMM_SKF_CASE(EPI_SEGMENTS_TAP)
+    default:
+      break;
+  }
+#undef PSSA_GEMM_SKF_CASE
+}
+
 template <typename T>
 static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int lda, const T* B,
                         int ldb, int M, int N, int K, int vl, int ve, const EpiParams& ep) {
@@ -786,6 +867,24 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
       launch_skinny_kind<uint16_t, 2, 8>(stream, ep.kind, grid, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
     }
     PSSA_LAUNCH_CHECK("gemm_skinny");
+    return Status::Ok();
+  }
+  if (!bf16 && vec_load && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 127) / 128) < 128) {
+    // fp32 with few token rows: the 128 x 128 tiles would leave most CUs
+    // idle (a 512-row product has 4 to 20 of them); one wave per 32 x 32
+    // tile instead (64 x 32 past 768 output columns).
+    const auto* a32 = static_cast<const float*>(A);
+    const auto* b32 = static_cast<const float*>(B);
+    if (N <= 768) {
+      const dim3 grid((N + 31) / 32, (M + 31) / 32);
+      if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
+      launch_skinny_f32_kind<1, 8>(stream, ep.kind, grid, a32, lda, b32, ldb, M, N, K, vec_epi, ep);
+    } else {
+      const dim3 grid((N + 31) / 32, (M + 63) / 64);
+      if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
+      launch_skinny_f32_kind<2, 8>(stream, ep.kind, grid, a32, lda, b32, ldb, M, N, K, vec_epi, ep);
+    }
+    PSSA_LAUNCH_CHECK("gemm_skinny_f32");
     return Status::Ok();
   }
   if (vec_bf16 && K % LDS_BK == 0) {

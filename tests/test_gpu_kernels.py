@@ -30,6 +30,25 @@ def test_gemm_f32_matches_oracle(hip, m, n, k):
     assert rel_err(y, O.gemm_xwt(x, w)) < 1e-5
 
 
+@pytest.mark.parametrize("n", [768, 1024])
+def test_gemm_f32_few_rows_equal_tiled_rows_bitwise(hip, n):
+    """A product of few token rows runs one wave per 32 x 32 (or 64 x 32)
+    tile; a wide one the 128 x 128 tiles.  Both follow the same MFMA order
+    over K, so the first rows of a 16384-row product equal the same rows
+    computed alone, bit for bit (the prefill / decode identity of fp32
+    models rests on it)."""
+    say("gemm f32 few rows == tiled", n)
+    rng = np.random.default_rng(n)
+    m, k = 16384, 768
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    big = hip.try_dispatch_gemm(x, w, m, n, k).reshape(m, n)
+    for rows in (1, 37, 64):
+        few = hip.try_dispatch_gemm(np.ascontiguousarray(x[:rows]), w, rows, n, k).reshape(rows, n)
+        np.testing.assert_array_equal(few.view(np.uint32), big[:rows].view(np.uint32))
+    assert rel_err(big[:64], O.gemm_xwt(x[:64], w)) < 1e-5
+
+
 @pytest.mark.parametrize("m,n,k,batch", [(5, 9, 8, 1), (64, 130, 776, 2), (257, 96, 768, 1), (31, 3, 20, 3)])
 def test_gemm_bf16_weights(hip, m, n, k, batch):
     say("gemm bf16", m, n, k, batch)

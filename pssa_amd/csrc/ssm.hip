@@ -233,7 +233,9 @@ constexpr int SSM_TC = 4;
 
 template <int J, int NW, int WPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void ssm_scan_kernel(SsmArgs a) {
-  constexpr int TC = SSM_TC;
+  // Steps staged per chunk: with few states per lane a chunk's compute is
+  // short, so 16 steps stand between a chunk's input loads and their use.
+  constexpr int TC = J <= 8 ? 4 * SSM_TC : SSM_TC;
   constexpr int NT = NW * 64;
   constexpr int GS = J < 16 ? J : 16;        // states per readout group
   constexpr int NG = J / GS;                 // readout groups per wave
@@ -311,6 +313,36 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   __syncthreads();
   for (int t0 = 0; t0 < T; t0 += TC) {
     if (t0 + TC < T) load(t0 + TC);
+    if constexpr (J <= 8) {
+      // Few states per lane (small d_state, where a grid of few lanes is
+      // bound by the step chain): per four steps the exponentials and input
+      // terms first, all independent of h, then the recurrence and readout.
+      // The same operations as below (one readout group), so the same bits.
+      for (int t4 = 0; t4 < TC; t4 += 4) {
+        float ab[4][J], ub[4][J];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dl = sD[t4 + i][lane];
+          const float u = dl * sX[t4 + i][lane];
+          const float* bt = &sB[t4 + i][wave * J];
+#pragma unroll
+          for (int q = 0; q < J; ++q) {
+            ab[i][q] = __builtin_amdgcn_exp2f(dl * r2[q]);
+            ub[i][q] = u * bt[q];
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* ct = &sC[t4 + i][wave * J];
+          float yp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int q = 0; q < J; ++q) h[q] = fmaf(ab[i][q], h[q], ub[i][q]);
+#pragma unroll
+          for (int q = 0; q < J; ++q) yp[q & 3] = fmaf(h[q], ct[q], yp[q & 3]);
+          sY[wave][t4 + i][lane] = (yp[0] + yp[1]) + (yp[2] + yp[3]);
+        }
+      }
+    } else
     for (int tt = 0; tt < TC; ++tt) {
       const float dl = sD[tt][lane];
       const float u = dl * sX[tt][lane];

@@ -123,6 +123,17 @@ struct DevBuf {
   }
 };
 
+// fp32 -> bf16 bits, rounded to nearest even, on gfx950's v_cvt_pk_bf16_f32
+// (one instruction per pair; the same bits as the integer rounding
+// u + 0x7FFF + lsb for every finite value).
+typedef __bf16 bf16x2_cvt_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_cvt_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
+  const f32x2_cvt_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_cvt_t));
+}
+__device__ __forceinline__ uint16_t bf16_bits_dev(float f) { return (uint16_t)bf16x2_bits(f, 0.0f); }
+
 }  // namespace pssa
 
 // The opaque context handed out through the C ABI.

@@ -206,11 +206,7 @@ struct PlasticArgs {
   int lanes, C, dk, d, r, wt_bf16;
 };
 
-__device__ __forceinline__ uint16_t to_bf16(float v) {
-  uint32_t b = __float_as_uint(v);
-  b += 0x7FFFu + ((b >> 16) & 1u);
-  return (uint16_t)(b >> 16);
-}
+__device__ __forceinline__ uint16_t to_bf16(float v) { return bf16_bits_dev(v); }
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll

@@ -23,14 +23,8 @@ namespace pssa {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
-}
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-}
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return bf16_bits_dev(f); }
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return bf16x2_bits(lo, hi); }
 
 // softplus(x) = x > 20 ? x : ln(1 + e^x) (src/linalg.rs:548-551).  ln(1+t) is
 // evaluated as ln(u) * t / (u - 1) with u = 1 + t, which cancels the rounding
@@ -45,6 +39,25 @@ __device__ __forceinline__ float softplus_f(float x) {
 // sigmoid(x) = 1 / (1 + e^-x) (src/linalg.rs:553-555), with the hardware
 // reciprocal (1 ulp).
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// The input projection's column segments without branches: one exponential
+// per element (e^x for the softplus columns, e^-x for the sigmoid and SiLU
+// ones) and selects.  Every result is the expression softplus_f, sigmoid_f
+// or x * sigmoid_f evaluates for that column, so the bits are theirs; a
+// branch per segment and case would be inlined into every element of the
+// epilogue (tens of KB of code beside the scan in the instruction cache).
+__device__ __forceinline__ float segment_f(const int (&seg)[4], float x, int col) {
+  const bool sp = col < seg[0];
+  const bool sg = col >= seg[1] && col < seg[2];
+  const bool sl = col >= seg[2] && col < seg[3];
+  const float t = __expf(sp ? x : -x);
+  const float u = 1.0f + t;
+  const float spv = x > 20.0f ? x
+                    : t < 2.44140625e-4f ? t - 0.5f * t * t
+                                          : __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.0f));
+  const float sgv = __builtin_amdgcn_rcpf(u);
+  return sp ? spv : sg ? sgv : sl ? x * sgv : x;
+}
 
 // Maps the hardware block id to a tile so that the blocks one XCD receives
 // (block ids congruent mod 8) cover one contiguous range of tiles.
@@ -70,49 +83,6 @@ struct Op<float> {
 };
 
 constexpr int BM = 128, BN = 128, NT = 128;
-
-// One output element's epilogue (fp32 result before the stores).
-template <int KIND>
-__device__ __forceinline__ float epi_value(const EpiParams& ep, float acc, int row, int col, float ad) {
-  if constexpr (KIND == EPI_STORE) {
-    return acc;
-  } else if constexpr (KIND == EPI_SCALE) {
-    return acc * ep.scale;
-  } else if constexpr (KIND == EPI_SEGMENTS || KIND == EPI_SEGMENTS_TAP) {
-    if (col < ep.seg[0]) return softplus_f(acc);
-    if (col < ep.seg[1]) return acc;
-    if (col < ep.seg[2]) return sigmoid_f(acc);
-    if (col < ep.seg[3]) return acc * sigmoid_f(acc);
-    return acc;
-  } else if constexpr (KIND == EPI_ADD_AUX) {
-    return acc + ep.aux[(size_t)row * ep.ld_aux + col];
-  } else if constexpr (KIND == EPI_SILU) {
-    return acc * sigmoid_f(acc);
-  } else if constexpr (KIND == EPI_ZRAW) {
-    // z_raw = (y * ssm_scale) + (g * m_proj) + adapter, left to right
-    // (src/pssa.rs:1190-1192).
-    const float yv = ep.y[(size_t)row * ep.ld_y + col];
-    const float gv = ep.g[(size_t)row * ep.ld_g + col];
-    return (yv * ep.scale + gv * acc) + ad;
-  } else {  // EPI_RESIDUAL
-    // z_final = z_raw + mlp_out; layer 0 publishes it, deeper layers add it
-    // with the 1/sqrt(depth) residual scale (src/pssa.rs:2332-2337).
-    const float zf = ep.aux[(size_t)row * ep.ld_aux + col] + acc;
-    if (ep.first) return zf;
-    return ep.out32[(size_t)row * ep.ld32 + col] + ep.scale * zf;
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store_one(const EpiParams& ep, int row, int col, float r) {
-  if (ep.out32) ep.out32[(size_t)row * ep.ld32 + col] = r;
-  if (ep.out16) {
-    if constexpr (sizeof(T) == 2)
-      static_cast<uint16_t*>(ep.out16)[(size_t)row * ep.ld16 + col] = (uint16_t)f32_to_bf16_bits(r);
-    else
-      static_cast<float*>(ep.out16)[(size_t)row * ep.ld16 + col] = r;
-  }
-}
 
 // Four consecutive columns col..col+3 of one row.  `vec`: all four are in
 // range and every operand row is 16-byte aligned at col.
@@ -140,49 +110,66 @@ __device__ __forceinline__ void load_quad(const EpiParams& ep, int row, int col,
   }
 }
 
+// The epilogue of four consecutive columns col..col+3 of one row.  With `vec`
+// all four are in range and every operand row is 16-byte aligned at col: the
+// row operands are the ones `in` holds and the stores are vectors.
+// Otherwise each column in range is read and written on its own.  The
+// arithmetic is written once for both (fp32, before the stores):
+//   z_raw     r = (y * ssm_scale) + (g * m_proj) + adapter, left to right
+//             (src/pssa.rs:1190-1192), tap = adapter;
+//   residual  z_final = z_raw + mlp_out, tap = z_final; layer 0 publishes it,
+//             deeper layers add it with the 1/sqrt(depth) residual scale
+//             (src/pssa.rs:2332-2337).
 template <typename T, int KIND>
 __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, int N, bool vec,
                                          const float (&acc)[4], const float (&ad)[4], const QuadIn& in) {
-  if (vec) {
-    float r[4], tp[4] = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (KIND == EPI_ZRAW) {
-      const float4 yv = in.p;
-      const float4 gv = in.q;
-      r[0] = (yv.x * ep.scale + gv.x * acc[0]) + ad[0];
-      r[1] = (yv.y * ep.scale + gv.y * acc[1]) + ad[1];
-      r[2] = (yv.z * ep.scale + gv.z * acc[2]) + ad[2];
-      r[3] = (yv.w * ep.scale + gv.w * acc[3]) + ad[3];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) tp[e] = ad[e];
-    } else if constexpr (KIND == EPI_ADD_AUX || KIND == EPI_RESIDUAL) {
-      const float4 av = in.p;
-      const float a4[4] = {av.x, av.y, av.z, av.w};
-      if constexpr (KIND == EPI_ADD_AUX) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = acc[e] + a4[e];
-      } else {
-        const float o4[4] = {in.q.x, in.q.y, in.q.z, in.q.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float zf = a4[e] + acc[e];
-          tp[e] = zf;
-          r[e] = ep.first ? zf : o4[e] + ep.scale * zf;
-        }
-      }
+  float p4[4] = {0.f, 0.f, 0.f, 0.f}, q4[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (epi_reads(KIND)) {
+    if (vec) {
+      p4[0] = in.p.x, p4[1] = in.p.y, p4[2] = in.p.z, p4[3] = in.p.w;
+      q4[0] = in.q.x, q4[1] = in.q.y, q4[2] = in.q.z, q4[3] = in.q.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) r[e] = epi_value<KIND>(ep, acc[e], row, col + e, 0.0f);
+      for (int e = 0; e < 4; ++e)
+        if (col + e < N) {
+          if constexpr (KIND == EPI_ZRAW) {
+            p4[e] = ep.y[(size_t)row * ep.ld_y + col + e];
+            q4[e] = ep.g[(size_t)row * ep.ld_g + col + e];
+          } else {
+            p4[e] = ep.aux[(size_t)row * ep.ld_aux + col + e];
+            if (KIND == EPI_RESIDUAL && !ep.first) q4[e] = ep.out32[(size_t)row * ep.ld32 + col + e];
+          }
+        }
     }
-    if constexpr (KIND == EPI_ZRAW || KIND == EPI_RESIDUAL) {
-      if (ep.tap)
-        *reinterpret_cast<float4*>(ep.tap + (size_t)row * ep.ld_tap + col) = make_float4(tp[0], tp[1], tp[2], tp[3]);
-    } else if constexpr (KIND == EPI_SEGMENTS_TAP) {
-      if (ep.tap)
+  }
+  float r[4], tp[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (col + e >= ep.seg[2] && col + e < ep.seg[3])
-            ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = r[e];
+  for (int e = 0; e < 4; ++e) {
+    const float a = acc[e];
+    tp[e] = 0.0f;
+    if constexpr (KIND == EPI_STORE) {
+      r[e] = a;
+    } else if constexpr (KIND == EPI_SCALE) {
+      r[e] = a * ep.scale;
+    } else if constexpr (KIND == EPI_SEGMENTS || KIND == EPI_SEGMENTS_TAP) {
+      r[e] = segment_f(ep.seg, a, col + e);
+    } else if constexpr (KIND == EPI_ADD_AUX) {
+      r[e] = a + p4[e];
+    } else if constexpr (KIND == EPI_SILU) {
+      r[e] = a * sigmoid_f(a);
+    } else if constexpr (KIND == EPI_ZRAW) {
+      r[e] = (p4[e] * ep.scale + q4[e] * a) + ad[e];
+      tp[e] = ad[e];
+    } else {  // EPI_RESIDUAL
+      const float zf = p4[e] + a;
+      tp[e] = zf;
+      r[e] = ep.first ? zf : q4[e] + ep.scale * zf;
     }
+  }
+  constexpr bool tap4 = KIND == EPI_ZRAW || KIND == EPI_RESIDUAL;
+  if (vec) {
+    if (tap4 && ep.tap)
+      *reinterpret_cast<float4*>(ep.tap + (size_t)row * ep.ld_tap + col) = make_float4(tp[0], tp[1], tp[2], tp[3]);
     if (ep.out32)
       *reinterpret_cast<float4*>(ep.out32 + (size_t)row * ep.ld32 + col) = make_float4(r[0], r[1], r[2], r[3]);
     if (ep.out16) {
@@ -198,16 +185,23 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (col + e < N) {
-        store_one<T>(ep, row, col + e, epi_value<KIND>(ep, acc[e], row, col + e, ad[e]));
-        if constexpr (KIND == EPI_ZRAW) {
-          if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ad[e];
-        } else if constexpr (KIND == EPI_SEGMENTS_TAP) {
-          if (ep.tap && col + e >= ep.seg[2] && col + e < ep.seg[3])
-            ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = epi_value<KIND>(ep, acc[e], row, col + e, ad[e]);
-        } else if constexpr (KIND == EPI_RESIDUAL) {
-          if (ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = ep.aux[(size_t)row * ep.ld_aux + col + e] + acc[e];
+        if (tap4 && ep.tap) ep.tap[(size_t)row * ep.ld_tap + col + e] = tp[e];
+        if (ep.out32) ep.out32[(size_t)row * ep.ld32 + col + e] = r[e];
+        if (ep.out16) {
+          if constexpr (sizeof(T) == 2)
+            static_cast<uint16_t*>(ep.out16)[(size_t)row * ep.ld16 + col + e] = (uint16_t)f32_to_bf16_bits(r[e]);
+          else
+            static_cast<float*>(ep.out16)[(size_t)row * ep.ld16 + col + e] = r[e];
         }
       }
+  }
+  if constexpr (KIND == EPI_SEGMENTS_TAP) {
+    // The SiLU segment's columns also go to the adapter-activation tap.
+    if (ep.tap)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < N && col + e >= ep.seg[2] && col + e < ep.seg[3])
+          ep.tap[(size_t)row * ep.ld_tap + (col + e - ep.seg[2])] = r[e];
   }
 }
 
@@ -483,7 +477,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   constexpr int RPI = 16;               // slab rows per DMA instruction (64 lanes x 16 B)
   constexpr int BPW = R / RPI / 4;      // DMA instructions per wave per slab
   static_assert((R / RPI) % 4 == 0, "slab rows must split over four waves");
-  __shared__ __attribute__((aligned(1024))) uint16_t sm[S][R * BK];
+  // The slab ring is dynamic LDS (gemm_lds_bytes): with a static array the
+  // compiler derives an LDS-bound occupancy and pads the VGPR count up to it
+  // (100 -> 129), which keeps the tile from sharing a SIMD with a scan.
+  extern __shared__ __attribute__((aligned(1024))) uint16_t gemm_lds_smem[];
+  auto sm = reinterpret_cast<uint16_t(*)[R * BK]>(gemm_lds_smem);
 
   const int tilesN = (N + BNt - 1) / BNt, tilesM = (M + BMt - 1) / BMt;
   const int tile = xcd_tile(blockIdx.x, tilesM * tilesN);
@@ -532,7 +530,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       __builtin_amdgcn_s_waitcnt(BPW | (0x7 << 4) | (0xF << 8));  // vmcnt(BPW)
     else
       __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));        // vmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_s_barrier();
     if (kt + S - 1 < nk) issue((kt + S - 1) % S, (kt + S - 1) * BK);
     const uint16_t* a = sm[kt % S];
     const uint16_t* b = sm[kt % S] + BMt * BK;
@@ -781,13 +779,18 @@ static void launch_kind(hipStream_t stream, int kind, dim3 grid, const T* A, int
 #undef PSSA_GEMM_CASE
 }
 
+// Bytes of the slab ring of a gemm_lds_kernel<*, NW> workgroup.
+constexpr size_t gemm_lds_bytes(int nw) { return (size_t)LDS_STAGES * (128 + 64 * nw) * LDS_BK * 2; }
+
 template <int NW>
 static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint16_t* A, int lda,
                             const uint16_t* B, int ldb, int M, int N, int K, int ve,
                             const EpiParams& ep) {
-#define PSSA_GEMM_LDS_CASE(KD)                                                               \
-  case KD:                                                                                   \
-    gemm_lds_kernel<KD, NW><<<grid, 256, 0, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+  constexpr size_t lds = gemm_lds_bytes(NW);
+  static_assert(lds <= 64 * 1024, "the ring fits the default dynamic LDS limit");
+#define PSSA_GEMM_LDS_CASE(KD)                                                                 \
+  case KD:                                                                                     \
+    gemm_lds_kernel<KD, NW><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
     break;
   switch (kind) {
     PSSA_GEMM_LDS_CASE(EPI_STORE)

@@ -90,11 +90,7 @@ __device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long v)
   return v;
 }
 
-__device__ __forceinline__ uint16_t bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+__device__ __forceinline__ uint16_t bf16_bits(float f) { return bf16_bits_dev(f); }
 
 __device__ __forceinline__ void put_weight(const RetrieveArgs& a, int n, int s, float w) {
   const size_t o = (size_t)n * a.capacity + s;

@@ -38,11 +38,7 @@ __global__ void embed_kernel(const uint32_t* __restrict__ ids, const float* __re
 
 // Affine RMSNorm with epsilon inside the root (src/pssa.rs:1080-1086).  One
 // wave per row.
-__device__ __forceinline__ uint16_t bf16_of(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+__device__ __forceinline__ uint16_t bf16_of(float f) { return bf16_bits_dev(f); }
 
 constexpr int RMS_REG = 16;  // rows of up to 1024 columns are held in registers
 

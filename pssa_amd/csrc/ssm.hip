@@ -205,11 +205,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
       atomicAdd(a.y + r * a.ld_y + i, v);
     } else {
       a.y[r * a.ld_y + i] = v;
-      if (a.y16) {
-        uint32_t bits = __float_as_uint(v);
-        bits += 0x7FFFu + ((bits >> 16) & 1u);
-        a.y16[r * a.ld_y16 + i] = (uint16_t)(bits >> 16);
-      }
+      if (a.y16) a.y16[r * a.ld_y16 + i] = bf16_bits_dev(v);
     }
   }
 }

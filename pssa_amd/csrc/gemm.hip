@@ -40,23 +40,17 @@ __device__ __forceinline__ float softplus_f(float x) {
 // reciprocal (1 ulp).
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
-// The input projection's column segments without branches: one exponential
-// per element (e^x for the softplus columns, e^-x for the sigmoid and SiLU
-// ones) and selects.  Every result is the expression softplus_f, sigmoid_f
-// or x * sigmoid_f evaluates for that column, so the bits are theirs; a
-// branch per segment and case would be inlined into every element of the
-// epilogue (tens of KB of code beside the scan in the instruction cache).
+// The input projection's column segments (src/pssa.rs:1091-1116): softplus,
+// identity, sigmoid, SiLU, identity.  The segment is the same for every
+// column a wave holds in practice (the boundaries fall on 32-column tiles at
+// the model's shapes), so the branches do not diverge and each element
+// evaluates only its own function.
 __device__ __forceinline__ float segment_f(const int (&seg)[4], float x, int col) {
-  const bool sp = col < seg[0];
-  const bool sg = col >= seg[1] && col < seg[2];
-  const bool sl = col >= seg[2] && col < seg[3];
-  const float t = __expf(sp ? x : -x);
-  const float u = 1.0f + t;
-  const float spv = x > 20.0f ? x
-                    : t < 2.44140625e-4f ? t - 0.5f * t * t
-                                          : __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.0f));
-  const float sgv = __builtin_amdgcn_rcpf(u);
-  return sp ? spv : sg ? sgv : sl ? x * sgv : x;
+  if (col < seg[0]) return softplus_f(x);
+  if (col < seg[1]) return x;
+  if (col < seg[2]) return sigmoid_f(x);
+  if (col < seg[3]) return x * sigmoid_f(x);
+  return x;
 }
 
 // Maps the hardware block id to a tile so that the blocks one XCD receives

@@ -474,6 +474,22 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * finite and >= 1 (src/inference.rs:97-99). */
 int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* lanes, float penalty, char* err, size_t err_len);
 
+/* InferenceConfig::{temperature, top_p, top_k} for the lanes' choice
+ * (sample(), src/inference.rs:128-178; validation :87-100).  temperature 0 (the
+ * default) is the greedy choice.  Above 0 each choice draws one value from the
+ * lane's SimpleRng (src/linalg.rs:5-28), which this call seeds with `seed` for
+ * every lane (the reference's engine uses SimpleRng::new(1337),
+ * src/inference.rs:73); the states then persist across decode calls and
+ * resets.  Probabilities are exp((logit - max) / temperature) over ids
+ * 1..V-1 after the repetition penalty, summed in id order; the first top_k
+ * in (probability desc, id asc) order, cut where their running sum reaches
+ * top_p, are drawn from.  Must satisfy temperature finite >= 0, top_p finite
+ * in (0, 1], top_k >= 1; top_k above 64 with temperature > 0 is
+ * PSSA_HIP_EUNSUPPORTED here.  An invalid probability mass fails the decode
+ * with "invalid sampling probability mass". */
+int pssa_hip_lanes_set_sampling(pssa_hip_lanes* lanes, float temperature, float top_p, size_t top_k,
+                                uint64_t seed, char* err, size_t err_len);
+
 int pssa_hip_decode(pssa_hip_lanes* lanes, const uint32_t* first_ids, size_t n_lanes,
                     size_t steps, int flags, uint32_t* out_ids, size_t out_len,
                     float* logits_last, size_t logits_len, char* err, size_t err_len);

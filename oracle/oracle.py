@@ -80,6 +80,9 @@ def lib() -> C.CDLL:
         "oracle_forward_features": ([vp, fp, C.c_uint32, fp], None),
         "oracle_greedy": ([fp, C.c_size_t], C.c_uint32),
         "oracle_sample_greedy": ([fp, C.c_size_t, u32p, C.c_size_t, C.c_float], C.c_int64),
+        "oracle_sample": ([fp, C.c_size_t, u32p, C.c_size_t, C.c_float, C.c_float, C.c_float, C.c_size_t,
+                           C.POINTER(C.c_uint64)], C.c_int64),
+
         "oracle_dense_scan": ([fp, fp, fp, C.c_size_t, C.c_size_t, C.c_size_t, fp, C.c_int], None),
         "oracle_hebbian_update": ([fp, fp, fp, fp, C.c_size_t, C.c_size_t], None),
         "oracle_forward_taps": ([vp, fp, C.c_uint32, fp, fp, fp, fp, fp], None),
@@ -452,6 +455,27 @@ def sample_greedy(logits, history, penalty: float = 1.0) -> int:
     lg = np.array(logits, dtype=np.float32, copy=True)
     hist = np.ascontiguousarray(history, dtype=np.uint32)
     return int(lib().oracle_sample_greedy(ptr(lg), lg.size, ptr(hist, C.c_uint32), hist.size, penalty))
+
+
+class Rng:
+    """SimpleRng (src/linalg.rs:5-28) state, advanced by oracle calls."""
+
+    def __init__(self, seed: int = 1337):
+        self.state = C.c_uint64(lib().oracle_rng_new(seed))
+
+    def next_u32(self) -> int:
+        return int(lib().oracle_rng_next_u32(C.byref(self.state)))
+
+
+def sample(logits, history, rng: Rng, temperature: float, top_p: float = 1.0, top_k: int = 1 << 30,
+           penalty: float = 1.0) -> int:
+    """sample() (src/inference.rs:102-178) with the repetition penalty over the
+    last 64 history ids; at temperature > 0 one draw from `rng`.  -1 for
+    non-finite logits, -2 for an invalid probability mass."""
+    lg = np.array(logits, dtype=np.float32, copy=True)
+    hist = np.ascontiguousarray(history, dtype=np.uint32)
+    return int(lib().oracle_sample(ptr(lg), lg.size, ptr(hist, C.c_uint32), hist.size, penalty, temperature, top_p,
+                                   top_k, C.byref(rng.state)))
 
 
 def dot(a, b) -> np.float32:

@@ -1005,6 +1005,75 @@ int64_t oracle_sample_greedy(float* logits, size_t v, const uint32_t* hist, size
   return (int64_t)oracle_greedy(logits, v);
 }
 
+// --- src/inference.rs:102-178 sample() at any temperature -----------------------
+// The repetition penalty over the last 64 ids, then greedy at temperature 0;
+// otherwise probs over ids 1..V-1 (the maximum over 1..V-1 subtracted before
+// dividing by the temperature, f32 exp, a sequential f32 sum), candidates in
+// (probability descending, id ascending) order, the first top_k of them cut
+// where the running f32 sum first reaches top_p, and one draw of
+// gen_range_f32(0, mass) from the caller's generator matched against the
+// running sum.  Returns the id, -1 for non-finite logits, -2 for an invalid
+// probability mass, -3 without candidates.
+int64_t oracle_sample(float* logits, size_t v, const uint32_t* hist, size_t n_hist, float penalty,
+                      float temperature, float top_p, size_t top_k, uint64_t* rng_state) {
+  if (temperature == 0.0f) return oracle_sample_greedy(logits, v, hist, n_hist, penalty);
+  for (size_t i = 0; i < v; i++)
+    if (!std::isfinite(logits[i])) return -1;
+  if (penalty > 1.0f) {
+    for (size_t j = n_hist > 64 ? n_hist - 64 : 0; j < n_hist; j++) {
+      float& l = logits[hist[j]];
+      if (l > 0.0f)
+        l /= penalty;
+      else
+        l *= penalty;
+    }
+  }
+  float mx = -INFINITY;
+  for (size_t i = 1; i < v; i++) mx = std::max(mx, logits[i]);
+  std::vector<float> probs(v, 0.0f);
+  float sum = 0.0f;
+  for (size_t i = 1; i < v; i++) {
+    probs[i] = std::exp((logits[i] - mx) / temperature);
+    sum += probs[i];
+  }
+  if (!std::isfinite(sum) || sum <= 0.0f) return -2;
+  std::vector<std::pair<uint32_t, float>> cand;
+  for (size_t i = 1; i < v; i++)
+    if (std::isfinite(probs[i])) cand.emplace_back((uint32_t)i, probs[i] / sum);
+  if (cand.empty()) return -3;
+  // total_cmp on non-negative finite probabilities is the numeric order.
+  std::sort(cand.begin(), cand.end(), [](const std::pair<uint32_t, float>& a, const std::pair<uint32_t, float>& b) {
+    return a.second != b.second ? a.second > b.second : a.first < b.first;
+  });
+  const size_t k = std::min(cand.size(), top_k);
+  size_t cutoff = k;
+  float cumulative = 0.0f;
+  for (size_t i = 0; i < k; i++) {
+    cumulative += cand[i].second;
+    if (cumulative >= top_p) {
+      cutoff = i + 1;
+      break;
+    }
+  }
+  const size_t nf = std::max<size_t>(cutoff, 1);
+  float mass = 0.0f;
+  for (size_t i = 0; i < nf; i++) mass += cand[i].second;
+  Rng rng(1);
+  rng.state = *rng_state;
+  const float draw = rng.gen_range(0.0f, mass);
+  *rng_state = rng.state;
+  float running = 0.0f;
+  uint32_t id = cand[nf - 1].first;
+  for (size_t i = 0; i < nf; i++) {
+    running += cand[i].second;
+    if (draw <= running) {
+      id = cand[i].first;
+      break;
+    }
+  }
+  return (int64_t)id;
+}
+
 void oracle_dense_scan(const float* a, const float* b, const float* h0, size_t batch, size_t L,
                        size_t s, float* h, int threads) {
   parallel_for(batch, threads, [&](size_t bi) {

@@ -209,6 +209,11 @@ uint32_t oracle_greedy(const float* logits, size_t v);
 // penalty over the last 64 history ids; logits are penalised in place.
 // Returns the id, or -1 for non-finite logits.
 int64_t oracle_sample_greedy(float* logits, size_t v, const uint32_t* hist, size_t n_hist, float penalty);
+// sample() at any temperature (src/inference.rs:102-178); rng_state is the
+// caller's SimpleRng state, advanced by one draw when temperature > 0.
+int64_t oracle_sample(float* logits, size_t v, const uint32_t* hist, size_t n_hist, float penalty,
+                      float temperature, float top_p, size_t top_k, uint64_t* rng_state);
+
 
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t, sequential. */
 void oracle_dense_scan(const float* a, const float* b, const float* h0, size_t batch,

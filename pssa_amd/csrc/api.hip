@@ -1139,7 +1139,8 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     PSSA_RETURN_IF(L->hist.alloc(lanes * pssa_hip_lanes::kHist * 4));
     PSSA_RETURN_IF(L->hist_n.alloc(lanes * 4));
     PSSA_RETURN_IF(L->hist_pos.alloc(lanes * 4));
-    PSSA_RETURN_IF(L->nonfinite.alloc(8));  // [0] non-finite logits, [1] non-finite capped bank value
+    // [0] non-finite logits, [1] non-finite capped bank value, [2] invalid sampling mass
+    PSSA_RETURN_IF(L->nonfinite.alloc(16));
     PSSA_RETURN_IF(clear_history(L.get()));
     PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming));
     for (int g = 0; g < pssa_hip_lanes::kMaxGroups - 1; ++g) {
@@ -1730,7 +1731,8 @@ Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
 
 Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   if (L->graph_exec && L->graph_lanes == n_lanes && L->graph_plastic == (plastic ? 1 : 0) &&
-      L->graph_hybrid_epoch == L->model->hybrid_epoch && L->graph_penalty == L->rep_penalty)
+      L->graph_hybrid_epoch == L->model->hybrid_epoch && L->graph_penalty == L->rep_penalty &&
+      L->graph_temperature == L->temperature && L->graph_top_p == L->top_p && L->graph_top_k == L->top_k)
     return Status::Ok();
   if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
   if (L->graph) (void)hipGraphDestroy(L->graph);
@@ -1752,6 +1754,9 @@ Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   L->graph_plastic = plastic ? 1 : 0;
   L->graph_hybrid_epoch = L->model->hybrid_epoch;
   L->graph_penalty = L->rep_penalty;
+  L->graph_temperature = L->temperature;
+  L->graph_top_p = L->top_p;
+  L->graph_top_k = L->top_k;
   return Status::Ok();
 }
 
@@ -1765,6 +1770,35 @@ int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* L, float penalty, char
     PSSA_RETURN_IF(need(std::isfinite(penalty) && penalty >= 1.0f, "repetition penalty must be finite and >= 1"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     L->rep_penalty = penalty;
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_lanes_set_sampling(pssa_hip_lanes* L, float temperature, float top_p, size_t top_k, uint64_t seed,
+                                char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    // InferenceConfig validation (src/inference.rs:87-100).
+    PSSA_RETURN_IF(need(std::isfinite(temperature) && temperature >= 0.0f, "temperature must be finite and >= 0"));
+    PSSA_RETURN_IF(need(std::isfinite(top_p) && top_p > 0.0f && top_p <= 1.0f, "top-p must be finite in (0, 1]"));
+    PSSA_RETURN_IF(need(top_k > 0, "top-k must be positive"));
+    if (temperature > 0.0f && top_k > 64)
+      return Status{PSSA_HIP_EUNSUPPORTED, "sampling on the device supports top-k up to 64"};
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    if (temperature > 0.0f) {
+      if (!L->rng.p) PSSA_RETURN_IF(L->rng.alloc(L->lanes * 8));
+      if (!L->probs.p) PSSA_RETURN_IF(L->probs.alloc(L->lanes * L->model->cfg.d_vocab * 4));
+      // SimpleRng::new (src/linalg.rs:7-11): every lane starts from `seed`.
+      std::vector<uint64_t> st0(L->lanes, seed == 0 ? 0x853c49e6748fea9bULL : seed);
+      PSSA_HIP_TRY(hipMemcpyAsync(L->rng.p, st0.data(), L->lanes * 8, hipMemcpyHostToDevice, st));
+      PSSA_RETURN_IF(sync(L->ctx));
+    }
+    L->temperature = temperature;
+    L->top_p = top_p;
+    L->top_k = (int)std::min<size_t>(top_k, 64);
     return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);
@@ -1800,7 +1834,7 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
     PSSA_RETURN_IF(ensure_decode_buffers(L, n_lanes, steps));
-    PSSA_RETURN_IF(pssa::launch_fill_zero(st, static_cast<float*>(L->nonfinite.p), 2));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(st, static_cast<float*>(L->nonfinite.p), 3));
     const int zero = 0;
     PSSA_HIP_TRY(hipMemcpyAsync(L->gen_pos.p, &zero, 4, hipMemcpyHostToDevice, st));
     // After a prefill the first generated token is the choice from its logits
@@ -1821,8 +1855,8 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     }
     PSSA_RETURN_IF(download(out_ids, L->gen_ids, steps * n_lanes * 4, st));
     if (logits_last) PSSA_RETURN_IF(download(logits_last, L->logits, n_lanes * V * 4, st));
-    int nonfinite[2] = {0, 0};
-    PSSA_RETURN_IF(download(nonfinite, L->nonfinite, 8, st));
+    int nonfinite[3] = {0, 0, 0};
+    PSSA_RETURN_IF(download(nonfinite, L->nonfinite, 12, st));
     // The last generated token has not been consumed: a continuation passes
     // it as first_ids.  `ids` now holds the step tokens.
     L->staged_lanes = L->staged_len = 0;
@@ -1832,6 +1866,7 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     if (nonfinite[0]) return Status::Invalid("model emitted non-finite logits");
     // clamp_value refuses a non-finite value (src/memory.rs:151-152).
     if (nonfinite[1]) return Status::Invalid("capped memory value must be finite");
+    if (nonfinite[2]) return Status::Invalid("invalid sampling probability mass");
     return Status::Ok();
   };
   return pssa::finish(body(), err, err_len);

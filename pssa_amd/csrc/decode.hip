@@ -175,6 +175,248 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
   }
 }
 
+// Sampling at temperature > 0 (sample(), src/inference.rs:128-178) for one
+// lane per workgroup, after the same penalty window as greedy_kernel:
+//  - the maximum over ids 1..V-1 of the penalised logits;
+//  - probs[v] = exp((logit - max) / T) into the lane's scratch row, the
+//    exponential in f64 rounded once to f32 (the correctly rounded f32 value;
+//    the reference's f32::exp is within half an ulp plus a hair of it);
+//  - their f32 sum in id order by one thread, as the reference adds them;
+//  - the top_k candidates in (probability desc, id asc) order, p = probs/sum,
+//    by top_k rounds of a workgroup arg-max over the candidates that rank
+//    after the last one chosen;
+//  - the top_p cut, the mass, one gen_range_f32(0, mass) draw from the lane's
+//    SimpleRng and the running-sum match, in one thread.
+// The surprise is the raw logits' logsumexp minus the chosen one, computed as
+// greedy_kernel computes it.
+constexpr int kMaxSampleTopK = 64;
+
+struct SampleArgs {
+  float temperature = 0.0f, top_p = 1.0f;
+  int top_k = 1;
+  unsigned long long* rng = nullptr;  // [lanes] SimpleRng states
+  float* probs = nullptr;             // [lanes, V] scratch
+  int* bad_mass = nullptr;            // raised on an invalid probability mass
+};
+
+// (pa, va) ranks before (pb, vb): higher probability, then lower id.
+__device__ __forceinline__ bool ranks_before(float pa, int va, float pb, int vb) {
+  return pa > pb || (pa == pb && va < vb);
+}
+
+__global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ logits, int V,
+                                                     uint32_t* __restrict__ ids,
+                                                     uint32_t* __restrict__ gen_ids,
+                                                     const int* __restrict__ gen_pos, int n_lanes,
+                                                     float* __restrict__ surprise, GreedyWindow gw, SampleArgs sa) {
+  constexpr int H = pssa_hip_lanes::kHist;
+  __shared__ uint32_t s_win[H];
+  __shared__ float s_val[H];
+  __shared__ int s_n;
+  __shared__ float smx[4], ssm[4], s_bp[4];
+  __shared__ int s_bv[4];
+  __shared__ float s_max, s_sum;
+  __shared__ float s_selp[kMaxSampleTopK];
+  __shared__ int s_selv[kMaxSampleTopK];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* lg = logits + (size_t)row * V;
+  float* pr = sa.probs + (size_t)row * V;
+  const bool pen = gw.penalty > 1.0f && gw.hist != nullptr;
+  if (gw.hist && tid == 0) {
+    int n = gw.hist_n[row], pos = gw.hist_pos[row];
+    if (gw.append_row_id) {
+      gw.hist[(size_t)row * H + pos] = ids[row];
+      pos = (pos + 1) % H;
+      n = n < H ? n + 1 : H;
+      gw.hist_pos[row] = pos;
+      gw.hist_n[row] = n;
+    }
+    s_n = pen ? n : 0;
+    for (int j = 0; j < n && pen; ++j) s_win[j] = gw.hist[(size_t)row * H + (pos - n + j + H) % H];
+  }
+  __syncthreads();
+  const int wn = s_n;
+  // Penalised logits of the window ids: each distinct id divided (positive) or
+  // multiplied by the penalty once per occurrence, kept at its first entry.
+  if (wave == 0 && lane < wn) {
+    const uint32_t id = s_win[lane];
+    int c = 0;
+    for (int j = 0; j < wn; ++j) c += s_win[j] == id;
+    float l = id < (uint32_t)V ? lg[id] : 0.0f;
+    for (int q = 0; q < c; ++q) l = l > 0.0f ? l / gw.penalty : l * gw.penalty;
+    s_val[lane] = l;
+  }
+  __syncthreads();
+  auto plogit = [&](int v) {
+    for (int j = 0; j < wn; ++j)
+      if (s_win[j] == (uint32_t)v) return s_val[j];
+    return lg[v];
+  };
+
+  // Maximum of the penalised logits over 1..V-1; logsumexp of the raw ones.
+  float mx = -INFINITY, m = -INFINITY, sacc = 0.0f;
+  int bad = 0;
+  for (int v0 = 0; v0 < V; v0 += 256 * GR_CHUNK) {
+    float x[GR_CHUNK];
+#pragma unroll
+    for (int k = 0; k < GR_CHUNK; ++k) {
+      const int v = v0 + k * 256 + tid;
+      x[k] = v < V ? lg[v] : -INFINITY;
+    }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < GR_CHUNK; ++k) {
+      const int v = v0 + k * 256 + tid;
+      if (v < V) bad |= !isfinite(x[k]);
+      if (v >= 1 && v < V) mx = fmaxf(mx, wn ? plogit(v) : x[k]);
+      cm = fmaxf(cm, x[k]);
+    }
+    float cs = 0.0f;
+    if (cm != -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < GR_CHUNK; ++k) cs += expf(x[k] - cm);
+    }
+    lse_merge(m, sacc, cm, cs);
+  }
+  bad = __syncthreads_or(bad);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    lse_merge(m, sacc, __shfl_xor(m, off, 64), __shfl_xor(sacc, off, 64));
+  }
+  if (lane == 0) {
+    smx[wave] = m;
+    ssm[wave] = sacc;
+    s_bp[wave] = mx;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) lse_merge(m, sacc, smx[w], ssm[w]);
+    s_max = fmaxf(fmaxf(s_bp[0], s_bp[1]), fmaxf(s_bp[2], s_bp[3]));
+  }
+  __syncthreads();
+  const float top = s_max;
+  const float temp = sa.temperature;
+  // Subtract before dividing (src/inference.rs:139-142).
+  for (int v = tid; v < V; v += 256)
+    pr[v] = v == 0 ? 0.0f : (float)exp((double)((plogit(v) - top) / temp));
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int v = 1; v < V; ++v) sum += pr[v];
+    s_sum = sum;
+  }
+  __syncthreads();
+  const float sum = s_sum;
+  const bool mass_ok = isfinite(sum) && sum > 0.0f;
+  const int K = mass_ok ? min(V - 1, min(sa.top_k, kMaxSampleTopK)) : 0;
+  float lp = INFINITY;
+  int lv = -1;
+  for (int r = 0; r < K; ++r) {
+    float bp = -1.0f;
+    int bv = INT32_MAX;
+    for (int v = 1 + tid; v < V; v += 256) {
+      const float p = pr[v] / sum;
+      if (ranks_before(lp, lv, p, v) && ranks_before(p, v, bp, bv)) {
+        bp = p;
+        bv = v;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float op = __shfl_xor(bp, off, 64);
+      const int ov = __shfl_xor(bv, off, 64);
+      if (ranks_before(op, ov, bp, bv)) {
+        bp = op;
+        bv = ov;
+      }
+    }
+    if (lane == 0) {
+      s_bp[wave] = bp;
+      s_bv[wave] = bv;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 4; ++w)
+        if (ranks_before(s_bp[w], s_bv[w], bp, bv)) {
+          bp = s_bp[w];
+          bv = s_bv[w];
+        }
+      s_selp[r] = bp;
+      s_selv[r] = bv;
+    }
+    __syncthreads();
+    lp = s_selp[r];
+    lv = s_selv[r];
+  }
+  if (tid == 0) {
+    int best = 0;
+    if (!mass_ok) {
+      if (sa.bad_mass) sa.bad_mass[0] = 1;
+    } else {
+      int cutoff = K;
+      float cumulative = 0.0f;
+      for (int i = 0; i < K; ++i) {
+        cumulative += s_selp[i];
+        if (cumulative >= sa.top_p) {
+          cutoff = i + 1;
+          break;
+        }
+      }
+      const int nf = cutoff > 1 ? cutoff : 1;
+      float mass = 0.0f;
+      for (int i = 0; i < nf; ++i) mass += s_selp[i];
+      // SimpleRng::next_u32 (xorshift64*) and gen_range_f32(0, mass)
+      // (src/linalg.rs:13-27).
+      unsigned long long x = sa.rng[row];
+      x ^= x >> 12;
+      x ^= x << 25;
+      x ^= x >> 27;
+      sa.rng[row] = x;
+      const uint32_t u = (uint32_t)((x * 0x2545F4914F6CDD1DULL) >> 32);
+      const float norm = (float)u / (float)4294967295u;
+      const float draw = norm * mass;  // low + norm * (high - low) with low = 0
+      float running = 0.0f;
+      best = s_selv[nf - 1];
+      for (int i = 0; i < nf; ++i) {
+        running += s_selp[i];
+        if (draw <= running) {
+          best = s_selv[i];
+          break;
+        }
+      }
+    }
+    ids[row] = (uint32_t)best;
+    if (gen_ids) gen_ids[(size_t)gen_pos[0] * n_lanes + row] = (uint32_t)best;
+    if (surprise) surprise[row] = (m + logf(sacc)) - lg[best];
+    if (bad && gw.nonfinite) gw.nonfinite[0] = 1;
+  }
+}
+
+// The lanes' choice from L->logits: greedy at temperature 0, sampled above.
+static Status launch_choice(pssa_hip_lanes* L, size_t n_lanes, const GreedyWindow& gw, uint32_t* gen_ids,
+                            const int* gen_pos, float* surprise) {
+  const hipStream_t st = L->ctx->stream;
+  const int V = (int)L->model->cfg.d_vocab;
+  if (L->temperature > 0.0f) {
+    SampleArgs sa;
+    sa.temperature = L->temperature;
+    sa.top_p = L->top_p;
+    sa.top_k = L->top_k;
+    sa.rng = L->rng.as<unsigned long long>();
+    sa.probs = L->probs.as<float>();
+    sa.bad_mass = L->nonfinite.as<int>() + 2;
+    sample_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(), gen_ids,
+                                                     gen_pos, (int)n_lanes, surprise, gw, sa);
+    PSSA_LAUNCH_CHECK("sample");
+  } else {
+    greedy_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(), gen_ids,
+                                                     gen_pos, (int)n_lanes, surprise, gw);
+    PSSA_LAUNCH_CHECK("greedy");
+  }
+  return Status::Ok();
+}
+
 // Per-layer operand pointers of the plastic write kernels (one launch covers
 // every block).
 static_assert(kMaxDepth <= 32, "ValueCaps holds one cap per block");
@@ -457,18 +699,14 @@ Status init_decode_attributes() {
 
 Status run_greedy_from_logits(pssa_hip_lanes* L, size_t n_lanes, bool record) {
   const hipStream_t st = L->ctx->stream;
-  const int V = (int)L->model->cfg.d_vocab;
   GreedyWindow gw;
   gw.hist = L->hist.as<uint32_t>();
   gw.hist_n = L->hist_n.as<int>();
   gw.hist_pos = L->hist_pos.as<int>();
   gw.penalty = L->rep_penalty;
   gw.nonfinite = L->nonfinite.as<int>();
-  greedy_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
-                                                   record ? L->gen_ids.as<uint32_t>() : nullptr,
-                                                   record ? L->gen_pos.as<int>() : nullptr, (int)n_lanes, nullptr,
-                                                   gw);
-  PSSA_LAUNCH_CHECK("greedy");
+  PSSA_RETURN_IF(launch_choice(L, n_lanes, gw, record ? L->gen_ids.as<uint32_t>() : nullptr,
+                               record ? L->gen_pos.as<int>() : nullptr, nullptr));
   if (record) {
     advance_pos_kernel<<<1, 64, 0, st>>>(L->gen_pos.as<int>());
     PSSA_LAUNCH_CHECK("advance");
@@ -481,7 +719,6 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   const pssa_hip_config& c = M->cfg;
   const hipStream_t st = L->ctx->stream;
   const int d = (int)c.d_latent, k = (int)c.d_mem_key, r = (int)c.adapter_rank, C = (int)c.mem_capacity;
-  const int V = (int)c.d_vocab;
   const size_t n = n_lanes;
   PSSA_RETURN_IF(run_prefill(L, n_lanes, 1, plastic, false));
   GreedyWindow gw;
@@ -491,10 +728,7 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   gw.penalty = L->rep_penalty;
   gw.append_row_id = 1;  // the token this step consumed
   gw.nonfinite = L->nonfinite.as<int>();
-  greedy_kernel<<<(unsigned)n, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
-                                             L->gen_ids.as<uint32_t>(), L->gen_pos.as<int>(), (int)n,
-                                             L->surprise.as<float>(), gw);
-  PSSA_LAUNCH_CHECK("greedy");
+  PSSA_RETURN_IF(launch_choice(L, n, gw, L->gen_ids.as<uint32_t>(), L->gen_pos.as<int>(), L->surprise.as<float>()));
   if (plastic) {
     PlasticArgs p{};
     for (size_t l = 0; l < c.depth; ++l) {

@@ -107,6 +107,15 @@ struct pssa_hip_lanes {
   pssa::DevBuf hist, hist_n, hist_pos, nonfinite;
   float rep_penalty = 1.0f;
   float graph_penalty = 1.0f;
+  // Sampling at temperature > 0 (sample(), src/inference.rs:128-178): the
+  // settings (temperature 0: the greedy choice), each lane's SimpleRng state
+  // and the per-lane probability scratch [lanes, V]; the captured step
+  // records the settings it was built with.
+  float temperature = 0.0f, top_p = 1.0f;
+  int top_k = 1;
+  pssa::DevBuf rng, probs;
+  float graph_temperature = 0.0f, graph_top_p = 1.0f;
+  int graph_top_k = 1;
   size_t dec_lanes = 0, gen_cap = 0;
   // Captured decode step (one per lane count and plasticity setting).
   hipGraph_t graph = nullptr;

@@ -505,6 +505,12 @@ class PSSALayer:
         """InferenceConfig::repetition_penalty for the greedy choice (1 = off)."""
         _abi.call(self._lib.pssa_hip_lanes_set_repetition_penalty, self.handle, penalty)
 
+    def set_sampling(self, temperature: float, top_p: float = 0.85, top_k: int = 24, seed: int = 1337) -> None:
+        """InferenceConfig::{temperature, top_p, top_k} for the lanes' choice
+        (sample(), src/inference.rs:128-178); temperature 0 is greedy.  Every
+        lane's generator restarts from SimpleRng::new(seed)."""
+        _abi.call(self._lib.pssa_hip_lanes_set_sampling, self.handle, temperature, top_p, top_k, seed)
+
     def get_plastic(self, layer: int) -> dict:
         """One block's adapter fast weights and bank state as held on the device."""
         c = self.cfg

@@ -416,3 +416,90 @@ def test_config5_width_and_depth_plastic_decode_matches_oracle(hip, dtype):
     say("near-tie choices", ties, "of", S * steps)
     assert ties <= S * steps // 20
     layer.close()
+
+
+def oracle_sampled_decode(w, ids, steps, penalty, temperature, top_p, top_k, seed=1337):
+    """The reference's generate loop (src/inference.rs:345-391) with sample()
+    at a temperature: one SimpleRng per lane (the engine's, seeded with
+    `seed`), the first token from the prefill logits, then forward + sample."""
+    om = O.OracleModel(w)
+    out = np.zeros((steps, ids.shape[0]), np.uint32)
+    for i, prompt in enumerate(ids):
+        st = om.zero_state()
+        rng = O.Rng(seed)
+        hist = [int(t) for t in prompt]
+        cur = O.sample(om.prefill(st, prompt), hist, rng, temperature, top_p, top_k, penalty)
+        out[0, i] = cur
+        for s in range(1, steps):
+            hist.append(cur)
+            cur = O.sample(om.forward_inference(st, cur), hist, rng, temperature, top_p, top_k, penalty)
+            out[s, i] = cur
+    return out
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decode_sampling_matches_oracle_sample(hip, graph):
+    """Decode at the reference's default InferenceConfig (temperature 0.7,
+    top-p 0.85, top-k 24, repetition penalty 1.25) against the oracle's
+    sample() with the same generators: the same ids, a different sequence from
+    the greedy one, and the generators carry on across decode calls."""
+    say("decode sampling, graph", graph)
+    w = small_model(seed=31)
+    ids = np.random.default_rng(11).integers(1, w.cfg.d_vocab, (3, 9), dtype=np.uint32)
+    steps = 12
+    ref = oracle_sampled_decode(w, ids, steps, 1.25, 0.7, 0.85, 24)
+    assert not np.array_equal(ref, oracle_penalised_decode(w, ids, steps, 1.25))
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=64)
+    layer.set_repetition_penalty(1.25)
+    layer.set_sampling(0.7, 0.85, 24, seed=1337)
+    layer.prefill_inference(ids)
+    np.testing.assert_array_equal(layer.decode(steps, graph=graph), ref)
+    # Continuing: the generators were not reset, so a second prompt pass
+    # after a reset draws the oracle's next values.
+    layer.set_sampling(0.7, 0.85, 24, seed=1337)
+    layer.reset_recurrent_state()
+    layer.prefill_inference(ids)
+    first = layer.decode(5, graph=graph)
+    rest = layer.decode(steps - 5, first_ids=first[-1], graph=graph)
+    np.testing.assert_array_equal(np.concatenate([first, rest]), ref)
+    # Temperature 0 is the greedy choice again and draws nothing.
+    layer.set_sampling(0.0)
+    layer.reset_recurrent_state()
+    layer.prefill_inference(ids)
+    np.testing.assert_array_equal(layer.decode(steps, graph=graph), oracle_penalised_decode(w, ids, steps, 1.25))
+    layer.close()
+
+
+def test_decode_sampling_wide_vocabulary_and_top_k(hip):
+    """A 3000-id vocabulary (several passes of the workgroup per row), top-k 64
+    and top-p 1 (every kept candidate drawn from), no penalty, seed 0 (the
+    generator's fixed non-zero start)."""
+    say("decode sampling, wide vocabulary")
+    cfg = PSSAConfig(depth=1, d_vocab=3000, d_latent=64, d_state=32, d_mem_key=8, mem_capacity=16)
+    w = ModelWeights.init(cfg, 3, "baseline")
+    w.populate_banks(4, count=cfg.mem_capacity)
+    ids = np.random.default_rng(2).integers(1, cfg.d_vocab, (2, 5), dtype=np.uint32)
+    ref = oracle_sampled_decode(w, ids, 10, 1.0, 1.3, 1.0, 64, seed=0)
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    layer.set_sampling(1.3, 1.0, 64, seed=0)
+    layer.prefill_inference(ids)
+    np.testing.assert_array_equal(layer.decode(10), ref)
+    layer.close()
+
+
+def test_sampling_validation(hip):
+    say("decode sampling validation")
+    w = small_model(seed=2, depth=1)
+    layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    for t in (-0.1, float("nan"), float("inf")):
+        with pytest.raises(HipError, match="temperature must be finite"):
+            layer.set_sampling(t)
+    for p in (0.0, 1.5, float("nan")):
+        with pytest.raises(HipError, match="top-p must be finite"):
+            layer.set_sampling(0.7, p)
+    with pytest.raises(HipError, match="top-k must be positive"):
+        layer.set_sampling(0.7, 0.85, 0)
+    with pytest.raises(HipError, match="top-k up to 64"):
+        layer.set_sampling(0.7, 0.85, 65)
+    layer.set_sampling(0.0, 0.85, 1000)  # greedy: any top-k
+    layer.close()

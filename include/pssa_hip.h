@@ -350,7 +350,9 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
 void pssa_hip_lanes_free(pssa_hip_lanes* lanes);
 /* reset_recurrent_state (src/pssa.rs:2245-2250) for every lane. */
 int pssa_hip_lanes_reset(pssa_hip_lanes* lanes, char* err, size_t err_len);
-/* carry layout [lanes, depth, d*s]. */
+/* carry layout [lanes, depth, loops, d*s] (loops = 1 unless
+ * pssa_hip_lanes_set_loops; the SSM part of copy_recurrent_state_to,
+ * src/pssa.rs:2263-2281). */
 int pssa_hip_lanes_get_carry(pssa_hip_lanes* lanes, float* out, size_t len, char* err,
                              size_t err_len);
 int pssa_hip_lanes_set_carry(pssa_hip_lanes* lanes, const float* in, size_t len, char* err,
@@ -473,6 +475,16 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * the benchmark's pure argmax; the reference's default is 1.25.  Must be
  * finite and >= 1 (src/inference.rs:97-99). */
 int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* lanes, float penalty, char* err, size_t err_len);
+
+/* set_loops (src/pssa.rs:2171-2184; forward_inference_features,
+ * src/pssa.rs:2338-2373): every block runs `loops` passes per token, each with
+ * its own carry and adding output / loops to the features it read; every
+ * block after the first returns input + features / sqrt(depth).  1..=32; 1 is
+ * the original model.  Loop 0 keeps each block's carry, the others start at
+ * zero; pssa_hip_lanes_reset zeroes all.  Prefill, forward_inference and the
+ * greedy or sampled decode run looped; the batched training forward, plastic
+ * decode and the hybrid read are PSSA_HIP_EUNSUPPORTED with loops > 1 here. */
+int pssa_hip_lanes_set_loops(pssa_hip_lanes* lanes, size_t loops, char* err, size_t err_len);
 
 /* InferenceConfig::{temperature, top_p, top_k} for the lanes' choice
  * (sample(), src/inference.rs:128-178; validation :87-100).  temperature 0 (the

@@ -43,6 +43,8 @@ def lib() -> C.CDLL:
         "oracle_bf16_round": ([C.c_float], C.c_float),
         "oracle_get_dot_avx2": ([], C.c_int),
         "oracle_rng_new": ([C.c_uint64], C.c_uint64),
+        "oracle_set_loops": ([C.c_size_t], None),
+        "oracle_get_loops": ([], C.c_size_t),
         "oracle_rng_next_u32": ([C.POINTER(C.c_uint64)], C.c_uint32),
         "oracle_dot": ([fp, fp, C.c_size_t], C.c_float),
         "oracle_softplus": ([C.c_float], C.c_float),
@@ -129,11 +131,14 @@ def _operands(method):
     @functools.wraps(method)
     def run(self, *args, **kwargs):
         prev = lib().oracle_get_bf16_operands()
+        prev_loops = lib().oracle_get_loops()
         lib().oracle_set_bf16_operands(1 if self.bf16_operands else 0)
+        lib().oracle_set_loops(self.loops)
         try:
             return method(self, *args, **kwargs)
         finally:
             lib().oracle_set_bf16_operands(prev)
+            lib().oracle_set_loops(prev_loops)
 
     return run
 
@@ -151,12 +156,22 @@ class OracleModel:
         self.bf16_operands = bf16_operands
         self.view, self.keep = weights.c_view()
         self.ref = C.cast(C.pointer(self.view), vp)
+        self.loops = 1
+
+    def set_loops(self, loops: int) -> None:
+        """set_loops (src/pssa.rs:2171-2184): every block runs `loops` passes
+        per token, each with its own carry (states made by zero_state)."""
+        if not 1 <= loops <= 32:
+            raise ValueError("--loops must be between 1 and 32")
+        self.loops = loops
 
     def sync(self):
         self.w.sync_from_c(self.keep)
 
     def zero_state(self, lanes: int | None = None) -> np.ndarray:
-        shape = (self.cfg.depth, self.cfg.d_latent * self.cfg.d_state)
+        """Carries [depth, d*s] ([depth, loops, d*s] with loops > 1), per lane."""
+        ds = self.cfg.d_latent * self.cfg.d_state
+        shape = (self.cfg.depth, ds) if self.loops == 1 else (self.cfg.depth, self.loops, ds)
         return np.zeros(shape if lanes is None else (lanes,) + shape, np.float32)
 
     def init_reference(self, seed: int) -> int:

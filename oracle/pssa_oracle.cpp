@@ -33,6 +33,11 @@ int g_dot_avx2 = 1;
 // rounds each product's activation operand to bf16 where the device does;
 // the weights are rounded by the caller.  Off: the reference's arithmetic.
 int g_bf16_ops = 0;
+// Recurrent depth loops (set_loops, src/pssa.rs:2171-2184): every block runs
+// this many passes per token, each with its own carry; a lane's state is
+// [depth, loops, d_latent * d_state] (loop 0 first, as
+// copy_recurrent_state_to, src/pssa.rs:2263-2281).
+size_t g_loops = 1;
 
 // Round to the nearest bf16 (ties to even), widened back to f32.
 inline float bf16r(float f) {
@@ -477,11 +482,30 @@ struct Runner {
   void features(float* state, uint32_t id) {
     const oracle_config& c = m->cfg;
     const size_t d = c.d_latent, ds = c.d_latent * c.d_state;
-    block_forward(m->blocks[0], c, sc[0], state, m->embed + (size_t)id * d, feat.data());
     const float scale = 1.0f / sqrtf((float)c.depth);
-    for (size_t l = 1; l < c.depth; l++) {
-      block_forward(m->blocks[l], c, sc[l], state + l * ds, feat.data(), out.data());
-      for (size_t i = 0; i < d; i++) feat[i] += scale * out[i];
+    const size_t loops = g_loops;
+    if (loops == 1) {
+      block_forward(m->blocks[0], c, sc[0], state, m->embed + (size_t)id * d, feat.data());
+      for (size_t l = 1; l < c.depth; l++) {
+        block_forward(m->blocks[l], c, sc[l], state + l * ds, feat.data(), out.data());
+        for (size_t i = 0; i < d; i++) feat[i] += scale * out[i];
+      }
+      return;
+    }
+    // --- src/pssa.rs:2338-2373: each block's passes add out / loops to the
+    // features they read; every block after the first then returns
+    // input + residual_scale * features.
+    const float loop_scale = 1.0f / (float)loops;
+    std::memcpy(feat.data(), m->embed + (size_t)id * d, d * 4);
+    std::vector<float> inputs(d);
+    for (size_t l = 0; l < c.depth; l++) {
+      if (l > 0) inputs = feat;
+      for (size_t k = 0; k < loops; k++) {
+        block_forward(m->blocks[l], c, sc[l], state + (l * loops + k) * ds, feat.data(), out.data());
+        for (size_t i = 0; i < d; i++) feat[i] += loop_scale * out[i];
+      }
+      if (l > 0)
+        for (size_t i = 0; i < d; i++) feat[i] = inputs[i] + scale * feat[i];
     }
   }
   // --- src/pssa.rs:2379-2385 inference_logits ------------------------------------
@@ -534,6 +558,8 @@ extern "C" {
 
 void oracle_set_dot_avx2(int enabled) { g_dot_avx2 = enabled ? 1 : 0; }
 void oracle_set_bf16_operands(int enabled) { g_bf16_ops = enabled ? 1 : 0; }
+void oracle_set_loops(size_t loops) { g_loops = loops < 1 ? 1 : loops; }
+size_t oracle_get_loops(void) { return g_loops; }
 float oracle_bf16_round(float x) { return bf16r(x); }
 int oracle_get_bf16_operands(void) { return g_bf16_ops; }
 int oracle_get_dot_avx2(void) { return g_dot_avx2; }
@@ -929,7 +955,7 @@ int oracle_prefill(const oracle_model* m, float* state, const uint32_t* ids, siz
 int oracle_prefill_lanes(const oracle_model* m, float* states, const uint32_t* ids, size_t lanes,
                          size_t n, float* logits, int threads) {
   const oracle_config& c = m->cfg;
-  size_t per = c.depth * c.d_latent * c.d_state;
+  size_t per = c.depth * g_loops * c.d_latent * c.d_state;
   std::atomic<int> rc(0);
   std::vector<size_t> done(lanes, 0);
   parallel_for(lanes, threads, [&](size_t l) {
@@ -1141,6 +1167,7 @@ void oracle_forward_taps(const oracle_model* m, float* state, uint32_t id, float
 int oracle_decode(oracle_model* m, float* states, uint32_t* ids, size_t lanes, size_t steps,
                   int plastic, uint64_t step_base, uint32_t* out_ids, float* logits_last,
                   float* surprise_last, int threads) {
+  if (g_loops != 1) return -9;  // the composed decode step is single-loop
   const oracle_config& c = m->cfg;
   const size_t d = c.d_latent, ds = c.d_latent * c.d_state, V = c.d_vocab, k = c.d_mem_key,
                r = c.adapter_rank, depth = c.depth;

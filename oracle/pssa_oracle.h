@@ -113,6 +113,10 @@ float oracle_bf16_round(float x);
 int oracle_get_dot_avx2(void);
 
 /* linalg primitives */
+/* Recurrent depth loops for the forward paths (1: the original model); a
+ * lane's state is then [depth, loops, d_latent * d_state]. */
+void oracle_set_loops(size_t loops);
+size_t oracle_get_loops(void);
 uint64_t oracle_rng_new(uint64_t seed);
 uint32_t oracle_rng_next_u32(uint64_t* state);
 float oracle_dot(const float* a, const float* b, size_t n);

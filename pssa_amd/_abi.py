@@ -177,6 +177,7 @@ def lib() -> C.CDLL:
                                          C.c_int),
         "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_lanes_set_sampling": ([vp, C.c_float, C.c_float, sz, C.c_uint64, err_t, sz], C.c_int),
+        "pssa_hip_lanes_set_loops": ([vp, sz, err_t, sz], C.c_int),
         "pssa_hip_model_set_memory_top_k": ([vp, sz, err_t, sz], C.c_int),
         "pssa_hip_model_set_value_cap": ([vp, C.c_float, err_t, sz], C.c_int),
         "pssa_hip_batch_forward": ([vp, C.POINTER(Sequence), sz, fp, fp, sz, fp, sz, err_t, sz], C.c_int),

@@ -80,7 +80,7 @@ float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_device) {
   const pssa_hip_config& c = L->model->cfg;
   const int d = (int)c.d_latent, s = (int)c.d_state;
-  const size_t mats = L->lanes * c.depth;
+  const size_t mats = L->lanes * c.depth * L->loops;
   for (size_t m0 = 0; m0 < mats; m0 += 65535) {
     const size_t cnt = std::min<size_t>(65535, mats - m0);
     const size_t off = m0 * (size_t)d * s;
@@ -1169,7 +1169,7 @@ int pssa_hip_lanes_reset(pssa_hip_lanes* L, char* err, size_t err_len) {
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const pssa_hip_config& c = L->model->cfg;
     PSSA_RETURN_IF(pssa::launch_fill_zero(L->ctx->stream, L->carry.as<float>(),
-                                          L->lanes * c.depth * c.d_latent * c.d_state));
+                                          L->lanes * c.depth * L->loops * c.d_latent * c.d_state));
     PSSA_RETURN_IF(clear_history(L));
     // No prefill logits to continue from (reset_recurrent_state is followed
     // by a fresh prefill, src/inference.rs:347-355).
@@ -1183,8 +1183,8 @@ int pssa_hip_lanes_get_carry(pssa_hip_lanes* L, float* out, size_t len, char* er
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L && out, "null argument"));
     const pssa_hip_config& c = L->model->cfg;
-    const size_t n = L->lanes * c.depth * c.d_latent * c.d_state;
-    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
+    const size_t n = L->lanes * c.depth * L->loops * c.d_latent * c.d_state;
+    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*loops*d_latent*d_state"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     DevBuf tmp;
@@ -1200,8 +1200,8 @@ int pssa_hip_lanes_set_carry(pssa_hip_lanes* L, const float* in, size_t len, cha
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L && in, "null argument"));
     const pssa_hip_config& c = L->model->cfg;
-    const size_t n = L->lanes * c.depth * c.d_latent * c.d_state;
-    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*d_latent*d_state"));
+    const size_t n = L->lanes * c.depth * L->loops * c.d_latent * c.d_state;
+    PSSA_RETURN_IF(need(len == n, "carry length must be lanes*depth*loops*d_latent*d_state"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     DevBuf tmp;
@@ -1250,7 +1250,7 @@ static Status ragged_locked(pssa_hip_lanes* L, const uint32_t* ids, const uint64
   const pssa_hip_config& c = L->model->cfg;
   const size_t V = c.d_vocab;
   const hipStream_t st = L->ctx->stream;
-  const size_t cw = c.depth * c.d_latent * c.d_state;
+  const size_t cw = c.depth * L->loops * c.d_latent * c.d_state;
   size_t tokens = 0;
   for (size_t i = 0; i < n_lanes; ++i) tokens += lens[i];
   if (tokens == 0) return Status::Ok();
@@ -1423,6 +1423,8 @@ int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, siz
     const pssa_hip_model* M = L->model;
     const pssa_hip_config& c = M->cfg;
     const size_t V = c.d_vocab;
+    if (L->loops != 1)
+      return Status{PSSA_HIP_EUNSUPPORTED, "the batched training forward runs one loop here (set_loops 1)"};
     std::vector<char> used(L->lanes, 0);
     size_t tokens = 0;
     for (size_t i = 0; i < n_seqs; ++i) {
@@ -1448,7 +1450,7 @@ int pssa_hip_batch_forward(pssa_hip_lanes* L, const pssa_hip_sequence* seqs, siz
     std::lock_guard<std::mutex> g(L->ctx->mu);
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
-    const size_t cw = c.depth * c.d_latent * c.d_state;  // floats of one lane's carry
+    const size_t cw = c.depth * L->loops * c.d_latent * c.d_state;  // floats of one lane's carry
     if (!L->tok_logits.p) {
       PSSA_RETURN_IF(L->tok_logits.alloc(L->max_tokens * V * 4));
       PSSA_RETURN_IF(L->tok_meta.alloc(2 * L->max_tokens * 4));
@@ -1775,6 +1777,40 @@ int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* L, float penalty, char
   return pssa::finish(body(), err, err_len);
 }
 
+int pssa_hip_lanes_set_loops(pssa_hip_lanes* L, size_t loops, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    PSSA_RETURN_IF(need(loops >= 1 && loops <= 32, "--loops must be between 1 and 32; use --loops 1 for the original model"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    if (loops == L->loops) return Status::Ok();
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    const pssa_hip_config& c = L->model->cfg;
+    const size_t hs = c.d_latent * c.d_state, per = L->lanes * c.depth;
+    // Loop 0 keeps each block's persistent carry; the other loops start from
+    // zero, as resize_loop_tape leaves them (src/pssa.rs:2147-2167).
+    DevBuf carry;
+    PSSA_RETURN_IF(carry.alloc(per * loops * hs * 4));
+    PSSA_RETURN_IF(pssa::launch_fill_zero(st, carry.as<float>(), per * loops * hs));
+    PSSA_HIP_TRY(hipMemcpy2DAsync(carry.p, loops * hs * 4, L->carry.p, L->loops * hs * 4, hs * 4, per,
+                                  hipMemcpyDeviceToDevice, st));
+    if (loops > 1 && !L->Xin.p) PSSA_RETURN_IF(L->Xin.alloc(L->max_tokens * c.d_latent * 4));
+    PSSA_RETURN_IF(sync(L->ctx));
+    std::swap(L->carry, carry);
+    L->loops = loops;
+    // The captured step and the prefill logits belong to the old carries.
+    if (L->graph_exec) (void)hipGraphExecDestroy(L->graph_exec);
+    if (L->graph) (void)hipGraphDestroy(L->graph);
+    L->graph_exec = nullptr;
+    L->graph = nullptr;
+    L->graph_lanes = 0;
+    L->logit_lanes = 0;
+    L->carry_work = DevBuf();
+    return Status::Ok();
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 int pssa_hip_lanes_set_sampling(pssa_hip_lanes* L, float temperature, float top_p, size_t top_k, uint64_t seed,
                                 char* err, size_t err_len) {
   auto body = [&]() -> Status {
@@ -1823,6 +1859,8 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
       PSSA_RETURN_IF(need(L->logit_lanes == n_lanes, "decode without first ids continues the last prefill of n_lanes lanes"));
     }
     const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
+    if (plastic && L->loops != 1)
+      return Status{PSSA_HIP_EUNSUPPORTED, "plastic decode runs one loop here (set_loops 1)"};
     if (plastic) {
       PSSA_RETURN_IF(need(pssa::bank_write_lds((int)L->model->cfg.mem_capacity, (int)n_lanes) <= 160 * 1024,
                           "plastic decode: mem_capacity and n_lanes exceed the bank-write LDS budget"));

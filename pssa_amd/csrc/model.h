@@ -111,6 +111,11 @@ struct pssa_hip_lanes {
   // settings (temperature 0: the greedy choice), each lane's SimpleRng state
   // and the per-lane probability scratch [lanes, V]; the captured step
   // records the settings it was built with.
+  // Recurrent depth loops (set_loops, src/pssa.rs:2171-2184): passes per
+  // block and token, each with its own carry ([lanes, depth, loops, s, d]);
+  // Xin keeps a looped layer's input rows.
+  size_t loops = 1;
+  pssa::DevBuf Xin;
   float temperature = 0.0f, top_p = 1.0f;
   int top_k = 1;
   pssa::DevBuf rng, probs;

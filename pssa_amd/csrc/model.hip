@@ -297,6 +297,15 @@ __global__ __launch_bounds__(256) void token_ce_kernel(const float* __restrict__
   }
 }
 
+// x = in + scale * x: a looped layer after the first returns its input plus
+// the scaled features its passes left (src/pssa.rs:2370-2372).
+__global__ void loop_combine_kernel(float* __restrict__ x, const float* __restrict__ in, float scale, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+#pragma clang fp contract(off)
+    x[i] = in[i] + scale * x[i];
+  }
+}
+
 // Prefill of lanes lane0 .. lane0+n_lanes-1 on stream `st`, enqueued in
 // pieces (embed, each layer, head) so that concurrent views can be enqueued
 // layer by layer.  Every buffer pointer is offset to the view's rows, so
@@ -339,7 +348,7 @@ class PrefillView {
     Mv_ = static_cast<char*>(L->Mval.p) + row0 * d * es;
     H1_ = static_cast<char*>(L->H1.p) + row0 * 2 * d * es;
     ids_ = (tr ? tr->ids : L->ids.as<uint32_t>()) + row0;
-    carry_ = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c_.depth * (size_t)d * s_;
+    carry_ = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c_.depth * L->loops * (size_t)d * s_;
     logits_ = L->logits.as<float>() + lane0 * (size_t)V;
     row0_ = row0;
   }
@@ -351,7 +360,28 @@ class PrefillView {
     return Status::Ok();
   }
 
+  // One layer: its loops passes over the view's rows (set_loops,
+  // src/pssa.rs:2338-2373).  With one loop the pass is the whole block step
+  // (layer 0's output replaces the embedding, deeper ones add
+  // output / sqrt(depth)).  With more, every pass adds output / loops to the
+  // rows it read, and a layer after the first then returns
+  // input + output_sum_rows / sqrt(depth), its input kept in Xin.
   Status layer(size_t l) {
+    const size_t loops = L_->loops;
+    if (loops == 1) return pass(l, 0);
+    const size_t n = rows_ * (size_t)d_;
+    float* xin = L_->Xin.as<float>() + row0_ * d_;
+    if (l > 0) PSSA_HIP_TRY(hipMemcpyAsync(xin, X_, n * 4, hipMemcpyDeviceToDevice, st_));
+    for (size_t lp = 0; lp < loops; ++lp) PSSA_RETURN_IF(pass(l, lp));
+    if (l > 0) {
+      loop_combine_kernel<<<(unsigned)std::min<size_t>((n + 255) / 256, 65536), 256, 0, st_>>>(
+          X_, xin, 1.0f / sqrtf((float)c_.depth), n);
+      PSSA_LAUNCH_CHECK("loop_combine");
+    }
+    return Status::Ok();
+  }
+
+  Status pass(size_t l, size_t lp) {
     const DevBlock& B = M_->blocks[l];
     const int d = d_, s = s_, k = k_, C = C_, r = r_, n_in = n_in_, m = m_, dt = dt_;
     const size_t rows = rows_, T = T_;
@@ -401,8 +431,8 @@ class PrefillView {
     sa.xn = XN_;
     sa.ld_x = d;
     sa.rates2 = B.rates2.as<float>();
-    sa.carry = carry_ + l * (size_t)d * s;
-    sa.carry_stride = (long)(c_.depth * (size_t)d * s);
+    sa.carry = carry_ + (l * L_->loops + lp) * (size_t)d * s;
+    sa.carry_stride = (long)(c_.depth * L_->loops * (size_t)d * s);
     sa.y = Y_;
     sa.ld_y = d;
     sa.T = (int)T;
@@ -511,8 +541,8 @@ class PrefillView {
     e_r.kind = EPI_RESIDUAL;
     e_r.aux = Zr_;
     e_r.ld_aux = d;
-    e_r.first = l == 0 ? 1 : 0;
-    e_r.scale = 1.0f / sqrtf((float)c_.depth);
+    e_r.first = l == 0 && L_->loops == 1 ? 1 : 0;
+    e_r.scale = L_->loops == 1 ? 1.0f / sqrtf((float)c_.depth) : 1.0f / (float)L_->loops;
     e_r.out32 = X_;
     e_r.ld32 = d;
     if (taps) {
@@ -653,6 +683,9 @@ Status run_train_segment(pssa_hip_lanes* L, size_t n_lanes, size_t T, const Trai
 
 static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool taps, const TrainRows* tr) {
   const hipStream_t st = L->ctx->stream;
+  if (L->loops > 1)
+    for (const DevBlock& B : L->model->blocks)
+      if (B.hybrid) return Status{PSSA_HIP_EUNSUPPORTED, "the hybrid read runs one loop here (set_loops 1)"};
   const pssa_hip_config& c = L->model->cfg;
   const int nz = ssm_state_blocks((int)c.d_state);
   float* ypart = L->Ypart.p ? L->Ypart.as<float>() : nullptr;

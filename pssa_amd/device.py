@@ -376,7 +376,16 @@ class PSSALayer:
         _abi.call(self._lib.pssa_hip_lanes_reset, self.handle)
 
     def carry_shape(self):
-        return (self.lanes, self.cfg.depth, self.cfg.d_latent * self.cfg.d_state)
+        """[lanes, depth, d*s], or [lanes, depth, loops, d*s] with loops > 1."""
+        ds = self.cfg.d_latent * self.cfg.d_state
+        loops = getattr(self, "loops", 1)
+        return (self.lanes, self.cfg.depth, ds) if loops == 1 else (self.lanes, self.cfg.depth, loops, ds)
+
+    def set_loops(self, loops: int) -> None:
+        """set_loops (src/pssa.rs:2171-2184): `loops` passes per block and
+        token, each with its own carry (loop 0 keeps the current one)."""
+        _abi.call(self._lib.pssa_hip_lanes_set_loops, self.handle, loops)
+        self.loops = loops
 
     def get_carry(self) -> np.ndarray:
         out = np.empty(self.carry_shape(), np.float32)

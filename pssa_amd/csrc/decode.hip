@@ -178,13 +178,14 @@ __global__ __launch_bounds__(256) void greedy_kernel(const float* __restrict__ l
 // Sampling at temperature > 0 (sample(), src/inference.rs:128-178) for one
 // lane per workgroup, after the same penalty window as greedy_kernel:
 //  - the maximum over ids 1..V-1 of the penalised logits;
-//  - probs[v] = exp((logit - max) / T) into the lane's scratch row, the
-//    exponential in f64 rounded once to f32 (the correctly rounded f32 value;
-//    the reference's f32::exp is within half an ulp plus a hair of it);
+//  - probs[v] = exp((logit - max) / T) into the lane's row (LDS, or a global
+//    scratch row for large vocabularies), the exponential in f64 rounded once
+//    to f32 (the correctly rounded f32 value; the reference's f32::exp is
+//    within half an ulp plus a hair of it);
 //  - their f32 sum in id order by one thread, as the reference adds them;
-//  - the top_k candidates in (probability desc, id asc) order, p = probs/sum,
-//    by top_k rounds of a workgroup arg-max over the candidates that rank
-//    after the last one chosen;
+//  - p = probs / sum in place, then the top_k candidates in (probability
+//    desc, id asc) order by top_k rounds of a workgroup arg-max over the
+//    threads' own best candidates;
 //  - the top_p cut, the mass, one gen_range_f32(0, mass) draw from the lane's
 //    SimpleRng and the running-sum match, in one thread.
 // The surprise is the raw logits' logsumexp minus the chosen one, computed as
@@ -204,24 +205,35 @@ __device__ __forceinline__ bool ranks_before(float pa, int va, float pb, int vb)
   return pa > pb || (pa == pb && va < vb);
 }
 
+// Vocabularies up to this size keep the lane's probability row in LDS, where
+// the one-thread ordered sum reads it at LDS latency; larger ones use the
+// global scratch row.
+constexpr int kSampleLdsMaxV = 36 * 1024;
+constexpr int kWinBloomWords = 64;  // 2048-bit filter of the penalty window ids
+
+template <bool ROW_LDS>
 __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ logits, int V,
                                                      uint32_t* __restrict__ ids,
                                                      uint32_t* __restrict__ gen_ids,
                                                      const int* __restrict__ gen_pos, int n_lanes,
                                                      float* __restrict__ surprise, GreedyWindow gw, SampleArgs sa) {
   constexpr int H = pssa_hip_lanes::kHist;
+  extern __shared__ __attribute__((aligned(16))) float s_row[];
   __shared__ uint32_t s_win[H];
   __shared__ float s_val[H];
+  __shared__ uint32_t s_bloom[kWinBloomWords];
   __shared__ int s_n;
-  __shared__ float smx[4], ssm[4], s_bp[4];
-  __shared__ int s_bv[4];
+  __shared__ float smx[4], ssm[4], s_pm[4];
+  __shared__ float s_bp[2][4];
+  __shared__ int s_bv[2][4];
   __shared__ float s_max, s_sum;
   __shared__ float s_selp[kMaxSampleTopK];
   __shared__ int s_selv[kMaxSampleTopK];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* lg = logits + (size_t)row * V;
-  float* pr = sa.probs + (size_t)row * V;
+  float* pr = ROW_LDS ? s_row : sa.probs + (size_t)row * V;
   const bool pen = gw.penalty > 1.0f && gw.hist != nullptr;
+  if (tid < kWinBloomWords) s_bloom[tid] = 0u;
   if (gw.hist && tid == 0) {
     int n = gw.hist_n[row], pos = gw.hist_pos[row];
     if (gw.append_row_id) {
@@ -245,11 +257,14 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ l
     float l = id < (uint32_t)V ? lg[id] : 0.0f;
     for (int q = 0; q < c; ++q) l = l > 0.0f ? l / gw.penalty : l * gw.penalty;
     s_val[lane] = l;
+    atomicOr(&s_bloom[(id >> 5) & (kWinBloomWords - 1)], 1u << (id & 31));
   }
   __syncthreads();
+  // An id whose filter bit is clear is not in the window.
   auto plogit = [&](int v) {
-    for (int j = 0; j < wn; ++j)
-      if (s_win[j] == (uint32_t)v) return s_val[j];
+    if (s_bloom[(v >> 5) & (kWinBloomWords - 1)] & (1u << (v & 31)))
+      for (int j = 0; j < wn; ++j)
+        if (s_win[j] == (uint32_t)v) return s_val[j];
     return lg[v];
   };
 
@@ -287,12 +302,12 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ l
   if (lane == 0) {
     smx[wave] = m;
     ssm[wave] = sacc;
-    s_bp[wave] = mx;
+    s_pm[wave] = mx;
   }
   __syncthreads();
   if (tid == 0) {
     for (int w = 1; w < 4; ++w) lse_merge(m, sacc, smx[w], ssm[w]);
-    s_max = fmaxf(fmaxf(s_bp[0], s_bp[1]), fmaxf(s_bp[2], s_bp[3]));
+    s_max = fmaxf(fmaxf(s_pm[0], s_pm[1]), fmaxf(s_pm[2], s_pm[3]));
   }
   __syncthreads();
   const float top = s_max;
@@ -302,53 +317,77 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ l
     pr[v] = v == 0 ? 0.0f : (float)exp((double)((plogit(v) - top) / temp));
   __syncthreads();
   if (tid == 0) {
+    // Adding probs[0] = 0 first leaves the sum +0, so the float4 reads can
+    // start at id 0; the adds stay one at a time in id order.
     float sum = 0.0f;
-    for (int v = 1; v < V; ++v) sum += pr[v];
+    const int v4 = ROW_LDS ? V & ~3 : 0;
+#pragma unroll 8
+    for (int v = 0; v < v4; v += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(pr + v);
+      sum += q.x;
+      sum += q.y;
+      sum += q.z;
+      sum += q.w;
+    }
+    for (int v = v4 > 1 ? v4 : 1; v < V; ++v) sum += pr[v];
     s_sum = sum;
   }
   __syncthreads();
   const float sum = s_sum;
   const bool mass_ok = isfinite(sum) && sum > 0.0f;
   const int K = mass_ok ? min(V - 1, min(sa.top_k, kMaxSampleTopK)) : 0;
-  float lp = INFINITY;
-  int lv = -1;
-  for (int r = 0; r < K; ++r) {
-    float bp = -1.0f;
-    int bv = INT32_MAX;
+  if (K > 0) {
+    for (int v = 1 + tid; v < V; v += 256) pr[v] = pr[v] / sum;
+  }
+  // Each thread keeps the best of its ids that rank after the last choice.
+  // A choice ranks before every id not yet chosen, so only the thread that
+  // owned it has to search again.
+  float bp = -1.0f;
+  int bv = INT32_MAX;
+  auto own_best = [&](float lp, int lv) {
+    bp = -1.0f;
+    bv = INT32_MAX;
     for (int v = 1 + tid; v < V; v += 256) {
-      const float p = pr[v] / sum;
+      const float p = pr[v];
       if (ranks_before(lp, lv, p, v) && ranks_before(p, v, bp, bv)) {
         bp = p;
         bv = v;
       }
     }
+  };
+  own_best(INFINITY, -1);
+  for (int r = 0; r < K; ++r) {
+    float wp = bp;
+    int wv = bv;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
-      const float op = __shfl_xor(bp, off, 64);
-      const int ov = __shfl_xor(bv, off, 64);
-      if (ranks_before(op, ov, bp, bv)) {
-        bp = op;
-        bv = ov;
+      const float op = __shfl_xor(wp, off, 64);
+      const int ov = __shfl_xor(wv, off, 64);
+      if (ranks_before(op, ov, wp, wv)) {
+        wp = op;
+        wv = ov;
       }
     }
+    // Two slots alternate by round, so one barrier per round suffices.
     if (lane == 0) {
-      s_bp[wave] = bp;
-      s_bv[wave] = bv;
+      s_bp[r & 1][wave] = wp;
+      s_bv[r & 1][wave] = wv;
     }
     __syncthreads();
+    float gp = s_bp[r & 1][0];
+    int gv = s_bv[r & 1][0];
+    for (int w = 1; w < 4; ++w)
+      if (ranks_before(s_bp[r & 1][w], s_bv[r & 1][w], gp, gv)) {
+        gp = s_bp[r & 1][w];
+        gv = s_bv[r & 1][w];
+      }
     if (tid == 0) {
-      for (int w = 1; w < 4; ++w)
-        if (ranks_before(s_bp[w], s_bv[w], bp, bv)) {
-          bp = s_bp[w];
-          bv = s_bv[w];
-        }
-      s_selp[r] = bp;
-      s_selv[r] = bv;
+      s_selp[r] = gp;
+      s_selv[r] = gv;
     }
-    __syncthreads();
-    lp = s_selp[r];
-    lv = s_selv[r];
+    if (bv == gv) own_best(gp, gv);
   }
+  __syncthreads();
   if (tid == 0) {
     int best = 0;
     if (!mass_ok) {
@@ -406,8 +445,12 @@ static Status launch_choice(pssa_hip_lanes* L, size_t n_lanes, const GreedyWindo
     sa.rng = L->rng.as<unsigned long long>();
     sa.probs = L->probs.as<float>();
     sa.bad_mass = L->nonfinite.as<int>() + 2;
-    sample_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(), gen_ids,
-                                                     gen_pos, (int)n_lanes, surprise, gw, sa);
+    if (V <= kSampleLdsMaxV)
+      sample_kernel<true><<<(unsigned)n_lanes, 256, (size_t)V * 4, st>>>(
+          L->logits.as<float>(), V, L->ids.as<uint32_t>(), gen_ids, gen_pos, (int)n_lanes, surprise, gw, sa);
+    else
+      sample_kernel<false><<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(),
+                                                              gen_ids, gen_pos, (int)n_lanes, surprise, gw, sa);
     PSSA_LAUNCH_CHECK("sample");
   } else {
     greedy_kernel<<<(unsigned)n_lanes, 256, 0, st>>>(L->logits.as<float>(), V, L->ids.as<uint32_t>(), gen_ids,
@@ -694,6 +737,8 @@ Status init_decode_attributes() {
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
   PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&hebbian_kernel),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&sample_kernel<true>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, kSampleLdsMaxV * 4));
   return Status::Ok();
 }
 

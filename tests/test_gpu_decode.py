@@ -470,17 +470,20 @@ def test_decode_sampling_matches_oracle_sample(hip, graph):
     layer.close()
 
 
-def test_decode_sampling_wide_vocabulary_and_top_k(hip):
-    """A 3000-id vocabulary (several passes of the workgroup per row), top-k 64
-    and top-p 1 (every kept candidate drawn from), no penalty, seed 0 (the
-    generator's fixed non-zero start)."""
-    say("decode sampling, wide vocabulary")
-    cfg = PSSAConfig(depth=1, d_vocab=3000, d_latent=64, d_state=32, d_mem_key=8, mem_capacity=16)
+@pytest.mark.parametrize("vocab,penalty", [(3000, 1.0), (40000, 1.25)])
+def test_decode_sampling_wide_vocabulary_and_top_k(hip, vocab, penalty):
+    """Wide vocabularies (several passes of the workgroup per row; 40000 ids
+    also take the global scratch row instead of LDS), top-k 64 and top-p 1
+    (every kept candidate drawn from), seed 0 (the generator's fixed non-zero
+    start), with and without the penalty window."""
+    say("decode sampling, wide vocabulary", vocab, penalty)
+    cfg = PSSAConfig(depth=1, d_vocab=vocab, d_latent=64, d_state=32, d_mem_key=8, mem_capacity=16)
     w = ModelWeights.init(cfg, 3, "baseline")
     w.populate_banks(4, count=cfg.mem_capacity)
     ids = np.random.default_rng(2).integers(1, cfg.d_vocab, (2, 5), dtype=np.uint32)
-    ref = oracle_sampled_decode(w, ids, 10, 1.0, 1.3, 1.0, 64, seed=0)
+    ref = oracle_sampled_decode(w, ids, 10, penalty, 1.3, 1.0, 64, seed=0)
     layer = PSSALayer(hip, w, lanes=2, max_tokens=16)
+    layer.set_repetition_penalty(penalty)
     layer.set_sampling(1.3, 1.0, 64, seed=0)
     layer.prefill_inference(ids)
     np.testing.assert_array_equal(layer.decode(10), ref)

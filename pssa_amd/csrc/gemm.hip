@@ -636,6 +636,10 @@ __global__ __launch_bounds__(64) void gemm_skinny_kernel(const TA* __restrict__ 
     for (int q = 0; q < RING; ++q) {
       step(q);
       fetch(k0 + RING + q, q);
+      // Each slot is refilled right after its MFMA.  Without the barrier the
+      // scheduler sank all RING refills below the last step's vmcnt(0), and
+      // every RING steps waited out a whole memory round trip.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // The remaining nk - k0 < RING steps are in slots 0 ..
@@ -719,6 +723,7 @@ __global__ __launch_bounds__(64) void gemm_skinny_f32_kernel(const float* __rest
     for (int q = 0; q < RING; ++q) {
       step(q);
       fetch(k0 + RING + q, q);
+      __builtin_amdgcn_sched_barrier(0);  // refill right after the step, as above
     }
   }
 #pragma unroll
@@ -848,21 +853,16 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   const int ve = bf16 ? 8 : 4;
   const int vec_load = (K % ve == 0) && (lda % ve == 0) && (ldb % ve == 0) && al16(A) && al16(B);
   const bool vec_bf16 = bf16 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B);
-  // Few token rows: the 128 x 256 tiling would leave most CUs idle.
-  // Narrow outputs (N <= 768) take one 32-row tile per wave, which doubles the
-  // waves in flight (measured 10-20% faster at 256 rows); wider ones two.
+  // Few token rows: the 128 x 256 tiling would leave most CUs idle.  One
+  // 32-row tile per wave, whatever the width: at 256 rows that gives
+  // (N/32) x 8 waves, about one per CU or more (measured 1% faster per decode
+  // step than two tiles per wave past 768 output columns).
   if (vec_bf16 && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
     const auto* a16 = static_cast<const uint16_t*>(A);
     const auto* b16 = static_cast<const uint16_t*>(B);
-    if (N <= 768) {
-      const dim3 grid((N + 31) / 32, (M + 31) / 32);
-      if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
-      launch_skinny_kind<uint16_t, 1, 16>(stream, ep.kind, grid, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
-    } else {
-      const dim3 grid((N + 31) / 32, (M + 63) / 64);
-      if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
-      launch_skinny_kind<uint16_t, 2, 8>(stream, ep.kind, grid, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
-    }
+    const dim3 grid((N + 31) / 32, (M + 31) / 32);
+    if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
+    launch_skinny_kind<uint16_t, 1, 16>(stream, ep.kind, grid, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
     PSSA_LAUNCH_CHECK("gemm_skinny");
     return Status::Ok();
   }

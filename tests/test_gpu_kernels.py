@@ -49,6 +49,27 @@ def test_gemm_f32_few_rows_equal_tiled_rows_bitwise(hip, n):
     assert rel_err(big[:64], O.gemm_xwt(x[:64], w)) < 1e-5
 
 
+@pytest.mark.parametrize("n,k", [(768, 768), (1056, 768), (736, 800), (1024, 800)])
+def test_gemm_bf16_few_rows_equal_tiled_rows_bitwise(hip, n, k):
+    """bf16 weights: few token rows run one wave per 32 x 32 (or 64 x 32)
+    tile with 64-element LDS slabs (800 = 12.5 slabs: a partial last slab),
+    many rows the 128 x 128 direct-to-LDS tiles.  Both feed the same
+    fragments to the same MFMA sequence over K, so the rows agree bit for bit
+    (the prefill / decode identity of bf16 models rests on it)."""
+    say("gemm bf16 few rows == tiled", n, k)
+    rng = np.random.default_rng(n + k)
+    m = 16384
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = bf16_round((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    wbits = (w.view(np.uint32) >> 16).astype(np.uint16)
+    big = hip.try_dispatch_gemm(x, wbits, m, n, k, w_dtype="bf16").reshape(m, n)
+    for rows in (1, 37, 64, 256):
+        few = hip.try_dispatch_gemm(np.ascontiguousarray(x[:rows]), wbits, rows, n, k, w_dtype="bf16").reshape(rows, n)
+        np.testing.assert_array_equal(few.view(np.uint32), big[:rows].view(np.uint32))
+    exact = bf16_round(x[:64]).astype(np.float64) @ w.astype(np.float64).T
+    assert rel_err(big[:64], exact) < 1e-5
+
+
 @pytest.mark.parametrize("m,n,k,batch", [(5, 9, 8, 1), (64, 130, 776, 2), (257, 96, 768, 1), (31, 3, 20, 3)])
 def test_gemm_bf16_weights(hip, m, n, k, batch):
     say("gemm bf16", m, n, k, batch)

@@ -890,17 +890,28 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
     const size_t n = (size_t)q0 + row;
     // ---- candidates: bounds in f32 (their rounding, ~1e-7 relative, is far
     // inside the RK_TIE slack) ----
-    const double qq = sc.qq[row];
-    const float qqf = (float)qq, qnf = (float)sqrt(qq);
+    // The scratch holds RK_SLOTS entries per row, so every slot's loads run
+    // unguarded and are in flight together (a load under `s < cnt` waited
+    // out its own round trip); slots past the count are masked below.
+    // |q|^2 is loaded after them, so its wait does not hold them back.
     float L[SPL];
     float lm = HUGE_VALF;
+    float4 tmv[SPL];
+    float dtv[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; ++j) {
+      tmv[j] = sc.terms[lane + 64 * j];
+      dtv[j] = sc.zdot[(size_t)row * RK_SLOTS + lane + 64 * j];
+    }
+    const double qq = sc.qq[row];
+    const float qqf = (float)qq, qnf = (float)sqrt(qq);
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
       const int s = lane + 64 * j;
       L[j] = HUGE_VALF;
       if (s < cnt) {
-        const float4 tm = sc.terms[s];
-        const float dot = sc.zdot[(size_t)row * RK_SLOTS + s];
+        const float4 tm = tmv[j];
+        const float dot = dtv[j];
         const float sqt = qqf + tm.x - 2.0f * dot;
         const float e = qnf * tm.y + 1e-6f * (qqf + tm.x + 2.0f * fabsf(dot));
         L[j] = (sqt - e) * tm.z;
@@ -932,7 +943,9 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int i = 256 * v + 4 * lane;
-      const float4 x = i < dk ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      // Clamped in-range address, masked after: no load under a branch.
+      float4 x = *reinterpret_cast<const float4*>(qrow + min(i, dk - 4));
+      if (i >= dk) x = make_float4(0.f, 0.f, 0.f, 0.f);
       qv[4 * v] = x.x, qv[4 * v + 1] = x.y, qv[4 * v + 2] = x.z, qv[4 * v + 3] = x.w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) qs = fma((double)qv[4 * v + e], (double)qv[4 * v + e], qs);
@@ -957,7 +970,8 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const int i = 256 * v + 4 * lane;
-          const float4 y = i < dk ? *reinterpret_cast<const float4*>(krow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+          float4 y = *reinterpret_cast<const float4*>(krow + min(i, dk - 4));
+          if (i >= dk) y = make_float4(0.f, 0.f, 0.f, 0.f);
           kf[g][4 * v] = y.x, kf[g][4 * v + 1] = y.y, kf[g][4 * v + 2] = y.z, kf[g][4 * v + 3] = y.w;
         }
       }

@@ -390,25 +390,27 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
     if (lane < na) {
 #pragma clang fp contract(off)
       const float* qrow = a.q + (size_t)(c0 + lane) * a.ld_q;
-      // Eight loads in flight before the dependent sums (the sums keep the
-      // reference's order).
+      // Sixteen loads in flight before the dependent sums (the sums keep the
+      // reference's order).  The loads read clamped in-range addresses and
+      // the sums skip the columns past d_key: a load under a per-element
+      // guard ended its block with a full wait, one round trip per element.
       double r2 = 0.0;
-      for (int i0 = 0; i0 < dk; i0 += 8) {
-        float v[8];
+      for (int i0 = 0; i0 < dk; i0 += 16) {
+        float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = i0 + k < dk ? qrow[i0 + k] : 0.0f;
+        for (int k = 0; k < 16; ++k) v[k] = qrow[min(i0 + k, dk - 1)];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 16; ++k)
           if (i0 + k < dk) r2 = r2 + (double)v[k] * (double)v[k];
       }
       const double r = sqrt(r2);
       scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
-      for (int i0 = 0; i0 < dk; i0 += 8) {
-        float v[8];
+      for (int i0 = 0; i0 < dk; i0 += 16) {
+        float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = i0 + k < dk ? qrow[i0 + k] : 0.0f;
+        for (int k = 0; k < 16; ++k) v[k] = qrow[min(i0 + k, dk - 1)];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < 16; ++k)
           if (i0 + k < dk) {
             const double pv = (double)(float)((double)v[k] * scale);
             qs = qs + pv * pv;
@@ -426,8 +428,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
       for (int g = 0; g < QG; ++g) {
         const int src = g < ng ? g0 + g : g0;
         const double sc = readlane_f64(scale, src);
+        const float qv = a.q[(size_t)(c0 + src) * a.ld_q + min(lane, dk - 1)];  // unguarded, as above
         if (lane < dk) {
-          const float qv = a.q[(size_t)(c0 + src) * a.ld_q + lane];
           const float pv = (float)((double)qv * sc);
           pw[g * dk + lane] = pv;
           if (a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;

@@ -514,10 +514,14 @@ __global__ __launch_bounds__(256) void hebbian_kernel(PlasticArgs p, int hb_i) {
   float* srate = sact + n * r;    // [lanes]
   const float* z = p.tap_z + (size_t)l * n * d;
   const float* a = p.tap_a + (size_t)l * n * d;
+  // Loads at a clamped in-range column, masked after: a load under the
+  // column guard ended its block with a full wait, one round trip per element.
 #pragma unroll 8
   for (int e = tid; e < n * hb_i; e += nt) {
     const int ln = e / hb_i, i = i0 + e % hb_i;
-    serr[e] = i < d ? fminf(fmaxf(z[(size_t)ln * d + i] - a[(size_t)ln * d + i], -4.0f), 4.0f) : 0.0f;
+    const size_t o = (size_t)ln * d + min(i, d - 1);
+    const float v = fminf(fmaxf(z[o] - a[o], -4.0f), 4.0f);
+    serr[e] = i < d ? v : 0.0f;
   }
   const float* act = p.tap_act + (size_t)l * n * r;
 #pragma unroll 8

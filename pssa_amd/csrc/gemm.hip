@@ -235,16 +235,28 @@ __device__ __forceinline__ void adapter_act_frag(const EpiParams& ep, int row, i
 // the z_raw epilogue, may be null) is the row's adapter fragment for
 // q0 = 0, loaded once by the caller for all tiles of the row.
 // The row operands of one tile's four quads (see QuadIn).
-template <int KIND>
+template <int KIND, bool CLAMP>
 __device__ __forceinline__ void epi_tile_load(const EpiParams& ep, int row, int n32, int M, int N,
                                               int vec_epi, int half, QuadIn (&in)[4]) {
   const int nb = n32 + half * 4;
+  // CLAMP, with vec_epi (every operand row 16-byte aligned): the quads load
+  // from a row clamped to M - 1 and a column clamped to the last aligned
+  // in-range quad, unguarded, so all four are in flight together (a load
+  // under the per-lane guard ended its block with a full wait).  epi_quad
+  // uses a quad only when it is wholly in range.  It costs registers: the
+  // tiled kernels take it for z_raw only (the residual tile would drop to
+  // three waves per SIMD beside the scan).
+  const bool clamp = CLAMP && vec_epi && N >= 4;
+  const int rr = min(row, M - 1), cmax = (N - 4) & ~3;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     in[g].p = in[g].q = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (epi_reads(KIND)) {
       const int col = nb + g * 8;
-      if (row < M && vec_epi && col + 3 < N) load_quad<KIND>(ep, row, col, in[g]);
+      if (clamp)
+        load_quad<KIND>(ep, rr, min(col, cmax), in[g]);
+      else if (row < M && vec_epi && col + 3 < N)
+        load_quad<KIND>(ep, row, col, in[g]);
     }
   }
 }
@@ -312,12 +324,12 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
   }
 }
 
-template <typename T, int KIND>
+template <typename T, int KIND, bool CLAMP = true>
 __device__ __forceinline__ void epilogue_32x32(const EpiParams& ep, const f32x16_t& acc, int row,
                                                int n32, int M, int N, int vec_epi, int half,
                                                int l32, const uint32_t* act0 = nullptr) {
   QuadIn in[4];
-  epi_tile_load<KIND>(ep, row, n32, M, N, vec_epi, half, in);
+  epi_tile_load<KIND, CLAMP>(ep, row, n32, M, N, vec_epi, half, in);
   epi_tile_store<T, KIND>(ep, acc, row, n32, M, N, vec_epi, half, l32, act0, in);
 }
 
@@ -556,8 +568,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     // prefill, where a scan workgroup shares the CU, then runs slower.
 #pragma unroll
     for (int u = 0; u < NW; ++u)
-      epilogue_32x32<uint16_t, KIND>(ep, acc[t][u], row, n0 + wn * NW * 32 + u * 32, M, N, vec_epi, half,
-                                     l32, KIND == EPI_ZRAW ? act0 : nullptr);
+      epilogue_32x32<uint16_t, KIND, KIND == EPI_ZRAW>(ep, acc[t][u], row, n0 + wn * NW * 32 + u * 32, M, N,
+                                                        vec_epi, half, l32, KIND == EPI_ZRAW ? act0 : nullptr);
   }
 }
 

@@ -424,13 +424,19 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
     for (int g0 = 0; g0 < na; g0 += QG) {
       const int ng = min(QG, na - g0);
       // Projected queries of this group into LDS (and the q_pnc tap).
+      // The group's query values load first, unguarded at a clamped column,
+      // and are scaled by every lane; only the stores are guarded (a load
+      // used only under `lane < dk` was sunk into that block and waited
+      // there, one round trip per query).
+      float qvg[QG];
+#pragma unroll
+      for (int g = 0; g < QG; ++g)
+        qvg[g] = a.q[(size_t)(c0 + (g < ng ? g0 + g : g0)) * a.ld_q + min(lane, dk - 1)];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
         const int src = g < ng ? g0 + g : g0;
-        const double sc = readlane_f64(scale, src);
-        const float qv = a.q[(size_t)(c0 + src) * a.ld_q + min(lane, dk - 1)];  // unguarded, as above
+        const float pv = (float)((double)qvg[g] * readlane_f64(scale, src));
         if (lane < dk) {
-          const float pv = (float)((double)qv * sc);
           pw[g * dk + lane] = pv;
           if (a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;
         }

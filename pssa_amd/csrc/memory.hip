@@ -794,7 +794,7 @@ __global__ __launch_bounds__(RK_THREADS) void ranked_dot_kernel(RetrieveArgs a, 
 //    value readout in ascending slot order.
 constexpr int RQ_WAVES = 4;                    // independent waves per workgroup
 constexpr int RQ_V = RK_MAX_DK / 256;          // float4 per lane for one row
-constexpr int RQ_QPW = 4;                      // queries per wave
+constexpr int RQ_QPW = 2;                      // queries per wave (measured: 1, 4, 8 no faster)
 constexpr int RQ_G = 2;                        // candidate rows per step
 constexpr int RK_MAX_DV4 = 256;                // vectorised readout: d_val <= 1024
 constexpr double RQ_SUM_REL = 4e-13;           // >= 2 * 1024 * 2^-53, with margin

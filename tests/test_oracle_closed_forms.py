@@ -8,6 +8,7 @@ import pytest
 
 from oracle import oracle as O
 from pssa_amd import ModelWeights, PSSAConfig
+from pssa_amd.weights import BlockWeights
 
 F32_MIN_SUB = np.float32(np.frombuffer(np.uint32(1).tobytes(), np.float32)[0])
 
@@ -249,6 +250,64 @@ def test_depth_two_with_silent_second_block_equals_depth_one():
     assert np.max(np.abs(f1 - f2)) > 1e-3
 
 
+# ---- docs/stacked-depth.md:14-20, src/pssa.rs:2059,2332-2337 ---------------------
+# h_0 = block_0(embed[token]); h_i = h_(i-1) + block_i(h_(i-1)) / sqrt(D) in f32,
+# residual scale 1/sqrt(D) for every added block (0.5 at depth 4,
+# tests/stacked_depth.rs:280).  Blocks 1..D-1 are made input-independent with a
+# known, nonzero output: gamma = 0 so x-hat = beta whatever the input, C = 0 so
+# y = 0, W_proj = 0 and W2 = 0, leaving z_final = the adapter's output
+# (U_fast + U_slow) SiLU(D_adapter beta).  Each block's output is taken from a
+# depth-1 model holding that block alone (whose output is not scaled), so the
+# expected features follow from the stacking rule only; a dropped or doubled
+# scale, a block skipped or run twice, or block 0 scaled fails.
+def _constant_block(b, rng):
+    b.norm_gamma[...] = 0
+    b.norm_beta[...] = rng.uniform(-1, 1, b.norm_beta.shape).astype(np.float32)
+    for name in ("w_c", "w_proj", "mlp_w2"):
+        getattr(b, name)[...] = 0
+    b.adapter_down[...] = rng.uniform(-0.5, 0.5, b.adapter_down.shape).astype(np.float32)
+    b.adapter_up[...] = rng.uniform(-0.5, 0.5, b.adapter_up.shape).astype(np.float32)
+    b.adapter_slow[...] = rng.uniform(-0.1, 0.1, b.adapter_slow.shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("depth", [2, 4, 12])
+def test_depth_residual_scale_closed_form(depth):
+    dims = dict(d_vocab=13, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=8)
+    cfg = PSSAConfig(depth=depth, **dims)
+    w = ModelWeights(cfg)
+    O.OracleModel(w).init_baseline(7)
+    O.OracleModel(w).populate_banks(3, 8)
+    rng = np.random.default_rng(depth)
+    for b in w.blocks[1:]:
+        _constant_block(b, rng)
+
+    def alone(block_index):
+        c1 = PSSAConfig(depth=1, **dims)
+        w1 = ModelWeights(c1)
+        w1.embed[:] = w.embed
+        w1.unembed[:] = w.unembed
+        src, dst = w.blocks[block_index], w1.blocks[0]
+        for name in BlockWeights.SHAPES:
+            getattr(dst, name)[...] = getattr(src, name)
+        dst.mem_count, dst.mem_write_head = src.mem_count, src.mem_write_head
+        return O.OracleModel(w1)
+
+    scale = np.float32(1) / np.sqrt(np.float32(depth))
+    if depth == 4:
+        assert scale == np.float32(0.5)
+    for token in (0, 5, 12):
+        o0 = alone(0)
+        expect = o0.features(o0.zero_state(), token).copy()
+        for l in range(1, depth):
+            ol = alone(l)
+            a = ol.features(ol.zero_state(), token)
+            assert np.max(np.abs(a)) > 1e-2  # a live branch, so its scale shows
+            expect = np.float32(expect + np.float32(scale * a))
+        om = O.OracleModel(w)
+        got = om.features(om.zero_state(), token)
+        np.testing.assert_array_equal(got, expect)
+
+
 # ---- src/feature_benchmark.rs:446-500 refractory protocol ------------------------
 def test_refractory_protocol_closed_form():
     import ctypes as C
@@ -433,7 +492,6 @@ def test_baseline_rates_give_spectral_radius_below_095():
     per-token transition at the initial step size softplus(0) = ln 2 is
     exp(ln 2 * A), below 0.95 for every mode; the timescales are log-spaced
     1/tau from 1.5 to 13.  The reference initialisation keeps its [1.5, 200]."""
-    from pssa_amd import ModelWeights, PSSAConfig
     cfg = PSSAConfig(depth=2, d_vocab=50, d_latent=16, d_state=64, d_mem_key=4, mem_capacity=8)
     for mode, tau_max in (("baseline", 13.0), ("reference", 200.0)):
         for w in (ModelWeights.init(cfg, 0, mode),):
@@ -471,7 +529,6 @@ def test_bf16_operand_rounding_and_mode_switch():
     got = np.array([r(v) for v in x], np.float32)
     np.testing.assert_array_equal(got, want)
     # The switch is per call: a bf16-mode model call leaves the mode off.
-    from pssa_amd import ModelWeights, PSSAConfig
     cfg = PSSAConfig(depth=1, d_vocab=20, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=6)
     w = ModelWeights.init(cfg, 1, "baseline").to_bf16_values()
     om = O.OracleModel(w, bf16_operands=True)

@@ -436,6 +436,7 @@ def bench_dense_scan(dev, args, log):
     def run():
         dev.dense_scan_resident(a_dev.ptr, b_dev.ptr, None, B, T, s, h_dev.ptr)
 
+    dev.dense_scan_reserve(B, T, s)
     run()
     dev.synchronize()
     reps = 5

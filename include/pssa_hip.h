@@ -323,16 +323,34 @@ int pssa_hip_retrieve_hybrid(pssa_hip_ctx* ctx, const float* q_pnc, size_t n_q, 
 /* Dense-transition scan h_t = A_t h_{t-1} + b_t (no reference counterpart:
  * the reference's SSM is diagonal; this is the standalone dense kernel).
  * a [batch, L, s, s] row-major (h_t[r] = sum_c A_t[r][c] h_{t-1}[c] + b_t[r]),
- * b [batch, L, s], h0 [batch, s] (NULL = zeros), h [batch, L, s]. */
+ * b [batch, L, s], h0 [batch, s] (NULL = zeros), h [batch, L, s].
+ * Accuracy: every h_t is an exact fp32 step (fused multiply-adds) from the
+ * state before it.  With s = 64 and L >= 256 (16-byte aligned a and b) the
+ * state entering each 32-step sub-chunk is carried through the composed
+ * maps of the sub-chunks before it in its 128-step window, products of
+ * bf16 hi/lo splits (about 2^-17 relative per factor); a composed map that
+ * is not finite or does not contract (Frobenius norm above 1) is not used,
+ * and those sub-chunks are replayed step by step in fp32 instead, so
+ * orthogonal or growing transitions get the exact recurrence's accuracy. */
 int pssa_hip_dense_scan(pssa_hip_ctx* ctx, const float* a, const float* b, const float* h0,
                         size_t batch, size_t seq_len, size_t d_state, float* h, char* err,
                         size_t err_len);
 
 /* Same recurrence on device-resident buffers (plain device pointers from any
- * allocator); asynchronous on the context stream. */
+ * allocator); asynchronous on the context stream once the context's scratch
+ * holds the two-level schedule's maps for this shape.  A first call with a
+ * larger shape grows that scratch (stream synchronise, free, allocate):
+ * call pssa_hip_dense_scan_reserve beforehand to keep every call
+ * asynchronous and allocation-free. */
 int pssa_hip_dense_scan_resident(pssa_hip_ctx* ctx, const float* d_a, const float* d_b,
                                  const float* d_h0, size_t batch, size_t seq_len, size_t d_state,
                                  float* d_h, char* err, size_t err_len);
+
+/* Grows the context's scratch (synchronously) to what a dense scan of this
+ * shape needs; later pssa_hip_dense_scan_resident calls of this or a
+ * smaller shape allocate nothing. */
+int pssa_hip_dense_scan_reserve(pssa_hip_ctx* ctx, size_t batch, size_t seq_len, size_t d_state, char* err,
+                                size_t err_len);
 
 /* ------------------------------------------------------------ model paths */
 

@@ -163,6 +163,7 @@ def lib() -> C.CDLL:
                                                 err_t, sz], C.c_int),
         "pssa_hip_dense_scan": ([vp, fp, fp, fp, sz, sz, sz, fp, err_t, sz], C.c_int),
         "pssa_hip_dense_scan_resident": ([vp, vp, vp, vp, sz, sz, sz, vp, err_t, sz], C.c_int),
+        "pssa_hip_dense_scan_reserve": ([vp, sz, sz, sz, err_t, sz], C.c_int),
         "pssa_hip_model_load": ([vp, C.POINTER(Weights), C.c_int, pp, err_t, sz], C.c_int),
         "pssa_hip_model_free": ([vp], None),
         "pssa_hip_lanes_create": ([vp, vp, sz, sz, pp, err_t, sz], C.c_int),

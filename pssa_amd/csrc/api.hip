@@ -1700,6 +1700,14 @@ int pssa_hip_model_get_hybrid(pssa_hip_model* M, size_t layer, float* gate, uint
 
 namespace {
 
+// Recurrent depth loops and the hybrid read are not combined on the device.
+Status loops_allow_hybrid(const pssa_hip_lanes* L) {
+  if (L->loops > 1)
+    for (const pssa::DevBlock& B : L->model->blocks)
+      if (B.hybrid) return Status{PSSA_HIP_EUNSUPPORTED, "the hybrid read runs one loop here (set_loops 1)"};
+  return Status::Ok();
+}
+
 Status ensure_decode_buffers(pssa_hip_lanes* L, size_t n_lanes, size_t steps) {
   const pssa_hip_config& c = L->model->cfg;
   if (L->dec_lanes < L->lanes) {
@@ -1783,6 +1791,9 @@ int pssa_hip_lanes_set_loops(pssa_hip_lanes* L, size_t loops, char* err, size_t 
     PSSA_RETURN_IF(need(loops >= 1 && loops <= 32, "--loops must be between 1 and 32; use --loops 1 for the original model"));
     std::lock_guard<std::mutex> g(L->ctx->mu);
     if (loops == L->loops) return Status::Ok();
+    if (loops > 1)
+      for (const pssa::DevBlock& B : L->model->blocks)
+        if (B.hybrid) return Status{PSSA_HIP_EUNSUPPORTED, "the hybrid read runs one loop here (set_loops 1)"};
     PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
     const hipStream_t st = L->ctx->stream;
     const pssa_hip_config& c = L->model->cfg;
@@ -1861,6 +1872,9 @@ int pssa_hip_decode(pssa_hip_lanes* L, const uint32_t* first_ids, size_t n_lanes
     const bool plastic = (flags & PSSA_HIP_DECODE_PLASTIC) != 0;
     if (plastic && L->loops != 1)
       return Status{PSSA_HIP_EUNSUPPORTED, "plastic decode runs one loop here (set_loops 1)"};
+    // Refused before the choice kernel runs: it records a token and advances
+    // every lane's generator.
+    PSSA_RETURN_IF(loops_allow_hybrid(L));
     if (plastic) {
       PSSA_RETURN_IF(need(pssa::bank_write_lds((int)L->model->cfg.mem_capacity, (int)n_lanes) <= 160 * 1024,
                           "plastic decode: mem_capacity and n_lanes exceed the bank-write LDS budget"));
@@ -1953,6 +1967,20 @@ int pssa_hip_dense_scan_resident(pssa_hip_ctx* ctx, const float* d_a, const floa
     PSSA_RETURN_IF(bind_dense_scan_scratch(ctx, (int)batch, (int)seq_len, (int)d_state));
     return pssa::launch_dense_scan(ctx->stream, d_a, d_b, d_h0, d_h, (int)batch, (int)seq_len, (int)d_state,
                                    ctx->scratch, ctx->scratch_bytes);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
+int pssa_hip_dense_scan_reserve(pssa_hip_ctx* ctx, size_t batch, size_t seq_len, size_t d_state, char* err,
+                                size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(check_ctx(ctx));
+    PSSA_RETURN_IF(need(batch && seq_len && d_state, "dense scan: dimensions must be positive"));
+    PSSA_RETURN_IF(need(d_state <= 64, "dense scan: d_state above 64 is not supported"));
+    if (batch > INT32_MAX || seq_len > INT32_MAX) return Status::Invalid("dense scan: too large");
+    std::lock_guard<std::mutex> g(ctx->mu);
+    PSSA_HIP_TRY(hipSetDevice(ctx->device));
+    return bind_dense_scan_scratch(ctx, (int)batch, (int)seq_len, (int)d_state);
   };
   return pssa::finish(body(), err, err_len);
 }

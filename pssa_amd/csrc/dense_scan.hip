@@ -233,8 +233,10 @@ __global__ __launch_bounds__(DS_THREADS) void dense_scan_ring_kernel(const float
 //    contracting transitions the composed map shrinks (about 0.9^32 at
 //    config 2), so its relative error of a few 1e-5 moves the carried state
 //    by a few 1e-6 of its size; the re-run of every step is exact fp32.
-// A map that is not finite is marked unusable, and a re-run that would need
-// it replays the earlier sub-chunks of its window in fp32 instead.
+// A map that is not finite, or does not contract (Frobenius norm above 1:
+// its split rounding would reach the later states undamped), is marked
+// unusable, and a re-run that would need it replays the earlier sub-chunks
+// of its window in fp32 instead.
 constexpr int TL_SUB = 4;                          // sub-chunks per window
 constexpr int TL_LC = 32;                          // steps per sub-chunk
 constexpr int TL_W = TL_SUB * TL_LC;               // steps per window
@@ -315,6 +317,7 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
   // P as B fragments, [buffer][hi/lo][k block][16-column tile][lane]
   __shared__ __attribute__((aligned(16))) tl_bf16x8_t pf_s[2][2][2][4][64];
   __shared__ int bad_s;
+  __shared__ float nrm_s[TL_CW];
   float* ring = &ring_s[0][0];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool loader = wave >= TL_CW;
@@ -515,11 +518,18 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
       cur ^= 1;
     });
     bool bad = false;
+    float sq = 0.0f;  // this lane's share of |P|_F^2
     if (!loader)
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) bad = bad || !(fabsf(pm[u][r]) <= 3.0e38f);
+        for (int r = 0; r < 4; ++r) {
+          bad = bad || !(fabsf(pm[u][r]) <= 3.0e38f);
+          sq = fmaf(pm[u][r], pm[u][r], sq);
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+    if (!loader && lane == 0) nrm_s[wave] = sq;
     if (!loader && (bad || (tid < DS_S && !(fabsf(vec_s[cur][tid]) <= 3.0e38f)))) atomicOr(&bad_s, 1);
     __syncthreads();
     float* out = a.agg + (((size_t)(w & 1) * a.batch + seq) * (TL_SUB - 1) + j) * TL_AGG;
@@ -530,7 +540,13 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
         for (int r = 0; r < 4; ++r)
           out[(16 * rt + 4 * g + r) * DS_S + 16 * (nt0 + u) + cl] = pm[u][r];
       if (tid < DS_S) out[DS_S * DS_S + tid] = vec_s[cur][tid];
-      if (tid == 0) out[DS_S * DS_S + DS_S] = bad_s ? 1.0f : 0.0f;
+      if (tid == 0) {
+        // A map that does not contract (|P|_F > 1) would carry its split
+        // rounding undamped into the states after it: replayed instead.
+        float f2 = 0.0f;
+        for (int w2 = 0; w2 < TL_CW; ++w2) f2 += nrm_s[w2];
+        out[DS_S * DS_S + DS_S] = (bad_s || !(f2 <= 1.0f)) ? 1.0f : 0.0f;
+      }
     }
     __syncthreads();
   }

@@ -287,6 +287,11 @@ class HipDevice:
         _abi.call(self._lib.pssa_hip_dense_scan_resident, self.handle, C.c_void_p(a_ptr), C.c_void_p(b_ptr),
                   C.c_void_p(h0_ptr) if h0_ptr else None, batch, L, s, C.c_void_p(h_ptr))
 
+    def dense_scan_reserve(self, batch: int, L: int, s: int) -> None:
+        """Sizes the context's scratch for dense scans up to this shape, so that
+        dense_scan_resident then runs without allocating."""
+        _abi.call(self._lib.pssa_hip_dense_scan_reserve, self.handle, batch, L, s)
+
 
 class DeviceBuffer:
     """A device allocation made through the C ABI (freed on close/GC)."""

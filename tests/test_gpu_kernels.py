@@ -447,6 +447,36 @@ def test_dense_scan_two_level_replays_when_a_map_is_not_finite(hip):
     np.testing.assert_array_equal(np.isfinite(h[1, 170]), np.isfinite(ref[1, 170]))
 
 
+@pytest.mark.parametrize("kind", ["orthogonal", "expanding"])
+def test_dense_scan_two_level_non_contracting_transitions(hip, kind):
+    """Transitions that do not contract: A_t orthogonal (u = 1), or A_t =
+    Q_t diag(u_t) with u_t ~ U[1.0, 1.004] (the state grows about e^4 over
+    the sequence).  Their composed maps are not used (Frobenius norm above
+    1); the sub-chunks are replayed in fp32, so the 2048-step scan meets the
+    fp32 gate against the sequential recurrence.  The resident entry point
+    runs the same shape after dense_scan_reserve."""
+    say("dense scan two-level non-contracting", kind)
+    B, T, s = 4, 2048, 64
+    rng = np.random.default_rng(31 if kind == "orthogonal" else 32)
+    pool = householder_pool(rng, B * T, s)
+    if kind == "orthogonal":
+        a = pool
+    else:
+        a = pool * (1.0 + 0.004 * rng.random((B * T, 1, s), dtype=np.float32))
+    a = np.ascontiguousarray(a.reshape(B, T, s, s), dtype=np.float32)
+    b = rng.standard_normal((B, T, s)).astype(np.float32)
+    h = hip.dense_scan(a, b, None)
+    ref = O.dense_scan(a, b, None, threads=4)
+    for i in range(B):
+        assert_parity(h[i], ref[i], 1e-4, f"{kind} sequence {i}")
+    hip.dense_scan_reserve(B, T, s)
+    a_dev, b_dev, h_dev = hip.upload(a), hip.upload(b), hip.empty((B, T, s), np.float32)
+    hip.dense_scan_resident(a_dev.ptr, b_dev.ptr, None, B, T, s, h_dev.ptr)
+    np.testing.assert_array_equal(h_dev.to_host(), h)
+    for buf in (a_dev, b_dev, h_dev):
+        buf.close()
+
+
 def householder_pool(rng, n, s):
     """n random orthogonal matrices, each a product of two Householder
     reflections (the pool config 2's transitions are drawn from)."""

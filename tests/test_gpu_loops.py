@@ -103,3 +103,39 @@ def test_set_loops_keeps_loop_zero_and_validates(hip):
     layer.set_loops(1)
     assert layer.get_carry().shape == (2, w.cfg.depth, w.cfg.d_latent * w.cfg.d_state)
     layer.close()
+
+
+def test_loops_with_hybrid_read_refused_before_any_kernel(hip):
+    """Loops and the hybrid read are not combined here: set_loops refuses while
+    the hybrid read is on, and a decode over looped lanes whose model turned
+    it on afterwards is refused before the choice kernel runs, so no lane's
+    generator advances and the prefill's logits are still there to continue
+    from (the sampled ids equal a fresh layer's)."""
+    say("loops x hybrid read refusal")
+    w = model(seed=6)
+    ids = np.random.default_rng(4).integers(1, w.cfg.d_vocab, (2, 7), dtype=np.uint32)
+
+    def fresh():
+        layer = PSSALayer(hip, w, lanes=2, max_tokens=64)
+        layer.set_sampling(0.8, 0.9, 8, 77)
+        return layer
+
+    a = fresh()
+    a.set_hybrid_read(True, 0.9)
+    with pytest.raises(HipError, match="one loop here"):
+        a.set_loops(2)
+    a.set_hybrid_read(False, 1.0)
+    a.set_loops(2)
+    a.prefill_inference(ids, want_logits=False)
+    a.set_hybrid_read(True, 0.9)
+    with pytest.raises(HipError, match="one loop here"):
+        a.decode(4, graph=True)
+    a.set_hybrid_read(False, 1.0)
+    got = a.decode(4, graph=True)
+    b = fresh()
+    b.set_loops(2)
+    b.prefill_inference(ids, want_logits=False)
+    want = b.decode(4, graph=True)
+    np.testing.assert_array_equal(got, want)
+    a.close()
+    b.close()

@@ -86,3 +86,53 @@ def test_noalloc_retrieval_validates_before_running(hip):
     rc = lib.pssa_hip_retrieve_resident_noalloc(hip.handle, None, 4, None, None, None, 8, 8, 16, 16, C.c_float(0.1),
                                                 2, None, None, None, buf, 256)
     assert rc == _abi.EINVAL and b"null buffer" in buf.value
+
+
+def _free_device_bytes():
+    import ctypes as C
+
+    hip_rt = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(0), C.c_size_t(0)
+    assert hip_rt.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_retrieval_allocates_nothing_on_a_fresh_context():
+    """On a context of its own, the allocation-free entry point runs first:
+    device memory in use does not move across a config-4-sized call (a
+    smaller call before it loads the kernels), while the allocating entry
+    point's first call of the same shape grows the context's scratch by
+    tens of MB, which shows the measurement sees such a growth."""
+    from pssa_amd import HipDevice
+
+    rng = np.random.default_rng(11)
+    C1, dk, n, k = 512, 768, 20000, 8
+    keys, vals = ball(rng, C1, dk), ball(rng, C1, dk)
+    q = ball(rng, n, dk)
+    nsq = squared_norms(keys)
+    dev = HipDevice(0)
+    bufs = [dev.upload(a) for a in (q, keys, nsq, vals)]
+    outs = [dev.empty((n, dk), np.float32), dev.empty((n,), np.float32), dev.empty((n, k), np.uint32)]
+
+    def call(fn, n_q):
+        fn(bufs[0].ptr, n_q, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, C1, C1, dk, dk, 0.1, k,
+           outs[0].ptr, outs[1].ptr, outs[2].ptr)
+        dev.synchronize()
+
+    say("fresh context: warm-up call, 64 queries")
+    call(dev.retrieve_resident_noalloc, 64)
+    free0 = _free_device_bytes()
+    say(f"fresh context: {n} queries through the allocation-free entry point")
+    call(dev.retrieve_resident_noalloc, n)
+    free1 = _free_device_bytes()
+    idx = outs[2].to_host()
+    say(f"fresh context: the allocating entry point, same shape")
+    call(dev.retrieve_resident, n)
+    free2 = _free_device_bytes()
+    np.testing.assert_array_equal(outs[2].to_host(), idx)
+    for b in bufs + outs:
+        b.close()
+    dev.close()
+    say(f"device bytes in use: +{free0 - free1} (allocation-free), +{free1 - free2} (allocating)")
+    assert abs(free0 - free1) < (1 << 20)
+    assert free1 - free2 >= (16 << 20)

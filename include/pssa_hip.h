@@ -485,6 +485,16 @@ int pssa_hip_lanes_read_logits(pssa_hip_lanes* lanes, float* out, size_t len, ch
  * fast weights change; its step counter advances by one per step.
  * PSSA_HIP_DECODE_GRAPH captures one step into a hipGraph (once per lane
  * count and flag set) and replays it; results equal the eager steps. */
+/* The per-block taps of the last plastic decode step, for lanes 0..n_lanes-1
+ * (n_lanes must be that step's lane count): the projected query q_pnc
+ * [n_lanes, d_mem_key], the block output z_final [n_lanes, d_latent]
+ * (memory value and Hebbian target), the adapter output [n_lanes, d_latent]
+ * and the adapter activations [n_lanes, adapter_rank] of block `layer`, the
+ * quantities the reference's write rule and dream_replay_value read
+ * (src/pssa.rs:1814-1832, 3705-3736).  Any output may be NULL. */
+int pssa_hip_lanes_get_taps(pssa_hip_lanes* lanes, size_t layer, size_t n_lanes, float* q_pnc, float* z_final,
+                            float* ad_out, float* act, char* err, size_t err_len);
+
 /* InferenceConfig::repetition_penalty for the lanes' greedy choice
  * (sample(), src/inference.rs:113-121): before each choice the logits of the
  * lane's last 64 consumed ids (prompt and generated, since the last

@@ -177,6 +177,7 @@ def lib() -> C.CDLL:
         "pssa_hip_prefill_cancellable": ([vp, u32p, sz, sz, sz, CANCEL_FN, vp, fp, sz, C.POINTER(sz), err_t, sz],
                                          C.c_int),
         "pssa_hip_lanes_set_repetition_penalty": ([vp, C.c_float, err_t, sz], C.c_int),
+        "pssa_hip_lanes_get_taps": ([vp, sz, sz, fp, fp, fp, fp, err_t, sz], C.c_int),
         "pssa_hip_lanes_set_sampling": ([vp, C.c_float, C.c_float, sz, C.c_uint64, err_t, sz], C.c_int),
         "pssa_hip_lanes_set_loops": ([vp, sz, err_t, sz], C.c_int),
         "pssa_hip_model_set_memory_top_k": ([vp, sz, err_t, sz], C.c_int),

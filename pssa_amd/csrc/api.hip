@@ -1774,6 +1774,32 @@ Status capture_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
 
 extern "C" {
 
+int pssa_hip_lanes_get_taps(pssa_hip_lanes* L, size_t layer, size_t n_lanes, float* q_pnc, float* z_final,
+                            float* ad_out, float* act, char* err, size_t err_len) {
+  auto body = [&]() -> Status {
+    PSSA_RETURN_IF(need(L != nullptr, "null lanes"));
+    std::lock_guard<std::mutex> g(L->ctx->mu);
+    const pssa_hip_config& c = L->model->cfg;
+    PSSA_RETURN_IF(need(L->tap_lanes > 0, "no plastic decode step has recorded taps"));
+    PSSA_RETURN_IF(need(n_lanes == L->tap_lanes, "n_lanes must be the last plastic step's lane count"));
+    PSSA_RETURN_IF(need(layer < c.depth, "layer out of range"));
+    PSSA_HIP_TRY(hipSetDevice(L->ctx->device));
+    const hipStream_t st = L->ctx->stream;
+    const size_t n = n_lanes, d = c.d_latent, k = c.d_mem_key, r = c.adapter_rank;
+    auto part = [&](float* dst, const DevBuf& src, size_t w) -> Status {
+      if (!dst) return Status::Ok();
+      PSSA_HIP_TRY(hipMemcpyAsync(dst, src.as<float>() + layer * n * w, n * w * 4, hipMemcpyDeviceToHost, st));
+      return Status::Ok();
+    };
+    PSSA_RETURN_IF(part(q_pnc, L->tap_q, k));
+    PSSA_RETURN_IF(part(z_final, L->tap_z, d));
+    PSSA_RETURN_IF(part(ad_out, L->tap_a, d));
+    PSSA_RETURN_IF(part(act, L->tap_act, r));
+    return sync(L->ctx);
+  };
+  return pssa::finish(body(), err, err_len);
+}
+
 int pssa_hip_lanes_set_repetition_penalty(pssa_hip_lanes* L, float penalty, char* err, size_t err_len) {
   auto body = [&]() -> Status {
     PSSA_RETURN_IF(need(L != nullptr, "null lanes"));

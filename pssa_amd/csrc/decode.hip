@@ -779,6 +779,7 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   gw.nonfinite = L->nonfinite.as<int>();
   PSSA_RETURN_IF(launch_choice(L, n, gw, L->gen_ids.as<uint32_t>(), L->gen_pos.as<int>(), L->surprise.as<float>()));
   if (plastic) {
+    L->tap_lanes = n;
     PlasticArgs p{};
     for (size_t l = 0; l < c.depth; ++l) {
       const DevBlock& B = M->blocks[l];

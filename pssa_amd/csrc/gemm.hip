@@ -30,6 +30,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return bf1
 // evaluated as ln(u) * t / (u - 1) with u = 1 + t, which cancels the rounding
 // of u (relative error a few ulp), and as t - t^2/2 for t < 2^-12.
 __device__ __forceinline__ float softplus_f(float x) {
+#pragma clang fp contract(off)
   if (x > 20.0f) return x;
   const float t = __expf(x);
   if (t < 2.44140625e-4f) return t - 0.5f * t * t;
@@ -38,7 +39,10 @@ __device__ __forceinline__ float softplus_f(float x) {
 }
 // sigmoid(x) = 1 / (1 + e^-x) (src/linalg.rs:553-555), with the hardware
 // reciprocal (1 ulp).
-__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) {
+#pragma clang fp contract(off)
+  return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 // The input projection's column segments (src/pssa.rs:1091-1116): softplus,
 // identity, sigmoid, SiLU, identity.  The segment is the same for every
@@ -46,11 +50,48 @@ __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rc
 // the model's shapes), so the branches do not diverge and each element
 // evaluates only its own function.
 __device__ __forceinline__ float segment_f(const int (&seg)[4], float x, int col) {
+#pragma clang fp contract(off)
   if (col < seg[0]) return softplus_f(x);
   if (col < seg[1]) return x;
   if (col < seg[2]) return sigmoid_f(x);
   if (col < seg[3]) return x * sigmoid_f(x);
   return x;
+}
+
+// One output element of an epilogue: the accumulator a, the row operands p
+// and q of its row and column (z_raw: y and g; add-aux and residual: aux and
+// the running out32), the adapter output ad; the tap value goes to tp.
+// Every operation rounds on its own (no contraction into fused multiply-
+// adds), as the reference evaluates them, so that each kernel's epilogue
+// gives the same bits whatever its instruction schedule:
+//   z_raw     r = (y * ssm_scale) + (g * m_proj) + adapter, left to right
+//             (src/pssa.rs:1190-1192), tap = adapter;
+//   residual  z_final = z_raw + mlp_out, tap = z_final; layer 0 publishes it,
+//             deeper layers add it with the 1/sqrt(depth) residual scale
+//             (src/pssa.rs:2332-2337).
+template <int KIND>
+__device__ __forceinline__ float epi_value(const EpiParams& ep, float a, float p, float q, float ad, int col,
+                                           float& tp) {
+#pragma clang fp contract(off)
+  tp = 0.0f;
+  if constexpr (KIND == EPI_STORE) {
+    return a;
+  } else if constexpr (KIND == EPI_SCALE) {
+    return a * ep.scale;
+  } else if constexpr (KIND == EPI_SEGMENTS || KIND == EPI_SEGMENTS_TAP) {
+    return segment_f(ep.seg, a, col);
+  } else if constexpr (KIND == EPI_ADD_AUX) {
+    return a + p;
+  } else if constexpr (KIND == EPI_SILU) {
+    return a * sigmoid_f(a);
+  } else if constexpr (KIND == EPI_ZRAW) {
+    tp = ad;
+    return (p * ep.scale + q * a) + ad;
+  } else {  // EPI_RESIDUAL
+    const float zf = p + a;
+    tp = zf;
+    return ep.first ? zf : q + ep.scale * zf;
+  }
 }
 
 // Maps the hardware block id to a tile so that the blocks one XCD receives
@@ -108,12 +149,7 @@ __device__ __forceinline__ void load_quad(const EpiParams& ep, int row, int col,
 // all four are in range and every operand row is 16-byte aligned at col: the
 // row operands are the ones `in` holds and the stores are vectors.
 // Otherwise each column in range is read and written on its own.  The
-// arithmetic is written once for both (fp32, before the stores):
-//   z_raw     r = (y * ssm_scale) + (g * m_proj) + adapter, left to right
-//             (src/pssa.rs:1190-1192), tap = adapter;
-//   residual  z_final = z_raw + mlp_out, tap = z_final; layer 0 publishes it,
-//             deeper layers add it with the 1/sqrt(depth) residual scale
-//             (src/pssa.rs:2332-2337).
+// arithmetic (epi_value) is the same for both.
 template <typename T, int KIND>
 __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, int N, bool vec,
                                          const float (&acc)[4], const float (&ad)[4], const QuadIn& in) {
@@ -138,28 +174,7 @@ __device__ __forceinline__ void epi_quad(const EpiParams& ep, int row, int col, 
   }
   float r[4], tp[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a = acc[e];
-    tp[e] = 0.0f;
-    if constexpr (KIND == EPI_STORE) {
-      r[e] = a;
-    } else if constexpr (KIND == EPI_SCALE) {
-      r[e] = a * ep.scale;
-    } else if constexpr (KIND == EPI_SEGMENTS || KIND == EPI_SEGMENTS_TAP) {
-      r[e] = segment_f(ep.seg, a, col + e);
-    } else if constexpr (KIND == EPI_ADD_AUX) {
-      r[e] = a + p4[e];
-    } else if constexpr (KIND == EPI_SILU) {
-      r[e] = a * sigmoid_f(a);
-    } else if constexpr (KIND == EPI_ZRAW) {
-      r[e] = (p4[e] * ep.scale + q4[e] * a) + ad[e];
-      tp[e] = ad[e];
-    } else {  // EPI_RESIDUAL
-      const float zf = p4[e] + a;
-      tp[e] = zf;
-      r[e] = ep.first ? zf : q4[e] + ep.scale * zf;
-    }
-  }
+  for (int e = 0; e < 4; ++e) r[e] = epi_value<KIND>(ep, acc[e], p4[e], q4[e], ad[e], col + e, tp[e]);
   constexpr bool tap4 = KIND == EPI_ZRAW || KIND == EPI_RESIDUAL;
   if (vec) {
     if (tap4 && ep.tap)

@@ -93,6 +93,7 @@ struct pssa_hip_lanes {
   pssa::DevBuf tap_gmean;    // [depth, lanes] mean memory-injection gate (hybrid write gate)
   pssa::DevBuf tap_zcap;     // [depth, lanes, d] z_final rows clamped to the value caps (bank writes)
   pssa::DevBuf bank_writer;  // [depth, capacity] writing lane of each slot in the current step
+  size_t tap_lanes = 0;      // lanes of the last plastic step whose taps the buffers hold
   // Batch training forward (allocated on its first call): the fp32 scaled
   // logits of every token row [max_tokens, V], each row's target id and
   // packed token index [2, max_tokens], the per-token losses in packed order

@@ -133,70 +133,96 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 
 // ---------------------------------------------------------------------------
 // One time step (decode): no staging, just the carry update.  A workgroup
-// owns one lane and 64 channels, and NB consecutive state blocks of 4*J
+// owns LPB lanes and 64 channels, and NB consecutive state blocks of 4*J
 // states (four waves each); with NB covering all of d_state it also finishes
 // the readout, adding the block sums in block order as the multi-block paths
 // do, and writes y (and its bf16 copy) directly.  The arithmetic and the
 // readout order are those of the kernels above, so a step here equals the
 // same step inside a prefill bit for bit.  The traffic is the carry read and
-// written once, streamed past the caches (plus the lane-shared rates from
-// L2).
-template <int J, int NB>
+// written once, streamed past the caches, plus the rates, which the LPB
+// lanes of a workgroup share: they load from L2 once per workgroup, and the
+// next lane's carry, B/C, delta and x loads are issued before this lane's
+// carry stores, so the loads of consecutive lanes overlap.
+template <int J, int NB, int LPB>
 __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
   constexpr int GS = J < 16 ? J : 16;
   constexpr int NG = J / GS;
   static_assert(J <= 32, "one B/C load per wave covers at most 32 states");
-  __shared__ float sY[NB * 4 * NG][64];
+  __shared__ float sY[LPB][NB * 4 * NG][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int i0 = blockIdx.x * 64, b = blockIdx.y;
+  const int i0 = blockIdx.x * 64, b0 = blockIdx.y * LPB;
   const int jw = blockIdx.z * NB * 4 * J + wave * J;
   const int i = i0 + lane;
   const bool ivalid = i < a.d;
   const int d = a.d, s = a.s;
-  const size_t r = b;  // T == 1: lane b's row
-  float* carry = a.carry + (size_t)b * a.carry_stride;
-  // Every load is issued before the first carry store: the wave's B values
-  // (lanes 0..J-1) and C values (lanes 32..32+J-1) in one load, broadcast
-  // with readlane, then the carry and rate of each of its J states.
   const int jb = jw + (lane & 31);
-  float bc = 0.0f;
-  if ((lane & 31) < J && jb < s) bc = lane < 32 ? a.bproj[r * a.ld_b + jb] : a.cproj[r * a.ld_c + jb];
-  const float dl = ivalid ? a.delta[r * a.ld_delta + i] : 0.0f;
-  const float u = dl * (ivalid ? a.xn[r * a.ld_x + i] : 0.0f);
-  float h[J], r2[J];
+  // One lane's step inputs: the wave's B values (lanes 0..J-1) and C values
+  // (lanes 32..32+J-1) in one load, broadcast with readlane; delta, the
+  // input term u = delta * x and the J carries.
+  struct LaneIn {
+    float h[J];
+    float bc, dl, u;
+  };
+  auto load_lane = [&](int b, LaneIn& L) {
+    const size_t r = b;  // T == 1: lane b's row
+    const float* carry = a.carry + (size_t)b * a.carry_stride;
+    L.bc = 0.0f;
+    if ((lane & 31) < J && jb < s) L.bc = lane < 32 ? a.bproj[r * a.ld_b + jb] : a.cproj[r * a.ld_c + jb];
+    L.dl = ivalid ? a.delta[r * a.ld_delta + i] : 0.0f;
+    L.u = L.dl * (ivalid ? a.xn[r * a.ld_x + i] : 0.0f);
+#pragma unroll
+    for (int q = 0; q < J; ++q) {
+      const int j = jw + q;
+      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
+    }
+  };
+  float r2[J];
+  LaneIn cur, nxt;
+  load_lane(b0, cur);
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    const bool ok = ivalid && j < s;
-    h[q] = ok ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
-    r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
+    r2[q] = (ivalid && j < s) ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
-  const int bc_bits = __float_as_int(bc);
 #pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int l = 0; l < LPB; ++l) {
+    const int b = b0 + l;
+    if (b >= a.lanes) break;  // uniform over the workgroup
+    LaneIn& L = (l & 1) ? nxt : cur;
+    LaneIn& N = (l & 1) ? cur : nxt;
+    if (l + 1 < LPB && b + 1 < a.lanes) load_lane(b + 1, N);
+    float* carry = a.carry + (size_t)b * a.carry_stride;
+    const int bc_bits = __float_as_int(L.bc);
 #pragma unroll
-    for (int qq = 0; qq < GS; ++qq) {
-      const int q = g * GS + qq;
-      const int j = jw + q;
-      const float bq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, q));
-      const float cq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, 32 + q));
-      const float ab = __builtin_amdgcn_exp2f(dl * r2[q]);
-      h[q] = fmaf(ab, h[q], u * bq);
-      yp4[qq & 3] = fmaf(h[q], cq, yp4[qq & 3]);
-      if (ivalid && j < s) __builtin_nontemporal_store(h[q], &carry[(size_t)j * d + i]);
+    for (int g = 0; g < NG; ++g) {
+      float yp4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int qq = 0; qq < GS; ++qq) {
+        const int q = g * GS + qq;
+        const int j = jw + q;
+        const float bq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, q));
+        const float cq = __int_as_float(__builtin_amdgcn_readlane(bc_bits, 32 + q));
+        const float ab = __builtin_amdgcn_exp2f(L.dl * r2[q]);
+        const float hv = fmaf(ab, L.h[q], L.u * bq);
+        yp4[qq & 3] = fmaf(hv, cq, yp4[qq & 3]);
+        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[(size_t)j * d + i]);
+      }
+      sY[l][wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }
-    sY[wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
   }
   __syncthreads();
-  if (wave == 0 && ivalid) {
+  // Wave l finishes lane b0 + l's readout (LPB <= NB * 4 waves).
+  static_assert(LPB <= NB * 4, "one wave per lane for the readout");
+  const int b = b0 + wave;
+  if (wave < LPB && b < a.lanes && ivalid) {
+    const size_t r = b;
     float v = 0.0f;
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
-      float bv = sY[blk * 4 * NG][lane];
+      float bv = sY[wave][blk * 4 * NG][lane];
 #pragma unroll
-      for (int g = 1; g < 4 * NG; ++g) bv += sY[blk * 4 * NG + g][lane];
+      for (int g = 1; g < 4 * NG; ++g) bv += sY[wave][blk * 4 * NG + g][lane];
       v = blk == 0 ? bv : v + bv;
     }
     if (a.y_part) {
@@ -416,17 +442,27 @@ bool ssm_needs_zeroed_y(int s) { return ssm_state_blocks(s) == 2; }
 // twice the waves, half the registers per lane) keeps the SIMDs fed.
 constexpr long kScanFullGrid = 768;
 
+// Lanes per decode-step workgroup (they share the rate loads).
+#ifndef PSSA_SSM_STEP_LPB
+#define PSSA_SSM_STEP_LPB 4
+#endif
+
 template <int J>
 static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
   dim3 grid((a.d + 63) / 64, a.lanes, (a.s + 4 * J - 1) / (4 * J));
   if (mat) {
     ssm_materialize_kernel<J, true><<<grid, 256, 0, stream>>>(a);
   } else if (a.T == 1) {
+    // At most one lane per wave of the workgroup (the readout's waves).
+    constexpr int LPB2 = PSSA_SSM_STEP_LPB < 8 ? PSSA_SSM_STEP_LPB : 8;
+    constexpr int LPB1 = PSSA_SSM_STEP_LPB < 4 ? PSSA_SSM_STEP_LPB : 4;
     if (grid.z == 2) {
       grid.z = 1;
-      ssm_step_kernel<J, 2><<<grid, 512, 0, stream>>>(a);
+      grid.y = (a.lanes + LPB2 - 1) / LPB2;
+      ssm_step_kernel<J, 2, LPB2><<<grid, 512, 0, stream>>>(a);
     } else {
-      ssm_step_kernel<J, 1><<<grid, 256, 0, stream>>>(a);
+      grid.y = (a.lanes + LPB1 - 1) / LPB1;
+      ssm_step_kernel<J, 1, LPB1><<<grid, 256, 0, stream>>>(a);
     }
   } else if (a.T < SSM_TC) {
     ssm_materialize_kernel<J, false><<<grid, 256, 0, stream>>>(a);

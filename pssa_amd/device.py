@@ -515,6 +515,18 @@ class PSSALayer:
         self._staged = None
         return (out, logits) if want_logits else out
 
+    def get_taps(self, layer: int, n_lanes: int) -> dict:
+        """Block `layer`'s taps of the last plastic decode step over n_lanes lanes:
+        q_pnc [n, k], z_final [n, d], adapter output [n, d], activations [n, r]."""
+        c = self.cfg
+        out = {"q_pnc": np.empty((n_lanes, c.d_mem_key), np.float32),
+               "z_final": np.empty((n_lanes, c.d_latent), np.float32),
+               "ad_out": np.empty((n_lanes, c.d_latent), np.float32),
+               "act": np.empty((n_lanes, c.adapter_rank), np.float32)}
+        _abi.call(self._lib.pssa_hip_lanes_get_taps, self.handle, layer, n_lanes, _abi.ptr(out["q_pnc"]),
+                  _abi.ptr(out["z_final"]), _abi.ptr(out["ad_out"]), _abi.ptr(out["act"]))
+        return out
+
     def set_repetition_penalty(self, penalty: float) -> None:
         """InferenceConfig::repetition_penalty for the greedy choice (1 = off)."""
         _abi.call(self._lib.pssa_hip_lanes_set_repetition_penalty, self.handle, penalty)

@@ -335,30 +335,41 @@ def sync_oracle_to_device(ref, layer, cfg):
         b.mem_write_head = dev["mem_write_head"]
 
 
+def lane_block_err(got, want, floor):
+    """Element-wise relative error |got - want| / max(|want|, floor) per
+    (lane, block) of carries [lanes, depth, d*s]."""
+    w64 = want.astype(np.float64)
+    return (np.abs(got.astype(np.float64) - w64) / np.maximum(np.abs(w64), floor)).max(axis=2)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_config5_width_and_depth_plastic_decode_matches_oracle(hip, dtype):
-    """Config 5's model and stream count: 256 streams x 12 blocks at d=768,
-    s=256, k=32, C=512, V=16384, an 8-token prompt, then three plastic
-    graph-replayed steps, each against the oracle taking the same step from
-    the same state: before each step the oracle is given the device's
-    carries, banks and fast weights, and both consume the same tokens.  fp32
-    weights meet the reference's arithmetic at 1e-4; bf16 weights meet the
-    oracle's restatement of the bf16 mode (same rounded weights, every
-    product's activation operand rounded) at 2e-2.
+    """Config 5 as the benchmark runs it: 256 streams x 12 blocks at d=768,
+    s=256, k=32, C=512, V=16384, a 512-token prefill per stream, the first
+    token from the prefill's logits and 127 free-running plastic graph steps
+    (128 generated ids), then three more plastic graph steps, each against
+    the oracle taking the same step from the same state: before each step
+    the oracle is given the device's carries, banks and fast weights, and
+    both consume the same tokens.  fp32 weights meet the reference's
+    arithmetic (its AVX2 dot tree) at 1e-4; bf16 weights meet the oracle's
+    restatement of the bf16 mode (same rounded weights, every product's
+    activation operand rounded) at 2e-2.
     Why per step: the random 105M model amplifies rounding differences
-    through the recurrence over time (a one-ulp weight perturbation moves the
-    reference's own logits by 3e-5 over an 8-token prefill, 1.4e-6 within
-    one step), and with bf16 operands any fp32-level difference flips some
-    roundings by one bf16 ulp (a 1e-6 change of the soft-read weights moves
-    one step's logits by 1.7e-3), so a free-running comparison would measure
-    the model's conditioning rather than the step.  For the same reason the
-    bf16 carries and written bank rows are gated normwise only: such a flip
-    moves individual state elements by a few percent of their size.  The
-    fp32 ones are gated normwise as well: over the 6e8 state elements of a
-    step one lane can depart further than the rest (measured: 4.5e-4 of one
-    element's size at step 1, lane 6, from block 6 on, with or without the
-    plastic writes; normwise 1.9e-5; a written row 1.1e-4), while the oracle
-    perturbed by one ulp in its weights stays within 6e-5 there.
+    through the recurrence over time, and with bf16 operands any fp32-level
+    difference flips some roundings by one bf16 ulp, so a free-running
+    comparison would measure the model's conditioning rather than the step.
+    fp32: carries, written bank rows (keys and values), confidences and
+    fast weights are gated element-wise at 1e-4 (assert_parity).  Each step
+    also runs the reference's other dot tree (portable instead of AVX2) from
+    the same state and reports how far the reference moves from itself: the
+    device's per-(lane, block) error is set beside that spread.  (After an
+    8-token prompt a few lanes amplify any rounding difference from block to
+    block; there the reference's two trees differ by up to 2e-4 of an
+    element's size, lane 6 block 9, and the device by 4.5e-4.  At this
+    512-token state the spread is about 2e-5 and the device within 3.5e-5.)
+    bf16: carries and written bank rows are gated normwise (a flipped bf16
+    rounding moves an element by a few percent of its size) and their
+    element-wise errors are reported.
     A chosen id may differ from the oracle's only where its two logits lie
     within the gate.  The 256-way lane-ordered protected writes into each
     block's shared bank (insert_protected, src/memory.rs:305-342) must make
@@ -372,45 +383,71 @@ def test_config5_width_and_depth_plastic_decode_matches_oracle(hip, dtype):
     ref = w.to_bf16_values() if bf16 else ModelWeights.init(cfg, 0, "baseline")
     if not bf16:
         ref.populate_banks(1)
+    ref_p = None if bf16 else ModelWeights.init(cfg, 0, "baseline")  # the portable-tree twin
     tol = 2e-2 if bf16 else 1e-4
-    S, P, steps = 256, 8, 3
+    S, P, free, steps = 256, 512, 128, 3
     ids = np.random.default_rng(31).integers(0, cfg.d_vocab, (S, P), dtype=np.uint32)
     layer = PSSALayer(hip, w, lanes=S, max_tokens=S * P, weight_dtype=dtype)
-    dev_lg = layer.prefill_inference(ids)
-    cur = np.array([O.greedy(dev_lg[i]) for i in range(S)], np.uint32)
+    layer.stage_ids(ids)
+    layer.prefill_staged()
+    gen = layer.decode(free, n_lanes=S, plastic=True, graph=True)
+    assert gen.shape == (free, S) and int(gen.max()) < cfg.d_vocab
+    say(f"{S} x {P}-token prefill and {free} free-running steps done")
+    cur = gen[-1].copy()
     ties = 0
     for t in range(steps):
         st = layer.get_carry()
+        step0 = layer.get_plastic(0)["step"]
         sync_oracle_to_device(ref, layer, cfg)
+        if not bf16:
+            sync_oracle_to_device(ref_p, layer, cfg)
         om = O.OracleModel(ref, bf16_operands=bf16)
         got, glog = layer.decode(1, first_ids=cur, plastic=True, graph=True, want_logits=True)
-        want, r_lg, _ = om.decode(st, cur, steps=1, plastic=True, step_base=t, threads=16)
+        st_p = None if bf16 else st.copy()
+        with O.Dot(True):
+            want, r_lg, _ = om.decode(st, cur, steps=1, plastic=True, step_base=step0, threads=16)
         for i in np.nonzero(got[0] != want[0])[0]:
             gap = abs(float(r_lg[i, got[0, i]]) - float(r_lg[i, want[0, i]]))
             assert gap <= tol * float(np.max(np.abs(r_lg[i]))), (t, i, got[0, i], want[0, i], gap)
             ties += 1
         assert_parity(glog, r_lg, tol, f"step {t} logits")
         car = layer.get_carry()
-        d_abs = np.abs(car.astype(np.float64) - st)
         rms = float(np.sqrt(np.mean(st.astype(np.float64) ** 2)))
-        worst = np.unravel_index(np.argmax(d_abs / np.maximum(np.abs(st), rms)), st.shape)
-        say(f"step {t} carries: worst element lane {worst[0]} block {worst[1]} index {worst[2]}: "
-            f"device {car[worst]:.6e} oracle {st[worst]:.6e} rms {rms:.3e}; per-block normwise "
-            + " ".join(f"{rel_err(car[:, l], st[:, l]):.1e}" for l in range(cfg.depth)))
         nw = rel_err(car, st)
-        say(f"step {t} carries: normwise {nw:.3e}, element-wise {elem_rel_err(car, st):.3e}")
+        ew = lane_block_err(car, st, rms)
+        say(f"step {t} carries: normwise {nw:.3e}, element-wise {ew.max():.3e} (lane {np.unravel_index(ew.argmax(), ew.shape)})")
         assert nw < tol
+        if not bf16:
+            # The same step under the reference's portable dot tree, from the
+            # same state (the device's carries, banks and fast weights).
+            om_p = O.OracleModel(ref_p)
+            with O.Dot(False):
+                om_p.decode(st_p, cur, steps=1, plastic=True, step_base=step0, threads=16)
+            spread = lane_block_err(st_p, st, rms)
+            worst = np.unravel_index(np.argmax(ew), ew.shape)
+            say(f"step {t} fp32 carries: reference tree spread max {spread.max():.3e}; device worst (lane, block) "
+                f"{worst}: {ew[worst]:.3e}, the reference's spread there {spread[worst]:.3e}")
+            assert_parity(car, st, tol, f"step {t} carries")
+        else:
+            say(f"step {t} bf16 carries: element-wise {elem_rel_err(car, st):.3e} (normwise gate)")
         for l in range(cfg.depth):
             dev = layer.get_plastic(l)
             rb = ref.blocks[l]
-            assert dev["step"] == t + 1
+            assert dev["step"] == step0 + 1
             assert dev["mem_count"] == rb.mem_count and dev["mem_write_head"] == rb.mem_write_head, (t, l)
             np.testing.assert_array_equal(dev["mem_last_seen"], rb.mem_last_seen)
             assert_parity(dev["mem_confidence"], rb.mem_confidence, tol, f"confidence {t} {l}")
             # Written rows are a lane's projected query and z_final: state
-            # vectors like the carries, gated normwise.
-            assert rel_err(dev["mem_keys"], rb.mem_keys) < tol, (t, l)
-            assert rel_err(dev["mem_values"], rb.mem_values) < tol, (t, l)
+            # vectors like the carries (element-wise at fp32, normwise at bf16).
+            if bf16:
+                assert rel_err(dev["mem_keys"], rb.mem_keys) < tol, (t, l)
+                assert rel_err(dev["mem_values"], rb.mem_values) < tol, (t, l)
+                say(f"step {t} block {l} bf16 written rows: element-wise keys "
+                    f"{elem_rel_err(dev['mem_keys'], rb.mem_keys):.3e}, values "
+                    f"{elem_rel_err(dev['mem_values'], rb.mem_values):.3e}")
+            else:
+                assert_parity(dev["mem_keys"], rb.mem_keys, tol, f"keys {t} {l}")
+                assert_parity(dev["mem_values"], rb.mem_values, tol, f"values {t} {l}")
             assert_parity(dev["adapter_up"], rb.adapter_up, tol, f"adapter_up {t} {l}")
         cur = want[0].copy()
     say("near-tie choices", ties, "of", S * steps)

@@ -313,7 +313,8 @@ static_assert((TL_RING - 2) * (TL_NI + 1) <= 63, "vmcnt holds at most 63");
 
 __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs a) {
   __shared__ __attribute__((aligned(1024))) float ring_s[TL_RING][DS_SLOT];
-  __shared__ __attribute__((aligned(16))) float vec_s[2][DS_S];
+  __shared__ __attribute__((aligned(16))) float vec_s[2][DS_S];   // compose: q
+  __shared__ __attribute__((aligned(16))) float vecR_s[2][DS_S];  // re-run: h
   // P as B fragments, [buffer][hi/lo][k block][16-column tile][lane]
   __shared__ __attribute__((aligned(16))) tl_bf16x8_t pf_s[2][2][2][4][64];
   __shared__ int bad_s;
@@ -340,36 +341,41 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
     asrc[i] = Aseq + r * DS_S + 4 * (p ^ (r & 15));
   }
   const float* bsrc = bseq + 4 * min(lane, DS_S / 4 - 1);
+  // Loads step t's A_t and b_t into ring slot `slot` (loader waves).
+  auto issue_step = [&](int slot_i, size_t t) {
+    float* slot = ring + slot_i * DS_SLOT;
+#pragma unroll
+    for (int i = 0; i < TL_NI; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + t * (DS_S * DS_S)),
+                                       (__attribute__((address_space(3))) void*)(slot + 4 * (lw * TL_NI + i) * 64),
+                                       16, 0, 0);
+    if (lw == 0 && lane < DS_S / 4)
+      __builtin_amdgcn_global_load_lds((const void*)(bsrc + t * DS_S),
+                                       (__attribute__((address_space(3))) void*)(slot + DS_S * DS_S), 16, 0, 0);
+  };
+  // The loader waves' wait for the slot whose loads are followed by `after`
+  // more slots in flight; the compute waves' LDS writes of the last step
+  // complete before the barrier.
+  auto step_wait = [&](int after) {
+    if (loader) {
+      if (lw == 0)
+        tl_wait_loads<TL_NI + 1>(after);
+      else
+        tl_wait_loads<TL_NI>(after);
+    } else {
+      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | (0xF) | (0x3 << 14));  // lgkmcnt(0)
+    }
+    asm volatile("s_barrier" ::: "memory");
+  };
   // Streams steps ts .. ts+nst-1 through the ring; compute(k, slot) runs on
   // the compute waves once step ts+k has landed, one barrier per step.
   auto stream = [&](int ts, int nst, auto&& compute) {
-    auto issue = [&](int k) {
-      float* slot = ring + (k % TL_RING) * DS_SLOT;
-      const size_t t = (size_t)(ts + k);
-#pragma unroll
-      for (int i = 0; i < TL_NI; ++i)
-        __builtin_amdgcn_global_load_lds((const void*)(asrc[i] + t * (DS_S * DS_S)),
-                                         (__attribute__((address_space(3))) void*)(slot + 4 * (lw * TL_NI + i) * 64),
-                                         16, 0, 0);
-      if (lw == 0 && lane < DS_S / 4)
-        __builtin_amdgcn_global_load_lds((const void*)(bsrc + t * DS_S),
-                                         (__attribute__((address_space(3))) void*)(slot + DS_S * DS_S), 16, 0, 0);
-    };
     if (loader)
-      for (int k = 0; k < TL_RING - 1 && k < nst; ++k) issue(k);
+      for (int k = 0; k < TL_RING - 1 && k < nst; ++k) issue_step(k % TL_RING, (size_t)(ts + k));
     for (int k = 0; k < nst; ++k) {
+      step_wait(min(TL_RING - 2, nst - 1 - k));
       if (loader) {
-        // Slot k has landed once at most the slots issued after it are in flight.
-        if (lw == 0)
-          tl_wait_loads<TL_NI + 1>(min(TL_RING - 2, nst - 1 - k));
-        else
-          tl_wait_loads<TL_NI>(min(TL_RING - 2, nst - 1 - k));
-      } else {
-        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | (0xF) | (0x3 << 14));  // lgkmcnt(0)
-      }
-      asm volatile("s_barrier" ::: "memory");
-      if (loader) {
-        if (k + TL_RING - 1 < nst) issue(k + TL_RING - 1);
+        if (k + TL_RING - 1 < nst) issue_step((k + TL_RING - 1) % TL_RING, (size_t)(ts + k + TL_RING - 1));
         continue;
       }
       compute(k, ring + (k % TL_RING) * DS_SLOT);
@@ -377,101 +383,100 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
     __syncthreads();
   };
 
-  // ---- re-run role: entry state of sub-chunk j of window w_rerun, then its
-  // steps exactly in fp32 ----
-  auto rerun_role = [&]() {
-  if (a.w_rerun >= 0) {
-    const int w = a.w_rerun;
-    const int wstart = w * TL_W, wend = min(L, wstart + TL_W);
-    const int t0 = wstart + j * TL_LC;
-    const int n = min(wend, t0 + TL_LC) - t0;
-    if (n > 0) {  // uniform over the workgroup
-      int cur = 0;
-      if (tid < DS_S)
-        vec_s[0][tid] = w == 0 ? (a.H0 ? a.H0[(size_t)seq * DS_S + tid] : 0.0f)
-                               : a.hend[(size_t)((w - 1) & 1) * hb + (size_t)seq * DS_S + tid];
-      const float* maps = a.agg + ((size_t)(w & 1) * a.batch + seq) * (TL_SUB - 1) * TL_AGG;
-      bool usable = true;
-      for (int i = 0; i < j; ++i) usable = usable && maps[(size_t)i * TL_AGG + DS_S * DS_S + DS_S] == 0.0f;
-      __syncthreads();
-      if (usable) {
-        for (int i = 0; i < j; ++i) {
-          if (rowwave) {
-            const float* P = maps + (size_t)i * TL_AGG;
-            const float* h = &vec_s[cur][0];
-            float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float4 pv = *reinterpret_cast<const float4*>(P + row * DS_S + 16 * part + 4 * q);
-              const float4 hv = *reinterpret_cast<const float4*>(h + 16 * part + 4 * q);
-              p[q] = fmaf(pv.x, hv.x, p[q]);
-              p[q] = fmaf(pv.y, hv.y, p[q]);
-              p[q] = fmaf(pv.z, hv.z, p[q]);
-              p[q] = fmaf(pv.w, hv.w, p[q]);
-            }
-            const float acc = quad_sum((p[0] + p[1]) + (p[2] + p[3]));
-            if (part == 0) vec_s[cur ^ 1][row] = acc + P[DS_S * DS_S + row];
-          }
-          __syncthreads();
-          cur ^= 1;
-        }
-      } else {
-        // A map is unusable: replay the window's earlier sub-chunks exactly.
-        stream(wstart, t0 - wstart, [&](int, const float* slot) {
-          if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
-          cur ^= 1;
-        });
-      }
-      float* Hseq = a.H + (size_t)seq * L * DS_S;
-      stream(t0, n, [&](int k, const float* slot) {
-        if (wave == 0 && k > 0) Hseq[(size_t)(t0 + k - 1) * DS_S + lane] = vec_s[cur][lane];
-        if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
-        cur ^= 1;
-      });
-      if (wave == 0) {
-        Hseq[(size_t)(t0 + n - 1) * DS_S + lane] = vec_s[cur][lane];
-        if (t0 + n == wend) a.hend[(size_t)(w & 1) * hb + (size_t)seq * DS_S + lane] = vec_s[cur][lane];
-      }
-      __syncthreads();
-    }
-  }
+  // ---- the two roles of a launch, each in three parts (start, one step,
+  // finish) so that they can share one barrier chain ----
+  // Re-run: sub-chunk j of window w_rerun, its steps exactly in fp32 from
+  // its entry state.
+  const int wr = a.w_rerun;
+  const int wr_start = wr * TL_W, wr_end = wr >= 0 ? min(L, wr_start + TL_W) : 0;
+  const int tr0 = wr_start + j * TL_LC;
+  const int nr = wr >= 0 ? max(0, min(wr_end, tr0 + TL_LC) - tr0) : 0;
+  // Compose: the map (P, q) of sub-chunk j < TL_SUB - 1 of window w_agg.
+  const int wc = a.w_agg;
+  const int tc0 = wc * TL_W + j * TL_LC;
+  const int nc = (wc >= 0 && j < TL_SUB - 1) ? max(0, min(min(L, wc * TL_W + TL_W), tc0 + TL_LC) - tc0) : 0;
+  float* Hseq = a.H + (size_t)seq * L * DS_S;
+  const float* rmaps = a.agg + ((size_t)(wr & 1) * a.batch + seq) * (TL_SUB - 1) * TL_AGG;
+  bool rusable = true;  // every map before sub-chunk j of the re-run's window
+  if (nr > 0)
+    for (int i = 0; i < j; ++i) rusable = rusable && rmaps[(size_t)i * TL_AGG + DS_S * DS_S + DS_S] == 0.0f;
+  int curR = 0, curC = 0, pb = 0;
+  const int g = lane >> 4, cl = lane & 15;
+  // Compute wave cw owns the 16-row tile rt = cw % 4 of the new P and the
+  // 16-column tiles 2 (cw / 4) and 2 (cw / 4) + 1.
+  const int rt = wave & 3, nt0 = 2 * (wave >> 2);
+  tl_f32x4_t pm[2];  // this wave's tile rows of P, column tiles nt0, nt0 + 1
 
+  // Re-run start: the window's entry state carried through the composed
+  // maps of sub-chunks 0 .. j-1 (h <- P h + q), or, when one of them is
+  // unusable, those sub-chunks replayed exactly (streamed on their own).
+  auto rerun_start = [&]() {
+    if (tid < DS_S)
+      vecR_s[0][tid] = wr == 0 ? (a.H0 ? a.H0[(size_t)seq * DS_S + tid] : 0.0f)
+                               : a.hend[(size_t)((wr - 1) & 1) * hb + (size_t)seq * DS_S + tid];
+    __syncthreads();
+    if (rusable) {
+      for (int i = 0; i < j; ++i) {
+        if (rowwave) {
+          const float* P = rmaps + (size_t)i * TL_AGG;
+          const float* h = &vecR_s[curR][0];
+          float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 pv = *reinterpret_cast<const float4*>(P + row * DS_S + 16 * part + 4 * q);
+            const float4 hv = *reinterpret_cast<const float4*>(h + 16 * part + 4 * q);
+            p[q] = fmaf(pv.x, hv.x, p[q]);
+            p[q] = fmaf(pv.y, hv.y, p[q]);
+            p[q] = fmaf(pv.z, hv.z, p[q]);
+            p[q] = fmaf(pv.w, hv.w, p[q]);
+          }
+          const float acc = quad_sum((p[0] + p[1]) + (p[2] + p[3]));
+          if (part == 0) vecR_s[curR ^ 1][row] = acc + P[DS_S * DS_S + row];
+        }
+        __syncthreads();
+        curR ^= 1;
+      }
+    } else {
+      stream(wr_start, tr0 - wr_start, [&](int, const float* slot) {
+        if (rowwave) tl_exact_step(slot, vecR_s[curR], vecR_s[curR ^ 1], row, part);
+        curR ^= 1;
+      });
+    }
+  };
+  auto rerun_step = [&](int k, const float* slot) {
+    if (wave == 0 && k > 0) Hseq[(size_t)(tr0 + k - 1) * DS_S + lane] = vecR_s[curR][lane];
+    if (rowwave) tl_exact_step(slot, vecR_s[curR], vecR_s[curR ^ 1], row, part);
+    curR ^= 1;
+  };
+  auto rerun_finish = [&]() {  // after a barrier that follows the last step
+    if (wave == 0) {
+      Hseq[(size_t)(tr0 + nr - 1) * DS_S + lane] = vecR_s[curR][lane];
+      if (tr0 + nr == wr_end) a.hend[(size_t)(wr & 1) * hb + (size_t)seq * DS_S + lane] = vecR_s[curR][lane];
+    }
   };
 
-  // ---- compose role: (P, q) of sub-chunk j < TL_SUB - 1 of window w_agg ----
-  auto compose_role = [&]() {
-  if (a.w_agg >= 0 && j < TL_SUB - 1) {
-    const int w = a.w_agg;
-    const int wstart = w * TL_W, wend = min(L, wstart + TL_W);
-    const int t0 = wstart + j * TL_LC;
-    const int n = min(wend, t0 + TL_LC) - t0;
-    if (n <= 0) return;  // uniform over the workgroup
-    int cur = 0;
+  // Compose: P <- A_t P on the matrix cores (both operands split into bf16
+  // hi + lo), q <- A_t q + b_t in exact fp32 beside it.
+  // This wave's values of P as bf16 halves of B fragments: values r = 0..3
+  // of tile nt go to k block rt/2, slots 4 (rt%2) + r.
+  auto put_rows = [&](int buf, const tl_f32x4_t (&v)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      __bf16 h[4], l[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        h[r] = (__bf16)v[u][r];
+        l[r] = (__bf16)(v[u][r] - (float)h[r]);
+      }
+      __bf16* ph = reinterpret_cast<__bf16*>(&pf_s[buf][0][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
+      __bf16* pl = reinterpret_cast<__bf16*>(&pf_s[buf][1][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ph[r] = h[r], pl[r] = l[r];
+    }
+  };
+  auto compose_start = [&]() {  // a barrier must follow before the first step
     if (tid < DS_S) vec_s[0][tid] = 0.0f;
     if (tid == 0) bad_s = 0;
-    __syncthreads();
-    const int g = lane >> 4, cl = lane & 15;
-    // Compute wave cw owns the 16-row tile rt = cw % 4 of the new P and the
-    // 16-column tiles 2 (cw / 4) and 2 (cw / 4) + 1.
-    const int rt = wave & 3, nt0 = 2 * (wave >> 2);
-    // This wave's values of P as bf16 halves of B fragments: values r = 0..3
-    // of tile nt go to k block rt/2, slots 4 (rt%2) + r.
-    auto put_rows = [&](int buf, const tl_f32x4_t (&v)[2]) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        __bf16 h[4], l[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          h[r] = (__bf16)v[u][r];
-          l[r] = (__bf16)(v[u][r] - (float)h[r]);
-        }
-        __bf16* ph = reinterpret_cast<__bf16*>(&pf_s[buf][0][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
-        __bf16* pl = reinterpret_cast<__bf16*>(&pf_s[buf][1][rt >> 1][nt0 + u][lane]) + 4 * (rt & 1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ph[r] = h[r], pl[r] = l[r];
-      }
-    };
-    tl_f32x4_t pm[2];  // this wave's tile rows of P, column tiles nt0, nt0 + 1
     if (!loader) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -479,44 +484,44 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
         for (int r = 0; r < 4; ++r) pm[u][r] = (16 * rt + 4 * g + r == 16 * (nt0 + u) + cl) ? 1.0f : 0.0f;
       put_rows(0, pm);
     }
-    __syncthreads();
-    int pb = 0;
-    stream(t0, n, [&](int k, const float* slot) {
-      // B fragments of the previous P for this wave's column tiles.
-      tl_bf16x8_t bh[2][2], bl[2][2];
+  };
+  auto compose_step = [&](int, const float* slot) {
+    // B fragments of the previous P for this wave's column tiles.
+    tl_bf16x8_t bh[2][2], bl[2][2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          bh[u][kb] = pf_s[pb][0][kb][nt0 + u][lane];
-          bl[u][kb] = pf_s[pb][1][kb][nt0 + u][lane];
-        }
-      // A_t fragments of this wave's rows: row 16 rt + l%16, columns
-      // 32 kb + 4 g .. +3 and 32 kb + 16 + 4 g .. +3.
-      tl_bf16x8_t ah[2], al[2];
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const float4 u = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + g));
-        const float4 v = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + 4 + g));
-        const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
-        tl_split(x, ah[kb], al[kb]);
+        bh[u][kb] = pf_s[pb][0][kb][nt0 + u][lane];
+        bl[u][kb] = pf_s[pb][1][kb][nt0 + u][lane];
       }
-      if (rowwave) tl_exact_step(slot, vec_s[cur], vec_s[cur ^ 1], row, part);
+    // A_t fragments of this wave's rows: row 16 rt + l%16, columns
+    // 32 kb + 4 g .. +3 and 32 kb + 16 + 4 g .. +3.
+    tl_bf16x8_t ah[2], al[2];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        tl_f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = 0; kb < 2; ++kb) {
+      const float4 u = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + g));
+      const float4 v = *reinterpret_cast<const float4*>(slot + tl_off(16 * rt + cl, 8 * kb + 4 + g));
+      const float x[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+      tl_split(x, ah[kb], al[kb]);
+    }
+    if (rowwave) tl_exact_step(slot, vec_s[curC], vec_s[curC ^ 1], row, part);
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kb], bh[u][kb], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bl[u][kb], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bh[u][kb], acc, 0, 0, 0);
-        }
-        pm[u] = acc;
+    for (int u = 0; u < 2; ++u) {
+      tl_f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kb], bh[u][kb], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bl[u][kb], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[kb], bh[u][kb], acc, 0, 0, 0);
       }
-      put_rows(pb ^ 1, pm);
-      pb ^= 1;
-      cur ^= 1;
-    });
+      pm[u] = acc;
+    }
+    put_rows(pb ^ 1, pm);
+    pb ^= 1;
+    curC ^= 1;
+  };
+  auto compose_finish = [&]() {  // after a barrier that follows the last step
     bool bad = false;
     float sq = 0.0f;  // this lane's share of |P|_F^2
     if (!loader)
@@ -530,16 +535,16 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
     if (!loader && lane == 0) nrm_s[wave] = sq;
-    if (!loader && (bad || (tid < DS_S && !(fabsf(vec_s[cur][tid]) <= 3.0e38f)))) atomicOr(&bad_s, 1);
+    if (!loader && (bad || (tid < DS_S && !(fabsf(vec_s[curC][tid]) <= 3.0e38f)))) atomicOr(&bad_s, 1);
     __syncthreads();
-    float* out = a.agg + (((size_t)(w & 1) * a.batch + seq) * (TL_SUB - 1) + j) * TL_AGG;
+    float* out = a.agg + (((size_t)(wc & 1) * a.batch + seq) * (TL_SUB - 1) + j) * TL_AGG;
     if (!loader) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           out[(16 * rt + 4 * g + r) * DS_S + 16 * (nt0 + u) + cl] = pm[u][r];
-      if (tid < DS_S) out[DS_S * DS_S + tid] = vec_s[cur][tid];
+      if (tid < DS_S) out[DS_S * DS_S + tid] = vec_s[curC][tid];
       if (tid == 0) {
         // A map that does not contract (|P|_F > 1) would carry its split
         // rounding undamped into the states after it: replayed instead.
@@ -549,20 +554,65 @@ __global__ __launch_bounds__(TL_THREADS) void dense_twolevel_kernel(TwoLevelArgs
       }
     }
     __syncthreads();
-  }
   };
 
-  // The roles of one workgroup are independent (the re-run reads the maps
-  // and end states of earlier launches).  Half the workgroups compose first,
-  // so that at any time some stream transitions while others run the
-  // matrix products.
-  if (seq & 1) {
-    compose_role();
-    rerun_role();
-  } else {
-    rerun_role();
-    compose_role();
+  if (nr > 0 && !rusable) {
+    // A map the re-run needs is unusable: the re-run replays and streams
+    // on its own, then the compose streams.
+    rerun_start();
+    stream(tr0, nr, rerun_step);
+    rerun_finish();
+    __syncthreads();
+    if (nc > 0) {
+      compose_start();
+      __syncthreads();
+      stream(tc0, nc, compose_step);
+      compose_finish();
+    }
+    return;
   }
+
+  // Both roles in one barrier chain: step k runs compose step k (8 waves,
+  // matrix cores) and re-run step k (4 waves, exact fp32) on two ring slots,
+  // so a launch costs max(nc, nr) dependent steps instead of nc + nr.  The
+  // ring holds loads in order: compose step k's slot before re-run step k's.
+  if (nr > 0) rerun_start();
+  if (nc > 0) compose_start();
+  __syncthreads();
+  const int K = max(nc, nr), n_load = nc + nr;
+  auto before = [&](int k) { return min(k, nc) + min(k, nr); };  // loads of the steps before k
+  // The loaders' cursor: the next load is step lk's compose (lrole 0) or
+  // re-run (lrole 1) slot.
+  int issued = 0, lk = 0, lrole = nc > 0 ? 0 : 1;
+  auto issue_next = [&]() {
+    issue_step(issued % TL_RING, (size_t)(lrole == 0 ? tc0 + lk : tr0 + lk));
+    ++issued;
+    if (lrole == 0 && lk < nr) {
+      lrole = 1;
+    } else {
+      ++lk;
+      lrole = lk < nc ? 0 : 1;
+    }
+  };
+  if (loader)
+    while (issued < min(n_load, TL_RING)) issue_next();
+  for (int k = 0; k < K; ++k) {
+    // This step's loads are complete once at most the loads issued after
+    // them are in flight (at most TL_RING - 1 slots).
+    step_wait(issued - before(k + 1));
+    if (loader) {
+      // The slots of the steps before k are free.
+      const int lim = min(n_load, before(k) + TL_RING);
+      while (issued < lim) issue_next();
+      continue;
+    }
+    const int p0 = before(k);
+    if (k < nc) compose_step(k, ring + (p0 % TL_RING) * DS_SLOT);
+    if (k < nr) rerun_step(k, ring + ((p0 + (k < nc ? 1 : 0)) % TL_RING) * DS_SLOT);
+  }
+  __syncthreads();
+  if (nr > 0) rerun_finish();
+  if (nc > 0) compose_finish();
 }
 
 size_t dense_scan_scratch_bytes(int batch, int L, int s) {

@@ -102,6 +102,25 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
   return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
 }
 
+#ifndef PSSA_GEMM_GROUP_M
+#define PSSA_GEMM_GROUP_M 8
+#endif
+// Row and column tile of tile index t: with GROUP_M > 0, groups of GROUP_M
+// row panels are walked column by column, so the tiles in flight on one XCD
+// share a few row panels and a few weight panels in its L2; 0: row-major.
+__device__ __forceinline__ void tile_coords(int t, int tilesM, int tilesN, int& mt, int& nt) {
+  constexpr int GM = PSSA_GEMM_GROUP_M;
+  if (GM == 0) {
+    mt = t / tilesN;
+    nt = t % tilesN;
+    return;
+  }
+  const int group = t / (GM * tilesN), first = group * GM;
+  const int gs = min(GM, tilesM - first), idx = t - group * GM * tilesN;
+  mt = first + idx % gs;
+  nt = idx / gs;
+}
+
 template <typename T>
 struct Op;
 template <>
@@ -506,7 +525,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
   const int tilesN = (N + BNt - 1) / BNt, tilesM = (M + BMt - 1) / BMt;
   const int tile = xcd_tile(blockIdx.x, tilesM * tilesN);
-  const int m0 = (tile / tilesN) * BMt, n0 = (tile % tilesN) * BNt;
+  int mt, nt;
+  tile_coords(tile, tilesM, tilesN, mt, nt);
+  const int m0 = mt * BMt, n0 = nt * BNt;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, l32 = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;

@@ -168,3 +168,121 @@ def test_reference_v6_fixture_loads():
     # Every byte before the embed row marks is consumed by the fields the
     # reader keeps: the file's payload ends right after those marks.
     assert np.all(b.mem_norm_sq[: b.mem_count] < 1.0)
+
+
+# ---- legacy V5 (src/checkpoint.rs:1444-1545) ---------------------------------
+def v5_bytes(w, mem_count):
+    """A V5 file of a depth-one model, as the reference's test writes one
+    (tests/checkpoint_repair.rs:380-440): u32 header words, u32-length f32
+    slices, physical A = -ln(1 + e^a_raw) in f32, the first mem_count slots."""
+    import ctypes
+
+    libm = ctypes.CDLL("libm.so.6")
+    for name in ("expf", "log1pf"):
+        getattr(libm, name).restype = ctypes.c_float
+        getattr(libm, name).argtypes = [ctypes.c_float]
+    c, b = w.cfg, w.blocks[0]
+    out = bytearray(b"PSSA" + struct.pack("<H", 5))
+    for n in (c.d_vocab, c.d_latent, c.d_state, c.d_mem_key, c.mem_capacity, 64, mem_count, 1):
+        out += struct.pack("<I", n)
+
+    def f(a):
+        nonlocal out
+        a = np.asarray(a, np.float32).ravel()
+        out += struct.pack("<I", a.size) + a.astype("<f4").tobytes()
+
+    f(w.embed)
+    f(b.norm_gamma)
+    f(b.norm_beta)
+    f([-libm.log1pf(libm.expf(float(x))) for x in b.a_raw.ravel()])
+    for name in ("w_delta", "w_b", "w_c", "w_qx", "w_qh", "w_gate", "w_proj", "mlp_w1", "mlp_w2"):
+        f(getattr(b, name))
+    f(w.unembed)
+    f(b.mem_keys[:mem_count])
+    f(b.mem_values[:mem_count])
+    out += struct.pack("<I", 16)
+    f(b.adapter_down)
+    f(b.adapter_up)
+    return bytes(out)
+
+
+def test_reference_legacy_v5_fixture_loads():
+    """tests/fixtures/legacy-v5-model.pssa (the reference's data/model.pssa):
+    inference-only, no vocabulary, step 0, write head 0, the 11 stored slots
+    with their norms recomputed, physical A converted to finite raw rates
+    (load_checkpoint returns LegacyV5InferenceOnly, tests/checkpoint_repair.rs:
+    460-467)."""
+    c = ck.load(__import__("os").path.join(GOLDEN, "legacy-v5-model.pssa"))
+    assert c.version == 5 and c.format == "LegacyV5InferenceOnly"
+    cfg = c.weights.cfg
+    assert (cfg.depth, cfg.d_vocab, cfg.d_latent, cfg.d_state, cfg.d_mem_key, cfg.mem_capacity) == \
+        (1, 88, 256, 16, 32, 512)
+    assert c.vocabulary == [] and c.step_counter == 0 and not c.carry.any()
+    b = c.weights.blocks[0]
+    assert b.mem_count == 11 and b.mem_write_head == 0
+    assert np.all(np.isfinite(b.a_raw))
+    # -softplus(a_raw) gives back the file's physical A (within a few ulp).
+    raw = open(__import__("os").path.join(GOLDEN, "legacy-v5-model.pssa"), "rb").read()
+    off = 38
+    for n in (88 * 256, 256, 256):
+        off += 4 + 4 * n
+    phys = np.frombuffer(raw[off + 4: off + 4 + 4 * 256 * 16], "<f4")
+    back = -np.logaddexp(0.0, b.a_raw.astype(np.float64)).ravel()
+    np.testing.assert_allclose(back, phys, rtol=4e-6)
+    norms = (b.mem_keys[:11].astype(np.float64) ** 2).sum(axis=1)
+    np.testing.assert_allclose(b.mem_norm_sq[:11], norms, rtol=1e-6)
+    assert np.all(b.mem_norm_sq[:11] < 1.0) and not b.mem_keys[11:].any() and not b.mem_norm_sq[11:].any()
+    assert not b.adapter_slow.any()
+
+
+def test_legacy_v5_round_trip_keeps_the_forward():
+    """tests/checkpoint_repair.rs:443-468: a model written as V5 (one bank
+    slot, zero consolidated fast weights) and loaded back gives the same
+    logits within 2e-6 (the raw rates pass through -softplus and its
+    inverse in f32)."""
+    from oracle import oracle as O
+
+    cfg = PSSAConfig(depth=1, d_vocab=5, d_latent=4, d_state=3, d_mem_key=2, mem_capacity=3)
+    w = ModelWeights.init(cfg, 7, "reference")
+    b = w.blocks[0]
+    b.adapter_slow[:] = 0.0
+    b.mem_keys[0] = [0.3, -0.2]
+    b.mem_values[0] = [0.5, -1.0, 0.25, 2.0]
+    b.mem_norm_sq[0] = 0.13
+    b.mem_count, b.mem_write_head = 1, 0
+    b.mem_keys[1:] = 0.0
+    b.mem_values[1:] = 0.0
+    loaded = ck.load_bytes(v5_bytes(w, 1))
+    assert loaded.format == "LegacyV5InferenceOnly"
+    lw = loaded.weights
+    assert lw.blocks[0].mem_count == 1
+    om, ol = O.OracleModel(w), O.OracleModel(lw)
+    la = om.forward_inference(om.zero_state(), 1)
+    lb = ol.forward_inference(ol.zero_state(), 1)
+    assert np.max(np.abs(la - lb)) < 2e-6
+
+
+def test_legacy_v5_malformed_count_and_rank_are_rejected():
+    """tests/checkpoint_repair.rs:470-488: a count above the stored slots and an
+    adapter rank other than 16 are refused; so are a truncated header and a
+    count above the capacity."""
+    cfg = PSSAConfig(depth=1, d_vocab=5, d_latent=4, d_state=3, d_mem_key=2, mem_capacity=3)
+    w = ModelWeights.init(cfg, 7, "reference")
+    w.blocks[0].mem_keys[0] = [0.3, -0.2]
+    good = bytearray(v5_bytes(w, 1))
+    ck.load_bytes(bytes(good))
+    x = bytearray(good)
+    x[30:34] = struct.pack("<I", 2)
+    with pytest.raises(ck.CheckpointError):
+        ck.load_bytes(bytes(x))
+    x[30:34] = struct.pack("<I", 4)
+    with pytest.raises(ck.CheckpointError, match="exceeds capacity"):
+        ck.load_bytes(bytes(x))
+    x = bytearray(good)
+    rank = len(x) - (4 + 64 * 4) * 2 - 4
+    assert struct.unpack("<I", x[rank:rank + 4])[0] == 16
+    x[rank:rank + 4] = struct.pack("<I", 15)
+    with pytest.raises(ck.CheckpointError, match="adapter rank"):
+        ck.load_bytes(bytes(x))
+    with pytest.raises(ck.CheckpointError, match="truncated"):
+        ck.load_bytes(bytes(good[:30]))

@@ -392,3 +392,37 @@ def test_reference_v6_fixture_model(hip):
         r = O.OracleModel(w).forward_inference(st[0], tok)
         assert_parity(g[0], r, 1e-5, "v6 step logits")
     layer.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_reference_legacy_v5_fixture_model(hip, dtype):
+    """The reference's legacy V5 checkpoint (tests/fixtures/legacy-v5-model.pssa,
+    load_v5, src/checkpoint.rs:1444-1545: inference-only, 11 bank slots, raw
+    rates from the stored physical A): a 3-lane prefill on the device against
+    the oracle on the loaded weights (bf16: against the oracle's bf16-operand
+    restatement on the rounded weights), then greedy decode ids."""
+    say("legacy v5 fixture model", dtype)
+    ck = checkpoint.load(os.path.join(GOLDEN, "legacy-v5-model.pssa"))
+    assert ck.format == "LegacyV5InferenceOnly"
+    w = ck.weights
+    ids = np.random.default_rng(3).integers(0, w.cfg.d_vocab, (3, 40), dtype=np.uint32)
+    layer = PSSALayer(hip, w, lanes=3, max_tokens=3 * 40, weight_dtype=dtype)
+    got = layer.prefill_inference(ids)
+    wr = w.to_bf16_values() if dtype == "bf16" else w
+    om = O.OracleModel(wr, bf16_operands=dtype == "bf16")
+    st = om.zero_state(3)
+    ref = om.prefill_lanes(st, ids, threads=3)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    assert_parity(got, ref, tol, f"v5 {dtype} prefill logits")
+    assert_parity(layer.get_carry(), st, tol, f"v5 {dtype} carries")
+    if dtype == "f32":
+        gen = layer.decode(4, graph=True)
+        for i in range(3):
+            s_i = st[i].copy()
+            cur = O.greedy(ref[i])
+            want = [cur]
+            for _ in range(3):
+                cur = O.greedy(om.forward_inference(s_i, cur))
+                want.append(cur)
+            np.testing.assert_array_equal(gen[:, i], want)
+    layer.close()

@@ -198,6 +198,7 @@ int pssa_hip_init(int device, pssa_hip_ctx** out, char* err, size_t err_len) {
     ctx->name = prop.name;
     ctx->cu_count = prop.multiProcessorCount;
     PSSA_HIP_TRY(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    PSSA_RETURN_IF(pssa::init_gemm_attributes());
     PSSA_RETURN_IF(pssa::init_retrieve_attributes());
     PSSA_RETURN_IF(pssa::init_decode_attributes());
     PSSA_RETURN_IF(pssa::init_dense_scan_attributes());

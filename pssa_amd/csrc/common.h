@@ -134,6 +134,10 @@ __device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
 }
 __device__ __forceinline__ uint16_t bf16_bits_dev(float f) { return (uint16_t)bf16x2_bits(f, 0.0f); }
 
+// s_waitcnt immediate for vmcnt(v) alone (gfx9: vmcnt bits [3:0] and [15:14],
+// expcnt and lgkmcnt left at their no-wait maxima).
+constexpr int vmcnt_only(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
+
 }  // namespace pssa
 
 // The opaque context handed out through the C ABI.

@@ -105,9 +105,6 @@ constexpr int DS_NI1 = (DS_CHUNKS - DS_NI0 * 64 + 63) / 64;  // second loader (8
 constexpr int DS_THREADS = (4 + DS_LOADERS) * 64;
 static_assert(DS_NI0 >= DS_NI1, "loader 0 carries the larger share");
 
-// s_waitcnt immediate for vmcnt(v) alone (gfx9: vmcnt bits [3:0] and [15:14],
-// expcnt and lgkmcnt left at their no-wait maxima).
-constexpr int vmcnt_only(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
 static_assert((DS_RING - 2) * DS_NI0 <= 63, "vmcnt holds at most 63");
 
 __device__ __forceinline__ float quad_sum(float v) {

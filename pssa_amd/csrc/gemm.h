@@ -63,4 +63,7 @@ Status launch_gemm_f32a(hipStream_t stream, const float* A, int lda, const uint1
 Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* out, int ld_out,
                       size_t rows, int cols);
 
+// Per-device set-up of the GEMM kernels (their dynamic LDS limits).
+Status init_gemm_attributes();
+
 }  // namespace pssa

@@ -262,6 +262,25 @@ __device__ __forceinline__ void adapter_act_frag(const EpiParams& ep, int row, i
   }
 }
 
+// bf16 pairs of U[urow, q0 + 8*half .. +7] (zero past the rank or the
+// columns): the A fragment of the adapter MFMA for weight row urow.
+__device__ __forceinline__ void adapter_u_frag(const EpiParams& ep, int urow, int N, int q0, int half,
+                                               uint32_t (&wu)[4]) {
+  const int q = q0 + half * 8;
+  const uint16_t* us = static_cast<const uint16_t*>(ep.U) + (size_t)urow * ep.rank + q;
+  if (urow < N && q + 8 <= ep.rank && ((uintptr_t)us & 15) == 0) {
+    const uint4 v = *reinterpret_cast<const uint4*>(us);
+    wu[0] = v.x, wu[1] = v.y, wu[2] = v.z, wu[3] = v.w;
+    return;
+  }
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const uint32_t u0 = (urow < N && q + 2 * p < ep.rank) ? us[2 * p] : 0u;
+    const uint32_t u1 = (urow < N && q + 2 * p + 1 < ep.rank) ? us[2 * p + 1] : 0u;
+    wu[p] = u0 | (u1 << 16);
+  }
+}
+
 // Epilogue of one 32x32 accumulator tile whose weight rows start at column
 // n32.  Accumulator layout (weights as the MFMA's first operand): lane l
 // holds token row `row` (= tile row + l%32) and output columns
@@ -298,7 +317,8 @@ __device__ __forceinline__ void epi_tile_load(const EpiParams& ep, int row, int 
 template <typename T, int KIND>
 __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16_t& acc, int row,
                                                int n32, int M, int N, int vec_epi, int half,
-                                               int l32, const uint32_t* act0, const QuadIn (&in)[4]) {
+                                               int l32, const uint32_t* act0, const QuadIn (&in)[4],
+                                               const uint32_t* u0 = nullptr) {
   const int nb = n32 + half * 4;
   f32x16_t adv;
 #pragma unroll
@@ -308,7 +328,6 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
     // in the same accumulator layout as the main product.
     const int urow = n32 + l32;
     if constexpr (sizeof(T) == 2) {
-      const uint16_t* U = static_cast<const uint16_t*>(ep.U);
       for (int q0 = 0; q0 < ep.rank; q0 += 16) {
         uint32_t wa[4], wu[4];
         if (q0 == 0 && act0) {
@@ -317,18 +336,11 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
         } else {
           adapter_act_frag(ep, row, M, q0, half, wa);
         }
-        const int q = q0 + half * 8;
-        const uint16_t* us = U + (size_t)urow * ep.rank + q;
-        if (urow < N && q + 8 <= ep.rank && ((uintptr_t)us & 15) == 0) {
-          const uint4 v = *reinterpret_cast<const uint4*>(us);
-          wu[0] = v.x, wu[1] = v.y, wu[2] = v.z, wu[3] = v.w;
-        } else {
+        if (q0 == 0 && u0) {
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const uint32_t u0 = (urow < N && q + 2 * p < ep.rank) ? us[2 * p] : 0u;
-            const uint32_t u1 = (urow < N && q + 2 * p + 1 < ep.rank) ? us[2 * p + 1] : 0u;
-            wu[p] = u0 | (u1 << 16);
-          }
+          for (int p = 0; p < 4; ++p) wu[p] = u0[p];
+        } else {
+          adapter_u_frag(ep, urow, N, q0, half, wu);
         }
         bf16x8_t fa, fu;
         __builtin_memcpy(&fa, wa, 16);
@@ -722,6 +734,142 @@ static void launch_skinny_kind(hipStream_t stream, int kind, dim3 grid, const TA
 #undef PSSA_GEMM_SK_CASE
 }
 
+// ---------------------------------------------------------------------------
+// bf16 GEMM for few token rows through LDS (decode steps, small batches).
+// A workgroup of WM x WN waves computes a (32*WM) x (32*WN) tile with one
+// 32 x 32 MFMA tile per wave, so each wave runs a single K chain, as the
+// skinny kernel's waves do.  Operand slabs of 64 K-elements (one 128-byte line
+// per row) move global -> LDS with global_load_lds_dwordx4, eight lanes per
+// row, through a ring of S slabs: every request reads a whole line, where the
+// skinny kernel's fragment loads take 32 bytes of 32 lines per instruction.
+// A slab row holds its eight 16-byte chunks with chunk c at position
+// c ^ ((r >> 1) & 7) (r = slab row), so the 16 lanes of a fragment read that
+// share a chunk index fall in distinct banks.  Each output element
+// accumulates its 16-wide K-steps in increasing order on
+// v_mfma_f32_32x32x16_bf16 with the operands placed as in the tiled kernels,
+// so the bits are theirs.  K % 64 == 0; rows past M or N load a clamped
+// in-range row and their results are discarded.
+#ifndef PSSA_FEW_WM
+#define PSSA_FEW_WM 1
+#endif
+#ifndef PSSA_FEW_WN
+#define PSSA_FEW_WN 1
+#endif
+#ifndef PSSA_FEW_S
+#define PSSA_FEW_S 4
+#endif
+constexpr int FEW_WM = PSSA_FEW_WM, FEW_WN = PSSA_FEW_WN, FEW_S = PSSA_FEW_S;
+constexpr size_t gemm_few_bytes() { return (size_t)FEW_S * 32 * (FEW_WM + FEW_WN) * 128; }
+
+template <int KIND, int WM, int WN, int S>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_few_kernel(const uint16_t* __restrict__ A, int lda,
+                                                                const uint16_t* __restrict__ B, int ldb,
+                                                                int M, int N, int K, int vec_epi,
+                                                                EpiParams ep) {
+  constexpr int NWV = WM * WN, BMt = 32 * WM, BNt = 32 * WN, R = BMt + BNt;
+  constexpr int SLAB = R * 64;      // bf16 elements per slab
+  constexpr int BPW = R / 8 / NWV;  // DMA instructions per wave per slab, eight rows each
+  static_assert(R % (8 * NWV) == 0, "slab rows must split evenly over the waves");
+  static_assert(S >= 2 && (S - 2) * BPW <= 63, "vmcnt holds at most 63");
+  extern __shared__ __attribute__((aligned(1024))) uint16_t gemm_few_smem[];
+
+  const int tilesM = (M + BMt - 1) / BMt, tilesN = (N + BNt - 1) / BNt;
+  int mt, nt;
+  tile_coords(xcd_tile(blockIdx.x, tilesM * tilesN), tilesM, tilesN, mt, nt);
+  const int m0 = mt * BMt, n0 = nt * BNt;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Instruction i of this wave fills slab rows (wave + NWV*i)*8 .. +7: lane L
+  // writes position L % 8 of row L / 8 of those, so it loads that row's
+  // chunk (L % 8) ^ swizzle.
+  const uint16_t* src[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int row = (wave + NWV * i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    src[i] = (row < BMt ? A + (size_t)min(m0 + row, M - 1) * lda
+                        : B + (size_t)min(n0 + row - BMt, N - 1) * ldb) + c * 8;
+  }
+  const int nk = K / 64;
+  // Slabs past the end reload the last one into the slot just read, which
+  // no later step reads, so every step waits for the same count.
+  auto issue = [&](int kt) {
+    const int k0 = min(kt, nk - 1) * 64;
+    uint16_t* dst = gemm_few_smem + (kt % S) * SLAB + wave * 8 * 64;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+                                       (__attribute__((address_space(3))) void*)(dst + NWV * i * 8 * 64), 16,
+                                       0, 0);
+  };
+
+  f32x16_t acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int kt = 0; kt < S - 1; ++kt) issue(kt);
+  // The epilogue's row operands (and the z_raw adapter's first fragments)
+  // load now, behind the first slabs, rather than after the products.
+  const int row = m0 + wm * 32 + l32, n32 = n0 + wn * 32;
+  QuadIn in[4];
+  epi_tile_load<KIND, true>(ep, row, n32, M, N, vec_epi, half, in);
+  uint32_t act0[4] = {0u, 0u, 0u, 0u}, u0[4] = {0u, 0u, 0u, 0u};
+  if constexpr (KIND == EPI_ZRAW) {
+    adapter_act_frag(ep, row, M, 0, half, act0);
+    adapter_u_frag(ep, n32 + l32, N, 0, half, u0);
+  }
+  const int ra = wm * 32 + l32, rb = BMt + wn * 32 + l32;  // slab rows of this lane's fragments
+  const int sa = (ra >> 1) & 7, sb = (rb >> 1) & 7;
+  for (int kt = 0; kt < nk; ++kt) {
+    // This wave's part of slab kt has landed once at most the S - 2 slabs
+    // issued after it are in flight; the barrier then covers every wave's
+    // part, and every wave has finished reading the slot refilled next.
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
+    __builtin_amdgcn_s_barrier();
+    issue(kt + S - 1);
+    const uint16_t* sl = gemm_few_smem + (kt % S) * SLAB;
+    // All eight fragments of the slab are read before the first product, so
+    // one LDS round trip precedes the four dependent MFMAs rather than each.
+    bf16x8_t fa[4], fb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = 2 * kk + half;
+      fa[kk] = *reinterpret_cast<const bf16x8_t*>(sl + ra * 64 + (c ^ sa) * 8);
+      fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the reloads past the end
+  epi_tile_store<uint16_t, KIND>(ep, acc, row, n32, M, N, vec_epi, half, l32,
+                                 KIND == EPI_ZRAW ? act0 : nullptr, in, KIND == EPI_ZRAW ? u0 : nullptr);
+}
+
+static void launch_few_kind(hipStream_t stream, int kind, unsigned blocks, const uint16_t* A, int lda,
+                            const uint16_t* B, int ldb, int M, int N, int K, int ve, const EpiParams& ep) {
+#define PSSA_GEMM_FEW_CASE(KD)                                                                 \
+  case KD:                                                                                     \
+    gemm_few_kernel<KD, FEW_WM, FEW_WN, FEW_S>                                                 \
+        <<<blocks, 64 * FEW_WM * FEW_WN, gemm_few_bytes(), stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+    break;
+  switch (kind) {
+    PSSA_GEMM_FEW_CASE(EPI_STORE)
+    PSSA_GEMM_FEW_CASE(EPI_SEGMENTS)
+    PSSA_GEMM_FEW_CASE(EPI_ADD_AUX)
+    PSSA_GEMM_FEW_CASE(EPI_ZRAW)
+    PSSA_GEMM_FEW_CASE(EPI_SILU)
+    PSSA_GEMM_FEW_CASE(EPI_RESIDUAL)
+    PSSA_GEMM_FEW_CASE(EPI_SCALE)
+    PSSA_GEMM_FEW_CASE(EPI_SEGMENTS_TAP)
+    default:
+      break;
+  }
+#undef PSSA_GEMM_FEW_CASE
+}
+
 // fp32 GEMM for few token rows: one wave per 32*MT token rows x 32 weight
 // rows, operand fragments straight from global memory through a register
 // ring of RING 8-deep K steps.  A lane holds the four K values
@@ -908,6 +1056,15 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   if (vec_bf16 && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
     const auto* a16 = static_cast<const uint16_t*>(A);
     const auto* b16 = static_cast<const uint16_t*>(B);
+#ifndef PSSA_FEW_OFF
+    if (K % 64 == 0) {
+      const long tiles = (long)((M + 32 * FEW_WM - 1) / (32 * FEW_WM)) * ((N + 32 * FEW_WN - 1) / (32 * FEW_WN));
+      if (tiles > 0x7fffffffL) return Status::Invalid("gemm: too many tiles");
+      launch_few_kind(stream, ep.kind, (unsigned)tiles, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
+      PSSA_LAUNCH_CHECK("gemm_few");
+      return Status::Ok();
+    }
+#endif
     const dim3 grid((N + 31) / 32, (M + 31) / 32);
     if (grid.y > 65535) return Status::Invalid("gemm: too many row groups");
     launch_skinny_kind<uint16_t, 1, 16>(stream, ep.kind, grid, a16, lda, b16, ldb, M, N, K, vec_epi, ep);
@@ -980,6 +1137,19 @@ Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* 
   if (g > 16384) g = 16384;
   to_bf16_kernel<<<(unsigned)g, 256, 0, stream>>>(in, ld_in, out, ld_out, rows, cols);
   PSSA_LAUNCH_CHECK("to_bf16");
+  return Status::Ok();
+}
+
+Status init_gemm_attributes() {
+  const void* few[] = {
+#define PSSA_GEMM_FEW_FN(KD) reinterpret_cast<const void*>(&gemm_few_kernel<KD, FEW_WM, FEW_WN, FEW_S>),
+      PSSA_GEMM_FEW_FN(EPI_STORE) PSSA_GEMM_FEW_FN(EPI_SEGMENTS) PSSA_GEMM_FEW_FN(EPI_ADD_AUX)
+      PSSA_GEMM_FEW_FN(EPI_ZRAW) PSSA_GEMM_FEW_FN(EPI_SILU) PSSA_GEMM_FEW_FN(EPI_RESIDUAL)
+      PSSA_GEMM_FEW_FN(EPI_SCALE) PSSA_GEMM_FEW_FN(EPI_SEGMENTS_TAP)
+#undef PSSA_GEMM_FEW_FN
+  };
+  for (const void* f : few)
+    PSSA_HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_few_bytes()));
   return Status::Ok();
 }
 

@@ -336,19 +336,30 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
   double* kk = rk + cap;                                               // [cap]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float* pw = reinterpret_cast<float*>(kk + cap) + wave * QG * dk;     // [QG][dk]
+  const int nw = gridDim.x * NWV;
+  const int per = (a.n + nw - 1) / nw;
+  const int qb = (blockIdx.x * NWV + wave) * per;
+  const int qe = min(a.n, qb + per);
+  // One query per wave (a decode step): its row loads now, across the lanes,
+  // so the round trip overlaps the key staging below.
+  const bool one = QG == 1 && per == 1;
+  float qlane = 0.0f;
+  if (one && qb < qe) qlane = a.q[(size_t)qb * a.ld_q + min(lane, dk - 1)];
   // Coalesced reads of the row-major keys, transposed on the way into LDS;
-  // eight loads per thread are issued before their stores.
+  // KU loads per thread are issued before their stores (a four-wave
+  // workgroup holds a 512 x 32 bank in one round of sixteen).
+  constexpr int KU = NWV <= 4 ? 16 : 8;
   if (dk % 4 == 0 && ((uintptr_t)a.keys & 15) == 0) {
     const int nv = cnt * dk / 4;
-    for (int e0 = tid; e0 < nv; e0 += 8 * 64 * NWV) {
-      float4 v[8];
+    for (int e0 = tid; e0 < nv; e0 += KU * 64 * NWV) {
+      float4 v[KU];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < KU; ++u) {
         const int e = e0 + u * 64 * NWV;
         v[u] = e < nv ? reinterpret_cast<const float4*>(a.keys)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < KU; ++u) {
         const int e = e0 + u * 64 * NWV;
         if (e < nv) {
           const int sl = (4 * e) / dk, i = 4 * e - sl * dk;
@@ -379,15 +390,30 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
 
   const float c2 = 2.0f / a.tau;
 
-  const int nw = gridDim.x * NWV;
-  const int per = (a.n + nw - 1) / nw;
-  const int qb = (blockIdx.x * NWV + wave) * per;
-  const int qe = min(a.n, qb + per);
   for (int c0 = qb; c0 < qe; c0 += 64) {
     const int na = min(64, qe - c0);
     // ---- projection, one query per lane (src/memory.rs:181-211) ----
     double scale = 1.0, qs = 0.0, rq = 1.0;
-    if (lane < na) {
+    if (one) {
+#pragma clang fp contract(off)
+      // The wave's one query, held across the lanes: the same sequential
+      // f64 sums, every lane reading the values in order.
+      double r2 = 0.0;
+      for (int i = 0; i < dk; ++i) {
+        const double v = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(qlane), i));
+        r2 = r2 + v * v;
+      }
+      const double r = sqrt(r2);
+      scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+      for (int i = 0; i < dk; ++i) {
+        const double v = (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(qlane), i));
+        const double pv = (double)(float)(v * scale);
+        qs = qs + pv * pv;
+      }
+      float q_sq = (float)qs;
+      if (qs < 1.0 && q_sq == 1.0f) q_sq = __uint_as_float(0x3f7fffffu);
+      rq = 1.0 / (1.0 - (double)q_sq);
+    } else if (lane < na) {
 #pragma clang fp contract(off)
       const float* qrow = a.q + (size_t)(c0 + lane) * a.ld_q;
       // Sixteen loads in flight before the dependent sums (the sums keep the
@@ -429,13 +455,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
       // used only under `lane < dk` was sunk into that block and waited
       // there, one round trip per query).
       float qvg[QG];
+      if (one) {
+        qvg[0] = qlane;
+      } else {
 #pragma unroll
-      for (int g = 0; g < QG; ++g)
-        qvg[g] = a.q[(size_t)(c0 + (g < ng ? g0 + g : g0)) * a.ld_q + min(lane, dk - 1)];
+        for (int g = 0; g < QG; ++g)
+          qvg[g] = a.q[(size_t)(c0 + (g < ng ? g0 + g : g0)) * a.ld_q + min(lane, dk - 1)];
+      }
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
         const int src = g < ng ? g0 + g : g0;
-        const float pv = (float)((double)qvg[g] * readlane_f64(scale, src));
+        const float pv = (float)((double)qvg[g] * (one ? scale : readlane_f64(scale, src)));
         if (lane < dk) {
           pw[g * dk + lane] = pv;
           if (a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;

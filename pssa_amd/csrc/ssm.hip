@@ -251,7 +251,10 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
 // group sums of the block added one after another in state order.  The
 // variant can therefore be chosen by occupancy alone without changing a bit
 // of the result, and a run of single-token steps still equals one prefill.
-constexpr int SSM_TC = 4;
+#ifndef PSSA_SSM_TC
+#define PSSA_SSM_TC 4
+#endif
+constexpr int SSM_TC = PSSA_SSM_TC;
 
 template <int J, int NW, int WPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void ssm_scan_kernel(SsmArgs a) {

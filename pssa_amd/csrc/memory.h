@@ -38,7 +38,24 @@ struct RetrieveArgs {
   double log_lam = 0.0;
   unsigned long long age_base = 0;
   int age_T = 0;
+  // Fused query product (a decode step's few-query soft read, see
+  // retrieve_fuses_query): with qw set the Euclidean query of row r is
+  // qa[r] . qw^T + qaux[r], qa [n, ld_qa] bf16 rows, qw [dk, qk] bf16
+  // (K-contiguous), qaux [n, ld_qaux] fp32, formed on the matrix cores in the
+  // tiled GEMMs' K order and summed with qaux as their ADD_AUX epilogue does,
+  // so it is the q a separate product writes; q is not read.
+  const uint16_t* qa = nullptr;
+  int ld_qa = 0;
+  const uint16_t* qw = nullptr;
+  int qk = 0;
+  const float* qaux = nullptr;
+  int ld_qaux = 0;
 };
+
+// Whether launch_retrieve forms the query product itself for these
+// arguments (qa, qw and qaux set): the few-query soft read with one query
+// per wave, d_key <= 32, qk % 128 == 0 and the panels within LDS.
+bool retrieve_fuses_query(const RetrieveArgs& a);
 
 // Scratch the ranked top-k path needs for these arguments (0: not taken).
 size_t retrieve_scratch_bytes(const RetrieveArgs& a);

@@ -318,6 +318,18 @@ static size_t soft_read_lds(int dk, int cap, int qg, int nwv) {
          (size_t)nwv * qg * dk * sizeof(float);
 }
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// The fused query product's LDS (after the soft read's own): each wave's raw
+// query row (32 floats), then the bf16 panels, 16-byte aligned: 32 weight
+// rows (clamped past d_key) and the workgroup's query rows, qk elements
+// each, chunk c of panel row r at position c ^ (r & 15).
+constexpr int SOFT_QP_ROWS = 32;
+static size_t soft_qp_lds(int qk, int nwv) {
+  return (size_t)nwv * 32 * sizeof(float) + 16 + (size_t)(SOFT_QP_ROWS + nwv) * qk * sizeof(uint16_t);
+}
+
 __device__ __forceinline__ double readlane_f64(double v, int l) {
   const long long b = __double_as_longlong(v);
   const int lo = __builtin_amdgcn_readlane((int)b, l);
@@ -325,7 +337,7 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
-template <int QG, int SPL, bool HYB, int NWV>
+template <int QG, int SPL, bool HYB, int NWV, bool QP = false>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) void soft_read_kernel(
     RetrieveArgs a) {
   extern __shared__ float smem[];
@@ -344,7 +356,33 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
   // so the round trip overlaps the key staging below.
   const bool one = QG == 1 && per == 1;
   float qlane = 0.0f;
-  if (one && qb < qe) qlane = a.q[(size_t)qb * a.ld_q + min(lane, dk - 1)];
+  // Fused query product (QP, one query per wave): the weight panel and the
+  // workgroup's query rows go to LDS by direct loads issued first; wave 0
+  // forms the products while the other waves finish the key terms.
+  static_assert(!QP || (QG == 1 && NWV > 1), "the fused query product serves one query per wave");
+  const size_t pq_off = soft_keys_floats(dk, cap) + 4 * (size_t)cap + (size_t)NWV * QG * dk;
+  float* pq = smem + pq_off;                                                         // [NWV][32]
+  uint16_t* sq = reinterpret_cast<uint16_t*>(smem + ((pq_off + NWV * 32 + 3) & ~(size_t)3));
+  float qx[16];
+  if constexpr (QP) {
+    const int cpr = a.qk / 8;                     // 16-byte chunks per panel row
+    const int n_ins = (SOFT_QP_ROWS + NWV) * cpr / 64;
+    for (int ins = wave; ins < n_ins; ins += NWV) {
+      const int e = ins * 64 + lane, r = e / cpr, c = (e - r * cpr) ^ (r & 15);
+      const uint16_t* src = r < SOFT_QP_ROWS
+                                ? a.qw + (size_t)min(r, dk - 1) * a.qk + c * 8
+                                : a.qa + (size_t)min((int)blockIdx.x * NWV + r - SOFT_QP_ROWS, a.n - 1) * a.ld_qa + c * 8;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (__attribute__((address_space(3))) void*)(sq + (size_t)ins * 512), 16, 0, 0);
+    }
+    // The addend of the rows wave 0's lanes will hold (see below).
+    const int l32 = lane & 31, qrow = min((int)blockIdx.x * NWV + min(l32, NWV - 1), a.n - 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      qx[i] = a.qaux[(size_t)qrow * a.ld_qaux + min(8 * (i / 4) + 4 * (lane >> 5) + i % 4, dk - 1)];
+  } else {
+    if (one && qb < qe) qlane = a.q[(size_t)qb * a.ld_q + min(lane, dk - 1)];
+  }
   // Coalesced reads of the row-major keys, transposed on the way into LDS;
   // KU loads per thread are issued before their stores (a four-wave
   // workgroup holds a 512 x 32 bank in one round of sixteen).
@@ -376,17 +414,59 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
       keyT[i * kp + sl] = a.keys[e];
     }
   }
+  if constexpr (QP) __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // this wave's panel loads
   __syncthreads();
-  for (int sl = tid; sl < cnt; sl += 64 * NWV) {
-    rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
-    double s2 = 0.0;
-    for (int i = 0; i < dk; ++i) {
-      const double kv = keyT[i * kp + sl];
-      s2 = fma(kv, kv, s2);
+  if (!QP || wave > 0) {
+    const int t0 = QP ? tid - 64 : tid, step = QP ? 64 * (NWV - 1) : 64 * NWV;
+    for (int sl = t0; sl < cnt; sl += step) {
+      rk[sl] = 1.0 / (1.0 - (double)a.norm_sq[sl]);
+      double s2 = 0.0;
+      for (int i = 0; i < dk; ++i) {
+        const double kv = keyT[i * kp + sl];
+        s2 = fma(kv, kv, s2);
+      }
+      kk[sl] = s2;
     }
-    kk[sl] = s2;
+  }
+  if constexpr (QP) {
+    if (wave == 0) {
+      // q = qa qw^T + qaux for the workgroup's NWV rows: one 32 x 32 tile
+      // whose token rows are those rows (lane l32 reads row min(l32, NWV-1)),
+      // K in 16-wide steps in increasing order on v_mfma_f32_32x32x16_bf16
+      // with the weights as the first operand, as in the tiled GEMMs; lane
+      // l32 < NWV then holds row l32's columns 8*(i/4) + 4*(lane/32) + i%4.
+      const int half = lane >> 5, l32 = lane & 31, ra = SOFT_QP_ROWS + min(l32, NWV - 1);
+      const uint16_t* wrow = sq + (size_t)l32 * a.qk;
+      const uint16_t* arow = sq + (size_t)ra * a.qk;
+      const int sw = l32 & 15, sa = ra & 15;
+      f32x16_t acc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+      for (int k0 = 0; k0 < a.qk; k0 += 64) {
+        bf16x8_t fa[4], fb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = k0 / 8 + 2 * q + half;
+          fb[q] = *reinterpret_cast<const bf16x8_t*>(wrow + (c ^ sw) * 8);
+          fa[q] = *reinterpret_cast<const bf16x8_t*>(arow + (c ^ sa) * 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[q], fa[q], acc, 0, 0, 0);
+      }
+      if (l32 < NWV) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int col = 8 * (i / 4) + 4 * half + i % 4;
+          if (col < dk) pq[l32 * 32 + col] = acc[i] + qx[i];  // the ADD_AUX epilogue's sum
+        }
+      }
+    }
   }
   __syncthreads();
+  if constexpr (QP) {
+    if (one && qb < qe) qlane = pq[wave * 32 + min(lane, dk - 1)];
+  }
 
   const float c2 = 2.0f / a.tau;
 
@@ -577,9 +657,6 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
 // 4. Selection by (distance bits, slot) through ranks counted over the
 //    candidates, softmax over the selected distances, and the value readout
 //    in ascending slot order, as retrieve_soft_into (src/memory.rs:344-407).
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
 constexpr int RK_SLOTS = 512;            // occupied slots handled
 constexpr int RK_BK = 32;                // key dimensions per slab and per exact chunk
 constexpr int RK_MAX_DK = 1024;
@@ -1282,6 +1359,11 @@ static Status allow_large_lds() {
       PSSA_SOFT_FN(1, 1, SOFT_WAVES_FEW) PSSA_SOFT_FN(1, 2, SOFT_WAVES_FEW) PSSA_SOFT_FN(1, 4, SOFT_WAVES_FEW)
       PSSA_SOFT_FN(1, 8, SOFT_WAVES_FEW)
 #undef PSSA_SOFT_FN
+#define PSSA_SOFT_QP_FN(SPL)                                                        \
+  reinterpret_cast<const void*>(&soft_read_kernel<1, SPL, false, SOFT_WAVES_FEW, true>), \
+      reinterpret_cast<const void*>(&soft_read_kernel<1, SPL, true, SOFT_WAVES_FEW, true>),
+      PSSA_SOFT_QP_FN(1) PSSA_SOFT_QP_FN(2) PSSA_SOFT_QP_FN(4) PSSA_SOFT_QP_FN(8)
+#undef PSSA_SOFT_QP_FN
   };
   for (const void* f : soft)
     PSSA_HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
@@ -1299,23 +1381,55 @@ Status prepare_retrieve(const RetrieveArgs& a) {
 }
 
 
+// Launch shape of the soft read: waves per workgroup, workgroups, queries per wave.
+static void soft_read_shape(const RetrieveArgs& a, int& nwv, int& blocks, int& per) {
+  // Few queries (a decode step): small workgroups spread them over more
+  // CUs, each staging the bank for fewer waves.
+  nwv = a.n <= SOFT_FEW_QUERIES ? SOFT_WAVES_FEW : SOFT_WAVES;
+  blocks = (a.n + nwv - 1) / nwv;
+  if (blocks > 512) blocks = 512;
+  per = (a.n + blocks * nwv - 1) / (blocks * nwv);
+}
+
+bool retrieve_fuses_query(const RetrieveArgs& a) {
+  if (!a.qa || !a.qw || !a.qaux || a.n <= 0 || !soft_read_fits(a)) return false;
+  int nwv = 0, blocks = 0, per = 0;
+  soft_read_shape(a, nwv, blocks, per);
+  return nwv == SOFT_WAVES_FEW && per == 1 && a.dk <= 32 && a.qk > 0 && a.qk % 128 == 0 &&
+         a.ld_qa % 8 == 0 && ((uintptr_t)a.qa & 15) == 0 && ((uintptr_t)a.qw & 15) == 0 &&
+         soft_read_lds(a.dk, a.capacity, 1, nwv) + soft_qp_lds(a.qk, nwv) <= 160 * 1024;
+}
+
 Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
   if (a.n <= 0) return Status::Ok();
+  if ((a.qa || a.qw || a.qaux) && !retrieve_fuses_query(a))
+    return Status::Invalid("retrieve: fused query product outside the few-query soft read");
   if (a.dk <= 0 || a.capacity <= 0 || a.count < 0 || a.count > a.capacity)
     return Status::Invalid("retrieve: bad bank shape");
   if (a.top_k < 0 || a.top_k > kMaxTopK) return Status::Invalid("retrieve: top_k must be in 0..=64");
   if (a.top_k == 0 && !a.weights && !a.weights16 && !a.out_val) return Status::Invalid("retrieve: no output");
   if (soft_read_fits(a)) {
-    // Few queries (a decode step): small workgroups spread them over more
-    // CUs, each staging the bank for fewer waves.
-    const int nwv = a.n <= SOFT_FEW_QUERIES ? SOFT_WAVES_FEW : SOFT_WAVES;
-    int blocks = (a.n + nwv - 1) / nwv;
-    if (blocks > 512) blocks = 512;
-    const int per = (a.n + blocks * nwv - 1) / (blocks * nwv);
+    int nwv = 0, blocks = 0, per = 0;
+    soft_read_shape(a, nwv, blocks, per);
     const int qg = per >= SOFT_QG && nwv == SOFT_WAVES ? SOFT_QG : 1;
-    const size_t lds = soft_read_lds(a.dk, a.capacity, qg, nwv);
+    const bool qp = a.qw != nullptr;  // retrieve_fuses_query held above
+    const size_t lds = soft_read_lds(a.dk, a.capacity, qg, nwv) + (qp ? soft_qp_lds(a.qk, nwv) : 0);
     if (lds > 64 * 1024) PSSA_RETURN_IF(allow_large_lds());
     const int spl = soft_spl(a.capacity);
+    if (qp) {
+#define PSSA_SOFT_QP_CASE(SPL)                                                                  \
+  if (spl == SPL) {                                                                             \
+    if (a.hgate)                                                                                \
+      soft_read_kernel<1, SPL, true, SOFT_WAVES_FEW, true><<<blocks, 64 * SOFT_WAVES_FEW, lds, stream>>>(a);  \
+    else                                                                                        \
+      soft_read_kernel<1, SPL, false, SOFT_WAVES_FEW, true><<<blocks, 64 * SOFT_WAVES_FEW, lds, stream>>>(a); \
+    PSSA_LAUNCH_CHECK("soft_read");                                                             \
+    return Status::Ok();                                                                        \
+  }
+      PSSA_SOFT_QP_CASE(1) PSSA_SOFT_QP_CASE(2) PSSA_SOFT_QP_CASE(4) PSSA_SOFT_QP_CASE(8)
+#undef PSSA_SOFT_QP_CASE
+      return Status::Invalid("retrieve: soft read shape");
+    }
 #define PSSA_SOFT_CASE(QG, SPL, NWV)                                                    \
   if (qg == QG && spl == SPL && nwv == NWV) {                                           \
     if (a.hgate)                                                                        \

@@ -446,24 +446,6 @@ class PrefillView {
       sa.ld_y16 = d;
     }
     PSSA_RETURN_IF(launch_ssm_scan(st, sa));
-    // q_euc = y W_qh^T + q_x.  In a bf16 model y enters the product rounded
-    // to bf16: the single-step scan writes that copy itself, otherwise the
-    // product rounds the fp32 readout as it loads it.
-    PSSA_RETURN_IF(tm_.mark(ST_GEMM_QH));
-    EpiParams e_q;
-    e_q.kind = EPI_ADD_AUX;
-    e_q.aux = P_ + o_qx;
-    e_q.ld_aux = n_in;
-    e_q.out32 = Q_;
-    e_q.ld32 = k;
-    if (bf16 && !step_y && d % 16 == 0)
-      PSSA_RETURN_IF(launch_gemm_f32a(st, Y_, d, static_cast<const uint16_t*>(B.w_qh.p), d, m, k, d, e_q));
-    else {
-      if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y_, d, static_cast<uint16_t*>(Yh_), d, rows, d));
-      PSSA_RETURN_IF(launch_gemm(st, dt, Yh_, d, B.w_qh.p, d, m, k, d, e_q));
-    }
-
-    PSSA_RETURN_IF(tm_.mark(ST_RETRIEVE));
     RetrieveArgs ra;
     ra.q = Q_;
     ra.ld_q = k;
@@ -489,6 +471,42 @@ class PrefillView {
       ra.weights16 = static_cast<uint16_t*>(Wm_);
     else
       ra.weights = static_cast<float*>(Wm_);
+    // In a bf16 decode step the soft read forms q itself from y's bf16 copy
+    // (the same products and sum as the GEMM below, one launch fewer).
+    bool fused_q = false;
+    if (bf16 && step_y) {
+      ra.qa = static_cast<const uint16_t*>(Yh_);
+      ra.ld_qa = d;
+      ra.qw = static_cast<const uint16_t*>(B.w_qh.p);
+      ra.qk = d;
+      ra.qaux = P_ + o_qx;
+      ra.ld_qaux = n_in;
+      fused_q = retrieve_fuses_query(ra);
+      if (!fused_q) {
+        ra.qa = nullptr;
+        ra.qw = nullptr;
+        ra.qaux = nullptr;
+      }
+    }
+    PSSA_RETURN_IF(tm_.mark(ST_GEMM_QH));
+    // q_euc = y W_qh^T + q_x.  In a bf16 model y enters the product rounded
+    // to bf16: the single-step scan writes that copy itself, otherwise the
+    // product rounds the fp32 readout as it loads it.
+    if (!fused_q) {
+      EpiParams e_q;
+      e_q.kind = EPI_ADD_AUX;
+      e_q.aux = P_ + o_qx;
+      e_q.ld_aux = n_in;
+      e_q.out32 = Q_;
+      e_q.ld32 = k;
+      if (bf16 && !step_y && d % 16 == 0)
+        PSSA_RETURN_IF(launch_gemm_f32a(st, Y_, d, static_cast<const uint16_t*>(B.w_qh.p), d, m, k, d, e_q));
+      else {
+        if (bf16 && !step_y) PSSA_RETURN_IF(launch_to_bf16(st, Y_, d, static_cast<uint16_t*>(Yh_), d, rows, d));
+        PSSA_RETURN_IF(launch_gemm(st, dt, Yh_, d, B.w_qh.p, d, m, k, d, e_q));
+      }
+    }
+    PSSA_RETURN_IF(tm_.mark(ST_RETRIEVE));
     PSSA_RETURN_IF(launch_retrieve(st, ra));
 
     // m_val = weights values (soft read readout).

@@ -140,6 +140,36 @@ def test_scan_variants_keep_token_loop_identity(hip):
     b.close()
 
 
+@pytest.mark.parametrize("hybrid", [False, True])
+def test_bf16_token_loop_equals_prefill_with_fused_query(hip, hybrid):
+    """bf16 weights at d_latent 256 and d_mem_key 32: a single-token step
+    forms the memory query inside the soft read (no separate query product),
+    a prefill runs the product as a GEMM; both give the same logits and
+    carries bit for bit (src/inference.rs:1069-1113).  Five lanes leave the
+    second four-query workgroup with three rows past the batch, which load
+    a clamped row and are discarded."""
+    say("bf16 token loop == prefill, fused query", hybrid)
+    cfg = PSSAConfig(depth=2, d_vocab=61, d_latent=256, d_state=32, d_mem_key=32, mem_capacity=64)
+    w = ModelWeights.init(cfg, 11, "baseline")
+    w.populate_banks(12, count=50)
+    if hybrid:
+        rng = np.random.default_rng(13)
+        for b in w.blocks:
+            b.mem_hybrid_gate[:50] = rng.uniform(0.05, 1.0, 50).astype(np.float32)
+            b.mem_hybrid_age[:50] = rng.integers(0, 60, 50).astype(np.uint64)
+        w.set_hybrid_read(True, 0.9)
+    ids = np.random.default_rng(14).integers(0, cfg.d_vocab, (5, 9), dtype=np.uint32)
+    a = PSSALayer(hip, w, lanes=5, max_tokens=5 * 9, weight_dtype="bf16")
+    b = PSSALayer(hip, w, lanes=5, max_tokens=5 * 9, weight_dtype="bf16")
+    la = a.prefill_inference(ids)
+    for t in range(ids.shape[1]):
+        lb = b.forward_inference(ids[:, t])
+    np.testing.assert_array_equal(la, lb)
+    np.testing.assert_array_equal(a.get_carry(), b.get_carry())
+    a.close()
+    b.close()
+
+
 def test_shape_errors_fail_before_anything_runs(hip):
     say("prefill shape errors")
     cfg = PSSAConfig(depth=1, d_vocab=10, d_latent=16, d_state=4, d_mem_key=4, mem_capacity=4)

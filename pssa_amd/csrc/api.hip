@@ -76,18 +76,12 @@ Status check_config(const pssa_hip_config& c) {
 float softplus_host(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
 // Carries are [lanes, depth, d, s] at the ABI (h_persistent, src/pssa.rs) and
-// [lanes, depth, s, d] on the device (the scan's coalesced layout).
+// [lanes, depth] matrices in the scan's channel-blocked layout on the device
+// (pssa::carry_at).
 Status carry_layout(pssa_hip_lanes* L, const float* in, float* out, bool to_device) {
   const pssa_hip_config& c = L->model->cfg;
-  const int d = (int)c.d_latent, s = (int)c.d_state;
-  const size_t mats = L->lanes * c.depth * L->loops;
-  for (size_t m0 = 0; m0 < mats; m0 += 65535) {
-    const size_t cnt = std::min<size_t>(65535, mats - m0);
-    const size_t off = m0 * (size_t)d * s;
-    PSSA_RETURN_IF(pssa::launch_transpose(L->ctx->stream, in + off, out + off, cnt, to_device ? d : s,
-                                          to_device ? s : d, 1.0f));
-  }
-  return Status::Ok();
+  return pssa::launch_carry_convert(L->ctx->stream, in, out, L->lanes * c.depth * L->loops, (int)c.d_latent,
+                                    (int)c.d_state, to_device);
 }
 
 // Clamps every slot of a block's bank values to `cap` (set_value_cap,
@@ -501,13 +495,14 @@ static Status run_stage_ssm(pssa_hip_ctx* ctx, const float* delta, const float* 
   PSSA_RETURN_IF(upload(dc, c_proj, ls * 4, st));
   PSSA_RETURN_IF(upload(t.carry_ds, initial, w * 4, st));
   PSSA_RETURN_IF(t.y.alloc(ld * 4));
-  // The scan keeps states and rates state-major ([s, d]); the stage API
-  // speaks the reference's [d, s].
+  // The scan keeps rates state-major ([s, d]) and states channel-blocked
+  // (pssa::carry_at); the stage API speaks the reference's [d, s].
   PSSA_RETURN_IF(dr2.alloc(w * 4));
   PSSA_RETURN_IF(t.carry.alloc(w * 4));
   PSSA_RETURN_IF(pssa::launch_transpose(st, dr.as<float>(), dr2.as<float>(), 1, (int)d_m, (int)d_s,
                                         1.4426950408889634f));
-  PSSA_RETURN_IF(pssa::launch_transpose(st, t.carry_ds.as<float>(), t.carry.as<float>(), 1, (int)d_m, (int)d_s, 1.0f));
+  PSSA_RETURN_IF(pssa::launch_carry_convert(st, t.carry_ds.as<float>(), t.carry.as<float>(), 1, (int)d_m, (int)d_s,
+                                            true));
   PSSA_RETURN_IF(pssa::launch_fill_zero(st, t.y.as<float>(), ld));
   pssa::SsmArgs a;
   a.delta = dd.as<float>();
@@ -553,7 +548,8 @@ static Status download_ssm(pssa_hip_ctx* ctx, SsmTape& t, float* bar_a, float* b
   const size_t ld = t.L * t.d, w = t.d * t.s;
   if (y_ssm) PSSA_RETURN_IF(download(y_ssm, t.y, ld * 4, st));
   if (final_state) {
-    PSSA_RETURN_IF(pssa::launch_transpose(st, t.carry.as<float>(), t.carry_ds.as<float>(), 1, (int)t.s, (int)t.d, 1.0f));
+    PSSA_RETURN_IF(pssa::launch_carry_convert(st, t.carry.as<float>(), t.carry_ds.as<float>(), 1, (int)t.d, (int)t.s,
+                                              false));
     PSSA_RETURN_IF(download(final_state, t.carry_ds, w * 4, st));
   }
   if (bar_a) PSSA_RETURN_IF(download(bar_a, t.bar_a, t.L * w * 4, st));

@@ -113,7 +113,7 @@ struct pssa_hip_lanes {
   // and the per-lane probability scratch [lanes, V]; the captured step
   // records the settings it was built with.
   // Recurrent depth loops (set_loops, src/pssa.rs:2171-2184): passes per
-  // block and token, each with its own carry ([lanes, depth, loops, s, d]);
+  // block and token, each with its own carry ([lanes, depth, loops] matrices of d*s);
   // Xin keeps a looped layer's input rows.
   size_t loops = 1;
   pssa::DevBuf Xin;

@@ -4,6 +4,14 @@
 
 namespace pssa {
 
+// Position of state j of channel i in one lane's carry: channel blocks of
+// 64 (the last one d % 64 wide), each state-major, so the 64 channels x all
+// states a step workgroup updates are one contiguous run.
+__host__ __device__ __forceinline__ size_t carry_at(int j, int i, int d, int s) {
+  const int i0 = i & ~63, w = d - i0 < 64 ? d - i0 : 64;
+  return (size_t)i0 * s + (size_t)j * w + (i - i0);
+}
+
 struct SsmArgs {
   const float* delta = nullptr;  // softplus'd step sizes, row r at delta + r*ld_delta
   int ld_delta = 0;
@@ -13,10 +21,10 @@ struct SsmArgs {
   int ld_c = 0;
   const float* xn = nullptr;     // normalised input x_t, [rows, d]
   int ld_x = 0;
-  // State-major layouts [s, d] (channel contiguous), so that the 64
-  // channels of a wave read and write 256 contiguous bytes per state.
+  // State-major layouts (channel contiguous), so that the 64 channels of a
+  // wave read and write 256 contiguous bytes per state.
   const float* rates2 = nullptr; // -softplus(a_raw) * log2(e), [s, d]
-  float* carry = nullptr;        // h, lane b at carry + b*carry_stride, [s, d]; read, then overwritten
+  float* carry = nullptr;        // h, lane b at carry + b*carry_stride, channel-blocked (carry_at); read, then overwritten
   long carry_stride = 0;
   float* y = nullptr;            // readout, [rows, d]
   int ld_y = 0;
@@ -58,6 +66,10 @@ Status launch_scale(hipStream_t stream, const float* in, float* out, size_t n, f
 
 // out[c, r] = in[r, c] for `count` consecutive [rows, cols] matrices (the
 // reference's [d, s] state layout <-> the scan's [s, d]), scaled by `scale`.
+// Carries of `count` matrices between the reference's [d, s] layout
+// (to_device) and the device's channel-blocked one (carry_at), or back.
+Status launch_carry_convert(hipStream_t stream, const float* in, float* out, size_t count, int d, int s,
+                            bool to_device);
 Status launch_transpose(hipStream_t stream, const float* in, float* out, size_t count, int rows,
                         int cols, float scale);
 

@@ -52,11 +52,11 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[(size_t)j * d + i] : 0.0f;
+    h[q] = ok ? carry[carry_at(j, i, d, s)] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
   if (MAT && blockIdx.z == 0 && wave == 0 && ivalid)
-    for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[(size_t)j * d + i];
+    for (int j = 0; j < s; ++j) a.states[(size_t)b * (T + 1) * ds + (size_t)i * s + j] = carry[carry_at(j, i, d, s)];
 
   for (int t0 = 0; t0 < T; t0 += MAT_TC) {
     for (int e = tid; e < MAT_TC * 64; e += 256) {
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[(size_t)j * d + i] = h[q];
+    if (ivalid && j < s) carry[carry_at(j, i, d, s)] = h[q];
   }
 }
 
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
 #pragma unroll
     for (int q = 0; q < J; ++q) {
       const int j = jw + q;
-      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[(size_t)j * d + i]) : 0.0f;
+      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[carry_at(j, i, d, s)]) : 0.0f;
     }
   };
   float r2[J];
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
         const float ab = __builtin_amdgcn_exp2f(L.dl * r2[q]);
         const float hv = fmaf(ab, L.h[q], L.u * bq);
         yp4[qq & 3] = fmaf(hv, cq, yp4[qq & 3]);
-        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[(size_t)j * d + i]);
+        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[carry_at(j, i, d, s)]);
       }
       sY[l][wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[(size_t)j * d + i] : 0.0f;
+    h[q] = ok ? carry[carry_at(j, i, d, s)] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
 
@@ -414,7 +414,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[(size_t)j * d + i] = h[q];
+    if (ivalid && j < s) carry[carry_at(j, i, d, s)] = h[q];
   }
 }
 
@@ -542,6 +542,47 @@ Status launch_transpose(hipStream_t stream, const float* in, float* out, size_t 
   dim3 grid((cols + 31) / 32, (rows + 31) / 32, (unsigned)count), block(32, 8);
   transpose_kernel<<<grid, block, 0, stream>>>(in, out, rows, cols, scale);
   PSSA_LAUNCH_CHECK("transpose");
+  return Status::Ok();
+}
+
+// Carries between the reference's [d, s] per matrix and the device's
+// channel-blocked layout (carry_at): one 64-channel x 64-state tile per
+// workgroup through LDS, so both sides move contiguous runs.
+__global__ __launch_bounds__(256) void carry_convert_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                            int d, int s, int to_device) {
+  __shared__ float tile[64][65];
+  const size_t m = blockIdx.z, ds = (size_t)d * s;
+  const float* src = in + m * ds;
+  float* dst = out + m * ds;
+  const int i0 = blockIdx.x * 64, j0 = blockIdx.y * 64;
+  const int w = min(64, d - i0), hs = min(64, s - j0);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if (to_device) {
+    for (int r = ty; r < w; r += 4)
+      if (tx < hs) tile[r][tx] = src[(size_t)(i0 + r) * s + j0 + tx];
+    __syncthreads();
+    float* blk = dst + (size_t)i0 * s;  // the channel block's run: state j at + j * w
+    for (int r = ty; r < hs; r += 4)
+      if (tx < w) blk[(size_t)(j0 + r) * w + tx] = tile[tx][r];
+  } else {
+    const float* sb = src + (size_t)i0 * s;
+    for (int r = ty; r < hs; r += 4)
+      if (tx < w) tile[tx][r] = sb[(size_t)(j0 + r) * w + tx];
+    __syncthreads();
+    for (int r = ty; r < w; r += 4)
+      if (tx < hs) dst[(size_t)(i0 + r) * s + j0 + tx] = tile[r][tx];
+  }
+}
+
+Status launch_carry_convert(hipStream_t stream, const float* in, float* out, size_t count, int d, int s,
+                            bool to_device) {
+  if (!count || d <= 0 || s <= 0) return Status::Ok();
+  for (size_t m0 = 0; m0 < count; m0 += 65535) {
+    const size_t cnt = count - m0 < 65535 ? count - m0 : 65535, off = m0 * (size_t)d * s;
+    dim3 grid((d + 63) / 64, (s + 63) / 64, (unsigned)cnt);
+    carry_convert_kernel<<<grid, 256, 0, stream>>>(in + off, out + off, d, s, to_device ? 1 : 0);
+    PSSA_LAUNCH_CHECK("carry_convert");
+  }
   return Status::Ok();
 }
 

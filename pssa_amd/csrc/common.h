@@ -134,6 +134,51 @@ __device__ __forceinline__ uint32_t bf16x2_bits(float lo, float hi) {
 }
 __device__ __forceinline__ uint16_t bf16_bits_dev(float f) { return (uint16_t)bf16x2_bits(f, 0.0f); }
 
+// RMSNorm of one row by one wave (src/pssa.rs:1080-1086).  Lane L holds
+// x[4L + 256k .. +3] for k < RMS_V4 (zero past d; d % 4 == 0, rows 16-byte
+// aligned); the squares are summed per lane in (k, component) order, then
+// across the wave by the xor butterfly.  Every kernel that normalises rows
+// (the standalone norm and the decode input product) goes through these two
+// functions, so they agree bit for bit.
+constexpr int RMS_V4 = 4;  // float4s per lane: rows of up to 1024 columns
+__device__ __forceinline__ void rms_load_v4(const float* x, int d, int lane, float4 (&xv)[RMS_V4]) {
+#pragma unroll
+  for (int k = 0; k < RMS_V4; ++k) {
+    const int i = 4 * lane + 256 * k;
+    xv[k] = i < d ? *reinterpret_cast<const float4*>(x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+// 1 / sqrt(mean square + 1e-5) of each of R rows a wave holds (rms_load_v4):
+// per row the same chain, the rows' butterfly steps interleaved so their
+// cross-lane exchanges are in flight together.
+template <int R>
+__device__ __forceinline__ void rms_inv_v4(const float4 (&xv)[R][RMS_V4], int d, float (&inv)[R]) {
+  float ss[R];
+#pragma unroll
+  for (int q = 0; q < R; ++q) {
+    ss[q] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RMS_V4; ++k) {
+      ss[q] = fmaf(xv[q][k].x, xv[q][k].x, ss[q]);
+      ss[q] = fmaf(xv[q][k].y, xv[q][k].y, ss[q]);
+      ss[q] = fmaf(xv[q][k].z, xv[q][k].z, ss[q]);
+      ss[q] = fmaf(xv[q][k].w, xv[q][k].w, ss[q]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    float o[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) o[q] = __shfl_xor(ss[q], off, 64);
+#pragma unroll
+    for (int q = 0; q < R; ++q) ss[q] += o[q];
+  }
+#pragma unroll
+  for (int q = 0; q < R; ++q) inv[q] = 1.0f / sqrtf(ss[q] / (float)d + 1e-5f);
+}
+// gamma * (x * inv) + beta, the multiply-add rounded once.
+__device__ __forceinline__ float rms_apply(float x, float inv, float g, float b) { return fmaf(g, x * inv, b); }
+
 // s_waitcnt immediate for vmcnt(v) alone (gfx9: vmcnt bits [3:0] and [15:14],
 // expcnt and lgkmcnt left at their no-wait maxima).
 constexpr int vmcnt_only(int v) { return (v & 0xF) | (((v >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }

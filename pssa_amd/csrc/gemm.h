@@ -63,6 +63,14 @@ Status launch_gemm_f32a(hipStream_t stream, const float* A, int lda, const uint1
 Status launch_to_bf16(hipStream_t stream, const float* in, int ld_in, uint16_t* out, int ld_out,
                       size_t rows, int cols);
 
+// The input projection with the block's RMSNorm folded in (decode steps):
+// XN[m] = rmsnorm(X[m]; gamma, beta) (fp32, as the standalone norm writes it)
+// and out = bf16(XN) B^T with ep's column-segment epilogue, bit for bit the
+// norm followed by launch_gemm.  Needs gemm_norm_fits(d), K = d, bf16 B.
+bool gemm_norm_fits(int d);
+Status launch_gemm_norm(hipStream_t stream, const float* X, const float* gamma, const float* beta, float* XN,
+                        const uint16_t* B, int ldb, int M, int N, int d, const EpiParams& ep);
+
 // Per-device set-up of the GEMM kernels (their dynamic LDS limits).
 Status init_gemm_attributes();
 

@@ -1026,6 +1026,146 @@ static Status check_epilogue(const EpiParams& ep, bool bf16, int& vec_epi) {
   return Status::Ok();
 }
 
+// ---------------------------------------------------------------------------
+// The decode step's input product with the block's RMSNorm folded in: a
+// workgroup of four waves owns 32 token rows x 128 weight rows.  Each wave
+// normalises 8 of the rows (rms_inv_v4 / rms_apply, the standalone norm's
+// arithmetic), writes their bf16 values into an LDS panel of the 32 whole
+// rows (chunk c of row r at c ^ (r & 15), conflict-free fragment reads) and,
+// in the first column tile, the fp32 rows to XN for the scan; the weight
+// slabs stream through the few-row kernel's direct-to-LDS ring meanwhile.
+// Each wave then runs one 32 x 32 tile's K chain (the tiled kernels' MFMA
+// order), so the result equals rmsnorm followed by the product bit for bit.
+// d % 128 == 0, d <= 256 * RMS_V4.
+constexpr int NORM_BN = 128;
+size_t gemm_norm_bytes(int d) { return (size_t)FEW_S * NORM_BN * 128 + (size_t)32 * d * 2; }
+
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_norm_kernel(const float* __restrict__ X, int d,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, float* __restrict__ XN,
+                                                        const uint16_t* __restrict__ B, int ldb, int M, int N,
+                                                        int vec_epi, EpiParams ep) {
+  constexpr int NWV = 4, S = FEW_S, SLAB = NORM_BN * 64, BPW = NORM_BN / 8 / NWV;
+  static_assert(S >= 2 && (S - 2) * BPW <= 63, "vmcnt holds at most 63");
+  extern __shared__ __attribute__((aligned(1024))) uint16_t gemm_norm_smem[];
+  uint16_t* panel = gemm_norm_smem + S * SLAB;  // [32][d] bf16, swizzled
+
+  const int tilesM = (M + 31) / 32, tilesN = (N + NORM_BN - 1) / NORM_BN;
+  int mt, nt;
+  tile_coords(xcd_tile(blockIdx.x, tilesM * tilesN), tilesM, tilesN, mt, nt);
+  const int m0 = mt * 32, n0 = nt * NORM_BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+
+  const uint16_t* src[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int row = (wave + NWV * i) * 8 + (lane >> 3);
+    src[i] = B + (size_t)min(n0 + row, N - 1) * ldb + ((lane & 7) ^ ((row >> 1) & 7)) * 8;
+  }
+  const int nk = d / 64;
+  auto issue = [&](int kt) {
+    const int k0 = min(kt, nk - 1) * 64;
+    uint16_t* dst = gemm_norm_smem + (kt % S) * SLAB + wave * 8 * 64;
+#pragma unroll
+    for (int i = 0; i < BPW; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+                                       (__attribute__((address_space(3))) void*)(dst + NWV * i * 8 * 64), 16,
+                                       0, 0);
+  };
+#pragma unroll
+  for (int kt = 0; kt < S - 1; ++kt) issue(kt);
+
+  // The normalised rows: wave w takes tile rows 8w .. 8w + 7.
+  float4 g[RMS_V4], bt[RMS_V4];
+#pragma unroll
+  for (int k = 0; k < RMS_V4; ++k) {
+    const int i = 4 * lane + 256 * k;
+    g[k] = i < d ? *reinterpret_cast<const float4*>(gamma + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    bt[k] = i < d ? *reinterpret_cast<const float4*>(beta + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // All eight rows' loads are in flight together (one round trip); the
+  // workgroup's LDS holds one workgroup per CU, so the registers are there.
+  {
+    constexpr int r0 = 0;
+    float4 xv[8][RMS_V4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      rms_load_v4(X + (size_t)min(m0 + wave * 8 + r0 + q, M - 1) * d, d, lane, xv[q]);
+    float inv8[8];
+    rms_inv_v4<8>(xv, d, inv8);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int r = wave * 8 + r0 + q;
+      const float inv = inv8[q];
+#pragma unroll
+      for (int k = 0; k < RMS_V4; ++k) {
+        const int i = 4 * lane + 256 * k;
+        if (i < d) {
+          const float4 x4 = xv[q][k];
+          const float4 v =
+              make_float4(rms_apply(x4.x, inv, g[k].x, bt[k].x), rms_apply(x4.y, inv, g[k].y, bt[k].y),
+                          rms_apply(x4.z, inv, g[k].z, bt[k].z), rms_apply(x4.w, inv, g[k].w, bt[k].w));
+          if (nt == 0 && m0 + r < M) *reinterpret_cast<float4*>(XN + (size_t)(m0 + r) * d + i) = v;
+          const int c = i >> 3;
+          *reinterpret_cast<uint2*>(panel + (size_t)r * d + (c ^ (r & 15)) * 8 + (i & 4)) =
+              make_uint2(bf16x2_bits(v.x, v.y), bf16x2_bits(v.z, v.w));
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x16_t acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+  const uint16_t* prow = panel + (size_t)l32 * d;
+  const int sp = l32 & 15, rb = wave * 32 + l32, sb = (rb >> 1) & 7;
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
+    __builtin_amdgcn_s_barrier();
+    issue(kt + S - 1);
+    const uint16_t* sl = gemm_norm_smem + (kt % S) * SLAB;
+    bf16x8_t fa[4], fb[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int c = 2 * kk + half;
+      fa[kk] = *reinterpret_cast<const bf16x8_t*>(prow + ((kt * 8 + c) ^ sp) * 8);
+      fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the reloads past the end
+  epilogue_32x32<uint16_t, KIND>(ep, acc, m0 + l32, n0 + wave * 32, M, N, vec_epi, half, l32);
+}
+
+bool gemm_norm_fits(int d) { return d > 0 && d % 128 == 0 && d <= 256 * RMS_V4; }
+
+Status launch_gemm_norm(hipStream_t stream, const float* X, const float* gamma, const float* beta, float* XN,
+                        const uint16_t* B, int ldb, int M, int N, int d, const EpiParams& ep) {
+  if (M <= 0 || N <= 0) return Status::Invalid("gemm: dimensions must be positive");
+  if (!gemm_norm_fits(d)) return Status::Invalid("gemm: the folded norm needs d % 128 == 0 and d <= 1024");
+  if (ep.kind != EPI_SEGMENTS && ep.kind != EPI_SEGMENTS_TAP)
+    return Status::Invalid("gemm: the folded norm serves the input projection");
+  if (ldb % 8 != 0 || !al16(B) || !al16(X) || !al16(XN) || !al16(gamma) || !al16(beta))
+    return Status::Invalid("gemm: the folded norm needs 16-byte aligned rows");
+  int vec_epi = 0;
+  PSSA_RETURN_IF(check_epilogue(ep, true, vec_epi));
+  const long tiles = (long)((M + 31) / 32) * ((N + NORM_BN - 1) / NORM_BN);
+  if (tiles > 0x7fffffffL) return Status::Invalid("gemm: too many tiles");
+  if (ep.kind == EPI_SEGMENTS)
+    gemm_norm_kernel<EPI_SEGMENTS><<<(unsigned)tiles, 256, gemm_norm_bytes(d), stream>>>(
+        X, d, gamma, beta, XN, B, ldb, M, N, vec_epi, ep);
+  else
+    gemm_norm_kernel<EPI_SEGMENTS_TAP><<<(unsigned)tiles, 256, gemm_norm_bytes(d), stream>>>(
+        X, d, gamma, beta, XN, B, ldb, M, N, vec_epi, ep);
+  PSSA_LAUNCH_CHECK("gemm_norm");
+  return Status::Ok();
+}
+
 Status launch_gemm_f32a(hipStream_t stream, const float* A, int lda, const uint16_t* B, int ldb, int M,
                         int N, int K, const EpiParams& ep) {
   if (M <= 0 || N <= 0 || K <= 0) return Status::Invalid("gemm: dimensions must be positive");
@@ -1150,6 +1290,10 @@ Status init_gemm_attributes() {
   };
   for (const void* f : few)
     PSSA_HIP_TRY(hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_few_bytes()));
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_norm_kernel<EPI_SEGMENTS>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_norm_bytes(256 * RMS_V4)));
+  PSSA_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_norm_kernel<EPI_SEGMENTS_TAP>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_norm_bytes(256 * RMS_V4)));
   return Status::Ok();
 }
 

@@ -55,6 +55,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   if (Z)
     for (int i = lane; i < d; i += 64) Z[r * d + i] = 0.0f;
   const float* x = X + r * d;
+  if (d % 4 == 0 && d <= 256 * RMS_V4) {  // 16-byte pieces, the decode input product's order
+    float4 xv[1][RMS_V4];
+    rms_load_v4(x, d, lane, xv[0]);
+    float inv1[1];
+    rms_inv_v4<1>(xv, d, inv1);
+    const float inv = inv1[0];
+#pragma unroll
+    for (int k = 0; k < RMS_V4; ++k) {
+      const int i = 4 * lane + 256 * k;
+      if (i < d) {
+        const float4 g = *reinterpret_cast<const float4*>(gamma + i);
+        const float4 b = *reinterpret_cast<const float4*>(beta + i);
+        const float4 x4 = xv[0][k];
+        const float4 v = make_float4(rms_apply(x4.x, inv, g.x, b.x), rms_apply(x4.y, inv, g.y, b.y),
+                                     rms_apply(x4.z, inv, g.z, b.z), rms_apply(x4.w, inv, g.w, b.w));
+        *reinterpret_cast<float4*>(XN + r * d + i) = v;
+        if (XNh)
+          *reinterpret_cast<uint2*>(XNh + r * d + i) = make_uint2(bf16x2_bits(v.x, v.y), bf16x2_bits(v.z, v.w));
+      }
+    }
+    return;
+  }
   if (d <= 64 * RMS_REG) {  // the row stays in registers; all loads issue at once
     float xv[RMS_REG];
     float ss = 0.0f;
@@ -72,7 +94,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     for (int k = 0; k < RMS_REG; ++k) {
       const int i = lane + 64 * k;
       if (i < d) {
-        const float v = gamma[i] * (xv[k] * inv) + beta[i];
+        const float v = rms_apply(xv[k], inv, gamma[i], beta[i]);
         XN[r * d + i] = v;
         if (XNh) XNh[r * d + i] = bf16_of(v);
       }
@@ -85,7 +107,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
   const float inv = 1.0f / sqrtf(ss / (float)d + 1e-5f);
   for (int i = lane; i < d; i += 64) {
-    const float v = gamma[i] * (x[i] * inv) + beta[i];
+    const float v = rms_apply(x[i], inv, gamma[i], beta[i]);
     XN[r * d + i] = v;
     if (XNh) XNh[r * d + i] = bf16_of(v);
   }
@@ -390,11 +412,15 @@ class PrefillView {
     // Column offsets inside the fused projection output P.
     const int o_b = d, o_c = d + s, o_qx = d + 2 * s, o_gate = d + 2 * s + k, o_act = 2 * d + 2 * s + k;
     const bool step_y = ssm_step_writes_y((int)T, s);
+    // In a bf16 decode step the input product normalises its rows itself.
+    const bool fold_norm = bf16 && step_y && gemm_norm_fits(d);
     PSSA_RETURN_IF(tm_.mark(ST_NORM));
-    rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
-        X_, B.gamma.as<float>(), B.beta.as<float>(), XN_, XNh16_,
-        ssm_needs_zeroed_y(s) && !step_y ? Y_ : nullptr, d, rows);
-    PSSA_LAUNCH_CHECK("rmsnorm");
+    if (!fold_norm) {
+      rmsnorm_kernel<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(
+          X_, B.gamma.as<float>(), B.beta.as<float>(), XN_, XNh16_,
+          ssm_needs_zeroed_y(s) && !step_y ? Y_ : nullptr, d, rows);
+      PSSA_LAUNCH_CHECK("rmsnorm");
+    }
 
     // [delta | B | C | q_x | gate | adapter act] = x W_in^T with softplus,
     // sigmoid and SiLU applied per column segment.
@@ -412,7 +438,11 @@ class PrefillView {
       e_in.tap = L_->tap_act.as<float>() + l * rows * r;
       e_in.ld_tap = r;
     }
-    PSSA_RETURN_IF(launch_gemm(st, dt, XNh_, d, B.w_in.p, d, m, n_in, d, e_in));
+    if (fold_norm)
+      PSSA_RETURN_IF(launch_gemm_norm(st, X_, B.gamma.as<float>(), B.beta.as<float>(), XN_,
+                                      static_cast<const uint16_t*>(B.w_in.p), d, m, n_in, d, e_in));
+    else
+      PSSA_RETURN_IF(launch_gemm(st, dt, XNh_, d, B.w_in.p, d, m, n_in, d, e_in));
     if (l == 0 && first_in_done_) PSSA_HIP_TRY(hipEventRecord(first_in_done_, st));
     if (taps && B.hybrid) {  // the write gate of a gated protected insert
       gate_mean_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(P_ + o_gate, n_in, d, (int)rows,

@@ -1190,10 +1190,11 @@ Status launch_gemm(hipStream_t stream, int dtype, const void* A, int lda, const 
   const int vec_load = (K % ve == 0) && (lda % ve == 0) && (ldb % ve == 0) && al16(A) && al16(B);
   const bool vec_bf16 = bf16 && lda % 8 == 0 && ldb % 8 == 0 && al16(A) && al16(B);
   // Few token rows: the 128 x 256 tiling would leave most CUs idle.  One
-  // 32-row tile per wave, whatever the width: at 256 rows that gives
-  // (N/32) x 8 waves, about one per CU or more (measured 1% faster per decode
-  // step than two tiles per wave past 768 output columns).
-  if (vec_bf16 && K % 16 == 0 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
+  // 32-row tile per wave up to 4096 output columns: at 256 rows that gives
+  // (N/32) x 8 waves, about one per CU or more.  Wider products (a vocabulary
+  // head) keep the tiled kernel: 128 rows x 16384 columns took 93 us as 2048
+  // one-wave tiles, each re-reading the rows, and 15 us as 128 tiled ones.
+  if (vec_bf16 && K % 16 == 0 && N <= 4096 && (long)((M + 127) / 128) * ((N + 255) / 256) < 128) {
     const auto* a16 = static_cast<const uint16_t*>(A);
     const auto* b16 = static_cast<const uint16_t*>(B);
 #ifndef PSSA_FEW_OFF

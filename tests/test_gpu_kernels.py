@@ -51,11 +51,12 @@ def test_gemm_f32_few_rows_equal_tiled_rows_bitwise(hip, n):
 
 @pytest.mark.parametrize("n,k", [(768, 768), (1056, 768), (736, 800), (1024, 800)])
 def test_gemm_bf16_few_rows_equal_tiled_rows_bitwise(hip, n, k):
-    """bf16 weights: few token rows run one wave per 32 x 32 (or 64 x 32)
-    tile with 64-element LDS slabs (800 = 12.5 slabs: a partial last slab),
-    many rows the 128 x 128 direct-to-LDS tiles.  Both feed the same
-    fragments to the same MFMA sequence over K, so the rows agree bit for bit
-    (the prefill / decode identity of bf16 models rests on it)."""
+    """bf16 weights: few token rows run one wave per 32 x 32 tile, with
+    64-wide K slabs through an LDS ring when K % 64 == 0 (768) and through a
+    register ring otherwise (800: a partial last slab); many rows run the
+    128 x 128 direct-to-LDS tiles.  All feed the same fragments to the same
+    MFMA sequence over K, so the rows agree bit for bit (the prefill / decode
+    identity of bf16 models rests on it)."""
     say("gemm bf16 few rows == tiled", n, k)
     rng = np.random.default_rng(n + k)
     m = 16384

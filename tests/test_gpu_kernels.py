@@ -49,7 +49,7 @@ def test_gemm_f32_few_rows_equal_tiled_rows_bitwise(hip, n):
     assert rel_err(big[:64], O.gemm_xwt(x[:64], w)) < 1e-5
 
 
-@pytest.mark.parametrize("n,k", [(768, 768), (1056, 768), (736, 800), (1024, 800)])
+@pytest.mark.parametrize("n,k", [(768, 768), (1056, 768), (1000, 128), (736, 800), (1024, 800)])
 def test_gemm_bf16_few_rows_equal_tiled_rows_bitwise(hip, n, k):
     """bf16 weights: few token rows run one wave per 32 x 32 tile, with
     64-wide K slabs through an LDS ring when K % 64 == 0 (768) and through a

@@ -140,23 +140,25 @@ def test_scan_variants_keep_token_loop_identity(hip):
     b.close()
 
 
-@pytest.mark.parametrize("hybrid", [False, True])
-def test_bf16_token_loop_equals_prefill_with_fused_query(hip, hybrid):
+@pytest.mark.parametrize("hybrid,capacity", [(False, 64), (True, 64), (False, 200), (True, 512)])
+def test_bf16_token_loop_equals_prefill_with_fused_query(hip, hybrid, capacity):
     """bf16 weights at d_latent 256 and d_mem_key 32: a single-token step
     forms the memory query inside the soft read (no separate query product),
     a prefill runs the product as a GEMM; both give the same logits and
     carries bit for bit (src/inference.rs:1069-1113).  Five lanes leave the
     second four-query workgroup with three rows past the batch, which load
-    a clamped row and are discarded."""
-    say("bf16 token loop == prefill, fused query", hybrid)
-    cfg = PSSAConfig(depth=2, d_vocab=61, d_latent=256, d_state=32, d_mem_key=32, mem_capacity=64)
+    a clamped row and are discarded; bank capacities 64, 200 and 512 take
+    the soft read's 1, 4 and 8 slots per lane."""
+    say("bf16 token loop == prefill, fused query", hybrid, capacity)
+    cfg = PSSAConfig(depth=2, d_vocab=61, d_latent=256, d_state=32, d_mem_key=32, mem_capacity=capacity)
     w = ModelWeights.init(cfg, 11, "baseline")
-    w.populate_banks(12, count=50)
+    count = capacity * 3 // 4
+    w.populate_banks(12, count=count)
     if hybrid:
         rng = np.random.default_rng(13)
         for b in w.blocks:
-            b.mem_hybrid_gate[:50] = rng.uniform(0.05, 1.0, 50).astype(np.float32)
-            b.mem_hybrid_age[:50] = rng.integers(0, 60, 50).astype(np.uint64)
+            b.mem_hybrid_gate[:count] = rng.uniform(0.05, 1.0, count).astype(np.float32)
+            b.mem_hybrid_age[:count] = rng.integers(0, 60, count).astype(np.uint64)
         w.set_hybrid_read(True, 0.9)
     ids = np.random.default_rng(14).integers(0, cfg.d_vocab, (5, 9), dtype=np.uint32)
     a = PSSALayer(hip, w, lanes=5, max_tokens=5 * 9, weight_dtype="bf16")

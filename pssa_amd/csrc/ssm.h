@@ -12,6 +12,19 @@ __host__ __device__ __forceinline__ size_t carry_at(int j, int i, int d, int s) 
   return (size_t)i0 * s + (size_t)j * w + (i - i0);
 }
 
+// The states jw, jw + 1, ... of channel i in one lane's carry: state jw + q
+// at base + q * stride (one base and a uniform stride instead of a 64-bit
+// address per state, which the scan would otherwise keep live until its
+// final stores).
+struct CarryCol {
+  size_t base;
+  int stride;
+};
+__host__ __device__ __forceinline__ CarryCol carry_col(int jw, int i, int d, int s) {
+  const int i0 = i & ~63, w = d - i0 < 64 ? d - i0 : 64;
+  return CarryCol{(size_t)i0 * s + (size_t)jw * w + (i - i0), w};
+}
+
 struct SsmArgs {
   const float* delta = nullptr;  // softplus'd step sizes, row r at delta + r*ld_delta
   int ld_delta = 0;

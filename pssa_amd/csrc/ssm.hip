@@ -48,11 +48,12 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 
   float h[J], r2[J];
   float* carry = a.carry + (size_t)b * a.carry_stride;
+  const CarryCol cc = carry_col(jw, i, d, s);
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[carry_at(j, i, d, s)] : 0.0f;
+    h[q] = ok ? carry[cc.base + q * cc.stride] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
   if (MAT && blockIdx.z == 0 && wave == 0 && ivalid)
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(256) void ssm_materialize_kernel(SsmArgs a) {
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[carry_at(j, i, d, s)] = h[q];
+    if (ivalid && j < s) carry[cc.base + q * cc.stride] = h[q];
   }
 }
 
@@ -157,6 +158,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
   const bool ivalid = i < a.d;
   const int d = a.d, s = a.s;
   const int jb = jw + (lane & 31);
+  const CarryCol cc = carry_col(jw, i, d, s);
   // One lane's step inputs: the wave's B values (lanes 0..J-1) and C values
   // (lanes 32..32+J-1) in one load, broadcast with readlane; delta, the
   // input term u = delta * x and the J carries.
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
 #pragma unroll
     for (int q = 0; q < J; ++q) {
       const int j = jw + q;
-      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[carry_at(j, i, d, s)]) : 0.0f;
+      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[cc.base + q * cc.stride]) : 0.0f;
     }
   };
   float r2[J];
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
         const float ab = __builtin_amdgcn_exp2f(L.dl * r2[q]);
         const float hv = fmaf(ab, L.h[q], L.u * bq);
         yp4[qq & 3] = fmaf(hv, cq, yp4[qq & 3]);
-        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[carry_at(j, i, d, s)]);
+        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[cc.base + q * cc.stride]);
       }
       sY[l][wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }
@@ -285,11 +287,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 
   float h[J], r2[J];
   float* carry = a.carry + (size_t)b * a.carry_stride;
+  const CarryCol cc = carry_col(jw, i, d, s);
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
     const bool ok = ivalid && j < s;
-    h[q] = ok ? carry[carry_at(j, i, d, s)] : 0.0f;
+    h[q] = ok ? carry[cc.base + q * cc.stride] : 0.0f;
     r2[q] = ok ? a.rates2[(size_t)j * d + i] : 0.0f;
   }
 
@@ -414,7 +417,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
 #pragma unroll
   for (int q = 0; q < J; ++q) {
     const int j = jw + q;
-    if (ivalid && j < s) carry[carry_at(j, i, d, s)] = h[q];
+    if (ivalid && j < s) carry[cc.base + q * cc.stride] = h[q];
   }
 }
 

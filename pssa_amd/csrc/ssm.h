@@ -15,7 +15,9 @@ __host__ __device__ __forceinline__ size_t carry_at(int j, int i, int d, int s) 
 // The states jw, jw + 1, ... of channel i in one lane's carry: state jw + q
 // at base + q * stride (one base and a uniform stride instead of a 64-bit
 // address per state, which the scan would otherwise keep live until its
-// final stores).
+// final stores, spilling).  The decode step keeps carry_at: with this form
+// its code grew by a thousand moves and the carry update took 109 us
+// instead of 80.
 struct CarryCol {
   size_t base;
   int stride;

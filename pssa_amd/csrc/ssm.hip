@@ -158,7 +158,6 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
   const bool ivalid = i < a.d;
   const int d = a.d, s = a.s;
   const int jb = jw + (lane & 31);
-  const CarryCol cc = carry_col(jw, i, d, s);
   // One lane's step inputs: the wave's B values (lanes 0..J-1) and C values
   // (lanes 32..32+J-1) in one load, broadcast with readlane; delta, the
   // input term u = delta * x and the J carries.
@@ -176,7 +175,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
 #pragma unroll
     for (int q = 0; q < J; ++q) {
       const int j = jw + q;
-      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[cc.base + q * cc.stride]) : 0.0f;
+      L.h[q] = (ivalid && j < s) ? __builtin_nontemporal_load(&carry[carry_at(j, i, d, s)]) : 0.0f;
     }
   };
   float r2[J];
@@ -208,7 +207,7 @@ __global__ __launch_bounds__(NB * 256) void ssm_step_kernel(SsmArgs a) {
         const float ab = __builtin_amdgcn_exp2f(L.dl * r2[q]);
         const float hv = fmaf(ab, L.h[q], L.u * bq);
         yp4[qq & 3] = fmaf(hv, cq, yp4[qq & 3]);
-        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[cc.base + q * cc.stride]);
+        if (ivalid && j < s) __builtin_nontemporal_store(hv, &carry[carry_at(j, i, d, s)]);
       }
       sY[l][wave * NG + g][lane] = (yp4[0] + yp4[1]) + (yp4[2] + yp4[3]);
     }

@@ -336,7 +336,7 @@ __global__ void loop_combine_kernel(float* __restrict__ x, const float* __restri
 class PrefillView {
  public:
   PrefillView(pssa_hip_lanes* L, hipStream_t st, size_t lane0, size_t n_lanes, size_t T, bool taps, bool timing,
-              hipEvent_t first_in_done, float* y_part, const TrainRows* tr, bool concurrent)
+              hipEvent_t first_in_done, float* y_part, const TrainRows* tr, bool concurrent, size_t tap_rows = 0)
       : L_(L), M_(L->model), c_(L->model->cfg), st_(st), n_lanes_(n_lanes), T_(T), taps_(taps),
         first_in_done_(first_in_done), y_part_(y_part), tr_(tr), concurrent_(concurrent),
         tm_{timing ? L : nullptr, st} {
@@ -373,6 +373,8 @@ class PrefillView {
     carry_ = (tr ? tr->carry : L->carry.as<float>()) + lane0 * c_.depth * L->loops * (size_t)d * s_;
     logits_ = L->logits.as<float>() + lane0 * (size_t)V;
     row0_ = row0;
+    // Taps are [layer][all rows of the step]; a lane group writes its rows.
+    tap_rows_ = tap_rows ? tap_rows : rows_;
   }
 
   Status embed() {
@@ -435,7 +437,7 @@ class PrefillView {
     e_in.ld32 = n_in;
     if (taps) {  // the adapter activations of this step, for the Hebbian update
       e_in.kind = EPI_SEGMENTS_TAP;
-      e_in.tap = L_->tap_act.as<float>() + l * rows * r;
+      e_in.tap = L_->tap_act.as<float>() + (l * tap_rows_ + row0_) * r;
       e_in.ld_tap = r;
     }
     if (fold_norm)
@@ -446,7 +448,7 @@ class PrefillView {
     if (l == 0 && first_in_done_) PSSA_HIP_TRY(hipEventRecord(first_in_done_, st));
     if (taps && B.hybrid) {  // the write gate of a gated protected insert
       gate_mean_kernel<<<(unsigned)((rows + 255) / 256), 256, 0, st>>>(P_ + o_gate, n_in, d, (int)rows,
-                                                                       L_->tap_gmean.as<float>() + l * rows);
+                                                                       L_->tap_gmean.as<float>() + l * tap_rows_ + row0_);
       PSSA_LAUNCH_CHECK("gate_mean");
     }
 
@@ -490,7 +492,7 @@ class PrefillView {
     ra.count_dev = B.meta.as<int>();
     ra.tau = c_.tau_mem;
     ra.top_k = B.top_k;
-    if (taps) ra.q_pnc = L_->tap_q.as<float>() + l * rows * k;
+    if (taps) ra.q_pnc = L_->tap_q.as<float>() + (l * tap_rows_ + row0_) * k;
     if (B.hybrid) {  // token t reads with the ages bumped t + 1 times
       ra.hgate = B.hgate.as<float>();
       ra.hage = B.hage.as<unsigned long long>();
@@ -566,7 +568,7 @@ class PrefillView {
     e_z.out32 = Zr_;
     e_z.ld32 = d;
     if (taps) {
-      e_z.tap = L_->tap_a.as<float>() + l * rows * d;
+      e_z.tap = L_->tap_a.as<float>() + (l * tap_rows_ + row0_) * d;
       e_z.ld_tap = d;
     }
     if (bf16) {
@@ -594,7 +596,7 @@ class PrefillView {
     e_r.out32 = X_;
     e_r.ld32 = d;
     if (taps) {
-      e_r.tap = L_->tap_z.as<float>() + l * rows * d;
+      e_r.tap = L_->tap_z.as<float>() + (l * tap_rows_ + row0_) * d;
       e_r.ld_tap = d;
     }
     return launch_gemm(st, dt, H1_, 2 * d, B.mlp_w2.p, 2 * d, m, d, 2 * d, e_r);
@@ -656,7 +658,7 @@ class PrefillView {
   Timer tm_;
   int d_ = 0, s_ = 0, k_ = 0, C_ = 0, r_ = 0, V_ = 0, n_in_ = 0, m_ = 0, dt_ = 0;
   bool bf16_ = false;
-  size_t rows_ = 0, row0_ = 0;
+  size_t rows_ = 0, row0_ = 0, tap_rows_ = 0;
   float *X_ = nullptr, *XN_ = nullptr, *P_ = nullptr, *Y_ = nullptr, *Q_ = nullptr, *Zr_ = nullptr;
   uint16_t* XNh16_ = nullptr;
   void *XNh_ = nullptr, *Yh_ = nullptr, *Zrh_ = nullptr, *Wm_ = nullptr, *Mv_ = nullptr, *H1_ = nullptr;
@@ -744,8 +746,17 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
   // later groups' work is queued as early as the first group's.  Two groups
   // measure best at the 32-lane prefill (three and four run 2-3% slower:
   // their smaller scans leave the CUs less evenly loaded).
-  const int G = (int)std::min<size_t>(kPrefillLaneGroups, n_lanes);
-  if (!taps && !L->timing && G >= 2 && T >= 64) {
+  // A decode step of many lanes runs lane groups the same way: one group's
+  // HBM-bound carry update beside the other groups' chains of latency-bound
+  // products, eagerly or as parallel branches of the captured step.  Three
+  // groups measured best at 256 lanes (graph replay 1.84 ms per step with
+  // one, 1.79 with two, 1.77 with three, 1.80 with four).
+#ifndef PSSA_DECODE_GROUPS
+#define PSSA_DECODE_GROUPS 3
+#endif
+  const bool step_groups = PSSA_DECODE_GROUPS >= 2 && T == 1 && n_lanes >= 64 && !L->timing;
+  const int G = (int)std::min<size_t>(step_groups ? PSSA_DECODE_GROUPS : kPrefillLaneGroups, n_lanes);
+  if ((!taps && !L->timing && G >= 2 && T >= 64) || (step_groups && G >= 2)) {
     PSSA_HIP_TRY(hipEventRecord(L->ev_fork, st));
     std::vector<PrefillView> views;
     views.reserve(G);
@@ -754,7 +765,8 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
       const size_t ng = n_lanes / G + ((size_t)g < n_lanes % G ? 1 : 0);
       const hipStream_t sg = g == 0 ? st : L->aux_stream[g - 1];
       float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
-      views.emplace_back(L, sg, lane0, ng, T, false, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true);
+      views.emplace_back(L, sg, lane0, ng, T, taps, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true,
+                         n_lanes * T);
       lane0 += ng;
     }
     for (int g = 0; g < G; ++g) {

@@ -176,6 +176,40 @@ def test_decode_at_105m_width_graph_equals_eager(hip):
     assert np.all(np.isfinite(outs[0][1]))
 
 
+@pytest.mark.parametrize("hybrid", [False, True])
+def test_lane_group_steps_eager_equal_graph_replay(hip, hybrid):
+    """Steps of 96 lanes run as lane groups on their own streams, eagerly or
+    as parallel branches of the captured step: at the config-5 width (bf16)
+    and with the plastic writes, both give the same ids, logits, carries,
+    taps-driven bank rows and Hebbian weights bit for bit (a lane's rows are
+    computed the same way in any group; the plastic writes follow the
+    join)."""
+    say("eager lane groups == graph", hybrid)
+    cfg = PSSAConfig(depth=2, d_vocab=4096, d_latent=768, d_state=256, d_mem_key=32, mem_capacity=512)
+    w = ModelWeights.init(cfg, 5, "baseline")
+    w.populate_banks(6, count=400)
+    if hybrid:
+        rng = np.random.default_rng(8)
+        for b in w.blocks:
+            b.mem_hybrid_gate[:400] = rng.uniform(0.05, 1.0, 400).astype(np.float32)
+            b.mem_hybrid_age[:400] = rng.integers(0, 60, 400).astype(np.uint64)
+        w.set_hybrid_read(True, 0.9)
+    lanes = 96
+    ids = np.random.default_rng(7).integers(0, cfg.d_vocab, (lanes, 8), dtype=np.uint32)
+    outs = []
+    for graph in (False, True):
+        layer = PSSALayer(hip, w, lanes=lanes, max_tokens=lanes * 8, weight_dtype="bf16")
+        layer.prefill_inference(ids)
+        g, lg = layer.decode(5, plastic=True, graph=graph, want_logits=True)
+        pl = [layer.get_plastic(l) for l in range(cfg.depth)]
+        outs.append((g, lg, layer.get_carry(), *[p["adapter_up"] for p in pl], *[p["mem_values"] for p in pl],
+                     *[p["mem_last_seen"] for p in pl]))
+        layer.close()
+    for x, y in zip(*outs):
+        np.testing.assert_array_equal(x, y)
+    assert np.all(np.isfinite(outs[0][1]))
+
+
 def test_plastic_decode_many_lanes_and_layers_matches_oracle(hip):
     """64 lanes x 12 blocks: the per-(block, lane) Hebbian rates and the
     per-block bank writes of one launch cover every block."""

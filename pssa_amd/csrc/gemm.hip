@@ -773,6 +773,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_few_kernel(const uint16_t* 
   constexpr int SLAB = R * 64;      // bf16 elements per slab
   constexpr int BPW = R / 8 / NWV;  // DMA instructions per wave per slab, eight rows each
   static_assert(R % (8 * NWV) == 0, "slab rows must split evenly over the waves");
+  // Few-row products are latency-bound chains; in a decode step they share
+  // the SIMDs with another lane group's HBM-bound carry update, whose waves
+  // keep the default priority (graph replay 1.77 -> 1.75 ms per step).
+  __builtin_amdgcn_s_setprio(2);
   static_assert(S >= 2 && (S - 2) * BPW <= 63, "vmcnt holds at most 63");
   extern __shared__ __attribute__((aligned(1024))) uint16_t gemm_few_smem[];
 
@@ -1052,6 +1056,7 @@ __global__ __launch_bounds__(256) void gemm_norm_kernel(const float* __restrict_
   constexpr int NWV = 4, S = FEW_S, SLAB = NORM_BN * 64, BPW = NORM_BN / 8 / NWV;
   static_assert(S >= 2 && (S - 2) * BPW <= 63, "vmcnt holds at most 63");
   extern __shared__ __attribute__((aligned(1024))) uint16_t gemm_norm_smem[];
+  __builtin_amdgcn_s_setprio(2);  // as gemm_few_kernel: a decode-step product
   uint16_t* panel = gemm_norm_smem + S * SLAB;  // [32][d] bf16, swizzled
 
   const int tilesM = (M + 31) / 32, tilesN = (N + NORM_BN - 1) / NORM_BN;

@@ -342,6 +342,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
     RetrieveArgs a) {
   extern __shared__ float smem[];
   const int cap = a.capacity, dk = a.dk, cnt = a.count_dev ? a.count_dev[0] : a.count;
+  if constexpr (QP) __builtin_amdgcn_s_setprio(2);  // a decode-step product, as gemm_few_kernel
   float* keyT = smem;                                                  // [dk][kp]
   const int kp = soft_pitch(cap);
   double* rk = reinterpret_cast<double*>(smem + soft_keys_floats(dk, cap));  // [cap]

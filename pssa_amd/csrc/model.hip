@@ -750,7 +750,10 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
   // HBM-bound carry update beside the other groups' chains of latency-bound
   // products, eagerly or as parallel branches of the captured step.  Three
   // groups measured best at 256 lanes (graph replay 1.84 ms per step with
-  // one, 1.79 with two, 1.77 with three, 1.80 with four).
+  // one, 1.79 with two, 1.77 with three, 1.80 with four).  The step's groups
+  // start together (no stagger: 1.77 -> 1.76 ms; with the products' raised
+  // wave priority 1.74), and group sizes rounded to the update's four lanes
+  // per workgroup measured the same.
 #ifndef PSSA_DECODE_GROUPS
 #define PSSA_DECODE_GROUPS 3
 #endif
@@ -765,15 +768,15 @@ static Status prefill_groups(pssa_hip_lanes* L, size_t n_lanes, size_t T, bool t
       const size_t ng = n_lanes / G + ((size_t)g < n_lanes % G ? 1 : 0);
       const hipStream_t sg = g == 0 ? st : L->aux_stream[g - 1];
       float* yp = ypart ? ypart + (size_t)nz * lane0 * T * c.d_latent : nullptr;
-      views.emplace_back(L, sg, lane0, ng, T, taps, false, g + 1 < G ? L->ev_first[g] : nullptr, yp, tr, true,
-                         n_lanes * T);
+      views.emplace_back(L, sg, lane0, ng, T, taps, false, g + 1 < G && !step_groups ? L->ev_first[g] : nullptr,
+                         yp, tr, true, n_lanes * T);
       lane0 += ng;
     }
     for (int g = 0; g < G; ++g) {
       if (g > 0) {
         const hipStream_t sg = L->aux_stream[g - 1];
         PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_fork, 0));
-        PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_first[g - 1], 0));
+        if (!step_groups) PSSA_HIP_TRY(hipStreamWaitEvent(sg, L->ev_first[g - 1], 0));
       }
       PSSA_RETURN_IF(views[g].embed());
       PSSA_RETURN_IF(views[g].layer(0));

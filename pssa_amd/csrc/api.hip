@@ -1140,6 +1140,8 @@ int pssa_hip_lanes_create(pssa_hip_ctx* ctx, const pssa_hip_model* model, size_t
     PSSA_RETURN_IF(L->nonfinite.alloc(16));
     PSSA_RETURN_IF(clear_history(L.get()));
     PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming));
+    PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_tail_fork, hipEventDisableTiming));
+    PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_tail_join, hipEventDisableTiming));
     for (int g = 0; g < pssa_hip_lanes::kMaxGroups - 1; ++g) {
       PSSA_HIP_TRY(hipStreamCreateWithFlags(&L->aux_stream[g], hipStreamNonBlocking));
       PSSA_HIP_TRY(hipEventCreateWithFlags(&L->ev_first[g], hipEventDisableTiming));

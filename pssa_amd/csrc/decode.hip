@@ -770,6 +770,15 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
   const int d = (int)c.d_latent, k = (int)c.d_mem_key, r = (int)c.adapter_rank, C = (int)c.mem_capacity;
   const size_t n = n_lanes;
   PSSA_RETURN_IF(run_prefill(L, n_lanes, 1, plastic, false));
+  // The Hebbian update (src/pssa.rs:1814-1832) reads only the forward's taps
+  // and writes only the fast weights, which nothing else in the step reads:
+  // it runs on an auxiliary stream beside the choice and the bank writes,
+  // and the step counter's advance waits for both.
+  const hipStream_t hs = L->aux_stream[0];
+  if (plastic) {
+    PSSA_HIP_TRY(hipEventRecord(L->ev_tail_fork, st));
+    PSSA_HIP_TRY(hipStreamWaitEvent(hs, L->ev_tail_fork, 0));
+  }
   GreedyWindow gw;
   gw.hist = L->hist.as<uint32_t>();
   gw.hist_n = L->hist_n.as<int>();
@@ -828,16 +837,18 @@ Status run_decode_step(pssa_hip_lanes* L, size_t n_lanes, bool plastic) {
     p.r = r;
     p.wt_bf16 = M->dtype == PSSA_HIP_BF16 ? 1 : 0;
     const int depth = (int)c.depth;
+    hebbian_rate_kernel<<<dim3((unsigned)((n + 3) / 4), depth), 256, 0, hs>>>(p);
+    PSSA_LAUNCH_CHECK("hebbian_rate");
+    const int hb_i = hebbian_rows(r);
+    hebbian_kernel<<<dim3((unsigned)((d + hb_i - 1) / hb_i), depth), hb_i * r, hebbian_lds(r, (int)n), hs>>>(p,
+                                                                                                         hb_i);
+    PSSA_LAUNCH_CHECK("hebbian");
+    PSSA_HIP_TRY(hipEventRecord(L->ev_tail_join, hs));
     bank_write_kernel<<<depth, 256, bank_write_lds(C, (int)n), st>>>(p);
     PSSA_LAUNCH_CHECK("bank_write");
     bank_copy_kernel<<<dim3((unsigned)((C + 63) / 64), (unsigned)((d + 63) / 64), depth), 256, 0, st>>>(p);
     PSSA_LAUNCH_CHECK("bank_copy");
-    hebbian_rate_kernel<<<dim3((unsigned)((n + 3) / 4), depth), 256, 0, st>>>(p);
-    PSSA_LAUNCH_CHECK("hebbian_rate");
-    const int hb_i = hebbian_rows(r);
-    hebbian_kernel<<<dim3((unsigned)((d + hb_i - 1) / hb_i), depth), hb_i * r, hebbian_lds(r, (int)n), st>>>(p,
-                                                                                                         hb_i);
-    PSSA_LAUNCH_CHECK("hebbian");
+    PSSA_HIP_TRY(hipStreamWaitEvent(st, L->ev_tail_join, 0));
     advance_kernel<<<1, 64, 0, st>>>(M->step.as<unsigned long long>(), L->gen_pos.as<int>());
   } else {
     advance_pos_kernel<<<1, 64, 0, st>>>(L->gen_pos.as<int>());

@@ -146,11 +146,15 @@ struct pssa_hip_lanes {
   hipStream_t aux_stream[kMaxGroups - 1] = {};
   hipEvent_t ev_fork = nullptr;
   hipEvent_t ev_first[kMaxGroups - 1] = {}, ev_join[kMaxGroups - 1] = {};
+  // Fork and join of a plastic decode step's Hebbian update (aux_stream[0]).
+  hipEvent_t ev_tail_fork = nullptr, ev_tail_join = nullptr;
   ~pssa_hip_lanes() {
     for (hipEvent_t e : events) (void)hipEventDestroy(e);
     if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
     if (graph) (void)hipGraphDestroy(graph);
     if (ev_fork) (void)hipEventDestroy(ev_fork);
+    if (ev_tail_fork) (void)hipEventDestroy(ev_tail_fork);
+    if (ev_tail_join) (void)hipEventDestroy(ev_tail_join);
     for (int g = 0; g < kMaxGroups - 1; ++g) {
       if (ev_first[g]) (void)hipEventDestroy(ev_first[g]);
       if (ev_join[g]) (void)hipEventDestroy(ev_join[g]);

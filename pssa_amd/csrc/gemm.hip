@@ -314,18 +314,16 @@ __device__ __forceinline__ void epi_tile_load(const EpiParams& ep, int row, int 
   }
 }
 
+// Adapter up-projection sum_q U[col,q] * act[row,q] of a z_raw tile on the
+// matrix cores, in the same accumulator layout as the main product (zero
+// for other epilogues).
 template <typename T, int KIND>
-__device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16_t& acc, int row,
-                                               int n32, int M, int N, int vec_epi, int half,
-                                               int l32, const uint32_t* act0, const QuadIn (&in)[4],
-                                               const uint32_t* u0 = nullptr) {
-  const int nb = n32 + half * 4;
+__device__ __forceinline__ f32x16_t epi_adapter(const EpiParams& ep, int row, int n32, int M, int N, int half,
+                                                int l32, const uint32_t* act0, const uint32_t* u0) {
   f32x16_t adv;
 #pragma unroll
   for (int i = 0; i < 16; ++i) adv[i] = 0.0f;
   if constexpr (KIND == EPI_ZRAW) {
-    // Adapter up-projection sum_q U[col,q] * act[row,q] on the matrix cores,
-    // in the same accumulator layout as the main product.
     const int urow = n32 + l32;
     if constexpr (sizeof(T) == 2) {
       for (int q0 = 0; q0 < ep.rank; q0 += 16) {
@@ -357,6 +355,16 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
       }
     }
   }
+  return adv;
+}
+
+template <typename T, int KIND>
+__device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16_t& acc, int row,
+                                               int n32, int M, int N, int vec_epi, int half,
+                                               int l32, const uint32_t* act0, const QuadIn (&in)[4],
+                                               const uint32_t* u0 = nullptr) {
+  const int nb = n32 + half * 4;
+  const f32x16_t adv = epi_adapter<T, KIND>(ep, row, n32, M, N, half, l32, act0, u0);
   if (row < M) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -368,6 +376,70 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
       }
     }
   }
+}
+
+// The epilogue of one whole 32 x 32 tile of the tiled kernel (rows < M,
+// columns < N, 16-byte aligned operand rows, no tap) through the wave's
+// 12 KB of LDS `ebuf`.  In the accumulator layout a lane holds one row and
+// four 4-column quads, so its row-operand loads and its stores each cover
+// 32 rows x 16 bytes per instruction.  Here the row operands (z_raw: y and
+// the gate; residual: z_raw and the running sum) arrive by direct-to-LDS
+// loads of eight whole 128-byte row segments each, every lane reads its
+// quads from LDS, and the values go back to LDS and leave as eight whole
+// 128-byte fp32 (64-byte bf16) row segments per store.  LDS holds [32 rows]
+// [8 chunks] of 16 bytes with chunk c of row r at slot c ^ (r & 7), so the
+// eight lanes of a 16-byte access phase hit eight distinct bank groups.
+// The arithmetic is epi_value's, as in epi_quad.
+template <int KIND>
+__device__ __forceinline__ void epi_tile_staged(const EpiParams& ep, const f32x16_t& acc, int r0, int n32,
+                                                int M, int N, int lane, int half, int l32,
+                                                const uint32_t* act0, float* ebuf) {
+  static_assert(KIND == EPI_ZRAW || KIND == EPI_RESIDUAL, "row-operand epilogues");
+  const bool has_q = KIND == EPI_ZRAW || !ep.first;
+  float* pb = ebuf;         // y or the z_raw operand
+  float* qb = ebuf + 1024;  // the gate or the running sum
+  float* sb = ebuf + 2048;  // the values
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    const size_t row = (size_t)(r0 + r);
+    const int col = n32 + 4 * c;
+    const float* ps = KIND == EPI_ZRAW ? ep.y + row * ep.ld_y + col : ep.aux + row * ep.ld_aux + col;
+    __builtin_amdgcn_global_load_lds((const void*)ps, (__attribute__((address_space(3))) void*)(pb + 256 * i),
+                                     16, 0, 0);
+    if (has_q) {
+      const float* qs = KIND == EPI_ZRAW ? ep.g + row * ep.ld_g + col : ep.out32 + row * ep.ld32 + col;
+      __builtin_amdgcn_global_load_lds((const void*)qs, (__attribute__((address_space(3))) void*)(qb + 256 * i),
+                                       16, 0, 0);
+    }
+  }
+  const f32x16_t adv = epi_adapter<uint16_t, KIND>(ep, r0 + l32, n32, M, N, half, l32, act0, nullptr);
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int pos = 4 * (l32 * 8 + ((half + 2 * g) ^ (l32 & 7)));
+    const float4 p = *reinterpret_cast<const float4*>(pb + pos);
+    const float4 q = has_q ? *reinterpret_cast<const float4*>(qb + pos) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float p4[4] = {p.x, p.y, p.z, p.w}, q4[4] = {q.x, q.y, q.z, q.w};
+    float v[4], tp;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      v[e] = epi_value<KIND>(ep, acc[g * 4 + e], p4[e], q4[e], adv[g * 4 + e], n32 + half * 4 + g * 8 + e, tp);
+    *reinterpret_cast<float4*>(sb + pos) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 8 + (lane >> 3), cs = lane & 7, c = cs ^ (r & 7);
+    const float4 v = *reinterpret_cast<const float4*>(sb + 4 * (r * 8 + cs));
+    const size_t row = (size_t)(r0 + r);
+    if (ep.out32) *reinterpret_cast<float4*>(ep.out32 + row * ep.ld32 + n32 + 4 * c) = v;
+    if (ep.out16)
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ep.out16) + row * ep.ld16 + n32 + 4 * c) =
+          make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  }
+  __builtin_amdgcn_wave_barrier();
 }
 
 template <typename T, int KIND, bool CLAMP = true>
@@ -519,7 +591,7 @@ constexpr int LDS_BK = 32, LDS_STAGES = 3;
 
 __device__ __forceinline__ int slab_swizzle(int r) { return (((r & 15) >> 1) ^ ((r & 15) >> 3)) & 3; }
 
-template <int KIND, int NW>
+template <int KIND, int NW, bool STG = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_lds_kernel(
     const uint16_t* __restrict__ A, int lda, const uint16_t* __restrict__ B, int ldb, int M, int N,
     int K, int vec_epi, EpiParams ep) {
@@ -606,6 +678,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
   }
 
+  if constexpr (STG) {
+    // Whole tiles: once every wave has read the last slab, each wave stages
+    // its tiles' epilogues in its own 12 KB of the ring.
+    static_assert(4 * 3 * 1024 * 4 <= S * R * BK * 2, "four 12 KB staging areas fit the ring");
+    __syncthreads();
+    float* ebuf = reinterpret_cast<float*>(gemm_lds_smem) + wave * 3 * 1024;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int r0 = m0 + wm * MT * 32 + t * 32;
+      uint32_t act0[4] = {0u, 0u, 0u, 0u};
+      if constexpr (KIND == EPI_ZRAW) adapter_act_frag(ep, r0 + l32, M, 0, half, act0);
+#pragma unroll
+      for (int u = 0; u < NW; ++u)
+        epi_tile_staged<KIND>(ep, acc[t][u], r0, n0 + wn * NW * 32 + u * 32, M, N, lane, half, l32, act0, ebuf);
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     const int row = m0 + wm * MT * 32 + t * 32 + l32;
@@ -990,6 +1079,20 @@ static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint1
                             const EpiParams& ep) {
   constexpr size_t lds = gemm_lds_bytes(NW);
   static_assert(lds <= 64 * 1024, "the ring fits the default dynamic LDS limit");
+  // The row-operand epilogues of whole 128 x 128 tiles stage through LDS
+  // (epi_tile_staged): vector operands, no tap.
+  if constexpr (NW == 2) {
+    if (ve && M % 128 == 0 && N % 128 == 0 && !ep.tap) {
+      if (kind == EPI_ZRAW) {
+        gemm_lds_kernel<EPI_ZRAW, NW, true><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep);
+        return;
+      }
+      if (kind == EPI_RESIDUAL) {
+        gemm_lds_kernel<EPI_RESIDUAL, NW, true><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep);
+        return;
+      }
+    }
+  }
 #define PSSA_GEMM_LDS_CASE(KD)                                                                 \
   case KD:                                                                                     \
     gemm_lds_kernel<KD, NW><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \

@@ -378,49 +378,57 @@ __device__ __forceinline__ void epi_tile_store(const EpiParams& ep, const f32x16
   }
 }
 
-// The epilogue of one whole 32 x 32 tile of the tiled kernel (rows < M,
-// columns < N, 16-byte aligned operand rows, no tap) through the wave's
-// 12 KB of LDS `ebuf`.  In the accumulator layout a lane holds one row and
-// four 4-column quads, so its row-operand loads and its stores each cover
-// 32 rows x 16 bytes per instruction.  Here the row operands (z_raw: y and
-// the gate; residual: z_raw and the running sum) arrive by direct-to-LDS
-// loads of eight whole 128-byte row segments each, every lane reads its
-// quads from LDS, and the values go back to LDS and leave as eight whole
-// 128-byte fp32 (64-byte bf16) row segments per store.  LDS holds [32 rows]
-// [8 chunks] of 16 bytes with chunk c of row r at slot c ^ (r & 7), so the
-// eight lanes of a 16-byte access phase hit eight distinct bank groups.
+// The epilogue of one 32 x 32 tile of the tiled kernel through the wave's
+// 12 KB of LDS `ebuf` (16-byte aligned operand rows, N % 4 == 0, no tap).
+// In the accumulator layout a lane holds one row and four 4-column quads, so
+// its row-operand loads and its stores would each cover 32 rows x 16 bytes
+// per instruction.  Here the row operands (z_raw: y and the gate; add-aux:
+// aux; residual: z_raw and the running sum) arrive by direct-to-LDS loads of
+// eight whole 128-byte row segments each, every lane reads its quads from
+// LDS, and the values go back to LDS and leave as eight whole 128-byte fp32
+// (64-byte bf16) row segments per store.  LDS holds [32 rows][8 chunks] of
+// 16 bytes with chunk c of row r at slot c ^ (r & 7), so the eight lanes of
+// a 16-byte access phase hit eight distinct bank groups.  Rows past M and
+// chunks past N load from clamped in-range addresses and are not stored.
 // The arithmetic is epi_value's, as in epi_quad.
 template <int KIND>
 __device__ __forceinline__ void epi_tile_staged(const EpiParams& ep, const f32x16_t& acc, int r0, int n32,
                                                 int M, int N, int lane, int half, int l32,
                                                 const uint32_t* act0, float* ebuf) {
-  static_assert(KIND == EPI_ZRAW || KIND == EPI_RESIDUAL, "row-operand epilogues");
-  const bool has_q = KIND == EPI_ZRAW || !ep.first;
-  float* pb = ebuf;         // y or the z_raw operand
+  constexpr bool reads = epi_reads(KIND);
+  const bool has_q = KIND == EPI_ZRAW || (KIND == EPI_RESIDUAL && !ep.first);
+  float* pb = ebuf;         // y, aux or the z_raw operand
   float* qb = ebuf + 1024;  // the gate or the running sum
   float* sb = ebuf + 2048;  // the values
+  if constexpr (reads) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = i * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
-    const size_t row = (size_t)(r0 + r);
-    const int col = n32 + 4 * c;
-    const float* ps = KIND == EPI_ZRAW ? ep.y + row * ep.ld_y + col : ep.aux + row * ep.ld_aux + col;
-    __builtin_amdgcn_global_load_lds((const void*)ps, (__attribute__((address_space(3))) void*)(pb + 256 * i),
-                                     16, 0, 0);
-    if (has_q) {
-      const float* qs = KIND == EPI_ZRAW ? ep.g + row * ep.ld_g + col : ep.out32 + row * ep.ld32 + col;
-      __builtin_amdgcn_global_load_lds((const void*)qs, (__attribute__((address_space(3))) void*)(qb + 256 * i),
-                                       16, 0, 0);
+    for (int i = 0; i < 4; ++i) {
+      const int r = i * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      const size_t row = (size_t)min(r0 + r, M - 1);
+      const int col = min(n32 + 4 * c, N - 4);
+      const float* ps = KIND == EPI_ZRAW ? ep.y + row * ep.ld_y + col : ep.aux + row * ep.ld_aux + col;
+      __builtin_amdgcn_global_load_lds((const void*)ps,
+                                       (__attribute__((address_space(3))) void*)(pb + 256 * i), 16, 0, 0);
+      if (has_q) {
+        const float* qs = KIND == EPI_ZRAW ? ep.g + row * ep.ld_g + col : ep.out32 + row * ep.ld32 + col;
+        __builtin_amdgcn_global_load_lds((const void*)qs,
+                                         (__attribute__((address_space(3))) void*)(qb + 256 * i), 16, 0, 0);
+      }
     }
   }
   const f32x16_t adv = epi_adapter<uint16_t, KIND>(ep, r0 + l32, n32, M, N, half, l32, act0, nullptr);
-  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-  __builtin_amdgcn_wave_barrier();
+  if constexpr (reads) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __builtin_amdgcn_wave_barrier();
+  }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int pos = 4 * (l32 * 8 + ((half + 2 * g) ^ (l32 & 7)));
-    const float4 p = *reinterpret_cast<const float4*>(pb + pos);
-    const float4 q = has_q ? *reinterpret_cast<const float4*>(qb + pos) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 p = make_float4(0.f, 0.f, 0.f, 0.f), q = p;
+    if constexpr (reads) {
+      p = *reinterpret_cast<const float4*>(pb + pos);
+      if (has_q) q = *reinterpret_cast<const float4*>(qb + pos);
+    }
     const float p4[4] = {p.x, p.y, p.z, p.w}, q4[4] = {q.x, q.y, q.z, q.w};
     float v[4], tp;
 #pragma unroll
@@ -434,10 +442,12 @@ __device__ __forceinline__ void epi_tile_staged(const EpiParams& ep, const f32x1
     const int r = i * 8 + (lane >> 3), cs = lane & 7, c = cs ^ (r & 7);
     const float4 v = *reinterpret_cast<const float4*>(sb + 4 * (r * 8 + cs));
     const size_t row = (size_t)(r0 + r);
-    if (ep.out32) *reinterpret_cast<float4*>(ep.out32 + row * ep.ld32 + n32 + 4 * c) = v;
-    if (ep.out16)
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ep.out16) + row * ep.ld16 + n32 + 4 * c) =
-          make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    if (r0 + r < M && n32 + 4 * c < N) {
+      if (ep.out32) *reinterpret_cast<float4*>(ep.out32 + row * ep.ld32 + n32 + 4 * c) = v;
+      if (ep.out16)
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(ep.out16) + row * ep.ld16 + n32 + 4 * c) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    }
   }
   __builtin_amdgcn_wave_barrier();
 }
@@ -1079,23 +1089,16 @@ static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint1
                             const EpiParams& ep) {
   constexpr size_t lds = gemm_lds_bytes(NW);
   static_assert(lds <= 64 * 1024, "the ring fits the default dynamic LDS limit");
-  // The row-operand epilogues of whole 128 x 128 tiles stage through LDS
-  // (epi_tile_staged): vector operands, no tap.
-  if constexpr (NW == 2) {
-    if (ve && M % 128 == 0 && N % 128 == 0 && !ep.tap) {
-      if (kind == EPI_ZRAW) {
-        gemm_lds_kernel<EPI_ZRAW, NW, true><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep);
-        return;
-      }
-      if (kind == EPI_RESIDUAL) {
-        gemm_lds_kernel<EPI_RESIDUAL, NW, true><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep);
-        return;
-      }
-    }
-  }
-#define PSSA_GEMM_LDS_CASE(KD)                                                                 \
-  case KD:                                                                                     \
-    gemm_lds_kernel<KD, NW><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep); \
+  // 128 x 128 tiles stage their epilogues through LDS (epi_tile_staged):
+  // vector operands, N % 4 == 0, no tap.
+  const bool stg = NW == 2 && ve && N % 4 == 0 && !ep.tap;
+#define PSSA_GEMM_LDS_CASE(KD)                                                                        \
+  case KD:                                                                                            \
+    if (stg && KD != EPI_SEGMENTS_TAP)                                                                \
+      gemm_lds_kernel<KD, NW, NW == 2 && KD != EPI_SEGMENTS_TAP><<<grid, 256, lds, stream>>>(         \
+          A, lda, B, ldb, M, N, K, ve, ep);                                                           \
+    else                                                                                              \
+      gemm_lds_kernel<KD, NW><<<grid, 256, lds, stream>>>(A, lda, B, ldb, M, N, K, ve, ep);          \
     break;
   switch (kind) {
     PSSA_GEMM_LDS_CASE(EPI_STORE)

@@ -993,7 +993,10 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
   __shared__ double s_sq[RQ_WAVES][RK_SLOTS];
   __shared__ float s_min[RQ_WAVES];
   constexpr int SPL = RK_SLOTS / 64;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index as a uniform value: the per-query row bases below then live
+  // in scalar registers and the loads take 32-bit offsets (64-bit per-slot
+  // addresses had been hoisted out of the query loop and spilled).
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dk = a.dk, cnt = a.count, K = a.top_k;
   uint16_t* cand = s_cand[wave];
   unsigned long long* ckey = s_key[wave];
@@ -1014,10 +1017,12 @@ __global__ __launch_bounds__(64 * RQ_WAVES) __attribute__((amdgpu_waves_per_eu(4
     float lm = HUGE_VALF;
     float4 tmv[SPL];
     float dtv[SPL];
+    const char* tbase = reinterpret_cast<const char*>(sc.terms);
+    const char* zbase = reinterpret_cast<const char*>(sc.zdot + (size_t)row * RK_SLOTS);
 #pragma unroll
     for (int j = 0; j < SPL; ++j) {
-      tmv[j] = sc.terms[lane + 64 * j];
-      dtv[j] = sc.zdot[(size_t)row * RK_SLOTS + lane + 64 * j];
+      tmv[j] = *reinterpret_cast<const float4*>(tbase + (uint32_t)(16 * (lane + 64 * j)));
+      dtv[j] = *reinterpret_cast<const float*>(zbase + (uint32_t)(4 * (lane + 64 * j)));
     }
     const double qq = sc.qq[row];
     const float qqf = (float)qq, qnf = (float)sqrt(qq);

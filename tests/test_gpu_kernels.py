@@ -71,6 +71,28 @@ def test_gemm_bf16_few_rows_equal_tiled_rows_bitwise(hip, n, k):
     assert rel_err(big[:64], exact) < 1e-5
 
 
+@pytest.mark.parametrize("m,n", [(16461, 1000), (16384 + 5, 2096), (4200, 772)])
+def test_gemm_bf16_tiled_partial_tiles_bitwise(hip, m, n):
+    """The tiled kernel's epilogue stages each 32 x 32 tile through LDS;
+    tiles cut off by M or N load clamped rows and columns and store only
+    what is in range.  Rows at both ends of a product whose last row and
+    column tiles are partial (772 columns: a last tile of one 4-column
+    chunk) equal the few-row kernel's bit for bit."""
+    say("gemm bf16 partial tiles", m, n)
+    k = 768
+    rng = np.random.default_rng(m + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = bf16_round((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    wbits = (w.view(np.uint32) >> 16).astype(np.uint16)
+    big = hip.try_dispatch_gemm(x, wbits, m, n, k, w_dtype="bf16").reshape(m, n)
+    for r0, rows in ((0, 37), (m - 37, 37), (m - 128 - 3, 64)):
+        few = hip.try_dispatch_gemm(np.ascontiguousarray(x[r0:r0 + rows]), wbits, rows, n, k,
+                                    w_dtype="bf16").reshape(rows, n)
+        np.testing.assert_array_equal(few.view(np.uint32), big[r0:r0 + rows].view(np.uint32))
+    exact = bf16_round(x[-64:]).astype(np.float64) @ w.astype(np.float64).T
+    assert rel_err(big[-64:], exact) < 1e-5
+
+
 @pytest.mark.parametrize("m,n,k,batch", [(5, 9, 8, 1), (64, 130, 776, 2), (257, 96, 768, 1), (31, 3, 20, 3)])
 def test_gemm_bf16_weights(hip, m, n, k, batch):
     say("gemm bf16", m, n, k, batch)

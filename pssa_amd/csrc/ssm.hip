@@ -476,6 +476,11 @@ static void launch_j(hipStream_t stream, const SsmArgs& a, bool mat) {
       ssm_scan_kernel<16, 8, 4><<<grid, 512, 0, stream>>>(a);
     else
       ssm_scan_kernel<32, 4, 3><<<grid, 256, 0, stream>>>(a);
+  } else if constexpr (J <= 8) {
+    // Few states per lane: a small model's grid of a few workgroups, each
+    // bound by its step chain, so occupancy gives nothing and the register
+    // budget of two waves per SIMD keeps the 16-step staging out of scratch.
+    ssm_scan_kernel<J, 4, 2><<<grid, 256, 0, stream>>>(a);
   } else {
     ssm_scan_kernel<J, 4, 3><<<grid, 256, 0, stream>>>(a);
   }

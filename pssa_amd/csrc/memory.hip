@@ -110,155 +110,179 @@ __device__ __forceinline__ float hybrid_decay(const RetrieveArgs& a, int s, int 
   return (float)exp((double)age * a.log_lam);
 }
 
+// Several waves per query: each computes the distances of every
+// RETRIEVE_WPQ-th 64-slot block (the per-slot sums are the only long chains,
+// and a 512-query prefill would otherwise leave half the SIMDs idle); the
+// first wave then selects, weights and reads out alone, as a one-wave read
+// would.  The waves of a query meet at workgroup barriers, so every wave of
+// a workgroup runs the same number of iterations.
+#ifndef RETRIEVE_QPB
+#define RETRIEVE_QPB 2
+#endif
+constexpr int RETRIEVE_WPQ = 4 / RETRIEVE_QPB;  // waves per query (4-wave workgroups)
 __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
   extern __shared__ float smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int pair = wave / RETRIEVE_WPQ, half = wave % RETRIEVE_WPQ;
   const int dk_pad = (a.dk + 3) & ~3;
-  float* sq = smem + wave * (dk_pad + a.capacity);  // this wave's query, then distances
+  float* sq = smem + pair * (dk_pad + a.capacity);  // this query's projection, then distances
   float* sdist = sq + dk_pad;
-  __shared__ uint32_t ssel[4][kMaxTopK];
+  __shared__ uint32_t ssel[RETRIEVE_QPB][kMaxTopK];
+  __shared__ float spart[RETRIEVE_QPB][RETRIEVE_WPQ];
   const int cnt = a.count_dev ? a.count_dev[0] : a.count;
 
-  for (int n = blockIdx.x * 4 + wave; n < a.n; n += gridDim.x * 4) {
-    const float* qrow = a.q + (size_t)n * a.ld_q;
-    for (int i = lane; i < a.dk; i += 64) sq[i] = qrow[i];
-    wave_sync();
-    // ---- diffeomorphic_project (src/memory.rs:194-211) ----
-    if (a.project) {
-      const double r = sqrt(sumsq_f64(sq, a.dk));
-      const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+  for (int n0 = blockIdx.x * RETRIEVE_QPB; n0 < a.n; n0 += gridDim.x * RETRIEVE_QPB) {
+    const int n = n0 + pair;
+    const bool live = n < a.n;
+    if (live && half == 0) {
+      const float* qrow = a.q + (size_t)n * a.ld_q;
+      for (int i = lane; i < a.dk; i += 64) sq[i] = qrow[i];
       wave_sync();
-      for (int i = lane; i < a.dk; i += 64) sq[i] = (float)((double)sq[i] * scale);
-      if (a.q_norm && lane == 0) a.q_norm[n] = (float)fmin(r, (double)FLT_MAX);
-      wave_sync();
-    }
-    if (a.q_pnc)
-      for (int i = lane; i < a.dk; i += 64) a.q_pnc[(size_t)n * a.dk + i] = sq[i];
-    const float q_sq = bank_norm_sq(sq, a.dk);
-
-    if (cnt == 0) {
-      for (int s = lane; s < a.capacity; s += 64) put_weight(a, n, s, 0.0f);
-      if (a.out_val)
-        for (int j = lane; j < a.dv; j += 64) a.out_val[(size_t)n * a.dv + j] = 0.0f;
-      if (a.out_min && lane == 0) a.out_min[n] = 0.0f;
-      if (a.out_idx)
-        for (int r = lane; r < a.top_k; r += 64) a.out_idx[(size_t)n * a.top_k + r] = 0xFFFFFFFFu;
-      wave_sync();
-      continue;
-    }
-    // ---- distances ----
-    float local_min = FLT_MAX;
-    for (int s = lane; s < cnt; s += 64) {
-      const float dist = poincare_dist(sq, q_sq, a.keys + (size_t)s * a.dk, a.norm_sq[s], a.dk);
-      sdist[s] = dist;
-      local_min = fminf(local_min, dist);
-    }
-    const float min_dist = wave_min(local_min);
-    wave_sync();
-    if (a.out_min && lane == 0) a.out_min[n] = min_dist;
-
-    if (a.top_k > 0 && a.top_k < cnt) {
-      // ---- exact top-k by (distance bits, slot) (src/memory.rs:380-392) ----
-      const int k = a.top_k;
-      for (int r = 0; r < k; ++r) {
-        unsigned long long best = ~0ull;
-        for (int s = lane; s < cnt; s += 64) {
-          const uint32_t bits = __float_as_uint(sdist[s]);
-          const unsigned long long key = ((unsigned long long)bits << 32) | (unsigned)s;
-          bool taken = false;
-          for (int p = 0; p < r; ++p) taken |= ssel[wave][p] == (uint32_t)s;
-          if (!taken && key < best) best = key;
-        }
-        best = wave_min_u64(best);
-        if (lane == 0) ssel[wave][r] = (uint32_t)(best & 0xFFFFFFFFu);
+      // ---- diffeomorphic_project (src/memory.rs:194-211) ----
+      if (a.project) {
+        const double r = sqrt(sumsq_f64(sq, a.dk));
+        const double scale = r == 0.0 ? 1.0 : fmin(r / (1.0 + r), kMaxRadius) / r;
+        wave_sync();
+        for (int i = lane; i < a.dk; i += 64) sq[i] = (float)((double)sq[i] * scale);
+        if (a.q_norm && lane == 0) a.q_norm[n] = (float)fmin(r, (double)FLT_MAX);
         wave_sync();
       }
-      if (lane == 0) {  // ascending slot order
-        for (int x = 1; x < k; ++x) {
-          const uint32_t v = ssel[wave][x];
-          int y = x - 1;
-          while (y >= 0 && ssel[wave][y] > v) {
-            ssel[wave][y + 1] = ssel[wave][y];
-            --y;
-          }
-          ssel[wave][y + 1] = v;
-        }
-      }
-      wave_sync();
-      // Hybrid read: (e * gate) * decay per live slot, unless every live
-      // weight is zero (then the plain softmax, src/memory.rs:640-650).
-      auto hyb_w = [&](int s, float e) { return (e * a.hgate[s]) * hybrid_decay(a, s, n); };
-      bool hyb = a.hgate != nullptr;
-      float sum = 0.0f;
-      if (hyb) {
-        for (int r = 0; r < k; ++r) {
-          const int s = ssel[wave][r];
-          sum += hyb_w(s, expf((min_dist - sdist[s]) / a.tau));
-        }
-        hyb = sum != 0.0f;
-      }
-      if (!hyb) {
-        sum = 0.0f;
-        for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[wave][r]]) / a.tau);
-      }
-      auto weight_of = [&](int s) {
-        const float e = expf((min_dist - sdist[s]) / a.tau);
-        return (hyb ? hyb_w(s, e) : e) / sum;
-      };
-      if (a.weights || a.weights16) {
-        for (int s = lane; s < a.capacity; s += 64) {
-          bool chosen = false;
-          for (int r = 0; r < k; ++r) chosen |= ssel[wave][r] == (uint32_t)s;
-          put_weight(a, n, s, chosen ? weight_of(s) : 0.0f);
-        }
-      }
-      if (a.out_idx)
-        for (int r = lane; r < k; r += 64) a.out_idx[(size_t)n * k + r] = ssel[wave][r];
-      if (a.out_val) {
-        for (int j = lane; j < a.dv; j += 64) {
-#pragma clang fp contract(off)
-          float acc = 0.0f;
-          for (int r = 0; r < k; ++r) {
-            const uint32_t s = ssel[wave][r];
-            const float w = weight_of((int)s);
-            acc = acc + w * a.values[(size_t)s * a.dv + j];
-          }
-          a.out_val[(size_t)n * a.dv + j] = acc;
-        }
-      }
-    } else {
-      // ---- full soft read (src/memory.rs:409-425); hybrid: every slot live ----
-      float part = 0.0f, part_h = 0.0f;
-      for (int s = lane; s < cnt; s += 64) {
-        const float e = expf((min_dist - sdist[s]) / a.tau);
-        sdist[s] = e;
-        part += e;
-        if (a.hgate) part_h += (e * a.hgate[s]) * hybrid_decay(a, s, n);
-      }
-      const float sum_p = wave_sum(part);
-      const float sum_h = a.hgate ? wave_sum(part_h) : 0.0f;
-      const bool hyb = a.hgate && sum_h != 0.0f;
-      const float sum = hyb ? sum_h : sum_p;
-      wave_sync();
-      for (int s = lane; s < a.capacity; s += 64) {
-        float w = 0.0f;
-        if (s < cnt) w = (hyb ? (sdist[s] * a.hgate[s]) * hybrid_decay(a, s, n) : sdist[s]) / sum;
-        if (s < cnt) sdist[s] = w;
-        put_weight(a, n, s, w);
-      }
-      wave_sync();
-      if (a.out_val) {
-        for (int j = lane; j < a.dv; j += 64) {
-          float acc = 0.0f;
-          for (int s = 0; s < cnt; ++s) acc = fmaf(sdist[s], a.values[(size_t)s * a.dv + j], acc);
-          a.out_val[(size_t)n * a.dv + j] = acc;
-        }
-      }
-      if (a.out_idx)
-        for (int r = lane; r < a.top_k; r += 64)
-          a.out_idx[(size_t)n * a.top_k + r] = r < cnt ? (uint32_t)r : 0xFFFFFFFFu;
+      if (a.q_pnc)
+        for (int i = lane; i < a.dk; i += 64) a.q_pnc[(size_t)n * a.dk + i] = sq[i];
     }
-    wave_sync();
+    __syncthreads();
+    // ---- distances: 64-slot blocks dealt round the query's waves ----
+    float q_sq = 0.0f;
+    if (live && cnt > 0) {
+      q_sq = bank_norm_sq(sq, a.dk);
+      float local_min = FLT_MAX;
+      for (int s = lane + 64 * half; s < cnt; s += 64 * RETRIEVE_WPQ) {
+        const float dist = poincare_dist(sq, q_sq, a.keys + (size_t)s * a.dk, a.norm_sq[s], a.dk);
+        sdist[s] = dist;
+        local_min = fminf(local_min, dist);
+      }
+      const float wmin = wave_min(local_min);
+      if (lane == 0) spart[pair][half] = wmin;
+    }
+    __syncthreads();
+    if (live && half == 0) {
+      if (cnt == 0) {
+        for (int s = lane; s < a.capacity; s += 64) put_weight(a, n, s, 0.0f);
+        if (a.out_val)
+          for (int j = lane; j < a.dv; j += 64) a.out_val[(size_t)n * a.dv + j] = 0.0f;
+        if (a.out_min && lane == 0) a.out_min[n] = 0.0f;
+        if (a.out_idx)
+          for (int r = lane; r < a.top_k; r += 64) a.out_idx[(size_t)n * a.top_k + r] = 0xFFFFFFFFu;
+      } else {
+        float min_dist = spart[pair][0];
+        for (int h = 1; h < RETRIEVE_WPQ; ++h) min_dist = fminf(min_dist, spart[pair][h]);
+        if (a.out_min && lane == 0) a.out_min[n] = min_dist;
+
+        if (a.top_k > 0 && a.top_k < cnt) {
+          // ---- exact top-k by (distance bits, slot) (src/memory.rs:380-392) ----
+          const int k = a.top_k;
+          for (int r = 0; r < k; ++r) {
+            unsigned long long best = ~0ull;
+            for (int s = lane; s < cnt; s += 64) {
+              const uint32_t bits = __float_as_uint(sdist[s]);
+              const unsigned long long key = ((unsigned long long)bits << 32) | (unsigned)s;
+              bool taken = false;
+              for (int p = 0; p < r; ++p) taken |= ssel[pair][p] == (uint32_t)s;
+              if (!taken && key < best) best = key;
+            }
+            best = wave_min_u64(best);
+            if (lane == 0) ssel[pair][r] = (uint32_t)(best & 0xFFFFFFFFu);
+            wave_sync();
+          }
+          if (lane == 0) {  // ascending slot order
+            for (int x = 1; x < k; ++x) {
+              const uint32_t v = ssel[pair][x];
+              int y = x - 1;
+              while (y >= 0 && ssel[pair][y] > v) {
+                ssel[pair][y + 1] = ssel[pair][y];
+                --y;
+              }
+              ssel[pair][y + 1] = v;
+            }
+          }
+          wave_sync();
+          // Hybrid read: (e * gate) * decay per live slot, unless every live
+          // weight is zero (then the plain softmax, src/memory.rs:640-650).
+          auto hyb_w = [&](int s, float e) { return (e * a.hgate[s]) * hybrid_decay(a, s, n); };
+          bool hyb = a.hgate != nullptr;
+          float sum = 0.0f;
+          if (hyb) {
+            for (int r = 0; r < k; ++r) {
+              const int s = ssel[pair][r];
+              sum += hyb_w(s, expf((min_dist - sdist[s]) / a.tau));
+            }
+            hyb = sum != 0.0f;
+          }
+          if (!hyb) {
+            sum = 0.0f;
+            for (int r = 0; r < k; ++r) sum += expf((min_dist - sdist[ssel[pair][r]]) / a.tau);
+          }
+          auto weight_of = [&](int s) {
+            const float e = expf((min_dist - sdist[s]) / a.tau);
+            return (hyb ? hyb_w(s, e) : e) / sum;
+          };
+          if (a.weights || a.weights16) {
+            for (int s = lane; s < a.capacity; s += 64) {
+              bool chosen = false;
+              for (int r = 0; r < k; ++r) chosen |= ssel[pair][r] == (uint32_t)s;
+              put_weight(a, n, s, chosen ? weight_of(s) : 0.0f);
+            }
+          }
+          if (a.out_idx)
+            for (int r = lane; r < k; r += 64) a.out_idx[(size_t)n * k + r] = ssel[pair][r];
+          if (a.out_val) {
+            for (int j = lane; j < a.dv; j += 64) {
+#pragma clang fp contract(off)
+              float acc = 0.0f;
+              for (int r = 0; r < k; ++r) {
+                const uint32_t s = ssel[pair][r];
+                const float w = weight_of((int)s);
+                acc = acc + w * a.values[(size_t)s * a.dv + j];
+              }
+              a.out_val[(size_t)n * a.dv + j] = acc;
+            }
+          }
+        } else {
+          // ---- full soft read (src/memory.rs:409-425); hybrid: every slot live ----
+          float part = 0.0f, part_h = 0.0f;
+          for (int s = lane; s < cnt; s += 64) {
+            const float e = expf((min_dist - sdist[s]) / a.tau);
+            sdist[s] = e;
+            part += e;
+            if (a.hgate) part_h += (e * a.hgate[s]) * hybrid_decay(a, s, n);
+          }
+          const float sum_p = wave_sum(part);
+          const float sum_h = a.hgate ? wave_sum(part_h) : 0.0f;
+          const bool hyb = a.hgate && sum_h != 0.0f;
+          const float sum = hyb ? sum_h : sum_p;
+          wave_sync();
+          for (int s = lane; s < a.capacity; s += 64) {
+            float w = 0.0f;
+            if (s < cnt) w = (hyb ? (sdist[s] * a.hgate[s]) * hybrid_decay(a, s, n) : sdist[s]) / sum;
+            if (s < cnt) sdist[s] = w;
+            put_weight(a, n, s, w);
+          }
+          wave_sync();
+          if (a.out_val) {
+            for (int j = lane; j < a.dv; j += 64) {
+              float acc = 0.0f;
+              for (int s = 0; s < cnt; ++s) acc = fmaf(sdist[s], a.values[(size_t)s * a.dv + j], acc);
+              a.out_val[(size_t)n * a.dv + j] = acc;
+            }
+          }
+          if (a.out_idx)
+            for (int r = lane; r < a.top_k; r += 64)
+              a.out_idx[(size_t)n * a.top_k + r] = r < cnt ? (uint32_t)r : 0xFFFFFFFFu;
+        }
+      }
+    }
+    // The next query's projection and distances overwrite this one's.
+    __syncthreads();
   }
 }
 
@@ -1486,10 +1510,10 @@ Status launch_retrieve(hipStream_t stream, const RetrieveArgs& a) {
     return Status::Ok();
   }
   const int dk_pad = (a.dk + 3) & ~3;
-  const size_t lds = (size_t)4 * (dk_pad + a.capacity) * sizeof(float);
+  const size_t lds = (size_t)RETRIEVE_QPB * (dk_pad + a.capacity) * sizeof(float);
   if (lds > 128 * 1024) return Status::Invalid("retrieve: d_key + capacity too large for LDS");
-  int blocks = (a.n + 3) / 4;
-  if (blocks > 4096) blocks = 4096;
+  int blocks = (a.n + RETRIEVE_QPB - 1) / RETRIEVE_QPB;
+  if (blocks > 8192) blocks = 8192;
   retrieve_kernel<<<blocks, 256, lds, stream>>>(a);
   PSSA_LAUNCH_CHECK("retrieve");
   return Status::Ok();

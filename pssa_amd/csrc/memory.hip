@@ -300,7 +300,9 @@ __global__ __launch_bounds__(256) void retrieve_kernel(RetrieveArgs a) {
 // f32 values are exact in f64 and each sum has relative error below
 // d_key * 2^-53, so the absolute error of |q - k|^2 stays near 1e-14 (the
 // distance of even coincident points moves by < 1e-6).  One key element read
-// from LDS and converted once serves QG queries' fused multiply-adds.
+// from LDS and converted once serves QG queries' fused multiply-adds; the
+// query values enter them as wave-uniform f64 operands (readlane from the
+// lane that holds that dimension).
 //
 // Only the soft weights depend on the distances (no ranking), so the rest is
 // evaluated in f32 with the hardware square root, log2 and exp2:
@@ -567,16 +569,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int g = 0; g < QG; ++g)
           qvg[g] = a.q[(size_t)(c0 + (g < ng ? g0 + g : g0)) * a.ld_q + min(lane, dk - 1)];
       }
+      // Lane i keeps dimension i of each projected query, widened to f64;
+      // the products take it as a wave-uniform operand by readlane (no LDS
+      // round trip per query and dimension).
+      double pvd[QG];
 #pragma unroll
       for (int g = 0; g < QG; ++g) {
         const int src = g < ng ? g0 + g : g0;
         const float pv = (float)((double)qvg[g] * (one ? scale : readlane_f64(scale, src)));
-        if (lane < dk) {
-          pw[g * dk + lane] = pv;
-          if (a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;
-        }
+        pvd[g] = (double)pv;
+        if (lane < dk && a.q_pnc && g < ng) a.q_pnc[(size_t)(c0 + src) * dk + lane] = pv;
       }
-      wave_sync();
       double dot[QG][SPL];
 #pragma unroll
       for (int g = 0; g < QG; ++g)
@@ -591,7 +594,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int j = 0; j < SPL; ++j) kv[j] = (double)kr[64 * j];
 #pragma unroll
         for (int g = 0; g < QG; ++g) {
-          const double pg = (double)pw[g * dk + i];
+          const double pg = readlane_f64(pvd[g], i);
 #pragma unroll
           for (int j = 0; j < SPL; ++j) dot[g][j] = fma(pg, kv[j], dot[g][j]);
         }

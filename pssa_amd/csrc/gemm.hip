@@ -431,9 +431,13 @@ __device__ __forceinline__ void epi_tile_staged(const EpiParams& ep, const f32x1
     }
     const float p4[4] = {p.x, p.y, p.z, p.w}, q4[4] = {q.x, q.y, q.z, q.w};
     float v[4], tp;
+    // Segments: the launch stages a segment epilogue only when every segment
+    // boundary falls on a 32-column edge, so the block's first column names
+    // the segment of all 32 (a uniform branch, no per-element compare).
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      v[e] = epi_value<KIND>(ep, acc[g * 4 + e], p4[e], q4[e], adv[g * 4 + e], n32 + half * 4 + g * 8 + e, tp);
+      v[e] = epi_value<KIND>(ep, acc[g * 4 + e], p4[e], q4[e], adv[g * 4 + e],
+                             KIND == EPI_SEGMENTS ? n32 : n32 + half * 4 + g * 8 + e, tp);
     *reinterpret_cast<float4*>(sb + pos) = make_float4(v[0], v[1], v[2], v[3]);
   }
   __builtin_amdgcn_wave_barrier();
@@ -1090,8 +1094,11 @@ static void launch_lds_kind(hipStream_t stream, int kind, dim3 grid, const uint1
   constexpr size_t lds = gemm_lds_bytes(NW);
   static_assert(lds <= 64 * 1024, "the ring fits the default dynamic LDS limit");
   // 128 x 128 tiles stage their epilogues through LDS (epi_tile_staged):
-  // vector operands, N % 4 == 0, no tap.
-  const bool stg = NW == 2 && ve && N % 4 == 0 && !ep.tap;
+  // vector operands, N % 4 == 0, no tap, and segment boundaries on 32-column
+  // edges (or at N and past it).
+  bool seg32 = true;
+  for (int i = 0; i < 4; ++i) seg32 = seg32 && (ep.seg[i] % 32 == 0 || ep.seg[i] >= N);
+  const bool stg = NW == 2 && ve && N % 4 == 0 && !ep.tap && (kind != EPI_SEGMENTS || seg32);
 #define PSSA_GEMM_LDS_CASE(KD)                                                                        \
   case KD:                                                                                            \
     if (stg && KD != EPI_SEGMENTS_TAP)                                                                \

@@ -626,28 +626,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   int mt, nt;
   tile_coords(tile, tilesM, tilesN, mt, nt);
   const int m0 = mt * BMt, n0 = nt * BNt;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index as a uniform value: the LDS slab addresses and the
+  // operand panel bases below are then scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Source rows of this wave's DMA instructions (row-major slab: A rows then B rows).
+  // Source rows of this wave's DMA instructions (row-major slab: A rows then
+  // B rows), as a 32-bit byte offset per lane from the tile's row panel in A
+  // or weight panel in B (a panel spans at most 128 rows), so that a slab's
+  // loads add K to a scalar base and read at a fixed per-lane offset.
   const int lr = lane >> 2, pc = lane & 3;
-  const uint16_t* src[BPW];
+  const char* const pa = reinterpret_cast<const char*>(A + (size_t)m0 * lda);
+  const char* const pb = reinterpret_cast<const char*>(B + (size_t)n0 * ldb);
+  uint32_t src_off[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int row = (wave + 4 * i) * RPI + lr;
     const int lc = pc ^ slab_swizzle(row);
     if (row < BMt)
-      src[i] = A + (size_t)min(m0 + row, M - 1) * lda + lc * 8;
+      src_off[i] = (uint32_t)(((size_t)(min(m0 + row, M - 1) - m0) * lda + lc * 8) * 2);
     else
-      src[i] = B + (size_t)min(n0 + row - BMt, N - 1) * ldb + lc * 8;
+      src_off[i] = (uint32_t)(((size_t)(min(n0 + row - BMt, N - 1) - n0) * ldb + lc * 8) * 2);
   }
   auto issue = [&](int slot, int k0) {
 #pragma unroll
-    for (int i = 0; i < BPW; ++i)
+    for (int i = 0; i < BPW; ++i) {
+      // Rows below BMt belong to A (wave + 4 i is uniform, so is the choice).
+      const char* base = ((wave + 4 * i) * RPI < BMt ? pa : pb) + 2 * (size_t)k0;
       __builtin_amdgcn_global_load_lds(
-          (const void*)(src[i] + k0),
+          (const void*)(base + src_off[i]),
           (__attribute__((address_space(3))) void*)(&sm[slot][((wave + 4 * i) * RPI) * BK]), 16, 0, 0);
+    }
   };
 
   f32x16_t acc[MT][NW];
@@ -663,32 +673,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   for (int st = 0; st < S - 1; ++st)
     if (st < nk) issue(st, st * BK);
   const int fr = slab_swizzle(l32);
-  for (int kt = 0; kt < nk; ++kt) {
-    // Slab kt is complete once at most the slabs issued after it are in flight.
-    static_assert(S == 3, "the wait below assumes one slab issued after the current one");
-    if (kt + 1 < nk)
-      __builtin_amdgcn_s_waitcnt(BPW | (0x7 << 4) | (0xF << 8));  // vmcnt(BPW)
-    else
-      __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));        // vmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    if (kt + S - 1 < nk) issue((kt + S - 1) % S, (kt + S - 1) * BK);
-    const uint16_t* a = sm[kt % S];
-    const uint16_t* b = sm[kt % S] + BMt * BK;
+  // The ring slot of slab kt is kt % S: stepping S slabs per outer iteration
+  // makes it a constant of each unrolled step, so every fragment address is
+  // a per-lane offset plus an immediate.
+  for (int kt0 = 0; kt0 < nk; kt0 += S) {
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int ch = (kk * 2 + half) ^ fr;
-      bf16x8_t fa[MT], fb[NW];
+    for (int j = 0; j < S; ++j) {
+      const int kt = kt0 + j;
+      if (kt >= nk) break;
+      // Slab kt is complete once at most the slabs issued after it are in flight.
+      static_assert(S == 3, "the wait below assumes one slab issued after the current one");
+      if (kt + 1 < nk)
+        __builtin_amdgcn_s_waitcnt(BPW | (0x7 << 4) | (0xF << 8));  // vmcnt(BPW)
+      else
+        __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8));        // vmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      if (kt + S - 1 < nk) issue((j + S - 1) % S, (kt + S - 1) * BK);
+      const uint16_t* a = sm[j];
+      const uint16_t* b = sm[j] + BMt * BK;
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
-        fa[t] = *reinterpret_cast<const bf16x8_t*>(a + (wm * MT * 32 + t * 32 + l32) * BK + ch * 8);
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int ch = (kk * 2 + half) ^ fr;
+        bf16x8_t fa[MT], fb[NW];
 #pragma unroll
-      for (int u = 0; u < NW; ++u)
-        fb[u] = *reinterpret_cast<const bf16x8_t*>(b + (wn * NW * 32 + u * 32 + l32) * BK + ch * 8);
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
+        for (int t = 0; t < MT; ++t)
+          fa[t] = *reinterpret_cast<const bf16x8_t*>(a + (wm * MT * 32 + t * 32 + l32) * BK + ch * 8);
 #pragma unroll
         for (int u = 0; u < NW; ++u)
-          acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[u], fa[t], acc[t][u], 0, 0, 0);
+          fb[u] = *reinterpret_cast<const bf16x8_t*>(b + (wn * NW * 32 + u * 32 + l32) * BK + ch * 8);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int u = 0; u < NW; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[u], fa[t], acc[t][u], 0, 0, 0);
+      }
     }
   }
 

@@ -912,32 +912,40 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_few_kernel(const uint16_t* 
   // Instruction i of this wave fills slab rows (wave + NWV*i)*8 .. +7: lane L
   // writes position L % 8 of row L / 8 of those, so it loads that row's
   // chunk (L % 8) ^ swizzle.
-  const uint16_t* src[BPW];
+  // As 32-bit byte offsets from the tile's row panel in A or weight panel
+  // in B, so that a slab's loads add K to a scalar base.
+  const char* const pa = reinterpret_cast<const char*>(A + (size_t)m0 * lda);
+  const char* const pb = reinterpret_cast<const char*>(B + (size_t)n0 * ldb);
+  uint32_t src_off[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int row = (wave + NWV * i) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
-    src[i] = (row < BMt ? A + (size_t)min(m0 + row, M - 1) * lda
-                        : B + (size_t)min(n0 + row - BMt, N - 1) * ldb) + c * 8;
+    src_off[i] = (uint32_t)(2 * ((row < BMt ? (size_t)(min(m0 + row, M - 1) - m0) * lda
+                                            : (size_t)(min(n0 + row - BMt, N - 1) - n0) * ldb) + c * 8));
   }
   const int nk = K / 64;
   // Slabs past the end reload the last one into the slot just read, which
-  // no later step reads, so every step waits for the same count.
-  auto issue = [&](int kt) {
+  // no later step reads, so every step waits for the same count.  `slot` is
+  // kt % S, a constant at every call.
+  auto issue = [&](int kt, int slot) {
     const int k0 = min(kt, nk - 1) * 64;
-    uint16_t* dst = gemm_few_smem + (kt % S) * SLAB + wave * 8 * 64;
+    uint16_t* dst = gemm_few_smem + slot * SLAB + wave * 8 * 64;
 #pragma unroll
-    for (int i = 0; i < BPW; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+    for (int i = 0; i < BPW; ++i) {
+      // Whether instruction i fills A or B rows is the same for every lane.
+      const char* base = ((wave + NWV * i) * 8 < BMt ? pa : pb) + 2 * (size_t)k0;
+      __builtin_amdgcn_global_load_lds((const void*)(base + src_off[i]),
                                        (__attribute__((address_space(3))) void*)(dst + NWV * i * 8 * 64), 16,
                                        0, 0);
+    }
   };
 
   f32x16_t acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
 #pragma unroll
-  for (int kt = 0; kt < S - 1; ++kt) issue(kt);
+  for (int kt = 0; kt < S - 1; ++kt) issue(kt, kt);
   // The epilogue's row operands (and the z_raw adapter's first fragments)
   // load now, behind the first slabs, rather than after the products.
   const int row = m0 + wm * 32 + l32, n32 = n0 + wn * 32;
@@ -950,26 +958,33 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_few_kernel(const uint16_t* 
   }
   const int ra = wm * 32 + l32, rb = BMt + wn * 32 + l32;  // slab rows of this lane's fragments
   const int sa = (ra >> 1) & 7, sb = (rb >> 1) & 7;
-  for (int kt = 0; kt < nk; ++kt) {
-    // This wave's part of slab kt has landed once at most the S - 2 slabs
-    // issued after it are in flight; the barrier then covers every wave's
-    // part, and every wave has finished reading the slot refilled next.
-    __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
-    __builtin_amdgcn_s_barrier();
-    issue(kt + S - 1);
-    const uint16_t* sl = gemm_few_smem + (kt % S) * SLAB;
-    // All eight fragments of the slab are read before the first product, so
-    // one LDS round trip precedes the four dependent MFMAs rather than each.
-    bf16x8_t fa[4], fb[4];
+  // S slabs per outer step, so each step's ring slot is a constant.
+  for (int kt0 = 0; kt0 < nk; kt0 += S) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = 2 * kk + half;
-      fa[kk] = *reinterpret_cast<const bf16x8_t*>(sl + ra * 64 + (c ^ sa) * 8);
-      fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+    for (int j = 0; j < S; ++j) {
+      const int kt = kt0 + j;
+      if (kt >= nk) break;
+      // This wave's part of slab kt has landed once at most the S - 2 slabs
+      // issued after it are in flight; the barrier then covers every wave's
+      // part, and every wave has finished reading the slot refilled next.
+      __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
+      __builtin_amdgcn_s_barrier();
+      issue(kt + S - 1, (j + S - 1) % S);
+      const uint16_t* sl = gemm_few_smem + j * SLAB;
+      // All eight fragments of the slab are read before the first product,
+      // so one LDS round trip precedes the four dependent MFMAs rather than
+      // each.
+      bf16x8_t fa[4], fb[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int c = 2 * kk + half;
+        fa[kk] = *reinterpret_cast<const bf16x8_t*>(sl + ra * 64 + (c ^ sa) * 8);
+        fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the reloads past the end
   epi_tile_store<uint16_t, KIND>(ep, acc, row, n32, M, N, vec_epi, half, l32,

@@ -1209,27 +1209,31 @@ __global__ __launch_bounds__(256) void gemm_norm_kernel(const float* __restrict_
   int mt, nt;
   tile_coords(xcd_tile(blockIdx.x, tilesM * tilesN), tilesM, tilesN, mt, nt);
   const int m0 = mt * 32, n0 = nt * NORM_BN;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, l32 = lane & 31;
 
-  const uint16_t* src[BPW];
+  // Weight rows as 32-bit byte offsets from the tile's weight panel, so that
+  // a slab's loads add K to a scalar base; `slot` is kt % S, a constant at
+  // every call.
+  const char* const pb = reinterpret_cast<const char*>(B + (size_t)n0 * ldb);
+  uint32_t src_off[BPW];
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int row = (wave + NWV * i) * 8 + (lane >> 3);
-    src[i] = B + (size_t)min(n0 + row, N - 1) * ldb + ((lane & 7) ^ ((row >> 1) & 7)) * 8;
+    src_off[i] = (uint32_t)(2 * ((size_t)(min(n0 + row, N - 1) - n0) * ldb + ((lane & 7) ^ ((row >> 1) & 7)) * 8));
   }
   const int nk = d / 64;
-  auto issue = [&](int kt) {
+  auto issue = [&](int kt, int slot) {
     const int k0 = min(kt, nk - 1) * 64;
-    uint16_t* dst = gemm_norm_smem + (kt % S) * SLAB + wave * 8 * 64;
+    uint16_t* dst = gemm_norm_smem + slot * SLAB + wave * 8 * 64;
 #pragma unroll
     for (int i = 0; i < BPW; ++i)
-      __builtin_amdgcn_global_load_lds((const void*)(src[i] + k0),
+      __builtin_amdgcn_global_load_lds((const void*)(pb + 2 * (size_t)k0 + src_off[i]),
                                        (__attribute__((address_space(3))) void*)(dst + NWV * i * 8 * 64), 16,
                                        0, 0);
   };
 #pragma unroll
-  for (int kt = 0; kt < S - 1; ++kt) issue(kt);
+  for (int kt = 0; kt < S - 1; ++kt) issue(kt, kt);
 
   // The normalised rows: wave w takes tile rows 8w .. 8w + 7.
   float4 g[RMS_V4], bt[RMS_V4];
@@ -1276,21 +1280,27 @@ __global__ __launch_bounds__(256) void gemm_norm_kernel(const float* __restrict_
   for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
   const uint16_t* prow = panel + (size_t)l32 * d;
   const int sp = l32 & 15, rb = wave * 32 + l32, sb = (rb >> 1) & 7;
-  for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
-    __builtin_amdgcn_s_barrier();
-    issue(kt + S - 1);
-    const uint16_t* sl = gemm_norm_smem + (kt % S) * SLAB;
-    bf16x8_t fa[4], fb[4];
+  // S slabs per outer step, so each step's ring slot is a constant.
+  for (int kt0 = 0; kt0 < nk; kt0 += S) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = 2 * kk + half;
-      fa[kk] = *reinterpret_cast<const bf16x8_t*>(prow + ((kt * 8 + c) ^ sp) * 8);
-      fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+    for (int j = 0; j < S; ++j) {
+      const int kt = kt0 + j;
+      if (kt >= nk) break;
+      __builtin_amdgcn_s_waitcnt(vmcnt_only((S - 2) * BPW));
+      __builtin_amdgcn_s_barrier();
+      issue(kt + S - 1, (j + S - 1) % S);
+      const uint16_t* sl = gemm_norm_smem + j * SLAB;
+      bf16x8_t fa[4], fb[4];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int c = 2 * kk + half;
+        fa[kk] = *reinterpret_cast<const bf16x8_t*>(prow + ((kt * 8 + c) ^ sp) * 8);
+        fb[kk] = *reinterpret_cast<const bf16x8_t*>(sl + rb * 64 + (c ^ sb) * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[kk], fa[kk], acc, 0, 0, 0);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // the reloads past the end
   epilogue_32x32<uint16_t, KIND>(ep, acc, m0 + l32, n0 + wave * 32, M, N, vec_epi, half, l32);

@@ -26,6 +26,19 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return bf16_bits_dev(f); }
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return bf16x2_bits(lo, hi); }
 
+// ln(u) for finite u >= 1: the hardware log2 times ln 2 taken in two parts
+// (ln 2 = C_HI + C_LO), the instruction sequence __logf compiles to for
+// normal finite inputs, without its rescaling of denormal inputs and its
+// infinity check, which cannot apply here.
+__device__ __forceinline__ float ln_ge1(float u) {
+#pragma clang fp contract(off)
+  constexpr float C_HI = 0x1.62e42ep-1f, C_LO = 0x1.efa39ep-25f;
+  const float l2 = __builtin_amdgcn_logf(u);
+  const float r = l2 * C_HI;
+  const float e = __builtin_fmaf(l2, C_LO, __builtin_fmaf(l2, C_HI, -r));
+  return __builtin_fmaf(C_HI, l2, e);
+}
+
 // softplus(x) = x > 20 ? x : ln(1 + e^x) (src/linalg.rs:548-551).  ln(1+t) is
 // evaluated as ln(u) * t / (u - 1) with u = 1 + t, which cancels the rounding
 // of u (relative error a few ulp), and as t - t^2/2 for t < 2^-12.
@@ -35,7 +48,7 @@ __device__ __forceinline__ float softplus_f(float x) {
   const float t = __expf(x);
   if (t < 2.44140625e-4f) return t - 0.5f * t * t;
   const float u = 1.0f + t;
-  return __logf(u) * (t * __builtin_amdgcn_rcpf(u - 1.0f));
+  return ln_ge1(u) * (t * __builtin_amdgcn_rcpf(u - 1.0f));
 }
 // sigmoid(x) = 1 / (1 + e^-x) (src/linalg.rs:553-555), with the hardware
 // reciprocal (1 ulp).
